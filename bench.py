@@ -1,0 +1,311 @@
+#!/usr/bin/env python
+"""Decode-step benchmark on one MI355X.
+
+A step is one pass of the hot path over one batch: fused RoPE + KV append of
+one new token per sequence (tt_rope_append_*) followed by GQA split-K decode
+attention over each sequence's L_b + 1 cached tokens (tt_gqa_decode_attn_*).
+Inputs are synthetic (seed 1337) and resident in HBM before the timed region.
+
+Default workload (the metric's batch-64 case):
+ragged paged bf16 decode attention, B = 64, 32 q heads / 8 KV heads, D = 128,
+L_b ~ U[128, 16384], page size 16, page table = seeded random permutation of
+the physical pages. --config c2 / c4 select configs 2 and 4.
+
+value = algorithmic bytes per step / time per step (GB/s, 1 GB = 1e9 B), with
+algorithmic bytes = unique K/V bytes read (+ fp8 scales) + q/out/new-token/page
+table I/O. The roofline object covers the decode-attention operator (the
+split kernel and its combine kernel) timed alone with HIP events on the
+stream it runs on. The CPU baseline times the reference's own op sequence
+(torch on the host, H_q-expanded cache, per sequence) on a bounded sample of
+the same sequences.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+METRIC = "decode-attn HBM GB/s (% of peak) + greedy decode tokens/sec at batch 64"
+
+CONFIGS = {
+    "c2": dict(name="C2 uniform contiguous bf16 decode attention", batch=32, hq=32, hkv=8, head_dim=128,
+               lo=4096, hi=4096, page=16, paged=False, fp8=False),
+    "c3": dict(name="C3 ragged paged bf16 GQA decode step", batch=64, hq=32, hkv=8, head_dim=128,
+               lo=128, hi=16384, page=16, paged=True, fp8=False),
+    "c4": dict(name="C4 ragged paged fp8-e4m3 GQA decode step", batch=128, hq=32, hkv=8, head_dim=128,
+               lo=1024, hi=32768, page=16, paged=True, fp8=True),
+}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    p.add_argument("--seed", type=int, default=1337)
+    p.add_argument("--split-tokens", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of timed CPU-baseline work")
+    return p.parse_args()
+
+
+def build_workload(cfg, seed, torch, ops):
+    dev = torch.device("cuda")
+    B, hq, hkv, D, P = cfg["batch"], cfg["hq"], cfg["hkv"], cfg["head_dim"], cfg["page"]
+    g = torch.Generator().manual_seed(seed)
+    if cfg["lo"] == cfg["hi"]:
+        ctx = torch.full((B,), cfg["lo"], dtype=torch.int64)
+    else:
+        ctx = torch.randint(cfg["lo"], cfg["hi"] + 1, (B,), generator=g)
+    total = ctx + 1  # tokens attended after the append
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    if cfg["paged"]:
+        need = (total + P - 1) // P
+        n_phys = int(need.sum())
+        perm = torch.randperm(n_phys, generator=g).to(torch.int32)
+        max_pages = int(need.max())
+        table = torch.full((B, max_pages), -1, dtype=torch.int32)
+        off = 0
+        for b in range(B):
+            n = int(need[b])
+            table[b, :n] = perm[off:off + n]
+            off += n
+        page_table = table.to(dev)
+        numel = n_phys * hkv * P * D
+        strides = (0, hkv * P * D, P * D)
+        capacity = max_pages * P
+        num_pages = n_phys
+    else:
+        cap = int(math.ceil(int(total.max()) / P) * P)
+        pages = cap // P
+        page_table = None
+        numel = B * hkv * pages * P * D
+        strides = (hkv * pages * P * D, P * D, pages * P * D)
+        capacity = cap
+        num_pages = 0
+    kind = "fp8" if cfg["fp8"] else "bf16"
+    if cfg["fp8"]:
+        k_store = torch.empty(numel, dtype=torch.uint8, device=dev)
+        v_store = torch.empty(numel, dtype=torch.uint8, device=dev)
+        k_scale = torch.empty(numel // D, dtype=torch.float32, device=dev)
+        v_scale = torch.empty(numel // D, dtype=torch.float32, device=dev)
+        chunk = 1 << 24  # rows of D per chunk
+        rows = numel // D
+        for dst, sc in ((k_store, k_scale), (v_store, v_scale)):
+            for r0 in range(0, rows, chunk):
+                r1 = min(rows, r0 + chunk)
+                x = torch.randn(r1 - r0, D, generator=gd, device=dev, dtype=torch.bfloat16).float()
+                s = x.abs().amax(dim=-1) / 448.0
+                codes = torch.where(s[:, None] > 0, x / torch.where(s > 0, s, 1.0)[:, None], 0.0)
+                dst[r0 * D:r1 * D] = codes.to(ops.FP8_DTYPE).view(torch.uint8).reshape(-1)
+                sc[r0:r1] = s
+                del x, codes
+    else:
+        k_store = torch.randn(numel, generator=gd, device=dev, dtype=torch.bfloat16)
+        v_store = torch.randn(numel, generator=gd, device=dev, dtype=torch.bfloat16)
+        k_scale = v_scale = None
+    layout = ops.KVLayout(k=k_store, v=v_store, strides=strides, num_heads=hkv, head_dim=D, page_size=P,
+                          capacity=capacity, kind=kind, page_table=page_table, num_pages=num_pages,
+                          k_scale=k_scale, v_scale=v_scale)
+    q_in = torch.randn(B, 1, hq, D, generator=gd, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    k_in = torch.randn(B, 1, hkv, D, generator=gd, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    v_in = torch.randn(B, 1, hkv, D, generator=gd, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    table_rows = int(total.max()) + 1
+    rope = ops.build_rope_table(table_rows, D, dtype=torch.bfloat16, device=dev)
+    return dict(ctx=ctx, total=total, layout=layout, q_in=q_in, k_in=k_in, v_in=v_in, rope=rope,
+                positions=ctx.to(torch.int32).to(dev), seq_lens=total.to(torch.int32).to(dev),
+                max_len=int(total.max()))
+
+
+def algorithmic_bytes(cfg, total):
+    """Bytes the step must move at minimum (SURVEY 8d accounting)."""
+    B, hq, hkv, D, P = cfg["batch"], cfg["hq"], cfg["hkv"], cfg["head_dim"], cfg["page"]
+    e = 1 if cfg["fp8"] else 2
+    tokens = int(total.sum())
+    kv = tokens * hkv * D * e * 2
+    scales = tokens * hkv * 4 * 2 if cfg["fp8"] else 0
+    pages = int(((total + P - 1) // P).sum()) * 4 if cfg["paged"] else 0
+    q_out = B * hq * D * 2 * 2
+    new_kv = B * hkv * D * (2 + e) * 2
+    attn_bytes = kv + scales + pages + q_out + B * 4
+    step_bytes = attn_bytes + B * hq * D * 2 * 2 + new_kv  # + rope q in/out
+    return step_bytes, attn_bytes, tokens
+
+
+def cpu_baseline(cfg, wl, torch, budget_s):
+    """Reference op sequence on the host, one sequence at a time (the reference
+    has one batch-wide length, so a ragged batch runs as batch-1 caches)."""
+    from oracle import ref_path
+
+    threads = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        threads = min(threads, int(env))
+    torch.set_num_threads(threads)
+    layout = wl["layout"]
+    hq, hkv, D, P = cfg["hq"], cfg["hkv"], cfg["head_dim"], cfg["page"]
+    rep = hq // hkv
+    total_time = 0.0
+    total_bytes = 0
+    n_seq = 0
+    tokens = 0
+    for b in range(cfg["batch"]):
+        L = int(wl["ctx"][b])
+        # gather sequence b's cached K/V (untimed setup): [L, hkv, D]
+        pos = torch.arange(L, device="cuda")
+        if layout.page_table is not None:
+            phys = layout.page_table[b].long()[pos // P]
+            base = phys * layout.strides[1] + (pos % P) * D
+        else:
+            base = b * layout.strides[0] + (pos // P) * layout.strides[1] + (pos % P) * D
+        idx = base[:, None, None] + (torch.arange(hkv, device="cuda") * layout.strides[2])[None, :, None] \
+            + torch.arange(D, device="cuda")[None, None, :]
+        if cfg["fp8"]:
+            sidx = (base[:, None] + (torch.arange(hkv, device="cuda") * layout.strides[2])[None, :]) // D
+            k = (layout.k[idx].view(torch.float8_e4m3fn).float() * layout.k_scale[sidx][..., None]).to(torch.bfloat16)
+            v = (layout.v[idx].view(torch.float8_e4m3fn).float() * layout.v_scale[sidx][..., None]).to(torch.bfloat16)
+        else:
+            k = layout.k[idx]
+            v = layout.v[idx]
+        k = k.permute(1, 0, 2).unsqueeze(0).cpu()  # [1, hkv, L, D]
+        v = v.permute(1, 0, 2).unsqueeze(0).cpu()
+        cache = ref_path.LayerPagedKVCache(1, hq, D, L + 1, P, torch.device("cpu"), torch.bfloat16)
+        cache.append(k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1))
+        q = wl["q_in"][b:b + 1].cpu()
+        kn = wl["k_in"][b:b + 1].cpu()
+        vn = wl["v_in"][b:b + 1].cpu()
+        del k, v
+        t0 = time.perf_counter()
+        y = ref_path.decode_attention_step(q, kn, vn, cache, hkv, position=L)
+        dt = time.perf_counter() - t0
+        assert y.shape == (1, hq, 1, D)
+        total_time += dt
+        e = 1 if cfg["fp8"] else 2
+        total_bytes += (L + 1) * hkv * D * e * 2 + ((L + 1) * hkv * 8 if cfg["fp8"] else 0)
+        tokens += L + 1
+        n_seq += 1
+        del cache
+        if total_time >= budget_s:
+            break
+    return {
+        "value": round(total_bytes / total_time / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n_seq} of {cfg['batch']} sequences ({tokens} cached tokens), one decode step each through "
+                   f"the reference op sequence (rope_impl, gqa_impl, H_q-expanded LayerPagedKVCache append/get_kv, "
+                   f"mask, SDPA) in torch bf16 on the host; bytes counted as for the GPU (unique K/V)"
+                   + ("; fp8 cache dequantised to bf16, the reference has no fp8" if cfg["fp8"] else "")),
+        "seconds": round(total_time, 3),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported in this build "
+              "(the multi-GPU decode layout is a design note, not a measured path)", file=sys.stderr)
+        return 2
+    import torch
+
+    from tinytron_amd import ops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (no CPU fallback)", file=sys.stderr)
+        return 1
+    cfg = CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    wl = build_workload(cfg, args.seed, torch, ops)
+    B, hq, D = cfg["batch"], cfg["hq"], cfg["head_dim"]
+    layout = wl["layout"]
+    q_rot = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(B, hq, D, dtype=torch.bfloat16, device="cuda")
+    ws = ops.Workspace("cuda")
+    split = args.split_tokens
+
+    # a plain copy of known size, for scaling rocprof FETCH/WRITE counters
+    calib = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")
+    calib_dst = torch.empty_like(calib)
+    calib_dst.copy_(calib)
+
+    def step():
+        ops.rope_append(wl["q_in"], wl["k_in"], wl["v_in"], wl["rope"], wl["positions"], layout, q_out=q_rot)
+        ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
+                             split_tokens=split, workspace=ws)
+
+    def attn_only():
+        ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
+                             split_tokens=split, workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / max(args.steps, 1)
+
+    # the dominant operator alone, same stream, same events
+    ev2 = torch.cuda.Event(enable_timing=True)
+    ev3 = torch.cuda.Event(enable_timing=True)
+    ev2.record()
+    for _ in range(args.steps):
+        attn_only()
+    ev3.record()
+    torch.cuda.synchronize()
+    attn_ms = ev2.elapsed_time(ev3) / max(args.steps, 1)
+
+    step_bytes, attn_bytes, tokens = algorithmic_bytes(cfg, wl["total"])
+    value = step_bytes / (ms * 1e-3) / 1e9
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    split_used = split or ops.split_tokens_for(B, cfg["hkv"], wl["max_len"])
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 cache, bf16 q/out" if cfg["fp8"] else "bf16",
+        "data": "synthetic",
+        "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
+        "config": {
+            "workload": cfg["name"],
+            "batch": B, "q_heads": hq, "kv_heads": cfg["hkv"], "head_dim": D,
+            "context": [cfg["lo"], cfg["hi"]], "page_size": cfg["page"], "paged": cfg["paged"],
+            "cached_tokens": tokens, "split_tokens": split_used, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode attention (decode_split_kernel + decode_combine_kernel)",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "avg_us": round(attn_ms * 1e3, 2),
+            "algorithmic_bytes": attn_bytes,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, wl, torch, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

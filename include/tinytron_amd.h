@@ -1,0 +1,225 @@
+/*
+ * tinytron_amd.h -- C ABI of the MI355X (gfx950) decode-step library.
+ *
+ * One shared library, libtinytron_amd.so, replaces the per-layer decode path
+ * of liangyuwang/Tinytron's Attention.forward
+ * (tinytron/model/modules/attn.py:378-440) under the unchanged engine loop
+ * (tinytron/inference/engine.py:195-225):
+ *
+ *   rope_impl(q, k, pos)                      attn.py:397 -> 13-63
+ *   gqa_impl(k, v) + cache.append(k, v)       attn.py:308-312, 324-325 -> cache.py:34-45
+ *   cache.get_kv() + build_cache_causal_mask  attn.py:326, 332-339 -> cache.py:47-51, attn.py:86-95
+ *   F.scaled_dot_product_attention(...)       attn.py:420-423
+ *
+ * Conventions (every entry point):
+ *   - All tensor pointers are device pointers owned by the caller; nothing is
+ *     allocated, freed or synchronised inside the library. Work is enqueued
+ *     on `stream` (a hipStream_t; NULL = the default stream).
+ *   - Strides are in elements. The innermost (head_dim) stride is 1; the
+ *     token-slot stride inside a cache page is head_dim.
+ *   - Return value: 0 on success; < 0 for an invalid argument (nothing was
+ *     launched; tt_last_error_string() says why); > 0 is the hipError_t of a
+ *     failed launch.
+ *   - The library keeps no mutable global state; calls on different streams
+ *     from different threads are independent. tt_last_error_string() is
+ *     per thread.
+ *
+ * KV-cache addressing (shared by append and attention). Token t of sequence
+ * b, KV head h, element d lives at element offset
+ *     base(b, t / P) + h * cache_strides[2] + (t % P) * head_dim + d
+ * with base(b, j) = b * cache_strides[0] + j * cache_strides[1] when
+ * page_table == NULL (the reference's contiguous [B, H, ceil(S/P), P, D]
+ * store, cache.py:27-32, with H = num_kv_heads), and
+ * base(b, j) = page_table[b * max_pages + j] * cache_strides[1] for a paged
+ * pool [num_pages, H, P, D] (page_table int32 [B, max_pages]).
+ * fp8 caches keep one fp32 scale per (token, KV head) at index
+ * (element offset of d = 0) / head_dim in k_scale / v_scale, i.e. the scale
+ * arrays follow the cache layout with head_dim collapsed.
+ */
+#ifndef TINYTRON_AMD_H
+#define TINYTRON_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TT_ABI_VERSION 1
+
+#define TT_OK 0
+#define TT_ERR_INVALID_ARGUMENT (-1)
+#define TT_ERR_UNSUPPORTED (-2)
+#define TT_ERR_WORKSPACE_TOO_SMALL (-3)
+
+/* A hipStream_t, kept opaque so that the header needs no HIP include. */
+typedef void *tt_stream_t;
+
+/* ABI version of the loaded library (TT_ABI_VERSION it was built with). */
+int tt_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *tt_last_error_string(void);
+
+/*
+ * Fused RoPE + KV-cache append, bf16 activations and bf16 cache.
+ *
+ * Replaces, for T new tokens per sequence:
+ *   rope_impl(q, k, position_ids)         attn.py:13-63, called at attn.py:397
+ *   LayerPagedKVCache.append(k, v)        cache.py:34-45 (called at attn.py:325)
+ * with the cache holding num_kv_heads heads (K/V appended before the GQA
+ * expansion of attn.py:308-312; the expansion is an index map in attention).
+ *
+ * q_in  [B, H_q,  T, D], strides q_in_strides  = {b, h, t}
+ * k_in  [B, H_kv, T, D], strides k_in_strides  = {b, h, t}
+ * v_in  [B, H_kv, T, D], strides v_in_strides  = {b, h, t}
+ * q_out [B, H_q,  T, D], strides q_out_strides = {b, h, t} (rotated q)
+ * rope_table [rope_table_len, D]: row p = [cos(p*f_0..p*f_{D/2-1}) |
+ *   sin(p*f_0..)] in the activation dtype, f_i = 1/theta^(2i/D) (the values
+ *   of attn.py:30-54; columns i and i+D/2 of the reference's cos are equal).
+ * positions [B] int32: slot of token 0 of sequence b (its length before the
+ *   append). Token t goes to slot positions[b] + t and is rotated by that
+ *   position.
+ * new_lens [B] int32 or NULL: sequence b writes only its first new_lens[b]
+ *   tokens to the cache (ragged prefill; the rest are padding). q_out is
+ *   rotated for all T tokens either way. NULL = all T.
+ * Each rounding point of the reference under bf16 autocast is reproduced:
+ *   out = bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)).
+ * Tokens whose slot is >= capacity, >= rope_table_len, or whose page lies
+ * outside the page table / pool are skipped (the caller checks overflow and
+ * raises, as cache.py:37-40 does).
+ */
+int tt_rope_append_bf16(const void *q_in, const int64_t q_in_strides[3],
+                        const void *k_in, const int64_t k_in_strides[3],
+                        const void *v_in, const int64_t v_in_strides[3],
+                        void *q_out, const int64_t q_out_strides[3],
+                        const void *rope_table, int64_t rope_table_len,
+                        const int32_t *positions, const int32_t *new_lens,
+                        const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                        void *k_cache, void *v_cache, const int64_t cache_strides[3],
+                        int64_t capacity, int64_t batch, int64_t num_new,
+                        int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                        int64_t page_size, tt_stream_t stream);
+
+/*
+ * As tt_rope_append_bf16, fp32 activations, table and cache (the reference
+ * without autocast, e.g. on its CPU path: engine.py:180-184). Each op rounds
+ * to fp32; nothing is fused into an FMA.
+ */
+int tt_rope_append_f32(const void *q_in, const int64_t q_in_strides[3],
+                       const void *k_in, const int64_t k_in_strides[3],
+                       const void *v_in, const int64_t v_in_strides[3],
+                       void *q_out, const int64_t q_out_strides[3],
+                       const void *rope_table, int64_t rope_table_len,
+                       const int32_t *positions, const int32_t *new_lens,
+                       const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                       void *k_cache, void *v_cache, const int64_t cache_strides[3],
+                       int64_t capacity, int64_t batch, int64_t num_new,
+                       int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, tt_stream_t stream);
+
+/*
+ * As tt_rope_append_bf16 with an fp8-e4m3fn cache (no counterpart in the
+ * reference, whose cache is in the engine dtype, cache.py:19,29-30).
+ * Per (token, KV head): absmax = max|x| over D of the rotated bf16 K (of the
+ * raw V), scale = absmax / 448 (fp32), code = e4m3fn_rne(x / scale); an
+ * all-zero row stores code 0 and scale 0. Scales are written to k_scale /
+ * v_scale (fp32, cache layout with head_dim collapsed).
+ */
+int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
+                       const void *k_in, const int64_t k_in_strides[3],
+                       const void *v_in, const int64_t v_in_strides[3],
+                       void *q_out, const int64_t q_out_strides[3],
+                       const void *rope_table, int64_t rope_table_len,
+                       const int32_t *positions, const int32_t *new_lens,
+                       const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                       void *k_cache, void *v_cache, float *k_scale, float *v_scale,
+                       const int64_t cache_strides[3],
+                       int64_t capacity, int64_t batch, int64_t num_new,
+                       int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, tt_stream_t stream);
+
+/*
+ * GQA decode attention over a ragged batch, bf16 cache, split-K
+ * (flash-decoding) with a combine pass.
+ *
+ * Replaces, for one new token per sequence (T = 1):
+ *   cache.get_kv()                             cache.py:47-51
+ *   gqa_impl expansion (q head h reads KV head h / (H_q/H_kv))  attn.py:66-83
+ *   build_cache_causal_mask (all True for T=1) attn.py:86-95, 332-339
+ *   F.scaled_dot_product_attention(q, K, V, attn_mask, dropout_p=0)  attn.py:420-423
+ *
+ * q   [B, H_q, D] bf16 (rotated), strides q_strides = {b, h}
+ * seq_lens [B] int32: number of cached tokens sequence b attends to
+ *   (including the token just appended); values are clamped to max_seq_len.
+ * max_seq_len: host-side upper bound of seq_lens (sizes the launch grid).
+ * out [B, H_q, D] bf16, strides out_strides = {b, h}. A sequence with
+ *   seq_lens[b] <= 0 gets zeros.
+ * sm_scale: softmax scale (1/sqrt(D) for the reference's SDPA default).
+ * split_tokens: tokens per split (multiple of 128), 0 = automatic.
+ * workspace: device scratch of at least tt_decode_workspace_bytes(...) bytes
+ *   for the same (batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+ *   split_tokens); its contents need no initialisation.
+ * Requirements: head_dim in {64, 128}; H_q % H_kv == 0 and
+ *   H_q / H_kv <= 16; page_size % 16 == 0; q, cache and out 16-byte aligned.
+ * Physical page numbers read from page_table are clamped into
+ *   [0, num_pages) so that a bad table cannot address outside the pool.
+ */
+int tt_gqa_decode_attn_bf16(const void *q, const int64_t q_strides[2],
+                            const void *k_cache, const void *v_cache,
+                            const int64_t cache_strides[3],
+                            const int32_t *seq_lens, int64_t max_seq_len,
+                            const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                            void *out, const int64_t out_strides[2],
+                            int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t page_size, float sm_scale,
+                            int64_t split_tokens, void *workspace, size_t workspace_bytes,
+                            tt_stream_t stream);
+
+/*
+ * As tt_gqa_decode_attn_bf16 with an fp8-e4m3fn cache and per-(token, head)
+ * fp32 scales (layout as in tt_rope_append_fp8). Dequantisation is
+ * float(code) * scale inside the kernel with fp32 accumulation; q and out
+ * stay bf16. (No counterpart in the reference.)
+ */
+int tt_gqa_decode_attn_fp8(const void *q, const int64_t q_strides[2],
+                           const void *k_cache, const void *v_cache,
+                           const float *k_scale, const float *v_scale,
+                           const int64_t cache_strides[3],
+                           const int32_t *seq_lens, int64_t max_seq_len,
+                           const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                           void *out, const int64_t out_strides[2],
+                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                           int64_t head_dim, int64_t page_size, float sm_scale,
+                           int64_t split_tokens, void *workspace, size_t workspace_bytes,
+                           tt_stream_t stream);
+
+/*
+ * As tt_gqa_decode_attn_bf16 with fp32 q, cache and out (the reference
+ * without autocast). Requirements as above except that 4-byte alignment
+ * suffices.
+ */
+int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2],
+                           const void *k_cache, const void *v_cache,
+                           const int64_t cache_strides[3],
+                           const int32_t *seq_lens, int64_t max_seq_len,
+                           const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                           void *out, const int64_t out_strides[2],
+                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                           int64_t head_dim, int64_t page_size, float sm_scale,
+                           int64_t split_tokens, void *workspace, size_t workspace_bytes,
+                           tt_stream_t stream);
+
+/* Split size the attention entry points use when split_tokens == 0. */
+int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
+
+/* Workspace bytes the attention entry points need (split_tokens 0 = auto). */
+size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                 int64_t head_dim, int64_t max_seq_len, int64_t split_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYTRON_AMD_H */

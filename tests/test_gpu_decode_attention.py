@@ -1,0 +1,152 @@
+"""GPU parity: split-K GQA decode attention vs the fp64 oracle.
+
+Tolerance: |out - ref| <= 2e-3 + 2e-2 * |ref|
+elementwise, for bf16 and fp8 caches (fp32 accumulation in the kernel).
+The fp8 reference is the oracle run on the dequantised cache values
+(float(code) * scale), i.e. "dequantise, then reference attention".
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle.attention import decode_attention as ref_attention
+from oracle.numerics import f32_to_bf16_bits
+from tests.kv_inputs import bf16_randn, contiguous_geometry, fill_cache_values, paged_geometry, sm_scale
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+RTOL, ATOL = 2e-2, 2e-3
+
+
+def _dev(arr, dtype):
+    if dtype == torch.bfloat16:
+        return torch.from_numpy(arr.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(DEV)
+
+
+def run_case(lengths, Hq=32, Hkv=8, D=128, P=16, paged=False, fp8=False, seed=0, split_tokens=0, f32=False,
+             zero_first=False):
+    from tinytron_amd import ops
+
+    rng = np.random.default_rng(seed)
+    lengths = np.asarray(lengths, dtype=np.int32)
+    B = len(lengths)
+    max_len = int(lengths.max())
+    if paged:
+        layout, numel, ptab, num_pages = paged_geometry(lengths, Hkv, D, P, rng)
+    else:
+        cap = ((max_len + P - 1) // P) * P
+        layout, numel = contiguous_geometry(B, Hkv, D, cap, P)
+    if f32:
+        keys = [rng.standard_normal((int(L), Hkv, D)).astype(np.float32) for L in lengths]
+        values = [rng.standard_normal((int(L), Hkv, D)).astype(np.float32) for L in lengths]
+        ks = np.full(numel, np.nan, np.float32)
+        vs = np.full(numel, np.nan, np.float32)
+        for b, L in enumerate(lengths):
+            for t in range(L):
+                for h in range(Hkv):
+                    off = layout.token_offset(b, h, t)
+                    ks[off:off + D] = keys[b][t, h]
+                    vs[off:off + D] = values[b][t, h]
+        data = {"keys": keys, "values": values, "k_store": ks, "v_store": vs}
+        qf = rng.standard_normal((B, Hq, D)).astype(np.float32)
+        q = _dev(qf, torch.float32)
+    else:
+        data = fill_cache_values(layout, numel, B, lengths, rng, fp8=fp8)
+        qb, qf = bf16_randn(rng, (B, Hq, D))
+        q = _dev(qb, torch.bfloat16)
+    if fp8:
+        k_store = _dev(data["k_store"], None)
+        v_store = _dev(data["v_store"], None)
+        kind = "fp8"
+    elif f32:
+        k_store = _dev(data["k_store"], None)
+        v_store = _dev(data["v_store"], None)
+        kind = "f32"
+    else:
+        k_store = _dev(data["k_store"], torch.bfloat16)
+        v_store = _dev(data["v_store"], torch.bfloat16)
+        kind = "bf16"
+    kv = ops.KVLayout(
+        k=k_store, v=v_store, strides=(layout.seq_stride, layout.page_stride, layout.head_stride),
+        num_heads=Hkv, head_dim=D, page_size=P, capacity=layout.capacity if paged else int(layout.capacity),
+        kind=kind, page_table=(torch.from_numpy(ptab).to(DEV) if paged else None),
+        num_pages=(num_pages if paged else 0),
+        k_scale=(_dev(data["k_scale"], None) if fp8 else None),
+        v_scale=(_dev(data["v_scale"], None) if fp8 else None),
+    )
+    dev_lens = lengths.copy()
+    if zero_first:
+        dev_lens[0] = 0
+    seq = torch.from_numpy(dev_lens).to(DEV)
+    out = ops.decode_attention(q, kv, seq, max_len, split_tokens=split_tokens)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    ref = ref_attention(qf, data["keys"], data["values"], Hkv, sm_scale(D))
+    return got, ref, data
+
+
+def assert_close(got, ref, rtol=RTOL, atol=ATOL):
+    assert np.all(np.isfinite(got)), "non-finite output"
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), f"{bad.sum()} / {bad.size} out of tolerance; max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("paged", [False, True])
+def test_bf16_ragged(D, paged):
+    lengths = [1, 15, 16, 17, 31, 32, 33, 100, 129, 300, 513, 1000]
+    got, ref, _ = run_case(lengths, D=D, paged=paged, seed=D + paged)
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp8_ragged(D, paged):
+    lengths = [1, 16, 33, 250, 700, 1100]
+    got, ref, _ = run_case(lengths, D=D, paged=paged, fp8=True, seed=7 + D)
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+def test_group_sizes(G):
+    Hkv = 2
+    got, ref, _ = run_case([40, 257, 600], Hq=Hkv * G, Hkv=Hkv, seed=G)
+    assert_close(got, ref)
+
+
+def test_single_token_is_v():
+    """L = 1: softmax over one key is 1, so out == v (bf16 exact)."""
+    got, ref, data = run_case([1, 1, 1], seed=3)
+    v = np.stack([data["values"][b][0] for b in range(3)])  # [B, Hkv, D]
+    exp = np.repeat(v, 4, axis=1)
+    assert np.array_equal(f32_to_bf16_bits(got), f32_to_bf16_bits(exp))
+
+
+@pytest.mark.parametrize("split", [128, 256, 1024])
+def test_split_invariance(split):
+    lengths = [900, 2000, 130]
+    got, ref, _ = run_case(lengths, split_tokens=split, seed=21)
+    assert_close(got, ref)
+
+
+def test_page_size_64_contiguous():
+    got, ref, _ = run_case([70, 200, 64], P=64, seed=9)
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_f32(paged):
+    got, ref, _ = run_case([1, 17, 100, 333], Hq=8, Hkv=2, D=64, paged=paged, f32=True, seed=4)
+    assert_close(got, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_zero_length_gives_zeros():
+    """seq_lens[b] <= 0: the sequence attends to nothing and gets zeros."""
+    got, ref, _ = run_case([5, 9, 33], seed=1, zero_first=True)
+    assert np.all(got[0] == 0.0)
+    assert_close(got[1:], ref[1:])

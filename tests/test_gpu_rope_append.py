@@ -1,0 +1,162 @@
+"""GPU parity: fused RoPE + KV append vs the CPU oracle, bit for bit.
+
+Covers the reference's contiguous LayerPagedKVCache layout (cache.py:27-42)
+and the paged pool, bf16 / fp32 / fp8-e4m3fn caches, ragged positions, T > 1
+with ragged new_lens, strided (transposed-view) inputs as Attention.forward
+produces them (attn.py:389-391), and untouched slots staying untouched.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import kvcache as okv
+from oracle.numerics import (bf16_bits_to_f32, f32_to_bf16_bits, quantize_e4m3_rows)
+from oracle.rope import rope_apply
+from tests.kv_inputs import bf16_randn, contiguous_geometry, paged_geometry
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _to_dev_bf16(bits: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+
+
+def _bits(t: "torch.Tensor") -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False):
+    from tinytron_amd import ops
+
+    rng = np.random.default_rng(seed)
+    B = 3
+    positions = np.array([5, 17, 0], dtype=np.int32)
+    new_lens = np.array([T, max(1, T - 1), T], dtype=np.int32) if ragged_new else np.full(B, T, np.int32)
+    cap_needed = positions + T
+    max_seq = 64
+    act = torch.float32 if kind == "f32" else torch.bfloat16
+    if paged:
+        layout, numel, ptab, num_pages = paged_geometry(cap_needed + 7, Hkv, D, P, rng)
+    else:
+        layout, numel = contiguous_geometry(B, Hkv, D, max_seq, P)
+    # inputs laid out [B, T, H, D] and viewed [B, H, T, D] as q_proj(x).view().transpose() gives
+    qb, qf = bf16_randn(rng, (B, T, Hq, D))
+    kb, kf = bf16_randn(rng, (B, T, Hkv, D))
+    vb, vf = bf16_randn(rng, (B, T, Hkv, D))
+    if kind == "f32":
+        qf = rng.standard_normal((B, T, Hq, D)).astype(np.float32)
+        kf = rng.standard_normal((B, T, Hkv, D)).astype(np.float32)
+        vf = rng.standard_normal((B, T, Hkv, D)).astype(np.float32)
+        q = torch.from_numpy(qf).to(DEV)
+        k = torch.from_numpy(kf).to(DEV)
+        v = torch.from_numpy(vf).to(DEV)
+    else:
+        q, k, v = _to_dev_bf16(qb), _to_dev_bf16(kb), _to_dev_bf16(vb)
+    q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    table = ops.build_rope_table(128, D, dtype=act, device=DEV)
+    table_np = table.float().cpu().numpy()
+
+    sentinel16 = np.uint16(0x7FC1)
+    if kind == "fp8":
+        k_store = torch.full((numel,), 0x7E, dtype=torch.uint8, device=DEV)
+        v_store = torch.full((numel,), 0x7E, dtype=torch.uint8, device=DEV)
+        k_scale = torch.full((numel // D,), -1.0, dtype=torch.float32, device=DEV)
+        v_scale = torch.full((numel // D,), -1.0, dtype=torch.float32, device=DEV)
+    elif kind == "bf16":
+        k_store = torch.full((numel,), int(sentinel16.view(np.int16)), dtype=torch.int16, device=DEV).view(torch.bfloat16)
+        v_store = k_store.clone()
+        k_scale = v_scale = None
+    else:
+        k_store = torch.full((numel,), -7.0, dtype=torch.float32, device=DEV)
+        v_store = k_store.clone()
+        k_scale = v_scale = None
+    dev_table = None if not paged else torch.from_numpy(ptab).to(DEV)
+    kv = ops.KVLayout(
+        k=k_store, v=v_store, strides=(layout.seq_stride, layout.page_stride, layout.head_stride),
+        num_heads=Hkv, head_dim=D, page_size=P, capacity=layout.capacity if paged else max_seq,
+        kind=kind, page_table=dev_table, num_pages=(num_pages if paged else 0),
+        k_scale=k_scale, v_scale=v_scale,
+    )
+    pos_t = torch.from_numpy(positions).to(DEV)
+    nl_t = torch.from_numpy(new_lens).to(DEV) if ragged_new else None
+    q_out = ops.rope_append(q, k, v, table, pos_t, kv, new_lens=nl_t)
+    torch.cuda.synchronize()
+
+    # ---- oracle ----
+    dt = "f32" if kind == "f32" else "bf16"
+    pos_bt = positions[:, None] + np.arange(T)[None, :]
+    rows = table_np[pos_bt]  # [B, T, D]
+    q_ref = rope_apply(qf, rows[:, :, None, :], dt)        # [B, T, Hq, D]
+    k_ref = rope_apply(kf, rows[:, :, None, :], dt)
+    v_ref = vf
+    # q_out: every token (new_lens only limits the cache write)
+    q_dev = q_out.float().cpu().numpy().transpose(0, 2, 1, 3)
+    if kind == "f32":
+        assert np.array_equal(q_dev.view(np.uint32), q_ref.view(np.uint32))
+    else:
+        assert np.array_equal(_bits(q_out).transpose(0, 2, 1, 3), f32_to_bf16_bits(q_ref))
+
+    if kind == "fp8":
+        exp_k = np.full(numel, 0x7E, np.uint8)
+        exp_v = np.full(numel, 0x7E, np.uint8)
+        exp_ks = np.full(numel // D, -1.0, np.float32)
+        exp_vs = np.full(numel // D, -1.0, np.float32)
+        okv.append_fp8(exp_k, exp_ks, layout, k_ref.transpose(0, 2, 1, 3), positions, new_lens)
+        okv.append_fp8(exp_v, exp_vs, layout, v_ref.transpose(0, 2, 1, 3), positions, new_lens)
+        got_k = k_store.cpu().numpy()
+        got_v = v_store.cpu().numpy()
+        assert np.array_equal(got_k, exp_k), f"k codes differ at {np.flatnonzero(got_k != exp_k)[:8]}"
+        assert np.array_equal(got_v, exp_v)
+        assert np.array_equal(k_scale.cpu().numpy().view(np.uint32), exp_ks.view(np.uint32))
+        assert np.array_equal(v_scale.cpu().numpy().view(np.uint32), exp_vs.view(np.uint32))
+    elif kind == "bf16":
+        exp_k = np.full(numel, sentinel16, np.uint16)
+        exp_v = np.full(numel, sentinel16, np.uint16)
+        okv.append(exp_k, layout, f32_to_bf16_bits(k_ref).transpose(0, 2, 1, 3), positions, new_lens)
+        okv.append(exp_v, layout, f32_to_bf16_bits(v_ref).transpose(0, 2, 1, 3), positions, new_lens)
+        assert np.array_equal(_bits(k_store), exp_k), f"k differs at {np.flatnonzero(_bits(k_store) != exp_k)[:8]}"
+        assert np.array_equal(_bits(v_store), exp_v)
+    else:
+        exp_k = np.full(numel, -7.0, np.float32)
+        exp_v = np.full(numel, -7.0, np.float32)
+        okv.append(exp_k, layout, k_ref.transpose(0, 2, 1, 3), positions, new_lens)
+        okv.append(exp_v, layout, v_ref.transpose(0, 2, 1, 3), positions, new_lens)
+        assert np.array_equal(k_store.cpu().numpy().view(np.uint32), exp_k.view(np.uint32))
+        assert np.array_equal(v_store.cpu().numpy().view(np.uint32), exp_v.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "f32"])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_append_decode(kind, paged, D):
+    _case(kind, paged, D, T=1, seed=11 + D)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("paged", [False, True])
+def test_rope_append_prefill_ragged(kind, paged):
+    _case(kind, paged, 128, T=9, seed=5, ragged_new=True)
+
+
+def test_rope_table_matches_closed_form():
+    """The table is an input of the bit-exact RoPE; its values follow the
+    reference's fp32 op sequence, so they sit within fp32 angle rounding
+    (pos * f * 2^-23, from pow and the product) of the fp64 closed form, and
+    within the same bound of the numpy oracle's table."""
+    from tinytron_amd import ops
+    from oracle.rope import rope_table
+
+    D, n = 128, 4096
+    t = ops.build_rope_table(n, D, dtype=torch.float32, device=DEV).cpu().numpy()
+    ref = rope_table(n, D, dtype="f32")
+    pos = np.arange(n, dtype=np.float64)[:, None]
+    inv = 1.0 / (10000.0 ** (np.arange(0, D, 2) / D))
+    exact = np.concatenate([np.cos(pos * inv), np.sin(pos * inv)], -1)
+    bound = np.concatenate([pos * inv, pos * inv], -1) * 2.0 ** -21 + 2e-7
+    assert np.all(np.abs(t - exact) <= bound)
+    assert np.all(np.abs(ref - exact) <= bound)
+    bf = ops.build_rope_table(n, D, dtype=torch.bfloat16, device=DEV).float().cpu().numpy()
+    assert np.all(np.abs(bf - exact) <= bound + np.abs(exact) * 2.0 ** -8)

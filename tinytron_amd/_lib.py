@@ -1,0 +1,102 @@
+"""ctypes binding of libtinytron_amd.so (the C ABI in include/tinytron_amd.h).
+
+The library is built in-tree (``python -m tinytron_amd.build``). Loading
+fails loudly when it is missing: there is no CPU or PyTorch fallback for the
+decode path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
+ABI_VERSION = 1
+
+TT_OK = 0
+TT_ERR_INVALID_ARGUMENT = -1
+TT_ERR_UNSUPPORTED = -2
+TT_ERR_WORKSPACE_TOO_SMALL = -3
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.c_void_p  # device int32 pointers are passed as raw addresses
+_f32 = ctypes.c_float
+_size = ctypes.c_size_t
+
+_ROPE_COMMON = [
+    _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,  # q_in, k_in, v_in, q_out (+ strides)
+    _vp, _i64,                                       # rope_table, rope_table_len
+    _i32p, _i32p,                                    # positions, new_lens
+    _i32p, _i64, _i64,                               # page_table, max_pages, num_pages
+    _vp, _vp,                                        # k_cache, v_cache
+]
+_ROPE_TAIL = [
+    _i64p,                                           # cache_strides
+    _i64, _i64, _i64, _i64, _i64, _i64, _i64,        # capacity, batch, num_new, hq, hkv, head_dim, page_size
+    _vp,                                             # stream
+]
+
+_ATTN_HEAD = [_vp, _i64p, _vp, _vp]                  # q, q_strides, k_cache, v_cache
+_ATTN_TAIL = [
+    _i64p,                                           # cache_strides
+    _i32p, _i64,                                     # seq_lens, max_seq_len
+    _i32p, _i64, _i64,                               # page_table, max_pages, num_pages
+    _vp, _i64p,                                      # out, out_strides
+    _i64, _i64, _i64, _i64, _i64,                    # batch, hq, hkv, head_dim, page_size
+    _f32, _i64,                                      # sm_scale, split_tokens
+    _vp, _size,                                      # workspace, workspace_bytes
+    _vp,                                             # stream
+]
+
+SIGNATURES = {
+    "tt_abi_version": ([], ctypes.c_int),
+    "tt_last_error_string": ([], ctypes.c_char_p),
+    "tt_rope_append_bf16": (_ROPE_COMMON + _ROPE_TAIL, ctypes.c_int),
+    "tt_rope_append_f32": (_ROPE_COMMON + _ROPE_TAIL, ctypes.c_int),
+    "tt_rope_append_fp8": (_ROPE_COMMON + [_vp, _vp] + _ROPE_TAIL, ctypes.c_int),
+    "tt_gqa_decode_attn_bf16": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
+    "tt_gqa_decode_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ATTN_TAIL, ctypes.c_int),
+    "tt_gqa_decode_attn_f32": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
+    "tt_decode_split_tokens": ([_i64, _i64, _i64], ctypes.c_int64),
+    "tt_decode_workspace_bytes": ([_i64, _i64, _i64, _i64, _i64, _i64], ctypes.c_size_t),
+}
+
+_LIB = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and type the library; raise if it is missing or stale."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH.name} is not built; run `python -m tinytron_amd.build` (hipcc, gfx950). "
+            "The decode path has no fallback."
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (argtypes, restype) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    version = lib.tt_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH.name} has ABI version {version}, expected {ABI_VERSION}; rebuild it")
+    _LIB = lib
+    return lib
+
+
+def strides(*values: int):
+    arr = (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+    return arr
+
+
+def check(status: int, what: str) -> None:
+    """Map a library status to the exception the reference would raise."""
+    if status == TT_OK:
+        return
+    msg = load().tt_last_error_string().decode(errors="replace")
+    if status < 0:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: HIP error {status}: {msg}")

@@ -1,0 +1,322 @@
+// extern "C" entry points of libtinytron_amd.so (declared in
+// include/tinytron_amd.h): argument validation, status codes and launches.
+// Nothing here allocates or synchronises; every launch goes on the caller's
+// stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/tinytron_amd.h"
+#include "tt_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return TT_OK;
+}
+
+int from_hip(hipError_t err, const char *what) {
+  if (err == hipSuccess) return ok();
+  g_last_error = std::string(what) + ": " + hipGetErrorString(err);
+  return (int)err;
+}
+
+bool aligned(const void *p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+#define TT_CHECK(cond, code, ...) \
+  do {                            \
+    if (!(cond)) return fail(code, __VA_ARGS__); \
+  } while (0)
+
+int check_layout(const int32_t *page_table, int64_t max_pages, int64_t num_pages, const int64_t cache_strides[3],
+                 int64_t page_size) {
+  TT_CHECK(cache_strides != nullptr, TT_ERR_INVALID_ARGUMENT, "cache_strides is NULL");
+  TT_CHECK(page_size > 0, TT_ERR_INVALID_ARGUMENT, "page_size must be positive, got %lld", (long long)page_size);
+  TT_CHECK(cache_strides[1] >= 0 && cache_strides[2] >= 0 && cache_strides[0] >= 0, TT_ERR_INVALID_ARGUMENT,
+           "cache strides must be non-negative");
+  if (page_table != nullptr) {
+    TT_CHECK(max_pages > 0 && num_pages > 0, TT_ERR_INVALID_ARGUMENT,
+             "paged cache needs max_pages > 0 and num_pages > 0 (got %lld, %lld)", (long long)max_pages,
+             (long long)num_pages);
+  }
+  return TT_OK;
+}
+
+int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_strides[3], const void *k_in,
+                       const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
+                       const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
+                       const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                       int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
+                       float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
+                       int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, tt_stream_t stream) {
+  TT_CHECK(q_in && k_in && v_in && q_out && rope_table && positions && k_cache && v_cache, TT_ERR_INVALID_ARGUMENT,
+           "a required pointer is NULL");
+  TT_CHECK(q_in_strides && k_in_strides && v_in_strides && q_out_strides, TT_ERR_INVALID_ARGUMENT,
+           "a stride array is NULL");
+  TT_CHECK(batch >= 0 && num_new >= 0, TT_ERR_INVALID_ARGUMENT, "batch and num_new must be >= 0");
+  TT_CHECK(num_q_heads > 0 && num_kv_heads > 0, TT_ERR_INVALID_ARGUMENT, "head counts must be positive");
+  TT_CHECK(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 128, TT_ERR_UNSUPPORTED,
+           "head_dim must be even and <= 128, got %lld", (long long)head_dim);
+  TT_CHECK(rope_table_len >= 0 && capacity >= 0, TT_ERR_INVALID_ARGUMENT, "negative table length or capacity");
+  TT_CHECK(batch <= 65535 && num_new <= 65535 && num_q_heads + num_kv_heads <= (1 << 30), TT_ERR_UNSUPPORTED,
+           "grid too large");
+  if (kind == tt::CacheKind::kFP8) {
+    TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+  }
+  int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
+  if (rc != TT_OK) return rc;
+  if (batch == 0 || num_new == 0) return ok();
+
+  tt::RopeAppendArgs a{};
+  a.q_in = q_in;
+  a.qi_sb = q_in_strides[0];
+  a.qi_sh = q_in_strides[1];
+  a.qi_st = q_in_strides[2];
+  a.k_in = k_in;
+  a.ki_sb = k_in_strides[0];
+  a.ki_sh = k_in_strides[1];
+  a.ki_st = k_in_strides[2];
+  a.v_in = v_in;
+  a.vi_sb = v_in_strides[0];
+  a.vi_sh = v_in_strides[1];
+  a.vi_st = v_in_strides[2];
+  a.q_out = q_out;
+  a.qo_sb = q_out_strides[0];
+  a.qo_sh = q_out_strides[1];
+  a.qo_st = q_out_strides[2];
+  a.table = rope_table;
+  a.table_len = rope_table_len;
+  a.positions = positions;
+  a.new_lens = new_lens;
+  a.page_table = page_table;
+  a.max_pages = max_pages;
+  a.num_pages = num_pages;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.c_seq = cache_strides[0];
+  a.c_page = cache_strides[1];
+  a.c_head = cache_strides[2];
+  a.capacity = capacity;
+  a.batch = (int)batch;
+  a.num_new = (int)num_new;
+  a.hq = (int)num_q_heads;
+  a.hkv = (int)num_kv_heads;
+  a.head_dim = (int)head_dim;
+  a.page_size = (int)page_size;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_rope_append(a, kind, (hipStream_t)stream), "rope_append launch");
+}
+
+int64_t resolve_split(int64_t split_tokens, int64_t batch, int64_t hkv, int64_t max_len) {
+  return split_tokens > 0 ? split_tokens : tt::auto_split_tokens(batch, hkv, max_len);
+}
+
+size_t workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t max_len, int64_t split) {
+  const int64_t g = hq / (hkv > 0 ? hkv : 1);
+  const int64_t splits = tt::num_splits(max_len, split);
+  const int64_t items = batch * hkv * splits * g;
+  return (size_t)(items * head_dim + items * 2) * sizeof(float);
+}
+
+int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2], const void *k_cache,
+                  const void *v_cache, const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                  const int32_t *seq_lens, int64_t max_seq_len, const int32_t *page_table, int64_t max_pages,
+                  int64_t num_pages, void *out, const int64_t out_strides[2], int64_t batch, int64_t num_q_heads,
+                  int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
+                  void *workspace, size_t ws_bytes, tt_stream_t stream) {
+  TT_CHECK(q && k_cache && v_cache && seq_lens && out, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(q_strides && out_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
+  TT_CHECK(batch >= 0 && batch <= 65535, TT_ERR_INVALID_ARGUMENT, "batch must be in [0, 65535]");
+  TT_CHECK(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, TT_ERR_INVALID_ARGUMENT,
+           "num_attention_heads must be divisible by num_key_value_heads");
+  TT_CHECK(num_q_heads / num_kv_heads <= 16, TT_ERR_UNSUPPORTED, "GQA group size %lld > 16 is not supported",
+           (long long)(num_q_heads / num_kv_heads));
+  TT_CHECK(num_kv_heads <= 65535 && num_q_heads <= 65535, TT_ERR_UNSUPPORTED, "too many heads");
+  TT_CHECK(head_dim == 64 || head_dim == 128, TT_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld",
+           (long long)head_dim);
+  TT_CHECK(page_size % 16 == 0, TT_ERR_UNSUPPORTED, "page_size must be a multiple of 16, got %lld",
+           (long long)page_size);
+  TT_CHECK(max_seq_len >= 0 && max_seq_len < (int64_t)1 << 30, TT_ERR_INVALID_ARGUMENT,
+           "max_seq_len out of range");
+  if (kind == tt::CacheKind::kFP8) {
+    TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+  }
+  int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
+  if (rc != TT_OK) return rc;
+  if (page_table != nullptr) {
+    TT_CHECK(max_seq_len <= max_pages * page_size, TT_ERR_INVALID_ARGUMENT,
+             "max_seq_len %lld exceeds the page table's %lld pages of %lld tokens", (long long)max_seq_len,
+             (long long)max_pages, (long long)page_size);
+  }
+  if (kind != tt::CacheKind::kF32) {
+    TT_CHECK(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
+             "q and cache pointers must be 16-byte aligned");
+    TT_CHECK(q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0, TT_ERR_INVALID_ARGUMENT,
+             "q strides must be multiples of 8 elements");
+    TT_CHECK(cache_strides[0] % 8 == 0 && cache_strides[1] % 8 == 0 && cache_strides[2] % 8 == 0,
+             TT_ERR_INVALID_ARGUMENT, "cache strides must be multiples of 8 elements");
+  } else {
+    TT_CHECK(aligned(q, 4) && aligned(k_cache, 4) && aligned(v_cache, 4) && aligned(out, 4),
+             TT_ERR_INVALID_ARGUMENT, "fp32 pointers must be 4-byte aligned");
+  }
+  const int64_t split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
+  TT_CHECK(split >= 128 && split % 128 == 0 && split <= (1 << 20), TT_ERR_INVALID_ARGUMENT,
+           "split_tokens must be a positive multiple of 128, got %lld", (long long)split_tokens);
+  const int64_t splits = tt::num_splits(max_seq_len, split);
+  TT_CHECK(splits <= 65535, TT_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
+  const size_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
+  TT_CHECK(workspace != nullptr && ws_bytes >= need, TT_ERR_WORKSPACE_TOO_SMALL,
+           "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+  TT_CHECK(aligned(workspace, 16), TT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  if (batch == 0) return ok();
+
+  tt::DecodeArgs a{};
+  a.q = q;
+  a.q_sb = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.c_seq = cache_strides[0];
+  a.c_page = cache_strides[1];
+  a.c_head = cache_strides[2];
+  a.seq_lens = seq_lens;
+  a.max_len = (int)max_seq_len;
+  a.page_table = page_table;
+  a.max_pages = max_pages;
+  a.num_pages = num_pages;
+  a.out = out;
+  a.o_sb = out_strides[0];
+  a.o_sh = out_strides[1];
+  const int64_t g = num_q_heads / num_kv_heads;
+  const int64_t items = batch * num_kv_heads * splits * g;
+  a.ws_o = static_cast<float *>(workspace);
+  a.ws_ml = static_cast<float *>(workspace) + items * head_dim;
+  a.batch = (int)batch;
+  a.hq = (int)num_q_heads;
+  a.hkv = (int)num_kv_heads;
+  a.group = (int)g;
+  a.page_size = (int)page_size;
+  a.split_tokens = (int)split;
+  a.max_splits = (int)splits;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_decode_attn(a, kind, (int)head_dim, (hipStream_t)stream), "decode attention launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int tt_abi_version(void) { return TT_ABI_VERSION; }
+
+const char *tt_last_error_string(void) { return g_last_error.c_str(); }
+
+int tt_rope_append_bf16(const void *q_in, const int64_t q_in_strides[3], const void *k_in,
+                        const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
+                        const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
+                        const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                        int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache,
+                        const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
+                        int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                        tt_stream_t stream) {
+  return rope_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, page_table, max_pages,
+                            num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides, capacity, batch, num_new,
+                            num_q_heads, num_kv_heads, head_dim, page_size, stream);
+}
+
+int tt_rope_append_f32(const void *q_in, const int64_t q_in_strides[3], const void *k_in,
+                       const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
+                       const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
+                       const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                       int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache,
+                       const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
+                       int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                       tt_stream_t stream) {
+  return rope_append_common(tt::CacheKind::kF32, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, page_table, max_pages,
+                            num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides, capacity, batch, num_new,
+                            num_q_heads, num_kv_heads, head_dim, page_size, stream);
+}
+
+int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3], const void *k_in,
+                       const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
+                       const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
+                       const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                       int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
+                       float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
+                       int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t page_size, tt_stream_t stream) {
+  return rope_append_common(tt::CacheKind::kFP8, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, page_table, max_pages,
+                            num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch, num_new,
+                            num_q_heads, num_kv_heads, head_dim, page_size, stream);
+}
+
+int tt_gqa_decode_attn_bf16(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                            const int64_t cache_strides[3], const int32_t *seq_lens, int64_t max_seq_len,
+                            const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *out,
+                            const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
+                            void *workspace, size_t workspace_bytes, tt_stream_t stream) {
+  return decode_common(tt::CacheKind::kBF16, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides,
+                       seq_lens, max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+}
+
+int tt_gqa_decode_attn_fp8(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                           const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                           const int32_t *seq_lens, int64_t max_seq_len, const int32_t *page_table,
+                           int64_t max_pages, int64_t num_pages, void *out, const int64_t out_strides[2],
+                           int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                           int64_t page_size, float sm_scale, int64_t split_tokens, void *workspace,
+                           size_t workspace_bytes, tt_stream_t stream) {
+  return decode_common(tt::CacheKind::kFP8, q, q_strides, k_cache, v_cache, k_scale, v_scale, cache_strides,
+                       seq_lens, max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+}
+
+int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                           const int64_t cache_strides[3], const int32_t *seq_lens, int64_t max_seq_len,
+                           const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *out,
+                           const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                           int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
+                           void *workspace, size_t workspace_bytes, tt_stream_t stream) {
+  return decode_common(tt::CacheKind::kF32, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides, seq_lens,
+                       max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+}
+
+int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len) {
+  return tt::auto_split_tokens(batch, num_kv_heads, max_seq_len);
+}
+
+size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t max_seq_len, int64_t split_tokens) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+  const int64_t split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
+  if (split <= 0) return 0;
+  return workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
+}
+
+}  // extern "C"

@@ -1,0 +1,592 @@
+// GQA split-K decode attention for gfx950 (CDNA4).
+//
+// Computes, for one new token per sequence, what the reference computes with
+// repeat_interleave + F.scaled_dot_product_attention over the cached keys
+// (attn.py:66-83, 420-423): out[b, h] = softmax(q[b,h] . K_b^T * scale) V_b
+// with K/V read from KV head h / G (G = H_q / H_kv).
+//
+// Work decomposition
+//   grid = (splits, H_kv, B); one workgroup = 4 waves = one (b, kv head,
+//   split) of `split_tokens` tokens; each wave streams a quarter of the split
+//   in 32-token tiles and keeps an online-softmax state for the G query heads
+//   of the group, so every K/V byte is read from HBM once for all G heads.
+//   The 4 wave states merge in LDS into one partial per split; a second
+//   kernel merges the splits of a (b, q head).
+//
+// Per 32-token tile, all on the matrix cores (v_mfma_f32_16x16x32_bf16):
+//   QK^T: A = 16 K rows (16-byte loads, one token per lane%16), B = q^T with
+//         the group's heads as columns -> S^T[token][head].
+//   V^T : the PV product contracts over tokens, but a 16-byte load gives a
+//         lane 8 head_dim values of one token. Multiplying the loaded V block
+//         by a 0/1 selection matrix on the MFMA (A = V block, B = identity)
+//         returns the block transposed across lanes, exactly (one nonzero
+//         product per output), with no LDS round trip.
+//   PV  : A = P (heads x tokens, as a bf16 hi + lo pair), B = V^T -> O[head][d]
+//         accumulated in fp32.
+// The token order inside a tile is the one the MFMA output layout produces,
+// used consistently for S, P and V^T, so no cross-lane shuffles are needed
+// except the 4-lane max reduction and the per-head rescale broadcast.
+//
+// fp8-e4m3fn caches: K codes become bf16 with v_cvt_scalef32_pk_bf16_fp8
+// (exact: every e4m3 value is a bf16 value), the per-token K scale multiplies
+// the score, the V transpose runs on the fp8 MFMA with an fp8 identity
+// (exact), and the per-token V scale multiplies P before its bf16 rounding.
+//
+// Tokens past a sequence's length are never loaded (predicated loads, zero
+// fill) and their scores are set to -inf, so garbage or NaN in unused cache
+// slots cannot reach the output.
+#include "tt_internal.h"
+#include "tt_numerics.h"
+
+namespace tt {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_fp8(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0,
+                                                    0, 0);
+}
+
+// 8 e4m3fn codes -> 8 bf16 (exact).
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(u32x2 v) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+template <bool kFP8>
+struct KVTraits;
+
+template <>
+struct KVTraits<false> {
+  using Frag = u32x4;  // 8 bf16
+  static __device__ __forceinline__ Frag load(const void *base, int64_t elem, bool valid) {
+    Frag v = {0u, 0u, 0u, 0u};
+    if (valid) v = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + elem);
+    return v;
+  }
+  static __device__ __forceinline__ bf16x8 as_bf16(Frag f) { return __builtin_bit_cast(bf16x8, f); }
+};
+
+template <>
+struct KVTraits<true> {
+  using Frag = u32x2;  // 8 fp8
+  static __device__ __forceinline__ Frag load(const void *base, int64_t elem, bool valid) {
+    Frag v = {0u, 0u};
+    if (valid) v = *reinterpret_cast<const u32x2 *>(static_cast<const uint8_t *>(base) + elem);
+    return v;
+  }
+  static __device__ __forceinline__ bf16x8 as_bf16(Frag f) { return fp8x8_to_bf16x8(f); }
+};
+
+template <int D, bool kFP8>
+struct Tile {
+  static constexpr int NDB = D / 32;
+  typename KVTraits<kFP8>::Frag k[2][NDB];
+  typename KVTraits<kFP8>::Frag v[2][NDB];
+  f32x4 ks[2];  // fp8: K scales of this lane's 4 score rows, per 16-token block
+  f32x4 vs[2];
+};
+
+// Element offset of token tb (multiple of 16) of (b, hk), d = 0. A 16-token
+// block never straddles a page because page_size % 16 == 0.
+__device__ __forceinline__ int64_t block_base(const DecodeArgs &a, int b, int hk, int tb, int D) {
+  const int j = tb / a.page_size;
+  const int slot = tb - j * a.page_size;
+  int64_t page_base;
+  if (a.page_table != nullptr) {
+    int64_t phys = a.page_table[(int64_t)b * a.max_pages + j];
+    phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
+    page_base = phys * a.c_page;
+  } else {
+    page_base = (int64_t)b * a.c_seq + (int64_t)j * a.c_page;
+  }
+  return page_base + (int64_t)hk * a.c_head + (int64_t)slot * D;
+}
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void load_tile(const DecodeArgs &a, int b, int hk, int t0, int L, int lane,
+                                          Tile<D, kFP8> &tile) {
+  using TR = KVTraits<kFP8>;
+  constexpr int NDB = D / 32;
+  const int m = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tb = t0 + 16 * tt;
+    if (tb < L) {
+      const int64_t base = block_base(a, b, hk, tb, D);
+      const bool valid = tb + m < L;
+      const int64_t row = base + (int64_t)m * D + 8 * g;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        tile.k[tt][db] = TR::load(a.k_cache, row + 32 * db, valid);
+        tile.v[tt][db] = TR::load(a.v_cache, row + 32 * db, valid);
+      }
+      if constexpr (kFP8) {
+        // scores of this lane are tokens tb + 4g + r, r = 0..3
+        const int64_t sidx = base / D + 4 * g;
+        f32x4 ks = {0.f, 0.f, 0.f, 0.f}, vs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (tb + 4 * g + r < L) {
+            ks[r] = a.k_scale[sidx + r];
+            vs[r] = a.v_scale[sidx + r];
+          }
+        }
+        tile.ks[tt] = ks;
+        tile.vs[tt] = vs;
+      }
+    } else {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        tile.k[tt][db] = TR::load(a.k_cache, 0, false);
+        tile.v[tt][db] = TR::load(a.v_cache, 0, false);
+      }
+      if constexpr (kFP8) {
+        tile.ks[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        tile.vs[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+}
+
+template <int D, bool kFP8>
+struct WaveState {
+  static constexpr int NDB = D / 32;
+  f32x4 o[2 * NDB];  // PV accumulators: d block c (16 columns), rows = heads 4g..4g+3
+  float m;           // running max of this lane's head (log2 units)
+  float l;           // running sum (lane-partial: this lane's tokens only)
+};
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L, int lane, const Tile<D, kFP8> &tile,
+                                             const bf16x8 (&qf)[D / 32], const typename KVTraits<kFP8>::Frag ident[2],
+                                             WaveState<D, kFP8> &st) {
+  using TR = KVTraits<kFP8>;
+  constexpr int NDB = D / 32;
+  const int g = lane >> 4;
+
+  // S^T[token][head]: lane (n + 16g), reg r = token t0 + 16*tt + 4g + r, head n.
+  f32x4 S[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    S[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) S[tt] = mfma_bf16(TR::as_bf16(tile.k[tt][db]), qf[db], S[tt]);
+  }
+
+  float s[8];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = t0 + 16 * tt + 4 * g + r;
+      float x = S[tt][r];
+      if constexpr (kFP8) x *= tile.ks[tt][r];
+      s[tt * 4 + r] = tok < L ? x * a.scale_log2 : kNegInf;
+    }
+  }
+  float mx = s[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(st.m, mx);  // finite: token t0 < L is in every head's column
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  float p[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
+    psum += p[i];
+  }
+  st.l = st.l * alpha + psum;
+  st.m = m_new;
+  if constexpr (kFP8) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] *= tile.vs[0][r];
+      p[4 + r] *= tile.vs[1][r];
+    }
+  }
+
+  // Rescale O rows (heads 4g + r) by their head's alpha, held by lane 4g + r.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+    for (int c = 0; c < 2 * NDB; ++c) st.o[c][r] *= ar;
+  }
+
+  // P as the A operand: row = head (lane % 16), k slots = this lane's 8 tokens.
+  // P = P_hi + P_lo with both halves bf16 (P_lo = P - P_hi is exact in fp32),
+  // so the PV product keeps ~16 mantissa bits of P instead of bf16's 8; the
+  // second MFMA per block is free in this memory-bound loop.
+  const f32x8 pv = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]};
+  const bf16x8 pa_hi = __builtin_convertvector(pv, bf16x8);
+  const f32x8 p_rem = pv - __builtin_convertvector(pa_hi, f32x8);
+  const bf16x8 pa_lo = __builtin_convertvector(p_rem, bf16x8);
+
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) {
+    const int db = c >> 1;
+    const int hi = c & 1;
+    f32x4 t0v, t1v;
+    if constexpr (kFP8) {
+      t0v = mfma_fp8(tile.v[0][db], ident[hi], zero);
+      t1v = mfma_fp8(tile.v[1][db], ident[hi], zero);
+    } else {
+      t0v = mfma_bf16(TR::as_bf16(tile.v[0][db]), TR::as_bf16(ident[hi]), zero);
+      t1v = mfma_bf16(TR::as_bf16(tile.v[1][db]), TR::as_bf16(ident[hi]), zero);
+    }
+    // lane (n + 16g): V[token t0 + 4g + r][d = 16c + n] (t0v), same for t0 + 16 (t1v)
+    const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
+    const bf16x8 vb = __builtin_convertvector(vv, bf16x8);
+    st.o[c] = mfma_bf16(pa_hi, vb, st.o[c]);
+    st.o[c] = mfma_bf16(pa_lo, vb, st.o[c]);
+  }
+}
+
+// Selection matrices for the V transpose: B[k][n] = 1 iff k == n (+16 for
+// the upper half), expressed in the (lane group, slot) coordinates in which
+// the A operand was loaded, so the result does not depend on how the
+// hardware orders the K index inside a lane.
+template <bool kFP8>
+__device__ __forceinline__ void make_identity(int lane, typename KVTraits<kFP8>::Frag ident[2]) {
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  if constexpr (kFP8) {
+    uint32_t w[2][2] = {{0u, 0u}, {0u, 0u}};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (8 * g + i == n) w[0][i >> 2] |= 0x38u << (8 * (i & 3));        // e4m3fn 1.0
+      if (8 * g + i == n + 16) w[1][i >> 2] |= 0x38u << (8 * (i & 3));
+    }
+    ident[0] = u32x2{w[0][0], w[0][1]};
+    ident[1] = u32x2{w[1][0], w[1][1]};
+  } else {
+    uint32_t w[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (8 * g + i == n) w[0][i >> 1] |= 0x3f80u << (16 * (i & 1));     // bf16 1.0
+      if (8 * g + i == n + 16) w[1][i >> 1] |= 0x3f80u << (16 * (i & 1));
+    }
+    ident[0] = u32x4{w[0][0], w[0][1], w[0][2], w[0][3]};
+    ident[1] = u32x4{w[1][0], w[1][1], w[1][2], w[1][3]};
+  }
+}
+
+template <int D, bool kFP8>
+__global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
+  constexpr int NDB = D / 32;
+  extern __shared__ float smem[];  // [4][G][D] outputs, then [4][16] m, [4][16] l
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int split = blockIdx.x;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const int G = a.group;
+  const int L = min(a.seq_lens[b], a.max_len);
+  const int s_begin = split * a.split_tokens;
+  if (s_begin >= L) return;  // uniform for the block
+  const int s_end = min(L, s_begin + a.split_tokens);
+  const int per_wave = a.split_tokens / kWavesPerBlock;
+  const int w_begin = s_begin + wave * per_wave;
+  const int w_end = min(s_end, w_begin + per_wave);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+
+  // q^T as the B operand: column n = query head hk*G + n (zero for n >= G).
+  bf16x8 qf[NDB];
+  {
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + n) * a.q_sh + 8 * g;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (n < G) v = *reinterpret_cast<const u32x4 *>(q + qrow + 32 * db);
+      qf[db] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  typename KVTraits<kFP8>::Frag ident[2];
+  make_identity<kFP8>(lane, ident);
+
+  WaveState<D, kFP8> st;
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = kNegInf;
+  st.l = 0.f;
+
+  if (w_begin < w_end) {
+    Tile<D, kFP8> ta, tb;
+    load_tile<D, kFP8>(a, b, hk, w_begin, L, lane, ta);
+    int t0 = w_begin;
+    while (true) {
+      if (t0 + kTileTokens < w_end) load_tile<D, kFP8>(a, b, hk, t0 + kTileTokens, L, lane, tb);
+      process_tile<D, kFP8>(a, t0, L, lane, ta, qf, ident, st);
+      t0 += kTileTokens;
+      if (t0 >= w_end) break;
+      if (t0 + kTileTokens < w_end) load_tile<D, kFP8>(a, b, hk, t0 + kTileTokens, L, lane, ta);
+      process_tile<D, kFP8>(a, t0, L, lane, tb, qf, ident, st);
+      t0 += kTileTokens;
+      if (t0 >= w_end) break;
+    }
+  }
+
+  // Merge the 4 wave states of the block in LDS.
+  float l = st.l;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  float *so = smem;
+  float *sm = smem + kWavesPerBlock * G * D;
+  float *sl = sm + kWavesPerBlock * 16;
+  if (g == 0) {
+    sm[wave * 16 + n] = st.m;
+    sl[wave * 16 + n] = l;
+  }
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int head = 4 * g + r;
+      if (head < G) so[(wave * G + head) * D + 16 * c + n] = st.o[c][r];
+    }
+  }
+  __syncthreads();
+  const int64_t item = ((int64_t)b * a.hkv + hk) * a.max_splits + split;
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int head = idx / D;
+    const int d = idx - head * D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) M = fmaxf(M, sm[w * 16 + head]);
+    float acc = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      const float e = __builtin_amdgcn_exp2f(sm[w * 16 + head] - M);
+      acc += e * so[(w * G + head) * D + d];
+      lsum += e * sl[w * 16 + head];
+    }
+    a.ws_o[(item * G + head) * D + d] = acc;
+    if (d == 0) {
+      a.ws_ml[(item * G + head) * 2 + 0] = M;
+      a.ws_ml[(item * G + head) * 2 + 1] = lsum;
+    }
+  }
+}
+
+// fp32 cache and activations: VALU path (small models run in fp32, e.g. the
+// reference without autocast). Same split / workspace contract as the MFMA
+// kernel. Each wave walks its tokens 64 at a time with one token per lane
+// for the scores, then one head_dim element per lane for P.V.
+template <int D>
+__global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
+  constexpr int DPL = D / 64;  // head_dim elements per lane
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int split = blockIdx.x;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const int G = a.group;
+  const int L = min(a.seq_lens[b], a.max_len);
+  const int s_begin = split * a.split_tokens;
+  if (s_begin >= L) return;
+  const int s_end = min(L, s_begin + a.split_tokens);
+  const int per_wave = a.split_tokens / kWavesPerBlock;
+  const int w_begin = s_begin + wave * per_wave;
+  const int w_end = min(s_end, w_begin + per_wave);
+
+  float *so = smem;                                  // [4][G][D]
+  float *sm = so + kWavesPerBlock * G * D;           // [4][16]
+  float *sl = sm + kWavesPerBlock * 16;              // [4][16]
+  float *sq = sl + kWavesPerBlock * 16;              // [G][D] query rows
+  float *sp = sq + G * D + wave * 64;                // per-wave [64] probabilities
+  const float *q = static_cast<const float *>(a.q);
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int h = idx / D;
+    sq[idx] = q[(int64_t)b * a.q_sb + (int64_t)(hk * G + h) * a.q_sh + (idx - h * D)];
+  }
+  __syncthreads();
+
+  const float *kc = static_cast<const float *>(a.k_cache);
+  const float *vc = static_cast<const float *>(a.v_cache);
+  float o[16][DPL];
+  float mrun[16], lrun[16];
+  for (int h = 0; h < 16; ++h) {
+    mrun[h] = kNegInf;
+    lrun[h] = 0.f;
+    for (int j = 0; j < DPL; ++j) o[h][j] = 0.f;
+  }
+  for (int t0 = w_begin; t0 < w_end; t0 += 64) {
+    const int tok = t0 + lane;
+    const bool valid = tok < w_end;
+    int64_t koff = 0;
+    if (valid) {
+      const int tb = tok & ~15;
+      koff = block_base(a, b, hk, tb, D) + (int64_t)(tok - tb) * D;
+    }
+    for (int h = 0; h < G && h < 16; ++h) {
+      float sc = kNegInf;
+      if (valid) {
+        float acc = 0.f;
+        for (int d = 0; d < D; ++d) acc += sq[h * D + d] * kc[koff + d];
+        sc = acc * a.scale_log2;
+      }
+      float mx = sc;
+      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float m_new = fmaxf(mrun[h], mx);
+      const float alpha = __builtin_amdgcn_exp2f(mrun[h] - m_new);
+      const float pr = valid ? __builtin_amdgcn_exp2f(sc - m_new) : 0.f;
+      float ps = pr;
+      for (int off = 32; off > 0; off >>= 1) ps += __shfl_xor(ps, off, 64);
+      lrun[h] = lrun[h] * alpha + ps;
+      mrun[h] = m_new;
+      sp[lane] = pr;
+      __builtin_amdgcn_wave_barrier();
+      const int nt = min(64, w_end - t0);
+      for (int j = 0; j < DPL; ++j) o[h][j] *= alpha;
+      for (int t = 0; t < nt; ++t) {
+        const int tk = t0 + t;
+        const int tb = tk & ~15;
+        const int64_t voff = block_base(a, b, hk, tb, D) + (int64_t)(tk - tb) * D;
+        const float pt = sp[t];
+        for (int j = 0; j < DPL; ++j) o[h][j] += pt * vc[voff + lane + 64 * j];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  if (lane < 16) {
+    sm[wave * 16 + lane] = kNegInf;
+    sl[wave * 16 + lane] = 0.f;
+  }
+  __builtin_amdgcn_wave_barrier();
+  for (int h = 0; h < G && h < 16; ++h) {
+    if (lane == 0) {
+      sm[wave * 16 + h] = mrun[h];
+      sl[wave * 16 + h] = lrun[h];
+    }
+    for (int j = 0; j < DPL; ++j) so[(wave * G + h) * D + lane + 64 * j] = o[h][j];
+  }
+  __syncthreads();
+  const int64_t item = ((int64_t)b * a.hkv + hk) * a.max_splits + split;
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int head = idx / D;
+    const int d = idx - head * D;
+    float M = kNegInf;
+    for (int w = 0; w < kWavesPerBlock; ++w) M = fmaxf(M, sm[w * 16 + head]);
+    float acc = 0.f, lsum = 0.f;
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      const float e = __builtin_amdgcn_exp2f(sm[w * 16 + head] - M);
+      acc += e * so[(w * G + head) * D + d];
+      lsum += e * sl[w * 16 + head];
+    }
+    a.ws_o[(item * G + head) * D + d] = acc;
+    if (d == 0) {
+      a.ws_ml[(item * G + head) * 2 + 0] = M;
+      a.ws_ml[(item * G + head) * 2 + 1] = lsum;
+    }
+  }
+}
+
+// Merge the splits of one (b, q head): out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
+template <int D, bool kBF16Out>
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 64;
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int G = a.group;
+  const int hk = hq / G;
+  const int head = hq - hk * G;
+  const int L = min(a.seq_lens[b], a.max_len);
+  const int nsplit = L <= 0 ? 0 : (L + a.split_tokens - 1) / a.split_tokens;
+  const int64_t item0 = ((int64_t)b * a.hkv + hk) * a.max_splits;
+  float M = kNegInf;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_ml[((item0 + s) * G + head) * 2]);
+  float acc[DPL];
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+  float lsum = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t it = (item0 + s) * G + head;
+    const float e = __builtin_amdgcn_exp2f(a.ws_ml[it * 2] - M);
+    lsum += e * a.ws_ml[it * 2 + 1];
+    for (int j = 0; j < DPL; ++j) acc[j] += e * a.ws_o[it * D + lane + 64 * j];
+  }
+  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+  const int64_t dst = (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh;
+  for (int j = 0; j < DPL; ++j) {
+    const float v = acc[j] * inv;
+    if constexpr (kBF16Out) {
+      static_cast<uint16_t *>(a.out)[dst + lane + 64 * j] = f32_to_bf16_bits(v);
+    } else {
+      static_cast<float *>(a.out)[dst + lane + 64 * j] = v;
+    }
+  }
+}
+
+template <int D>
+hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
+  const dim3 grid(a.max_splits, a.hkv, a.batch);
+  const dim3 block(64 * kWavesPerBlock);
+  const size_t lds = sizeof(float) * (kWavesPerBlock * a.group * D + 2 * kWavesPerBlock * 16);
+  switch (kind) {
+    case CacheKind::kBF16:
+      hipLaunchKernelGGL((decode_split_kernel<D, false>), grid, block, lds, stream, a);
+      break;
+    case CacheKind::kFP8:
+      hipLaunchKernelGGL((decode_split_kernel<D, true>), grid, block, lds, stream, a);
+      break;
+    case CacheKind::kF32: {
+      const size_t lds32 = lds + sizeof(float) * (a.group * D + kWavesPerBlock * 64);
+      hipLaunchKernelGGL((decode_split_kernel_f32<D>), grid, block, lds32, stream, a);
+      break;
+    }
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const dim3 cgrid(a.hq, a.batch);
+  if (kind == CacheKind::kF32) {
+    hipLaunchKernelGGL((decode_combine_kernel<D, false>), cgrid, dim3(64), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_combine_kernel<D, true>), cgrid, dim3(64), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
+  // Aim for >= 8 workgroups per CU (256 CUs) over the longest sequence while
+  // keeping splits long enough that the partial write (G*(D+2) floats) stays
+  // a small fraction of the K/V bytes a split reads.
+  const int64_t target_blocks = 256 * 8;
+  int64_t split = 1024;
+  while (split > 128 && batch * hkv * ((max_len + split - 1) / split) < target_blocks) split /= 2;
+  return split;
+}
+
+hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
+  if (head_dim == 64) return launch_d<64>(a, kind, stream);
+  return launch_d<128>(a, kind, stream);
+}
+
+}  // namespace tt

@@ -1,0 +1,173 @@
+// Fused RoPE + KV-cache append for gfx950.
+//
+// One 64-lane wave per (row, new token, sequence), where rows 0..H_q-1 are
+// query heads (rotated into q_out) and rows H_q..H_q+H_kv-1 are KV heads
+// (K rotated, V copied, both written into the cache slot of the token).
+// Lane i < D/2 owns the rotation pair (x_i, x_{i+D/2}), which is the pair
+// rotate_half mixes (attn.py:56-59), so the wave holds a whole head row and
+// the fp8 absmax is a single wave reduction.
+//
+// The work is a few hundred KB per decode step and is latency bound; its
+// role is to produce bytes identical to the reference's rope_impl
+// (attn.py:13-63) and cache append (cache.py:41-42) at the slot given by the
+// per-sequence position.
+#include "tt_internal.h"
+#include "tt_numerics.h"
+
+namespace tt {
+namespace {
+
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float load(const void *p, int64_t i) {
+    return static_cast<const float *>(p)[i];
+  }
+  static __device__ __forceinline__ void store(void *p, int64_t i, float v) {
+    static_cast<float *>(p)[i] = v;
+  }
+  static __device__ __forceinline__ float rnd(float v) { return v; }
+};
+
+struct BF16Tag {};
+
+template <>
+struct Elem<BF16Tag> {
+  static __device__ __forceinline__ float load(const void *p, int64_t i) {
+    return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  }
+  static __device__ __forceinline__ void store(void *p, int64_t i, float v) {
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+  }
+  static __device__ __forceinline__ float rnd(float v) { return round_bf16(v); }
+};
+
+// out1 = r(r(x1*c) + r(-x2*s)), out2 = r(r(x2*c) + r(x1*s)), r = rounding to
+// the activation type; the three ops of attn.py:61 in the reference's order.
+template <typename A>
+__device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float &o1, float &o2) {
+#pragma clang fp contract(off)
+  const float a1 = Elem<A>::rnd(x1 * c);
+  const float b1 = Elem<A>::rnd((-x2) * s);
+  const float a2 = Elem<A>::rnd(x2 * c);
+  const float b2 = Elem<A>::rnd(x1 * s);
+  o1 = Elem<A>::rnd(a1 + b1);
+  o2 = Elem<A>::rnd(a2 + b2);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Slot element offset of token `pos` of sequence b, KV head hk; -1 if the
+// slot is outside the cache (capacity, page table or pool).
+__device__ __forceinline__ int64_t slot_offset(const RopeAppendArgs &a, int b, int hk, int64_t pos) {
+  if (pos < 0 || pos >= a.capacity) return -1;
+  const int64_t j = pos / a.page_size;
+  const int64_t slot = pos - j * a.page_size;
+  int64_t base;
+  if (a.page_table != nullptr) {
+    if (j >= a.max_pages) return -1;
+    const int64_t phys = a.page_table[(int64_t)b * a.max_pages + j];
+    if (phys < 0 || phys >= a.num_pages) return -1;
+    base = phys * a.c_page;
+  } else {
+    base = (int64_t)b * a.c_seq + j * a.c_page;
+  }
+  return base + (int64_t)hk * a.c_head + slot * a.head_dim;
+}
+
+template <typename A, bool kFP8>
+__global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
+  const int row = blockIdx.x;
+  const int t = blockIdx.y;
+  const int b = blockIdx.z;
+  const int i = threadIdx.x;
+  const int64_t pos = (int64_t)a.positions[b] + t;
+  if (pos < 0 || pos >= a.table_len) return;
+  const int half = a.head_dim >> 1;
+  const bool active = i < half;
+  float c = 0.f, s = 0.f;
+  if (active) {
+    c = Elem<A>::load(a.table, pos * a.head_dim + i);
+    s = Elem<A>::load(a.table, pos * a.head_dim + half + i);
+  }
+
+  if (row < a.hq) {
+    if (!active) return;
+    const int64_t src = (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st;
+    const float x1 = Elem<A>::load(a.q_in, src + i);
+    const float x2 = Elem<A>::load(a.q_in, src + half + i);
+    float o1, o2;
+    rotate_pair<A>(x1, x2, c, s, o1, o2);
+    const int64_t dst = (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh + (int64_t)t * a.qo_st;
+    Elem<A>::store(a.q_out, dst + i, o1);
+    Elem<A>::store(a.q_out, dst + half + i, o2);
+    return;
+  }
+
+  if (a.new_lens != nullptr && t >= a.new_lens[b]) return;  // padding token: no cache write
+  const int hk = row - a.hq;
+  const int64_t off = slot_offset(a, b, hk, pos);  // wave-uniform
+  if (off < 0) return;
+  float k1 = 0.f, k2 = 0.f, v1 = 0.f, v2 = 0.f;
+  if (active) {
+    const int64_t ks = (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
+    const int64_t vs = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh + (int64_t)t * a.vi_st;
+    rotate_pair<A>(Elem<A>::load(a.k_in, ks + i), Elem<A>::load(a.k_in, ks + half + i), c, s, k1, k2);
+    v1 = Elem<A>::load(a.v_in, vs + i);
+    v2 = Elem<A>::load(a.v_in, vs + half + i);
+  }
+
+  if constexpr (!kFP8) {
+    if (active) {
+      Elem<A>::store(a.k_cache, off + i, k1);
+      Elem<A>::store(a.k_cache, off + half + i, k2);
+      Elem<A>::store(a.v_cache, off + i, v1);
+      Elem<A>::store(a.v_cache, off + half + i, v2);
+    }
+  } else {
+    // Per-(token, head) symmetric scale: absmax / 448, codes e4m3fn(x / scale).
+    const float kmax = wave_max(fmaxf(fabsf(k1), fabsf(k2)));
+    const float vmax = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
+    const float kscale = kmax / 448.0f;
+    const float vscale = vmax / 448.0f;
+    if (active) {
+      uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
+      uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
+      kc[off + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k1 / kscale);
+      kc[off + half + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k2 / kscale);
+      vc[off + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v1 / vscale);
+      vc[off + half + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v2 / vscale);
+    }
+    if (i == 0) {
+      a.k_scale[off / a.head_dim] = kscale;
+      a.v_scale[off / a.head_dim] = vscale;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
+  const dim3 grid(a.hq + a.hkv, a.num_new, a.batch);
+  const dim3 block(64);
+  switch (kind) {
+    case CacheKind::kBF16:
+      hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false>), grid, block, 0, stream, a);
+      break;
+    case CacheKind::kF32:
+      hipLaunchKernelGGL((rope_append_kernel<float, false>), grid, block, 0, stream, a);
+      break;
+    case CacheKind::kFP8:
+      hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true>), grid, block, 0, stream, a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tt

@@ -1,0 +1,68 @@
+// Internal launch interface between the C ABI layer (abi.hip) and the
+// kernels (rope_append.hip, decode_attn.hip). Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tt {
+
+enum class CacheKind { kBF16, kF32, kFP8 };
+
+struct RopeAppendArgs {
+  const void *q_in;
+  int64_t qi_sb, qi_sh, qi_st;
+  const void *k_in;
+  int64_t ki_sb, ki_sh, ki_st;
+  const void *v_in;
+  int64_t vi_sb, vi_sh, vi_st;
+  void *q_out;
+  int64_t qo_sb, qo_sh, qo_st;
+  const void *table;
+  int64_t table_len;
+  const int32_t *positions;
+  const int32_t *new_lens;
+  const int32_t *page_table;
+  int64_t max_pages, num_pages;
+  void *k_cache;
+  void *v_cache;
+  float *k_scale;
+  float *v_scale;
+  int64_t c_seq, c_page, c_head;
+  int64_t capacity;
+  int batch, num_new, hq, hkv, head_dim, page_size;
+};
+
+struct DecodeArgs {
+  const void *q;
+  int64_t q_sb, q_sh;
+  const void *k_cache;
+  const void *v_cache;
+  const float *k_scale;
+  const float *v_scale;
+  int64_t c_seq, c_page, c_head;
+  const int32_t *seq_lens;
+  int max_len;
+  const int32_t *page_table;
+  int64_t max_pages, num_pages;
+  void *out;
+  int64_t o_sb, o_sh;
+  float *ws_o;   // [B][H_kv][max_splits][G][D] unnormalised partial outputs
+  float *ws_ml;  // [B][H_kv][max_splits][G][2] (running max in log2 units, sum)
+  int batch, hq, hkv, group, page_size, split_tokens, max_splits;
+  float scale_log2;  // sm_scale * log2(e)
+};
+
+hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream);
+hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
+
+// Partition helpers shared by the ABI layer and the launchers.
+int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);
+inline int64_t num_splits(int64_t max_len, int64_t split_tokens) {
+  return max_len <= 0 ? 1 : (max_len + split_tokens - 1) / split_tokens;
+}
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kTileTokens = 32;  // tokens per wave iteration (two 16-row MFMA blocks)
+
+}  // namespace tt

@@ -1,0 +1,220 @@
+"""PyTorch-facing wrappers of the gfx950 decode-step kernels.
+
+Tensors are validated here (device, dtype, shape, strides), then their raw
+device pointers go through the C ABI (include/tinytron_amd.h) on the current
+torch stream. There is no fallback: every entry point needs the HIP library
+and CUDA(HIP) tensors.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+FP8_DTYPE = torch.float8_e4m3fn
+
+
+def build_rope_table(num_positions: int, head_dim: int, theta: float = 10000.0,
+                     dtype: torch.dtype = torch.bfloat16, device="cuda") -> torch.Tensor:
+    """[num_positions, D] table = [cos(p f_i) | sin(p f_i)], i < D/2, in ``dtype``.
+
+    Built on ``device`` with the reference's own op sequence
+    (tinytron/model/modules/attn.py:30-54: inv_freq, the fp32 outer product,
+    cos/sin, cast to the activation dtype), so on the GPU it holds the bytes
+    the reference's rope_impl computes there. Only the first half of
+    ``emb = cat(freqs, freqs)`` is kept; the second half is identical.
+    """
+    if head_dim % 2 != 0:
+        raise ValueError(f"head_dim must be even for RoPE, got {head_dim}")
+    dev = torch.device(device)
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=dev) / head_dim))
+    pos = torch.arange(num_positions, device=dev).unsqueeze(0).float()
+    freqs = torch.einsum("bt,d->btd", pos, inv_freq)[0]
+    return torch.cat([freqs.cos().to(dtype), freqs.sin().to(dtype)], dim=-1).contiguous()
+
+
+@dataclass
+class KVLayout:
+    """Device view of one layer's cache as the kernels address it.
+
+    ``k``/``v`` are the storage tensors (bf16, fp32, or uint8 e4m3fn codes);
+    ``strides`` = (seq, page, head) element strides; ``page_table`` is None
+    for the contiguous [B, H, pages, P, D] store or an int32 [B, max_pages]
+    device tensor for the pool [num_pages, H, P, D]. fp8 scales are fp32 in
+    the cache layout with head_dim collapsed.
+    """
+
+    k: torch.Tensor
+    v: torch.Tensor
+    strides: tuple
+    num_heads: int
+    head_dim: int
+    page_size: int
+    capacity: int
+    kind: str  # "bf16" | "f32" | "fp8"
+    page_table: torch.Tensor | None = None
+    num_pages: int = 0
+    k_scale: torch.Tensor | None = None
+    v_scale: torch.Tensor | None = None
+
+    @property
+    def max_pages(self) -> int:
+        return 0 if self.page_table is None else int(self.page_table.shape[1])
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tinytron_amd kernels need GPU tensors (no CPU fallback)")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _act_kind(dtype: torch.dtype) -> str:
+    if dtype == torch.bfloat16:
+        return "bf16"
+    if dtype == torch.float32:
+        return "f32"
+    raise ValueError(f"unsupported activation dtype {dtype}")
+
+
+def _check_lastdim(name: str, t: torch.Tensor, dims: int) -> None:
+    if t.dim() != dims:
+        raise ValueError(f"{name} must have {dims} dims, got shape {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must be contiguous in head_dim")
+
+
+def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.Tensor,
+                positions: torch.Tensor, layout: KVLayout, q_out: torch.Tensor | None = None,
+                new_lens: torch.Tensor | None = None) -> torch.Tensor:
+    """RoPE q and k at per-sequence positions, append k/v to the cache.
+
+    q [B, H_q, T, D], k/v [B, H_kv, T, D] (any strides, head_dim contiguous);
+    positions int32 [B] = slot of token 0 per sequence; returns rotated q.
+    Restates rope_impl (attn.py:13-63) + LayerPagedKVCache.append
+    (cache.py:34-45) in one launch.
+    """
+    _require_cuda(q, k, v, table, positions, layout.k, layout.v)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_lastdim(name, t, 4)
+    B, Hq, T, D = q.shape
+    if k.shape != (B, layout.num_heads, T, D) or v.shape != k.shape:
+        raise ValueError(f"k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)} / cache heads")
+    if D != layout.head_dim:
+        raise ValueError(f"head_dim {D} does not match the cache's {layout.head_dim}")
+    kind = _act_kind(q.dtype)
+    if k.dtype != q.dtype or v.dtype != q.dtype or table.dtype != q.dtype:
+        raise ValueError("q, k, v and the rope table must share one dtype")
+    if layout.kind == "fp8" and kind != "bf16":
+        raise ValueError("an fp8 cache takes bf16 activations")
+    if layout.kind != "fp8" and layout.kind != kind:
+        raise ValueError(f"cache dtype {layout.kind} does not match activations {kind}")
+    if table.dim() != 2 or table.shape[1] != D or not table.is_contiguous():
+        raise ValueError("rope table must be a contiguous [positions, head_dim] tensor")
+    if positions.dtype != torch.int32 or positions.shape != (B,):
+        raise ValueError("positions must be int32 [B]")
+    if new_lens is not None and (new_lens.dtype != torch.int32 or new_lens.shape != (B,)):
+        raise ValueError("new_lens must be int32 [B]")
+    if q_out is None:
+        q_out = torch.empty(B, Hq, T, D, dtype=q.dtype, device=q.device)
+    _check_lastdim("q_out", q_out, 4)
+    lib = _lib.load()
+    common = [
+        _ptr(q), _lib.strides(*q.stride()[:3]), _ptr(k), _lib.strides(*k.stride()[:3]),
+        _ptr(v), _lib.strides(*v.stride()[:3]), _ptr(q_out), _lib.strides(*q_out.stride()[:3]),
+        _ptr(table), table.shape[0], _ptr(positions), _ptr(new_lens),
+        _ptr(layout.page_table), layout.max_pages, layout.num_pages,
+        _ptr(layout.k), _ptr(layout.v),
+    ]
+    tail = [_lib.strides(*layout.strides), layout.capacity, B, T, Hq, layout.num_heads, D,
+            layout.page_size, _stream(q.device)]
+    if layout.kind == "fp8":
+        st = lib.tt_rope_append_fp8(*common, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
+    elif layout.kind == "bf16":
+        st = lib.tt_rope_append_bf16(*common, *tail)
+    else:
+        st = lib.tt_rope_append_f32(*common, *tail)
+    _lib.check(st, "rope_append")
+    return q_out
+
+
+class Workspace:
+    """Grow-only device scratch for the split-K partials of one stream."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.buf = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+def split_tokens_for(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
+    return int(_lib.load().tt_decode_split_tokens(batch, num_kv_heads, max_seq_len))
+
+
+def workspace_bytes(batch: int, hq: int, hkv: int, head_dim: int, max_seq_len: int, split_tokens: int = 0) -> int:
+    return int(_lib.load().tt_decode_workspace_bytes(batch, hq, hkv, head_dim, max_seq_len, split_tokens))
+
+
+def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, max_seq_len: int,
+                     out: torch.Tensor | None = None, sm_scale: float | None = None, split_tokens: int = 0,
+                     workspace: Workspace | None = None) -> torch.Tensor:
+    """GQA decode attention of q [B, H_q, D] over each sequence's seq_lens[b] cached tokens.
+
+    Restates get_kv + gqa_impl + the all-True decode mask + SDPA
+    (cache.py:47-51, attn.py:66-95, 420-423). ``max_seq_len`` is a host-side
+    bound of seq_lens used to size the grid.
+    """
+    _require_cuda(q, layout.k, layout.v, seq_lens)
+    _check_lastdim("q", q, 3)
+    B, Hq, D = q.shape
+    kind = _act_kind(q.dtype)
+    if layout.kind == "fp8":
+        if kind != "bf16":
+            raise ValueError("an fp8 cache takes bf16 queries")
+    elif layout.kind != kind:
+        raise ValueError(f"cache dtype {layout.kind} does not match q {kind}")
+    if D != layout.head_dim:
+        raise ValueError(f"head_dim {D} does not match the cache's {layout.head_dim}")
+    if seq_lens.dtype != torch.int32 or seq_lens.shape != (B,):
+        raise ValueError("seq_lens must be int32 [B]")
+    if max_seq_len > layout.capacity:
+        raise ValueError(f"max_seq_len {max_seq_len} exceeds the cache capacity {layout.capacity}")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
+    _check_lastdim("out", out, 3)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    hkv = layout.num_heads
+    need = workspace_bytes(B, Hq, hkv, D, max_seq_len, split_tokens)
+    ws = (workspace or Workspace(q.device)).get(need)
+    lib = _lib.load()
+    head = [_ptr(q), _lib.strides(*q.stride()[:2]), _ptr(layout.k), _ptr(layout.v)]
+    tail = [
+        _lib.strides(*layout.strides), _ptr(seq_lens), int(max_seq_len),
+        _ptr(layout.page_table), layout.max_pages, layout.num_pages,
+        _ptr(out), _lib.strides(*out.stride()[:2]),
+        B, Hq, hkv, D, layout.page_size, float(sm_scale), int(split_tokens),
+        _ptr(ws), ws.numel(), _stream(q.device),
+    ]
+    if layout.kind == "fp8":
+        st = lib.tt_gqa_decode_attn_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
+    elif layout.kind == "bf16":
+        st = lib.tt_gqa_decode_attn_bf16(*head, *tail)
+    else:
+        st = lib.tt_gqa_decode_attn_f32(*head, *tail)
+    _lib.check(st, "decode_attention")
+    return out
