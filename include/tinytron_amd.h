@@ -157,12 +157,15 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
  * out [B, H_q, D] bf16, strides out_strides = {b, h}. A sequence with
  *   seq_lens[b] <= 0 gets zeros.
  * sm_scale: softmax scale (1/sqrt(D) for the reference's SDPA default).
- * split_tokens: tokens per split (multiple of 128), 0 = automatic.
+ * split_tokens: tokens per split: 128, 256, 512 or 1024; 0 = automatic.
  * workspace: device scratch of at least tt_decode_workspace_bytes(...) bytes
  *   for the same (batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
  *   split_tokens); its contents need no initialisation.
  * Requirements: head_dim in {64, 128}; H_q % H_kv == 0 and
- *   H_q / H_kv <= 16; page_size % 16 == 0; q, cache and out 16-byte aligned.
+ *   H_q / H_kv <= 16; a paged pool has a power-of-two page_size >= 16; the
+ *   contiguous store has dense pages (cache_strides[1] == page_size *
+ *   head_dim, as the reference's [B, H, pages, P, D] store), any page_size;
+ *   q and cache 16-byte aligned, their strides multiples of 8 elements.
  * Physical page numbers read from page_table are clamped into
  *   [0, num_pages) so that a bad table cannot address outside the pool.
  */

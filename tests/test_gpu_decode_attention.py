@@ -127,15 +127,24 @@ def test_single_token_is_v():
     assert np.array_equal(f32_to_bf16_bits(got), f32_to_bf16_bits(exp))
 
 
-@pytest.mark.parametrize("split", [128, 256, 1024])
+@pytest.mark.parametrize("split", [128, 256, 512, 1024])
 def test_split_invariance(split):
     lengths = [900, 2000, 130]
     got, ref, _ = run_case(lengths, split_tokens=split, seed=21)
     assert_close(got, ref)
 
 
-def test_page_size_64_contiguous():
-    got, ref, _ = run_case([70, 200, 64], P=64, seed=9)
+@pytest.mark.parametrize("P", [64, 100, 128])
+def test_contiguous_page_sizes(P):
+    """The contiguous store takes any page size (the reference default is 128)."""
+    got, ref, _ = run_case([70, 200, 64, 129], P=P, seed=9)
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("P", [32, 64])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_page_sizes(P, fp8):
+    got, ref, _ = run_case([70, 200, 64, 129], P=P, paged=True, fp8=fp8, seed=P)
     assert_close(got, ref)
 
 

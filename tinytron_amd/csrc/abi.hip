@@ -152,8 +152,6 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   TT_CHECK(num_kv_heads <= 65535 && num_q_heads <= 65535, TT_ERR_UNSUPPORTED, "too many heads");
   TT_CHECK(head_dim == 64 || head_dim == 128, TT_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld",
            (long long)head_dim);
-  TT_CHECK(page_size % 16 == 0, TT_ERR_UNSUPPORTED, "page_size must be a multiple of 16, got %lld",
-           (long long)page_size);
   TT_CHECK(max_seq_len >= 0 && max_seq_len < (int64_t)1 << 30, TT_ERR_INVALID_ARGUMENT,
            "max_seq_len out of range");
   if (kind == tt::CacheKind::kFP8) {
@@ -161,10 +159,18 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   }
   int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
   if (rc != TT_OK) return rc;
+  int page_shift = 0;
   if (page_table != nullptr) {
+    while (page_shift < 30 && ((int64_t)1 << page_shift) < page_size) ++page_shift;
+    TT_CHECK(page_size >= 16 && ((int64_t)1 << page_shift) == page_size, TT_ERR_UNSUPPORTED,
+             "paged pools need a power-of-two page_size >= 16, got %lld", (long long)page_size);
     TT_CHECK(max_seq_len <= max_pages * page_size, TT_ERR_INVALID_ARGUMENT,
              "max_seq_len %lld exceeds the page table's %lld pages of %lld tokens", (long long)max_seq_len,
              (long long)max_pages, (long long)page_size);
+  } else {
+    TT_CHECK(cache_strides[1] == page_size * head_dim, TT_ERR_UNSUPPORTED,
+             "the contiguous store needs dense pages (page stride %lld != page_size * head_dim)",
+             (long long)cache_strides[1]);
   }
   if (kind != tt::CacheKind::kF32) {
     TT_CHECK(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
@@ -178,8 +184,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
              TT_ERR_INVALID_ARGUMENT, "fp32 pointers must be 4-byte aligned");
   }
   const int64_t split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
-  TT_CHECK(split >= 128 && split % 128 == 0 && split <= (1 << 20), TT_ERR_INVALID_ARGUMENT,
-           "split_tokens must be a positive multiple of 128, got %lld", (long long)split_tokens);
+  TT_CHECK(split == 128 || split == 256 || split == 512 || split == 1024, TT_ERR_INVALID_ARGUMENT,
+           "split_tokens must be 0 (auto), 128, 256, 512 or 1024, got %lld", (long long)split_tokens);
   const int64_t splits = tt::num_splits(max_seq_len, split);
   TT_CHECK(splits <= 65535, TT_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
   const size_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
@@ -215,7 +221,7 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.hq = (int)num_q_heads;
   a.hkv = (int)num_kv_heads;
   a.group = (int)g;
-  a.page_size = (int)page_size;
+  a.page_shift = page_shift;
   a.split_tokens = (int)split;
   a.max_splits = (int)splits;
   a.scale_log2 = sm_scale * 1.4426950408889634f;

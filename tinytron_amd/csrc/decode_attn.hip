@@ -70,100 +70,93 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(u32x2 v) {
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+constexpr int kBufferFlags = 0x00020000;  // gfx9 raw buffer: dword data format, no swizzle
+
+// Every lane loads 16 bytes per load: lane (m + 16g) reads row (token) m of a
+// 16-token block at byte offset 16g + 64u, u < D*E/64. For bf16 a 16-byte
+// fragment is one 32-wide k step of a 16x16x32 MFMA (d = 32u + 8g + i); for
+// fp8 it is two k steps (hh = 0, 1: d = 64u + 16g + 8hh + i). The query
+// operand is loaded in the same d order, so Q.K^T is unchanged.
 template <bool kFP8>
 struct KVTraits;
 
 template <>
 struct KVTraits<false> {
-  using Frag = u32x4;  // 8 bf16
-  static __device__ __forceinline__ Frag load(const void *base, int64_t elem, bool valid) {
-    Frag v = {0u, 0u, 0u, 0u};
-    if (valid) v = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + elem);
-    return v;
-  }
-  static __device__ __forceinline__ bf16x8 as_bf16(Frag f) { return __builtin_bit_cast(bf16x8, f); }
+  static constexpr int kElemBytes = 2;
+  static constexpr int kStepsPerFrag = 1;
+  static __device__ __forceinline__ bf16x8 step(u32x4 f, int) { return __builtin_bit_cast(bf16x8, f); }
+  // d of k-slot (g, i) of k step s
+  static __device__ __forceinline__ int q_offset(int s, int g) { return 32 * s + 8 * g; }
 };
 
 template <>
 struct KVTraits<true> {
-  using Frag = u32x2;  // 8 fp8
-  static __device__ __forceinline__ Frag load(const void *base, int64_t elem, bool valid) {
-    Frag v = {0u, 0u};
-    if (valid) v = *reinterpret_cast<const u32x2 *>(static_cast<const uint8_t *>(base) + elem);
-    return v;
+  static constexpr int kElemBytes = 1;
+  static constexpr int kStepsPerFrag = 2;
+  static __device__ __forceinline__ bf16x8 step(u32x4 f, int hh) {
+    return hh == 0 ? fp8x8_to_bf16x8(u32x2{f[0], f[1]}) : fp8x8_to_bf16x8(u32x2{f[2], f[3]});
   }
-  static __device__ __forceinline__ bf16x8 as_bf16(Frag f) { return fp8x8_to_bf16x8(f); }
+  static __device__ __forceinline__ int q_offset(int s, int g) { return 64 * (s >> 1) + 16 * g + 8 * (s & 1); }
 };
 
 template <int D, bool kFP8>
 struct Tile {
-  static constexpr int NDB = D / 32;
-  typename KVTraits<kFP8>::Frag k[2][NDB];
-  typename KVTraits<kFP8>::Frag v[2][NDB];
+  static constexpr int NU = D * KVTraits<kFP8>::kElemBytes / 64;  // 16-byte fragments per lane per row
+  u32x4 k[2][NU];
+  u32x4 v[2][NU];
   f32x4 ks[2];  // fp8: K scales of this lane's 4 score rows, per 16-token block
   f32x4 vs[2];
 };
 
-// Element offset of token tb (multiple of 16) of (b, hk), d = 0. A 16-token
-// block never straddles a page because page_size % 16 == 0.
-__device__ __forceinline__ int64_t block_base(const DecodeArgs &a, int b, int hk, int tb, int D) {
-  const int j = tb / a.page_size;
-  const int slot = tb - j * a.page_size;
-  int64_t page_base;
+// Element offset of token tb (a multiple of 16) of (b, hk), d = 0; tb must
+// lie in a page the sequence owns. A 16-token block never straddles a page:
+// paged pools have power-of-two pages of >= 16 tokens, and the contiguous
+// store is addressed linearly (its pages are dense, page stride = P * D).
+__device__ __forceinline__ int64_t block_elem(const DecodeArgs &a, int b, int hk, int tb, int D) {
   if (a.page_table != nullptr) {
-    int64_t phys = a.page_table[(int64_t)b * a.max_pages + j];
+    int64_t phys = a.page_table[(int64_t)b * a.max_pages + (tb >> a.page_shift)];
     phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
-    page_base = phys * a.c_page;
-  } else {
-    page_base = (int64_t)b * a.c_seq + (int64_t)j * a.c_page;
+    return phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tb & ((1 << a.page_shift) - 1)) * D;
   }
-  return page_base + (int64_t)hk * a.c_head + (int64_t)slot * D;
+  return (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)tb * D;
 }
 
+// Element offset of any token t < length of (b, hk), d = 0.
+__device__ __forceinline__ int64_t token_elem(const DecodeArgs &a, int b, int hk, int t, int D) {
+  const int tb = t & ~15;
+  return block_elem(a, b, hk, tb, D) + (int64_t)(t - tb) * D;
+}
+
+// Loads one 16-token block whose element offset `elem` was resolved in the
+// prologue. Rows past the sequence end are outside the buffer range
+// (num_records) and read as zero: no branch, no out-of-bounds access, and no
+// garbage (possibly NaN) reaches the MFMAs.
 template <int D, bool kFP8>
-__device__ __forceinline__ void load_tile(const DecodeArgs &a, int b, int hk, int t0, int L, int lane,
-                                          Tile<D, kFP8> &tile) {
-  using TR = KVTraits<kFP8>;
-  constexpr int NDB = D / 32;
+__device__ __forceinline__ void load_block(const DecodeArgs &a, int64_t elem, int rows, int lane,
+                                           u32x4 (&k)[Tile<D, kFP8>::NU], u32x4 (&v)[Tile<D, kFP8>::NU],
+                                           f32x4 &ks, f32x4 &vs) {
+  constexpr int E = KVTraits<kFP8>::kElemBytes;
+  constexpr int NU = Tile<D, kFP8>::NU;
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(static_cast<const char *>(a.k_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
   const int m = lane & 15;
   const int g = lane >> 4;
+  const int off = m * D * E + 16 * g;
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int tb = t0 + 16 * tt;
-    if (tb < L) {
-      const int64_t base = block_base(a, b, hk, tb, D);
-      const bool valid = tb + m < L;
-      const int64_t row = base + (int64_t)m * D + 8 * g;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        tile.k[tt][db] = TR::load(a.k_cache, row + 32 * db, valid);
-        tile.v[tt][db] = TR::load(a.v_cache, row + 32 * db, valid);
-      }
-      if constexpr (kFP8) {
-        // scores of this lane are tokens tb + 4g + r, r = 0..3
-        const int64_t sidx = base / D + 4 * g;
-        f32x4 ks = {0.f, 0.f, 0.f, 0.f}, vs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (tb + 4 * g + r < L) {
-            ks[r] = a.k_scale[sidx + r];
-            vs[r] = a.v_scale[sidx + r];
-          }
-        }
-        tile.ks[tt] = ks;
-        tile.vs[tt] = vs;
-      }
-    } else {
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        tile.k[tt][db] = TR::load(a.k_cache, 0, false);
-        tile.v[tt][db] = TR::load(a.v_cache, 0, false);
-      }
-      if constexpr (kFP8) {
-        tile.ks[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        tile.vs[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
+  for (int u = 0; u < NU; ++u) {
+    k[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * u, 0, 0));
+    v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off + 64 * u, 0, 0));
+  }
+  if constexpr (kFP8) {
+    // this lane's score rows are tokens tb + 4g + r, r = 0..3
+    const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + elem / D, (short)0,
+                                                       rows * 4, kBufferFlags);
+    const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + elem / D, (short)0,
+                                                       rows * 4, kBufferFlags);
+    ks = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rks, 16 * g, 0, 0));
+    vs = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvs, 16 * g, 0, 0));
   }
 }
 
@@ -177,8 +170,8 @@ struct WaveState {
 
 template <int D, bool kFP8>
 __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L, int lane, const Tile<D, kFP8> &tile,
-                                             const bf16x8 (&qf)[D / 32], const typename KVTraits<kFP8>::Frag ident[2],
-                                             WaveState<D, kFP8> &st) {
+                                             const bf16x8 (&qf)[D / 32], const bf16x8 (&ident16)[2],
+                                             const u32x2 (&ident8)[2], WaveState<D, kFP8> &st) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
   const int g = lane >> 4;
@@ -189,10 +182,14 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
   for (int tt = 0; tt < 2; ++tt) {
     S[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) S[tt] = mfma_bf16(TR::as_bf16(tile.k[tt][db]), qf[db], S[tt]);
+    for (int s = 0; s < NDB; ++s) {
+      const int u = s / TR::kStepsPerFrag;
+      S[tt] = mfma_bf16(TR::step(tile.k[tt][u], s % TR::kStepsPerFrag), qf[s], S[tt]);
+    }
   }
 
   float s[8];
+  bool valid[8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
@@ -200,6 +197,7 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
       const int tok = t0 + 16 * tt + 4 * g + r;
       float x = S[tt][r];
       if constexpr (kFP8) x *= tile.ks[tt][r];
+      valid[tt * 4 + r] = tok < L;
       s[tt * 4 + r] = tok < L ? x * a.scale_log2 : kNegInf;
     }
   }
@@ -220,10 +218,12 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
   st.l = st.l * alpha + psum;
   st.m = m_new;
   if constexpr (kFP8) {
+    // fold the per-token V scale into P; masked tokens stay exactly 0 (select,
+    // not multiply, in case a scale slot past the end holds a non-finite value)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      p[r] *= tile.vs[0][r];
-      p[4 + r] *= tile.vs[1][r];
+      p[r] = valid[r] ? p[r] * tile.vs[0][r] : 0.f;
+      p[4 + r] = valid[4 + r] ? p[4 + r] * tile.vs[1][r] : 0.f;
     }
   }
 
@@ -247,17 +247,22 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) {
-    const int db = c >> 1;
+    // block c: bf16 c = 2u + hi; fp8 c = 4u + 2hh + hi (column order in o_col_d)
     const int hi = c & 1;
     f32x4 t0v, t1v;
     if constexpr (kFP8) {
-      t0v = mfma_fp8(tile.v[0][db], ident[hi], zero);
-      t1v = mfma_fp8(tile.v[1][db], ident[hi], zero);
+      const int u = c >> 2;
+      const int hh = (c >> 1) & 1;
+      const u32x2 v0 = hh ? u32x2{tile.v[0][u][2], tile.v[0][u][3]} : u32x2{tile.v[0][u][0], tile.v[0][u][1]};
+      const u32x2 v1 = hh ? u32x2{tile.v[1][u][2], tile.v[1][u][3]} : u32x2{tile.v[1][u][0], tile.v[1][u][1]};
+      t0v = mfma_fp8(v0, ident8[hi], zero);
+      t1v = mfma_fp8(v1, ident8[hi], zero);
     } else {
-      t0v = mfma_bf16(TR::as_bf16(tile.v[0][db]), TR::as_bf16(ident[hi]), zero);
-      t1v = mfma_bf16(TR::as_bf16(tile.v[1][db]), TR::as_bf16(ident[hi]), zero);
+      const int u = c >> 1;
+      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, tile.v[0][u]), ident16[hi], zero);
+      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, tile.v[1][u]), ident16[hi], zero);
     }
-    // lane (n + 16g): V[token t0 + 4g + r][d = 16c + n] (t0v), same for t0 + 16 (t1v)
+    // lane (n + 16g): V[token t0 + 4g + r][o_col_d(c, n)] (t0v), same for t0 + 16 (t1v)
     const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
     const bf16x8 vb = __builtin_convertvector(vv, bf16x8);
     st.o[c] = mfma_bf16(pa_hi, vb, st.o[c]);
@@ -265,69 +270,113 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
   }
 }
 
+// head_dim index of output column n of PV block c (see process_tile).
+template <bool kFP8>
+__device__ __forceinline__ int o_col_d(int c, int n) {
+  if constexpr (kFP8) {
+    const int u = c >> 2, hh = (c >> 1) & 1, hi = c & 1;
+    return 64 * u + 16 * (2 * hi + (n >> 3)) + 8 * hh + (n & 7);
+  } else {
+    return 16 * c + n;
+  }
+}
+
 // Selection matrices for the V transpose: B[k][n] = 1 iff k == n (+16 for
 // the upper half), expressed in the (lane group, slot) coordinates in which
 // the A operand was loaded, so the result does not depend on how the
 // hardware orders the K index inside a lane.
-template <bool kFP8>
-__device__ __forceinline__ void make_identity(int lane, typename KVTraits<kFP8>::Frag ident[2]) {
+__device__ __forceinline__ void make_identity(int lane, bf16x8 (&ident16)[2], u32x2 (&ident8)[2]) {
   const int n = lane & 15;
   const int g = lane >> 4;
-  if constexpr (kFP8) {
-    uint32_t w[2][2] = {{0u, 0u}, {0u, 0u}};
+  uint32_t w8[2][2] = {{0u, 0u}, {0u, 0u}};
+  uint32_t w16[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (8 * g + i == n) w[0][i >> 2] |= 0x38u << (8 * (i & 3));        // e4m3fn 1.0
-      if (8 * g + i == n + 16) w[1][i >> 2] |= 0x38u << (8 * (i & 3));
+  for (int i = 0; i < 8; ++i) {
+    if (8 * g + i == n) {
+      w8[0][i >> 2] |= 0x38u << (8 * (i & 3));        // e4m3fn 1.0
+      w16[0][i >> 1] |= 0x3f80u << (16 * (i & 1));    // bf16 1.0
     }
-    ident[0] = u32x2{w[0][0], w[0][1]};
-    ident[1] = u32x2{w[1][0], w[1][1]};
-  } else {
-    uint32_t w[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (8 * g + i == n + 16) {
+      w8[1][i >> 2] |= 0x38u << (8 * (i & 3));
+      w16[1][i >> 1] |= 0x3f80u << (16 * (i & 1));
+    }
+  }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (8 * g + i == n) w[0][i >> 1] |= 0x3f80u << (16 * (i & 1));     // bf16 1.0
-      if (8 * g + i == n + 16) w[1][i >> 1] |= 0x3f80u << (16 * (i & 1));
-    }
-    ident[0] = u32x4{w[0][0], w[0][1], w[0][2], w[0][3]};
-    ident[1] = u32x4{w[1][0], w[1][1], w[1][2], w[1][3]};
+  for (int h = 0; h < 2; ++h) {
+    ident8[h] = u32x2{w8[h][0], w8[h][1]};
+    ident16[h] = __builtin_bit_cast(bf16x8, u32x4{w16[h][0], w16[h][1], w16[h][2], w16[h][3]});
   }
 }
 
-template <int D, bool kFP8>
+template <int D, bool kFP8, int kTiles>
 __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
+  using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
+  constexpr int kWaveTokens = kTiles * kTileTokens;
+  constexpr int kBlocks = 2 * kTiles;  // 16-token blocks per wave
   extern __shared__ float smem[];  // [4][G][D] outputs, then [4][16] m, [4][16] l
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int split = blockIdx.x;
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
   const int G = a.group;
   const int L = min(a.seq_lens[b], a.max_len);
-  const int s_begin = split * a.split_tokens;
+  const int s_begin = split * (kWavesPerBlock * kWaveTokens);
   if (s_begin >= L) return;  // uniform for the block
-  const int s_end = min(L, s_begin + a.split_tokens);
-  const int per_wave = a.split_tokens / kWavesPerBlock;
-  const int w_begin = s_begin + wave * per_wave;
-  const int w_end = min(s_end, w_begin + per_wave);
+  const int w_begin = s_begin + wave * kWaveTokens;
   const int n = lane & 15;
   const int g = lane >> 4;
 
-  // q^T as the B operand: column n = query head hk*G + n (zero for n >= G).
+  // Resolve every block's address up front (page-table reads are scalar and
+  // independent), so the streaming loop below has no dependent loads.
+  // Blocks past the end keep a valid in-sequence token for the lookup and
+  // zero rows.
+  int64_t belem[kBlocks];
+  int brows[kBlocks];
+  if (a.page_table != nullptr) {
+    // one load for the whole wave: lane i fetches the entry of the wave's
+    // i-th page (clamped to the sequence's last page), then each block reads
+    // its entry with v_readlane into scalar registers.
+    const int j_first = min(w_begin, L - 1) >> a.page_shift;
+    const int j_last = (L - 1) >> a.page_shift;
+    const int pmask = (1 << a.page_shift) - 1;
+    int entry = 0;
+    if (lane < kBlocks) entry = a.page_table[(int64_t)b * a.max_pages + min(j_first + lane, j_last)];
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      const int tb = w_begin + 16 * i;
+      const int tc = min(tb, (L - 1) & ~15);
+      int64_t phys = __builtin_amdgcn_readlane(entry, (tc >> a.page_shift) - j_first);
+      phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
+      brows[i] = min(max(L - tb, 0), 16);
+      belem[i] = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & pmask) * D;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kBlocks; ++i) {
+      const int tb = w_begin + 16 * i;
+      brows[i] = min(max(L - tb, 0), 16);
+      belem[i] = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)min(tb, (L - 1) & ~15) * D;
+    }
+  }
+
+  // q^T as the B operand: column n = query head hk*G + n (zero for n >= G),
+  // k step s holding the head_dim values the K fragments hold.
   bf16x8 qf[NDB];
   {
     const uint16_t *q = static_cast<const uint16_t *>(a.q);
-    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + n) * a.q_sh + 8 * g;
+    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + n) * a.q_sh;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int s = 0; s < NDB; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (n < G) v = *reinterpret_cast<const u32x4 *>(q + qrow + 32 * db);
-      qf[db] = __builtin_bit_cast(bf16x8, v);
+      if (n < G) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
+      qf[s] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  typename KVTraits<kFP8>::Frag ident[2];
-  make_identity<kFP8>(lane, ident);
+  bf16x8 ident16[2];
+  u32x2 ident8[2];
+  make_identity(lane, ident16, ident8);
 
   WaveState<D, kFP8> st;
 #pragma unroll
@@ -335,20 +384,21 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
   st.m = kNegInf;
   st.l = 0.f;
 
-  if (w_begin < w_end) {
-    Tile<D, kFP8> ta, tb;
-    load_tile<D, kFP8>(a, b, hk, w_begin, L, lane, ta);
-    int t0 = w_begin;
-    while (true) {
-      if (t0 + kTileTokens < w_end) load_tile<D, kFP8>(a, b, hk, t0 + kTileTokens, L, lane, tb);
-      process_tile<D, kFP8>(a, t0, L, lane, ta, qf, ident, st);
-      t0 += kTileTokens;
-      if (t0 >= w_end) break;
-      if (t0 + kTileTokens < w_end) load_tile<D, kFP8>(a, b, hk, t0 + kTileTokens, L, lane, ta);
-      process_tile<D, kFP8>(a, t0, L, lane, tb, qf, ident, st);
-      t0 += kTileTokens;
-      if (t0 >= w_end) break;
+  // kTiles 32-token tiles per wave, fully unrolled, the next tile's loads in
+  // flight while the current one is on the matrix cores. Tiles past the end
+  // of the sequence load nothing (zero-row buffer ranges) and are skipped.
+  Tile<D, kFP8> buf[2];
+  load_block<D, kFP8>(a, belem[0], brows[0], lane, buf[0].k[0], buf[0].v[0], buf[0].ks[0], buf[0].vs[0]);
+  load_block<D, kFP8>(a, belem[1], brows[1], lane, buf[0].k[1], buf[0].v[1], buf[0].ks[1], buf[0].vs[1]);
+#pragma unroll
+  for (int it = 0; it < kTiles; ++it) {
+    const int t0 = w_begin + it * kTileTokens;
+    if (it + 1 < kTiles) {
+      Tile<D, kFP8> &nx = buf[(it + 1) & 1];
+      load_block<D, kFP8>(a, belem[2 * it + 2], brows[2 * it + 2], lane, nx.k[0], nx.v[0], nx.ks[0], nx.vs[0]);
+      load_block<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, nx.k[1], nx.v[1], nx.ks[1], nx.vs[1]);
     }
+    if (t0 < L) process_tile<D, kFP8>(a, t0, L, lane, buf[it & 1], qf, ident16, ident8, st);
   }
 
   // Merge the 4 wave states of the block in LDS.
@@ -367,7 +417,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int head = 4 * g + r;
-      if (head < G) so[(wave * G + head) * D + 16 * c + n] = st.o[c][r];
+      if (head < G) so[(wave * G + head) * D + o_col_d<kFP8>(c, n)] = st.o[c][r];
     }
   }
   __syncthreads();
@@ -441,8 +491,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
     const bool valid = tok < w_end;
     int64_t koff = 0;
     if (valid) {
-      const int tb = tok & ~15;
-      koff = block_base(a, b, hk, tb, D) + (int64_t)(tok - tb) * D;
+      koff = token_elem(a, b, hk, tok, D);
     }
     for (int h = 0; h < G && h < 16; ++h) {
       float sc = kNegInf;
@@ -466,8 +515,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
       for (int j = 0; j < DPL; ++j) o[h][j] *= alpha;
       for (int t = 0; t < nt; ++t) {
         const int tk = t0 + t;
-        const int tb = tk & ~15;
-        const int64_t voff = block_base(a, b, hk, tb, D) + (int64_t)(tk - tb) * D;
+        const int64_t voff = token_elem(a, b, hk, tk, D);
         const float pt = sp[t];
         for (int j = 0; j < DPL; ++j) o[h][j] += pt * vc[voff + lane + 64 * j];
       }
@@ -543,25 +591,45 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
   }
 }
 
+template <int D, bool kFP8>
+hipError_t launch_mfma(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hipStream_t stream) {
+  switch (a.split_tokens / (kWavesPerBlock * kTileTokens)) {
+    case 2:
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 2>), grid, block, lds, stream, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 4>), grid, block, lds, stream, a);
+      break;
+    case 8:
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 8>), grid, block, lds, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 1>), grid, block, lds, stream, a);
+      break;
+  }
+  return hipGetLastError();
+}
+
 template <int D>
 hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
   const dim3 grid(a.max_splits, a.hkv, a.batch);
   const dim3 block(64 * kWavesPerBlock);
   const size_t lds = sizeof(float) * (kWavesPerBlock * a.group * D + 2 * kWavesPerBlock * 16);
+  hipError_t err = hipSuccess;
   switch (kind) {
     case CacheKind::kBF16:
-      hipLaunchKernelGGL((decode_split_kernel<D, false>), grid, block, lds, stream, a);
+      err = launch_mfma<D, false>(a, grid, block, lds, stream);
       break;
     case CacheKind::kFP8:
-      hipLaunchKernelGGL((decode_split_kernel<D, true>), grid, block, lds, stream, a);
+      err = launch_mfma<D, true>(a, grid, block, lds, stream);
       break;
     case CacheKind::kF32: {
       const size_t lds32 = lds + sizeof(float) * (a.group * D + kWavesPerBlock * 64);
       hipLaunchKernelGGL((decode_split_kernel_f32<D>), grid, block, lds32, stream, a);
+      err = hipGetLastError();
       break;
     }
   }
-  hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const dim3 cgrid(a.hq, a.batch);
   if (kind == CacheKind::kF32) {

@@ -49,7 +49,8 @@ struct DecodeArgs {
   int64_t o_sb, o_sh;
   float *ws_o;   // [B][H_kv][max_splits][G][D] unnormalised partial outputs
   float *ws_ml;  // [B][H_kv][max_splits][G][2] (running max in log2 units, sum)
-  int batch, hq, hkv, group, page_size, split_tokens, max_splits;
+  int batch, hq, hkv, group, split_tokens, max_splits;
+  int page_shift;    // paged pools: log2(page_size); the contiguous store is addressed linearly
   float scale_log2;  // sm_scale * log2(e)
 };
 
