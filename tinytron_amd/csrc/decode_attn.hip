@@ -6,7 +6,7 @@
 // with K/V read from KV head h / G (G = H_q / H_kv).
 //
 // Work decomposition
-//   grid = (splits, H_kv, B); one workgroup = 4 waves = one (b, kv head,
+//   grid = (H_kv, splits, B); one workgroup = 4 waves = one (b, kv head,
 //   split) of `split_tokens` tokens; each wave streams a quarter of the split
 //   in 32-token tiles and keeps an online-softmax state for the G query heads
 //   of the group, so every K/V byte is read from HBM once for all G heads.
@@ -317,8 +317,10 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
   extern __shared__ float smem[];  // [4][G][D] outputs, then [4][16] m, [4][16] l
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int split = blockIdx.x;
-  const int hk = blockIdx.y;
+  // KV heads are the fastest grid dimension: workgroups that run together
+  // read the head blocks of the same physical pages (adjacent in the pool).
+  const int hk = blockIdx.x;
+  const int split = blockIdx.y;
   const int b = blockIdx.z;
   const int G = a.group;
   const int L = min(a.seq_lens[b], a.max_len);
@@ -592,7 +594,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
 }
 
 template <int D, bool kFP8>
-hipError_t launch_mfma(const DecodeArgs &a, dim3 grid, dim3 block, size_t lds, hipStream_t stream) {
+hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds, hipStream_t stream) {
+  const dim3 grid(a.hkv, a.max_splits, a.batch);
   switch (a.split_tokens / (kWavesPerBlock * kTileTokens)) {
     case 2:
       hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 2>), grid, block, lds, stream, a);
@@ -618,10 +621,10 @@ hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
   hipError_t err = hipSuccess;
   switch (kind) {
     case CacheKind::kBF16:
-      err = launch_mfma<D, false>(a, grid, block, lds, stream);
+      err = launch_mfma<D, false>(a, block, lds, stream);
       break;
     case CacheKind::kFP8:
-      err = launch_mfma<D, true>(a, grid, block, lds, stream);
+      err = launch_mfma<D, true>(a, block, lds, stream);
       break;
     case CacheKind::kF32: {
       const size_t lds32 = lds + sizeof(float) * (a.group * D + kWavesPerBlock * 64);
