@@ -84,7 +84,8 @@ def e4m3fn_encode(x) -> np.ndarray:
     """
     x = np.asarray(x, dtype=np.float32)
     sign = ((x.view(np.uint32) >> 24) & 0x80).astype(np.uint8)
-    a = np.abs(x).astype(np.float64)
+    bad = ~np.isfinite(x) | (np.abs(x) > 464.0)
+    a = np.where(bad, 0.0, np.abs(x).astype(np.float64))
     code = np.zeros(x.shape, dtype=np.int64)
 
     sub = a < 2.0 ** -6
@@ -103,7 +104,6 @@ def e4m3fn_encode(x) -> np.ndarray:
     normal_code = ((e.astype(np.int64) + 7) << 3) | (q - 8)
     code = np.where(sub, code, normal_code)
 
-    bad = ~np.isfinite(x) | (a > 464.0)
     code = np.where(bad, _E4M3_NAN, code)
     return (code.astype(np.uint8) | sign).astype(np.uint8)
 

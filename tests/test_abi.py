@@ -1,0 +1,120 @@
+"""The C ABI library: loads, exports every symbol include/tinytron_amd.h
+declares, reports its version, sizes workspaces, and rejects invalid
+arguments with the documented status codes before launching anything.
+
+These tests make no compute call. The argument-rejection cases pass fake
+(non-dereferenced) device pointers, so they run only where no GPU is
+visible: every case must fail validation, and none may ever launch.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tinytron_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tinytron_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tt_[a-z0-9_]+)\s*\(", text)))
+
+
+def _no_gpu():
+    try:
+        import torch
+
+        return not torch.cuda.is_available()
+    except Exception:
+        return True
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
+
+
+def test_abi_version():
+    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 1
+
+
+def test_workspace_and_split_sizing():
+    lib = _lib.load()
+    # C3: B 64, 32/8 heads, D 128, longest sequence 16385 tokens
+    split = lib.tt_decode_split_tokens(64, 8, 16385)
+    assert split in (128, 256, 512, 1024)
+    nbytes = lib.tt_decode_workspace_bytes(64, 32, 8, 128, 16385, split)
+    splits = -(-16385 // split)
+    assert nbytes == 64 * 8 * splits * 4 * (128 + 2) * 4
+    assert lib.tt_decode_workspace_bytes(0, 32, 8, 128, 100, 0) == 0
+
+
+FAKE = 0x10000  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def _attn(lib, **kw):
+    args = dict(q=FAKE, q_strides=(4096, 128), k=FAKE, v=FAKE, cache_strides=(0, 2048 * 8, 2048),
+                seq_lens=FAKE, max_len=100, page_table=FAKE, max_pages=10, num_pages=100, out=FAKE,
+                out_strides=(4096, 128), batch=2, hq=32, hkv=8, head_dim=128, page_size=16, sm_scale=0.088,
+                split=0, ws=FAKE, ws_bytes=1 << 30)
+    args.update(kw)
+    a = args
+    return lib.tt_gqa_decode_attn_bf16(
+        a["q"], _lib.strides(*a["q_strides"]), a["k"], a["v"], _lib.strides(*a["cache_strides"]),
+        a["seq_lens"], a["max_len"], a["page_table"], a["max_pages"], a["num_pages"], a["out"],
+        _lib.strides(*a["out_strides"]), a["batch"], a["hq"], a["hkv"], a["head_dim"], a["page_size"],
+        a["sm_scale"], a["split"], a["ws"], a["ws_bytes"], None)
+
+
+@pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(q=None), _lib.TT_ERR_INVALID_ARGUMENT, "NULL"),
+    (dict(head_dim=96, q_strides=(4096, 96)), _lib.TT_ERR_UNSUPPORTED, "head_dim"),
+    (dict(hq=48, hkv=2), _lib.TT_ERR_UNSUPPORTED, "group size"),
+    (dict(hq=30, hkv=8), _lib.TT_ERR_INVALID_ARGUMENT, "divisible"),
+    (dict(split=300), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),
+    (dict(ws_bytes=16), _lib.TT_ERR_WORKSPACE_TOO_SMALL, "workspace"),
+    (dict(page_size=24), _lib.TT_ERR_UNSUPPORTED, "power-of-two"),
+    (dict(max_len=161), _lib.TT_ERR_INVALID_ARGUMENT, "exceeds the page table"),
+    (dict(page_table=None, cache_strides=(1 << 20, 4096, 1 << 16)), _lib.TT_ERR_UNSUPPORTED, "dense pages"),
+    (dict(q=FAKE + 2), _lib.TT_ERR_INVALID_ARGUMENT, "aligned"),
+])
+def test_attention_rejects_invalid_arguments(kw, code, msg):
+    lib = _lib.load()
+    assert _attn(lib, **kw) == code
+    assert msg in lib.tt_last_error_string().decode()
+
+
+@pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
+def test_rope_append_rejects_invalid_arguments():
+    lib = _lib.load()
+    s3 = _lib.strides(1, 1, 1)
+    common = [FAKE, s3, FAKE, s3, FAKE, s3, FAKE, s3, FAKE, 100, FAKE, None, None, 0, 0, FAKE, FAKE]
+    tail = [_lib.strides(0, 2048, 256), 64, 2, 1, 8, 2]
+    # odd head_dim
+    assert lib.tt_rope_append_bf16(*common, *tail, 127, 16, None) == _lib.TT_ERR_UNSUPPORTED
+    # fp8 without scales
+    assert lib.tt_rope_append_fp8(*common, None, None, *tail, 128, 16, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert "k_scale" in lib.tt_last_error_string().decode()
+    # page_size 0 (the reference raises for page_size <= 0, cache.py:22-23)
+    assert lib.tt_rope_append_bf16(*common, *tail, 128, 0, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert "page_size must be positive" in lib.tt_last_error_string().decode()
+    # paged without pool size
+    common_paged = list(common)
+    common_paged[12] = FAKE
+    assert lib.tt_rope_append_bf16(*common_paged, *tail, 128, 16, None) == _lib.TT_ERR_INVALID_ARGUMENT
+
+
+def test_status_maps_to_python_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.TT_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(700, "x")
+    _lib.check(0, "x")
