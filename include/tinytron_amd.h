@@ -84,6 +84,10 @@ const char *tt_last_error_string(void);
  * new_lens [B] int32 or NULL: sequence b writes only its first new_lens[b]
  *   tokens to the cache (ragged prefill; the rest are padding). q_out is
  *   rotated for all T tokens either way. NULL = all T.
+ * lens_out [B] int32 or NULL: receives positions[b] + (tokens written for
+ *   sequence b), i.e. the sequence's length after the append (the
+ *   reference's current_length update, cache.py:43-44). It must not alias
+ *   positions; callers alternate two length buffers between steps.
  * Each rounding point of the reference under bf16 autocast is reproduced:
  *   out = bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)).
  * Tokens whose slot is >= capacity, >= rope_table_len, or whose page lies
@@ -95,7 +99,7 @@ int tt_rope_append_bf16(const void *q_in, const int64_t q_in_strides[3],
                         const void *v_in, const int64_t v_in_strides[3],
                         void *q_out, const int64_t q_out_strides[3],
                         const void *rope_table, int64_t rope_table_len,
-                        const int32_t *positions, const int32_t *new_lens,
+                        const int32_t *positions, const int32_t *new_lens, int32_t *lens_out,
                         const int32_t *page_table, int64_t max_pages, int64_t num_pages,
                         void *k_cache, void *v_cache, const int64_t cache_strides[3],
                         int64_t capacity, int64_t batch, int64_t num_new,
@@ -112,7 +116,7 @@ int tt_rope_append_f32(const void *q_in, const int64_t q_in_strides[3],
                        const void *v_in, const int64_t v_in_strides[3],
                        void *q_out, const int64_t q_out_strides[3],
                        const void *rope_table, int64_t rope_table_len,
-                       const int32_t *positions, const int32_t *new_lens,
+                       const int32_t *positions, const int32_t *new_lens, int32_t *lens_out,
                        const int32_t *page_table, int64_t max_pages, int64_t num_pages,
                        void *k_cache, void *v_cache, const int64_t cache_strides[3],
                        int64_t capacity, int64_t batch, int64_t num_new,
@@ -132,7 +136,7 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
                        const void *v_in, const int64_t v_in_strides[3],
                        void *q_out, const int64_t q_out_strides[3],
                        const void *rope_table, int64_t rope_table_len,
-                       const int32_t *positions, const int32_t *new_lens,
+                       const int32_t *positions, const int32_t *new_lens, int32_t *lens_out,
                        const int32_t *page_table, int64_t max_pages, int64_t num_pages,
                        void *k_cache, void *v_cache, float *k_scale, float *v_scale,
                        const int64_t cache_strides[3],

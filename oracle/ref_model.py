@@ -1,0 +1,91 @@
+"""torch-CPU restatement of the reference's dense GPT and generate loop
+(test infrastructure; end-to-end token parity and the E2E CPU baseline).
+
+Follows tinytron/model/gpt.py:33-115, modules/norm.py:14-19,
+modules/mlp.py:44-45, modules/attn.py:378-440 (local decode path with the
+H_q-expanded LayerPagedKVCache) and inference/engine.py:144-228 (greedy via
+top_k = 1), op for op, in fp32 on the CPU (the reference's CPU path runs
+without autocast, engine.py:180-184). Weights come from a state dict.
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+import torch.nn.functional as F
+
+from . import ref_path
+
+
+class RefGPT:
+    def __init__(self, state_dict: dict, num_layer: int, num_attention_heads: int, num_key_value_heads: int,
+                 dtype=torch.float32):
+        self.w = {k: v.detach().to("cpu", dtype) for k, v in state_dict.items() if torch.is_tensor(v)}
+        self.L = num_layer
+        self.hq = num_attention_heads
+        self.hkv = num_key_value_heads
+        self.C = self.w["wte.weight"].shape[1]
+        self.D = self.C // self.hq
+
+    @staticmethod
+    def _rms(x, w):
+        x32 = x.to(torch.float32)
+        var = x32.pow(2).mean(-1, keepdim=True)
+        return w * (x32 * torch.rsqrt(var + 1e-6)).to(x.dtype)
+
+    def _attn(self, i, x, cache, position_offset):
+        B, T, C = x.shape
+        p = f"blocks.{i}.attn."
+        q = F.linear(x, self.w[p + "q_proj.weight"]).view(B, T, self.hq, self.D).transpose(-2, -3)
+        k = F.linear(x, self.w[p + "k_proj.weight"]).view(B, T, self.hkv, self.D).transpose(-2, -3)
+        v = F.linear(x, self.w[p + "v_proj.weight"]).view(B, T, self.hkv, self.D).transpose(-2, -3)
+        pos = torch.arange(position_offset, position_offset + T).unsqueeze(0)
+        q, k = ref_path.rope_impl(q, k, pos)
+        k, v = ref_path.gqa_impl(k, v, self.hkv, self.hq)
+        past_len = cache.append(k, v)
+        k, v = cache.get_kv()
+        mask, causal = None, True
+        if past_len > 0:
+            mask = ref_path.build_cache_causal_mask(T, k.size(2), past_len, x.device)
+            causal = False
+        y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0.0, is_causal=causal)
+        y = y.transpose(-2, -3).reshape(B, T, C)
+        return F.linear(y, self.w[p + "c_proj.weight"])
+
+    def forward(self, idx, caches, position_offset):
+        x = F.embedding(idx, self.w["wte.weight"])
+        for i in range(self.L):
+            p = f"blocks.{i}."
+            x = x + self._attn(i, self._rms(x, self.w[p + "ln_1.weight"]), caches[i], position_offset)
+            h = self._rms(x, self.w[p + "ln_2.weight"])
+            m = F.linear(F.silu(F.linear(h, self.w[p + "mlp.gate_proj.weight"])) * F.linear(h, self.w[p + "mlp.up_proj.weight"]),
+                         self.w[p + "mlp.down_proj.weight"])
+            x = x + m
+        x = self._rms(x, self.w["lnf.weight"])
+        return F.linear(x, self.w["wte.weight"])
+
+    @torch.no_grad()
+    def generate_greedy(self, prompt: torch.Tensor, max_new_tokens: int, block_size: int, page_size: int = 128,
+                        max_steps_timed: int | None = None):
+        """engine.py:144-228 with temperature 1, top_k 1 (argmax). Returns
+        (tokens [B, T + n], decode tokens/s, logits of every step)."""
+        B, T = prompt.shape
+        caches = [ref_path.LayerPagedKVCache(B, self.hq, self.D, block_size, page_size, "cpu", torch.float32)
+                  for _ in range(self.L)]
+        logits = self.forward(prompt, caches, 0)
+        tokens = [prompt]
+        step_logits = [logits[:, -1].clone()]
+        cur = T
+        t0 = time.perf_counter()
+        steps = 0
+        for _ in range(max_new_tokens):
+            nxt = torch.argmax(logits[:, -1].float(), dim=-1)
+            tokens.append(nxt[:, None])
+            cur += 1
+            steps += 1
+            logits = self.forward(nxt[:, None], caches, cur - 1)
+            step_logits.append(logits[:, -1].clone())
+            if max_steps_timed is not None and steps >= max_steps_timed:
+                break
+        dt = time.perf_counter() - t0
+        return torch.cat(tokens, 1), B * steps / dt, step_logits

@@ -96,7 +96,7 @@ def test_attention_rejects_invalid_arguments(kw, code, msg):
 def test_rope_append_rejects_invalid_arguments():
     lib = _lib.load()
     s3 = _lib.strides(1, 1, 1)
-    common = [FAKE, s3, FAKE, s3, FAKE, s3, FAKE, s3, FAKE, 100, FAKE, None, None, 0, 0, FAKE, FAKE]
+    common = [FAKE, s3, FAKE, s3, FAKE, s3, FAKE, s3, FAKE, 100, FAKE, None, None, None, 0, 0, FAKE, FAKE]
     tail = [_lib.strides(0, 2048, 256), 64, 2, 1, 8, 2]
     # odd head_dim
     assert lib.tt_rope_append_bf16(*common, *tail, 127, 16, None) == _lib.TT_ERR_UNSUPPORTED
@@ -106,9 +106,14 @@ def test_rope_append_rejects_invalid_arguments():
     # page_size 0 (the reference raises for page_size <= 0, cache.py:22-23)
     assert lib.tt_rope_append_bf16(*common, *tail, 128, 0, None) == _lib.TT_ERR_INVALID_ARGUMENT
     assert "page_size must be positive" in lib.tt_last_error_string().decode()
+    # lens_out aliasing positions
+    aliased = list(common)
+    aliased[12] = FAKE
+    assert lib.tt_rope_append_bf16(*aliased, *tail, 128, 16, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert "alias" in lib.tt_last_error_string().decode()
     # paged without pool size
     common_paged = list(common)
-    common_paged[12] = FAKE
+    common_paged[13] = FAKE
     assert lib.tt_rope_append_bf16(*common_paged, *tail, 128, 16, None) == _lib.TT_ERR_INVALID_ARGUMENT
 
 

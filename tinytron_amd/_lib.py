@@ -27,7 +27,7 @@ _size = ctypes.c_size_t
 _ROPE_COMMON = [
     _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,  # q_in, k_in, v_in, q_out (+ strides)
     _vp, _i64,                                       # rope_table, rope_table_len
-    _i32p, _i32p,                                    # positions, new_lens
+    _i32p, _i32p, _i32p,                             # positions, new_lens, lens_out
     _i32p, _i64, _i64,                               # page_table, max_pages, num_pages
     _vp, _vp,                                        # k_cache, v_cache
 ]

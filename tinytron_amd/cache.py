@@ -1,0 +1,349 @@
+"""KV caches for the gfx950 decode path.
+
+Drop-in counterparts of tinytron/inference/cache.py:
+
+* ``LayerPagedKVCache`` keeps the reference's constructor
+  ``(batch_size, num_heads, head_dim, max_seq_len, page_size, device, dtype)``,
+  storage ``[B, H, ceil(S/P), P, D]`` with the flat view
+  ``[B, H, ceil(S/P)*P, D]`` (cache.py:27-32), ``append(k, v) -> previous
+  length`` with the reference's overflow ``ValueError`` (cache.py:34-45),
+  ``get_kv()`` (cache.py:47-51) and ``current_length``. It is built with
+  ``num_heads = num_key_value_heads``: K/V are appended before the GQA
+  expansion, so the cache holds each KV head once and the attention kernel
+  maps query head h to KV head h // (H_q / H_kv).
+* ``PagedLayerKVCache`` is a physical page pool ``[num_pages, H, P, D]``
+  addressed through an int32 page table ``[B, max_pages]`` (no counterpart in
+  the reference, whose "paged" store is dense).
+* ``PagedKVCache`` is the model-level list with ``from_model_config`` and
+  ``get_layer_cache`` (cache.py:54-97).
+
+Beyond the reference protocol both layer caches keep one length per sequence
+(the reference has one batch-wide ``current_length``, cache.py:26) in two
+device int32 buffers that alternate between steps (the fused append writes
+the new lengths into the other buffer, so no separate increment runs), with a
+host mirror for overflow checks and launch sizing. The fused path is
+``rope_append`` + ``attend``; ``append``/``get_kv`` are the reference
+protocol for callers that bring their own attention.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import ops
+
+FP8 = torch.float8_e4m3fn
+
+
+def cache_kind(dtype: torch.dtype) -> str:
+    if dtype == torch.bfloat16:
+        return "bf16"
+    if dtype == torch.float32:
+        return "f32"
+    if dtype == FP8:
+        return "fp8"
+    raise ValueError(f"unsupported KV cache dtype {dtype}")
+
+
+def _quantize_rows(x: torch.Tensor):
+    """Per-(token, head) fp8 quantization: scale = absmax/448, code = e4m3(x/scale)."""
+    xf = x.float()
+    scale = xf.abs().amax(dim=-1) / 448.0
+    safe = torch.where(scale > 0, scale, torch.ones_like(scale))
+    codes = (xf / safe[..., None]).to(FP8).view(torch.uint8)
+    codes = torch.where((scale > 0)[..., None], codes, torch.zeros_like(codes))
+    return codes, scale
+
+
+class _LayerCacheBase:
+    """Length bookkeeping and the fused append/attend path shared by both layouts."""
+
+    def _init_lengths(self, batch_size: int, device) -> None:
+        self.batch_size = batch_size
+        self._lens_dev = [torch.zeros(batch_size, dtype=torch.int32, device=device),
+                          torch.zeros(batch_size, dtype=torch.int32, device=device)]
+        self._cur = 0
+        self._host_lens = [0] * batch_size
+        self._pending_new_lens = None
+        self.workspace = None
+
+    # -- lengths ---------------------------------------------------------------
+    @property
+    def seq_lens(self) -> torch.Tensor:
+        """Device int32 [B]: tokens cached per sequence."""
+        return self._lens_dev[self._cur]
+
+    @property
+    def seq_lens_host(self) -> list:
+        return list(self._host_lens)
+
+    @property
+    def current_length(self) -> int:
+        """Longest sequence; equals the reference's batch-wide length when lengths are uniform."""
+        return max(self._host_lens) if self._host_lens else 0
+
+    def capacity_of(self, b: int) -> int:
+        raise NotImplementedError
+
+    def _check_room(self, adds) -> None:
+        for b, add in enumerate(adds):
+            end = self._host_lens[b] + int(add)
+            cap = self.capacity_of(b)
+            if end > cap:
+                raise ValueError(f"KV cache overflow: requested sequence length {end}, max supported is {cap}")
+
+    def set_lengths(self, lens) -> None:
+        """Declare that sequence b holds lens[b] tokens (e.g. after external writes)."""
+        lens = [int(x) for x in lens]
+        for b, n in enumerate(lens):
+            if n < 0 or n > self.capacity_of(b):
+                raise ValueError(f"KV cache overflow: requested sequence length {n}, max supported is {self.capacity_of(b)}")
+        self._host_lens = lens
+        self.seq_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+
+    def set_pending_new_lens(self, new_lens) -> None:
+        """Ragged prefill: the next multi-token append writes only new_lens[b] tokens of sequence b."""
+        self._pending_new_lens = None if new_lens is None else [int(x) for x in new_lens]
+
+    # -- fused path ------------------------------------------------------------
+    def rope_append(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rope_table: torch.Tensor,
+                    new_lens=None) -> torch.Tensor:
+        """RoPE + append in one kernel at each sequence's own position; returns rotated q.
+
+        rope_impl (attn.py:13-63) + append (cache.py:34-45) with per-sequence
+        positions; raises the reference's overflow ValueError before launching.
+        """
+        T = q.shape[2]
+        if new_lens is None and T > 1:
+            new_lens = self._pending_new_lens
+        adds = [T] * self.batch_size if new_lens is None else [min(int(n), T) for n in new_lens]
+        self._check_room(adds)
+        nl = None
+        if new_lens is not None:
+            nl = torch.tensor(adds, dtype=torch.int32).to(self.seq_lens.device, non_blocking=True)
+        nxt = 1 - self._cur
+        q_rot = ops.rope_append(q, k, v, rope_table, self._lens_dev[self._cur], self.layout, new_lens=nl,
+                                lens_out=self._lens_dev[nxt])
+        self._cur = nxt
+        self._host_lens = [a + b for a, b in zip(self._host_lens, adds)]
+        return q_rot
+
+    def attend(self, q: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """GQA decode attention of q [B, H_q, D] over every cached token of each sequence."""
+        if self.workspace is None:
+            self.workspace = ops.Workspace(q.device)
+        return ops.decode_attention(q, self.layout, self.seq_lens, self.current_length, out=out,
+                                    workspace=self.workspace)
+
+    # -- gathers for the protocol / prefill ----------------------------------------
+    def _token_index(self, b: int, length: int) -> torch.Tensor:
+        """Element offsets [length] of tokens 0..length-1 of sequence b, head 0, d 0."""
+        raise NotImplementedError
+
+    def gather(self, b: int, length: int, dtype: torch.dtype | None = None):
+        """Dense (K, V) [1, H, length, D] of sequence b (dequantized for fp8)."""
+        lay = self.layout
+        D, H = lay.head_dim, lay.num_heads
+        base = self._token_index(b, length)                                   # [L]
+        idx = base[None, :, None] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None, None] \
+            + torch.arange(D, device=base.device)[None, None, :]              # [H, L, D]
+        if lay.kind == "fp8":
+            sidx = (base[None, :] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None]) // D
+            k = lay.k[idx].view(FP8).float() * lay.k_scale[sidx][..., None]
+            v = lay.v[idx].view(FP8).float() * lay.v_scale[sidx][..., None]
+            dt = dtype or torch.bfloat16
+            return k.to(dt)[None], v.to(dt)[None]
+        return lay.k[idx][None], lay.v[idx][None]
+
+    def _write_tokens(self, b: int, start: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k/v [H, T, D] into slots start..start+T-1 of sequence b (no RoPE)."""
+        lay = self.layout
+        D, H = lay.head_dim, lay.num_heads
+        T = k.shape[1]
+        base = self._token_index(b, start + T)[start:]
+        idx = base[None, :, None] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None, None] \
+            + torch.arange(D, device=base.device)[None, None, :]
+        if lay.kind == "fp8":
+            sidx = (base[None, :] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None]) // D
+            kc, ks = _quantize_rows(k)
+            vc, vs = _quantize_rows(v)
+            lay.k[idx] = kc
+            lay.v[idx] = vc
+            lay.k_scale[sidx] = ks
+            lay.v_scale[sidx] = vs
+        else:
+            lay.k[idx] = k.to(lay.k.dtype)
+            lay.v[idx] = v.to(lay.v.dtype)
+
+    # -- reference protocol -------------------------------------------------------
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> int:
+        """cache.py:34-45: write k/v [B, H, T, D] after each sequence's tokens, return the previous length."""
+        T = k.size(2)
+        self._check_room([T] * self.batch_size)
+        previous = self.current_length
+        for b in range(self.batch_size):
+            self._write_tokens(b, self._host_lens[b], k[b], v[b])
+        self.set_lengths([n + T for n in self._host_lens])
+        return previous
+
+    def get_kv(self):
+        """cache.py:47-51: (K, V) [B, H, current_length, D] (dense copies for the pool and fp8)."""
+        L = self.current_length
+        ks, vs = zip(*(self.gather(b, L) for b in range(self.batch_size)))
+        return torch.cat(ks, 0), torch.cat(vs, 0)
+
+
+class LayerPagedKVCache(_LayerCacheBase):
+    """The reference's per-layer store (cache.py:11-51), H = num_key_value_heads."""
+
+    def __init__(self, batch_size: int, num_heads: int, head_dim: int, max_seq_len: int, page_size: int,
+                 device, dtype: torch.dtype) -> None:
+        if page_size <= 0:
+            raise ValueError(f"page_size must be positive, got {page_size}")
+        self.max_seq_len = max_seq_len
+        self.page_size = page_size
+        kind = cache_kind(dtype)
+        num_pages = math.ceil(max_seq_len / page_size)
+        shape = (batch_size, num_heads, num_pages, page_size, head_dim)
+        store = torch.uint8 if kind == "fp8" else dtype
+        self._k_pages = torch.empty(shape, device=device, dtype=store)
+        self._v_pages = torch.empty(shape, device=device, dtype=store)
+        self._k_flat = self._k_pages.view(batch_size, num_heads, num_pages * page_size, head_dim)
+        self._v_flat = self._v_pages.view(batch_size, num_heads, num_pages * page_size, head_dim)
+        k_scale = v_scale = None
+        if kind == "fp8":
+            k_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
+            v_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
+        pd = page_size * head_dim
+        self.layout = ops.KVLayout(
+            k=self._k_pages.view(-1), v=self._v_pages.view(-1),
+            strides=(num_heads * num_pages * pd, pd, num_pages * pd), num_heads=num_heads, head_dim=head_dim,
+            page_size=page_size, capacity=max_seq_len, kind=kind, k_scale=k_scale, v_scale=v_scale)
+        self._init_lengths(batch_size, device)
+
+    def capacity_of(self, b: int) -> int:
+        return self.max_seq_len
+
+    def _token_index(self, b: int, length: int) -> torch.Tensor:
+        lay = self.layout
+        t = torch.arange(length, device=lay.k.device)
+        return b * lay.strides[0] + t * lay.head_dim
+
+    def get_kv(self):
+        if self.layout.kind != "fp8" and len(set(self._host_lens)) == 1:
+            L = self.current_length
+            return self._k_flat[:, :, :L, :], self._v_flat[:, :, :L, :]
+        return super().get_kv()
+
+
+class PagedLayerKVCache(_LayerCacheBase):
+    """Physical page pool [num_pages, H, P, D] + page table [B, max_pages] (int32).
+
+    Sequence b's token t lives in physical page page_table[b, t // P] at slot
+    t % P. Page size must be a power of two >= 16 (one 16-token MFMA block
+    never straddles a page).
+    """
+
+    def __init__(self, page_table: torch.Tensor, num_pages: int, num_heads: int, head_dim: int, page_size: int,
+                 device, dtype: torch.dtype) -> None:
+        if page_size <= 0:
+            raise ValueError(f"page_size must be positive, got {page_size}")
+        if page_size < 16 or page_size & (page_size - 1):
+            raise ValueError(f"paged pools need a power-of-two page_size >= 16, got {page_size}")
+        kind = cache_kind(dtype)
+        self.page_size = page_size
+        self.num_pages = num_pages
+        table_cpu = page_table.to(torch.int32).cpu()
+        if table_cpu.dim() != 2:
+            raise ValueError("page_table must be [B, max_pages]")
+        self._pages_of = [int((row >= 0).sum()) for row in table_cpu]
+        if table_cpu.numel() and int(table_cpu.max()) >= num_pages:
+            raise ValueError("page_table refers to pages beyond the pool")
+        self.page_table = table_cpu.to(device)
+        store = torch.uint8 if kind == "fp8" else dtype
+        shape = (num_pages, num_heads, page_size, head_dim)
+        self._k = torch.empty(shape, device=device, dtype=store)
+        self._v = torch.empty(shape, device=device, dtype=store)
+        k_scale = v_scale = None
+        if kind == "fp8":
+            k_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
+            v_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
+        self.layout = ops.KVLayout(
+            k=self._k.view(-1), v=self._v.view(-1), strides=(0, num_heads * page_size * head_dim, page_size * head_dim),
+            num_heads=num_heads, head_dim=head_dim, page_size=page_size,
+            capacity=int(table_cpu.shape[1]) * page_size, kind=kind, page_table=self.page_table,
+            num_pages=num_pages, k_scale=k_scale, v_scale=v_scale)
+        self.max_seq_len = self.layout.capacity
+        self._init_lengths(int(table_cpu.shape[0]), device)
+
+    def capacity_of(self, b: int) -> int:
+        return self._pages_of[b] * self.page_size
+
+    def _token_index(self, b: int, length: int) -> torch.Tensor:
+        lay = self.layout
+        t = torch.arange(length, device=lay.k.device)
+        phys = self.page_table[b].long()[t // self.page_size]
+        return phys * lay.strides[1] + (t % self.page_size) * lay.head_dim
+
+
+def random_page_table(capacities, page_size: int, seed: int = 1337, extra_pages: int = 0):
+    """Pages for each sequence's capacity, assigned in (sequence, logical page)
+    order from a seeded random permutation of the pool. Unused entries are -1.
+    Returns (page_table int32 [B, max_pages] on the CPU, num_pages)."""
+    need = [max(1, math.ceil(int(c) / page_size)) for c in capacities]
+    total = sum(need) + extra_pages
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    table = torch.full((len(need), max(need) if need else 1), -1, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(need):
+        table[b, :n] = perm[off:off + n]
+        off += n
+    return table, total
+
+
+class PagedKVCache:
+    """Model-level cache: one layer cache per transformer layer (cache.py:54-97)."""
+
+    def __init__(self, layer_caches) -> None:
+        self._layer_caches = list(layer_caches)
+        ws = None
+        for c in self._layer_caches:  # layers run one after another on one stream
+            if ws is None:
+                ws = ops.Workspace(c.layout.k.device)
+            c.workspace = ws
+
+    @classmethod
+    def from_model_config(cls, model_config, batch_size: int, page_size: int, device, dtype: torch.dtype,
+                          *, kv_cache_dtype: torch.dtype | None = None, seq_capacity=None,
+                          paged_pool: bool = False, page_seed: int = 1337) -> "PagedKVCache":
+        """As cache.py:58-94 with num_heads = num_key_value_heads.
+
+        ``kv_cache_dtype`` (default: ``dtype``) may be torch.float8_e4m3fn.
+        ``paged_pool`` builds a page pool per layer sharing one seeded random
+        page table sized for ``seq_capacity`` (tokens per sequence, default
+        block_size).
+        """
+        heads = model_config.num_key_value_heads
+        head_dim = model_config.hidden_size // model_config.num_attention_heads
+        cdt = kv_cache_dtype or dtype
+        if not paged_pool:
+            layers = [LayerPagedKVCache(batch_size, heads, head_dim, model_config.block_size, page_size, device, cdt)
+                      for _ in range(model_config.num_layer)]
+            return cls(layers)
+        caps = seq_capacity if seq_capacity is not None else [model_config.block_size] * batch_size
+        table, n_pages = random_page_table(caps, page_size, seed=page_seed)
+        layers = [PagedLayerKVCache(table, n_pages, heads, head_dim, page_size, device, cdt)
+                  for _ in range(model_config.num_layer)]
+        return cls(layers)
+
+    def get_layer_cache(self, layer_idx: int):
+        return self._layer_caches[layer_idx]
+
+    def __len__(self) -> int:
+        return len(self._layer_caches)
+
+    def set_pending_new_lens(self, new_lens) -> None:
+        for c in self._layer_caches:
+            c.set_pending_new_lens(new_lens)

@@ -60,7 +60,7 @@ int check_layout(const int32_t *page_table, int64_t max_pages, int64_t num_pages
 int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_strides[3], const void *k_in,
                        const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
                        const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
-                       const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                       const int32_t *positions, const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table,
                        int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
                        float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
                        int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
@@ -79,9 +79,12 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
   if (kind == tt::CacheKind::kFP8) {
     TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
   }
+  TT_CHECK(lens_out == nullptr || ((const void *)lens_out != (const void *)positions &&
+                                   (const void *)lens_out != (const void *)new_lens),
+           TT_ERR_INVALID_ARGUMENT, "lens_out must not alias positions or new_lens");
   int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
   if (rc != TT_OK) return rc;
-  if (batch == 0 || num_new == 0) return ok();
+  if (batch == 0) return ok();
 
   tt::RopeAppendArgs a{};
   a.q_in = q_in;
@@ -104,6 +107,7 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
   a.table_len = rope_table_len;
   a.positions = positions;
   a.new_lens = new_lens;
+  a.lens_out = lens_out;
   a.page_table = page_table;
   a.max_pages = max_pages;
   a.num_pages = num_pages;
@@ -240,13 +244,13 @@ const char *tt_last_error_string(void) { return g_last_error.c_str(); }
 int tt_rope_append_bf16(const void *q_in, const int64_t q_in_strides[3], const void *k_in,
                         const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
                         const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
-                        const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                        const int32_t *positions, const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table,
                         int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache,
                         const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
                         int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                         tt_stream_t stream) {
   return rope_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
-                            q_out_strides, rope_table, rope_table_len, positions, new_lens, page_table, max_pages,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table, max_pages,
                             num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides, capacity, batch, num_new,
                             num_q_heads, num_kv_heads, head_dim, page_size, stream);
 }
@@ -254,13 +258,13 @@ int tt_rope_append_bf16(const void *q_in, const int64_t q_in_strides[3], const v
 int tt_rope_append_f32(const void *q_in, const int64_t q_in_strides[3], const void *k_in,
                        const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
                        const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
-                       const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                       const int32_t *positions, const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table,
                        int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache,
                        const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
                        int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                        tt_stream_t stream) {
   return rope_append_common(tt::CacheKind::kF32, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
-                            q_out_strides, rope_table, rope_table_len, positions, new_lens, page_table, max_pages,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table, max_pages,
                             num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides, capacity, batch, num_new,
                             num_q_heads, num_kv_heads, head_dim, page_size, stream);
 }
@@ -268,13 +272,13 @@ int tt_rope_append_f32(const void *q_in, const int64_t q_in_strides[3], const vo
 int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3], const void *k_in,
                        const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
                        const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
-                       const int32_t *positions, const int32_t *new_lens, const int32_t *page_table,
+                       const int32_t *positions, const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table,
                        int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
                        float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
                        int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                        int64_t page_size, tt_stream_t stream) {
   return rope_append_common(tt::CacheKind::kFP8, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
-                            q_out_strides, rope_table, rope_table_len, positions, new_lens, page_table, max_pages,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table, max_pages,
                             num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch, num_new,
                             num_q_heads, num_kv_heads, head_dim, page_size, stream);
 }

@@ -87,6 +87,11 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const int t = blockIdx.y;
   const int b = blockIdx.z;
   const int i = threadIdx.x;
+  if (a.lens_out != nullptr && row == 0 && t == 0 && threadIdx.x == 0) {
+    const int n = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
+    a.lens_out[b] = a.positions[b] + n;
+  }
+  if (t >= a.num_new) return;  // num_new == 0 launches one row only for lens_out
   const int64_t pos = (int64_t)a.positions[b] + t;
   if (pos < 0 || pos >= a.table_len) return;
   const int half = a.head_dim >> 1;
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
 }  // namespace
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
-  const dim3 grid(a.hq + a.hkv, a.num_new, a.batch);
+  const dim3 grid(a.hq + a.hkv, a.num_new > 0 ? a.num_new : 1, a.batch);
   const dim3 block(64);
   switch (kind) {
     case CacheKind::kBF16:

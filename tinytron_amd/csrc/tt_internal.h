@@ -22,6 +22,7 @@ struct RopeAppendArgs {
   int64_t table_len;
   const int32_t *positions;
   const int32_t *new_lens;
+  int32_t *lens_out;
   const int32_t *page_table;
   int64_t max_pages, num_pages;
   void *k_cache;

@@ -1,0 +1,138 @@
+"""Autoregressive engine over the gfx950 decode path.
+
+Restates ``InferenceEngine`` (tinytron/inference/engine.py:16-261): the same
+constructor arguments, ``generate`` signature, prefill -> sample -> write
+token -> one-token model call loop (engine.py:195-225), EOS handling and the
+same statistics (decode tokens/s = B * decode steps / decode wall time,
+engine.py:236-243). Added: ragged prompts (``prompt_lens``), KV caches that
+hold H_kv heads, a paged pool with a seeded random page table, and fp8 KV.
+
+Each step's model call is unchanged: ``model(next[B, 1], use_cache=True,
+past_key_values=cache, position_offset=...)``; positions come from the
+cache's per-sequence lengths, so there is no host synchronisation in the
+loop (the reference syncs once per layer at attn.py:395).
+"""
+from __future__ import annotations
+
+import time
+
+import torch
+
+from .cache import PagedKVCache
+from .model import GPT, ModelConfig
+from .sampler import sample_next_token, sample_next_token_with_log_prob
+
+
+class InferenceEngine:
+    def __init__(self, model_config: ModelConfig, checkpoint_path: str | None = None, device: str = "cuda",
+                 dtype: torch.dtype = torch.bfloat16, use_paged_kv_cache: bool = True, kv_cache_page_size: int = 128,
+                 kv_cache_dtype: torch.dtype | None = None, paged_pool: bool = False, page_seed: int = 1337,
+                 model: GPT | None = None):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("the tinytron_amd engine runs on the GPU (no CPU fallback)")
+        if self.device.index is None:
+            torch.cuda.set_device(0)
+            self.device = torch.device("cuda:0")
+        else:
+            torch.cuda.set_device(self.device)
+        if not use_paged_kv_cache:
+            raise ValueError("the gfx950 decode path needs a KV cache (use_paged_kv_cache=True)")
+        self.model_config = model_config
+        self.kv_cache_page_size = kv_cache_page_size
+        self.kv_cache_dtype = kv_cache_dtype
+        self.paged_pool = paged_pool
+        self.page_seed = page_seed
+        self.dtype = dtype
+        self.model = model if model is not None else GPT(model_config, device=self.device, dtype=dtype)
+        if checkpoint_path:
+            state = torch.load(checkpoint_path, map_location=self.device, weights_only=True)
+            self.model.load_state_dict(state)
+        self.model.eval()
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, temperature: float = 1.0,
+                 top_k: int | None = None, top_p: float | None = None, eos_token_id: int | None = None,
+                 return_stats: bool = False, return_logprobs: bool = False, prompt_lens=None):
+        """engine.py:144-261. ``prompt_lens`` (optional, [B]) marks ragged
+        prompts inside a right-padded ``input_ids``; the returned tokens are
+        right-padded likewise and ``stats["lengths"]`` gives each length."""
+        if input_ids.dim() != 2:
+            raise ValueError(f"input_ids must be [B, T], got shape={tuple(input_ids.shape)}")
+        prompt = input_ids.to(self.device)
+        batch_size, prompt_len = prompt.shape
+        lens = [prompt_len] * batch_size if prompt_lens is None else [int(x) for x in prompt_lens]
+        if len(lens) != batch_size or min(lens) < 1 or max(lens) > prompt_len:
+            raise ValueError("prompt_lens must give 1 <= len <= T for every sequence")
+        total_len = max(lens) + max_new_tokens
+        if total_len > self.model_config.block_size:
+            raise ValueError(
+                f"Requested total sequence length {total_len} exceeds block_size {self.model_config.block_size}")
+        tokens = torch.zeros(batch_size, total_len, dtype=prompt.dtype, device=self.device)
+        tokens[:, :prompt_len] = prompt
+        cache = PagedKVCache.from_model_config(
+            self.model_config, batch_size=batch_size, page_size=self.kv_cache_page_size, device=self.device,
+            dtype=self.dtype, kv_cache_dtype=self.kv_cache_dtype,
+            seq_capacity=[n + max_new_tokens for n in lens], paged_pool=self.paged_pool, page_seed=self.page_seed)
+        cache.set_pending_new_lens(lens)
+        lens_t = torch.tensor(lens, device=self.device)
+        rows = torch.arange(batch_size, device=self.device)
+
+        prefill_tokens = int(sum(lens))
+        prefill_t0 = time.perf_counter()
+        logits, cache = self.model(prompt, use_cache=True, past_key_values=cache, position_offset=0,
+                                   logits_index=lens_t - 1)
+        cache.set_pending_new_lens(None)
+        next_logits = logits[:, -1, :]
+        torch.cuda.synchronize(self.device)
+        prefill_t1 = time.perf_counter()
+
+        decode_steps = 0
+        token_log_probs = []
+        cur = lens_t.clone()
+        uniform = len(set(lens)) == 1
+        decode_t0 = time.perf_counter()
+        for step in range(max_new_tokens):
+            if return_logprobs:
+                next_token, next_log_prob = sample_next_token_with_log_prob(next_logits, temperature, top_k, top_p)
+                token_log_probs.append(next_log_prob)
+            else:
+                next_token = sample_next_token(next_logits, temperature, top_k, top_p)
+            tokens[rows, cur] = next_token
+            cur += 1
+            decode_steps += 1
+            if eos_token_id is not None and torch.all(next_token == eos_token_id):
+                break
+            position = (lens[0] + step) if uniform else 0
+            logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
+                                       position_offset=position)
+            next_logits = logits[:, -1, :]
+        torch.cuda.synchronize(self.device)
+        decode_t1 = time.perf_counter()
+
+        out_len = max(lens) + decode_steps
+        tokens = tokens[:, :out_len]
+        if not return_stats and not return_logprobs:
+            return tokens
+        extras = {}
+        prefill_time = max(prefill_t1 - prefill_t0, 1e-9)
+        decode_time = max(decode_t1 - decode_t0, 1e-9)
+        decode_tokens = int(batch_size * decode_steps)
+        if return_stats:
+            extras.update({
+                "prefill_tokens_per_sec": prefill_tokens / prefill_time,
+                "decode_tokens_per_sec": decode_tokens / decode_time if decode_steps > 0 else 0.0,
+                "prefill_tokens": float(prefill_tokens),
+                "decode_tokens": float(decode_tokens),
+                "lengths": [n + decode_steps for n in lens],
+            })
+        if return_logprobs:
+            log_probs = (torch.stack(token_log_probs, dim=1) if token_log_probs
+                         else torch.empty(batch_size, 0, dtype=torch.float32, device=self.device))
+            extras.update({
+                "prompt_len": float(prompt_len),
+                "decode_steps": float(decode_steps),
+                "token_log_probs": log_probs,
+                "response_mask": torch.ones_like(log_probs, dtype=torch.float32),
+            })
+        return tokens, extras

@@ -1,0 +1,257 @@
+"""Dense GQA GPT around the gfx950 decode path.
+
+Mirrors the reference's model stack (tinytron/model/gpt.py:20-115,
+modules/attn.py:102-440, modules/norm.py:6-19, modules/mlp.py:16-45,
+config.py:7-29) with the same module names, parameter names, shapes, seeded
+init and forward signatures, so state dicts load unchanged and the engine's
+model call (engine.py:188, 220-225) is the same.
+
+Numerics follow the reference under bf16 autocast (engine.py:180-185)
+without autocast's per-call weight casts: projection weights are stored in
+the compute dtype, the residual stream, norms and the embedding stay fp32,
+and every projection takes bf16 inputs and returns bf16 -- the values
+autocast produces from fp32 weights.
+
+``Attention.forward`` is the drop-in of attn.py:378-440: with one of this
+package's caches, a decode step (T = 1) is one fused RoPE + KV-append kernel
+and one split-K GQA attention kernel; prefill (T > 1) writes the cache with
+the same append kernel and attends with SDPA per sequence. No CPU fallback.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .cache import LayerPagedKVCache, PagedLayerKVCache
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    """config.py:7-29 (the dense fields the decode path uses)."""
+
+    seed: int = 1337
+    block_size: int = 4096
+    vocab_size: int = 50304
+    num_layer: int = 32
+    num_attention_heads: int = 128
+    num_key_value_heads: int = 8
+    hidden_size: int = 1024
+    intermediate_size: int = 4096
+    dropout: float = 0.0
+    init_std: float = 0.013
+    tied_lm_head: bool = True
+    rope_theta: float = 10000.0
+
+
+_ROPE_TABLES: dict = {}
+
+
+def rope_table_for(n_positions: int, head_dim: int, theta: float, dtype: torch.dtype, device) -> torch.Tensor:
+    """Shared cos/sin table (attn.py:30-54) covering at least n_positions."""
+    key = (str(torch.device(device)), head_dim, float(theta), dtype)
+    t = _ROPE_TABLES.get(key)
+    if t is None or t.shape[0] < n_positions:
+        n = max(n_positions, 4096 if t is None else 2 * t.shape[0])
+        t = ops.build_rope_table(n, head_dim, theta, dtype=dtype, device=device)
+        _ROPE_TABLES[key] = t
+    return t
+
+
+def _is_fused_cache(past_kv) -> bool:
+    return isinstance(past_kv, (LayerPagedKVCache, PagedLayerKVCache))
+
+
+class Attention(nn.Module):
+    """attn.py:102-440 (single-GPU path) with the fused gfx950 decode step."""
+
+    def __init__(self, config: ModelConfig, layer_idx: int, device=None, dtype=torch.float32):
+        super().__init__()
+        assert config.hidden_size % config.num_attention_heads == 0
+        self.config = config
+        self.layer_idx = layer_idx
+        self.num_attention_heads = config.num_attention_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        if self.num_attention_heads % self.num_key_value_heads != 0:
+            raise ValueError("num_attention_heads must be divisible by num_key_value_heads")
+        self.head_dim = config.hidden_size // config.num_attention_heads
+        self.n_embd = config.hidden_size
+        kw = dict(bias=False, device=device, dtype=dtype)
+        self.q_proj = nn.Linear(config.hidden_size, self.num_attention_heads * self.head_dim, **kw)
+        self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
+        self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
+        self.c_proj = nn.Linear(config.hidden_size, config.hidden_size, **kw)
+        self._init_weights(config.seed, layer_idx)
+
+    def _init_weights(self, base_seed: int, layer_idx: int) -> None:
+        """attn.py:148-160: every projection of layer i drawn after seeding seed + i."""
+        for lin in (self.q_proj, self.k_proj, self.v_proj, self.c_proj):
+            g = torch.Generator(device=lin.weight.device).manual_seed(base_seed + layer_idx)
+            with torch.no_grad():
+                w = torch.empty(lin.weight.shape, dtype=torch.float32, device=lin.weight.device)
+                w.normal_(0.0, self.config.init_std, generator=g)
+                lin.weight.copy_(w)
+
+    def forward(self, x: torch.Tensor, past_kv=None, use_cache: bool = False, position_offset: int = 0):
+        B, T, C = x.size()
+        act = self.q_proj.weight.dtype
+        xa = x.to(act)
+        q = self.q_proj(xa).view(B, T, self.num_attention_heads, self.head_dim).transpose(1, 2)
+        k = self.k_proj(xa).view(B, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
+        v = self.v_proj(xa).view(B, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
+        if not _is_fused_cache(past_kv):
+            raise TypeError("tinytron_amd.Attention needs a tinytron_amd KV cache "
+                            "(LayerPagedKVCache / PagedLayerKVCache); there is no uncached fallback")
+        lens = past_kv.seq_lens_host
+        if len(set(lens)) == 1 and lens[0] != position_offset:
+            raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
+        table = rope_table_for(past_kv.max_seq_len + T, self.head_dim, self.config.rope_theta, act, x.device)
+        if T == 1:
+            q_rot = past_kv.rope_append(q, k, v, table)                     # [B, H_q, 1, D]
+            y = past_kv.attend(q_rot.view(B, self.num_attention_heads, self.head_dim))
+            y = y.view(B, 1, C)
+        else:
+            y = self._prefill(q, k, v, past_kv, table, lens)
+        y = self.c_proj(y)
+        return y, (past_kv if use_cache else None)
+
+    def _prefill(self, q, k, v, cache, table, lens_before):
+        """T > 1: append all (ragged) prompt tokens with the fused kernel, then
+        causal SDPA per sequence over its cached prefix (attn.py:321-341)."""
+        B, _, T, D = q.shape
+        new = cache._pending_new_lens or [T] * B
+        q_rot = cache.rope_append(q, k, v, table, new_lens=new)
+        rep = self.num_attention_heads // self.num_key_value_heads
+        y = torch.zeros(B, T, self.n_embd, dtype=q.dtype, device=q.device)
+        for b in range(B):
+            n = int(new[b])
+            if n == 0:
+                continue
+            past = int(lens_before[b])
+            K, V = cache.gather(b, past + n, dtype=q.dtype)                 # [1, H_kv, past+n, D]
+            K = K.repeat_interleave(rep, dim=1).contiguous()
+            V = V.repeat_interleave(rep, dim=1).contiguous()
+            qb = q_rot[b:b + 1, :, :n].contiguous()
+            if past == 0:
+                yb = F.scaled_dot_product_attention(qb, K, V, is_causal=True)
+            else:
+                qpos = past + torch.arange(n, device=q.device).unsqueeze(-1)
+                mask = torch.arange(past + n, device=q.device).unsqueeze(0) <= qpos
+                yb = F.scaled_dot_product_attention(qb, K, V, attn_mask=mask)
+            y[b, :n] = yb[0].transpose(0, 1).reshape(n, self.n_embd)
+        return y
+
+
+class RMSNorm(nn.Module):
+    """norm.py:6-19 (named LayerNorm in the reference): fp32 math, eps 1e-6."""
+
+    def __init__(self, config: ModelConfig, device=None):
+        super().__init__()
+        self.variance_epsilon = 1e-6
+        self.weight = nn.Parameter(torch.ones(config.hidden_size, device=device))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        input_dtype = x.dtype
+        x = x.to(torch.float32)
+        variance = x.pow(2).mean(-1, keepdim=True)
+        x = x * torch.rsqrt(variance + self.variance_epsilon)
+        return self.weight * x.to(input_dtype)
+
+
+class MLP(nn.Module):
+    """mlp.py:16-45: SwiGLU, seeded like the attention projections."""
+
+    def __init__(self, config: ModelConfig, layer_idx: int, device=None, dtype=torch.float32):
+        super().__init__()
+        kw = dict(bias=False, device=device, dtype=dtype)
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, **kw)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, **kw)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, **kw)
+        self.act_fn = nn.SiLU()
+        for lin in (self.gate_proj, self.up_proj, self.down_proj):
+            g = torch.Generator(device=lin.weight.device).manual_seed(config.seed + layer_idx)
+            with torch.no_grad():
+                w = torch.empty(lin.weight.shape, dtype=torch.float32, device=lin.weight.device)
+                w.normal_(0.0, config.init_std, generator=g)
+                lin.weight.copy_(w)
+
+    def forward(self, x: torch.Tensor, use_cache: bool = False) -> torch.Tensor:
+        xa = x.to(self.gate_proj.weight.dtype)
+        return self.down_proj(self.act_fn(self.gate_proj(xa)) * self.up_proj(xa))
+
+
+class Block(nn.Module):
+    """gpt.py:20-45 (dense)."""
+
+    def __init__(self, config: ModelConfig, layer_idx: int, device=None, dtype=torch.float32):
+        super().__init__()
+        self.ln_1 = RMSNorm(config, device)
+        self.attn = Attention(config, layer_idx, device, dtype)
+        self.ln_2 = RMSNorm(config, device)
+        self.mlp = MLP(config, layer_idx, device, dtype)
+
+    def forward(self, x, past_kv=None, use_cache=False, position_offset=0):
+        attn_out, new_kv = self.attn(self.ln_1(x), past_kv=past_kv, use_cache=use_cache,
+                                     position_offset=position_offset)
+        x = x + attn_out
+        x = x + self.mlp(self.ln_2(x), use_cache=use_cache)
+        return x, None, new_kv
+
+
+class GPT(nn.Module):
+    """gpt.py:49-115 (dense, inference). ``dtype`` is the compute dtype of the
+    projections; the embedding table and the residual stream stay fp32 and the
+    tied lm_head uses a ``dtype`` copy of it, as autocast would."""
+
+    def __init__(self, config: ModelConfig, device=None, dtype=torch.float32):
+        super().__init__()
+        self.config = config
+        self.compute_dtype = dtype
+        self.wte = nn.Embedding(config.vocab_size, config.hidden_size, device=device)
+        self.blocks = nn.ModuleList([Block(config, i, device, dtype) for i in range(config.num_layer)])
+        self.lnf = RMSNorm(config, device)
+        g = torch.Generator(device=self.wte.weight.device).manual_seed(config.seed)
+        with torch.no_grad():
+            self.wte.weight.normal_(0.0, config.init_std, generator=g)
+        if not config.tied_lm_head:
+            raise ValueError("only the tied lm_head of the reference's default config is supported")
+        self._lm_head_weight = None
+
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        # reference checkpoints carry the tied lm_head as its own key (gpt.py:60-62)
+        state_dict.pop(prefix + "lm_head.weight", None)
+        self._lm_head_weight = None
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+
+    def lm_head_weight(self) -> torch.Tensor:
+        w = self._lm_head_weight
+        if w is None or w.device != self.wte.weight.device or w.dtype != self.compute_dtype:
+            w = self.wte.weight.detach().to(self.compute_dtype)
+            self._lm_head_weight = w
+        return w
+
+    def forward(self, idx: torch.Tensor, targets=None, past_key_values=None, use_cache: bool = False,
+                position_offset: int = 0, logits_index: torch.Tensor | None = None):
+        """gpt.py:84-115. ``logits_index`` ([B], optional, prefill only)
+        computes logits at one position per sequence ([B, 1, V]) instead of
+        all T."""
+        B, T = idx.size()
+        assert T <= self.config.block_size, f"Cannot forward sequence of length {T}, block size is only {self.config.block_size}"
+        x = self.wte(idx)
+        paged_cache = past_key_values if hasattr(past_key_values, "get_layer_cache") else None
+        if paged_cache is None:
+            raise TypeError("tinytron_amd.GPT runs with a tinytron_amd PagedKVCache")
+        for layer_idx, block in enumerate(self.blocks):
+            x, _, _ = block(x, past_kv=paged_cache.get_layer_cache(layer_idx), use_cache=use_cache,
+                            position_offset=position_offset)
+        if logits_index is not None:
+            x = x[torch.arange(B, device=x.device), logits_index].unsqueeze(1)
+        x = self.lnf(x)
+        logits = F.linear(x.to(self.compute_dtype), self.lm_head_weight())
+        if use_cache:
+            return logits, paged_cache
+        return logits

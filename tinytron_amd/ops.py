@@ -96,11 +96,12 @@ def _check_lastdim(name: str, t: torch.Tensor, dims: int) -> None:
 
 def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.Tensor,
                 positions: torch.Tensor, layout: KVLayout, q_out: torch.Tensor | None = None,
-                new_lens: torch.Tensor | None = None) -> torch.Tensor:
+                new_lens: torch.Tensor | None = None, lens_out: torch.Tensor | None = None) -> torch.Tensor:
     """RoPE q and k at per-sequence positions, append k/v to the cache.
 
     q [B, H_q, T, D], k/v [B, H_kv, T, D] (any strides, head_dim contiguous);
-    positions int32 [B] = slot of token 0 per sequence; returns rotated q.
+    positions int32 [B] = slot of token 0 per sequence; lens_out (int32 [B],
+    optional) receives the lengths after the append; returns rotated q.
     Restates rope_impl (attn.py:13-63) + LayerPagedKVCache.append
     (cache.py:34-45) in one launch.
     """
@@ -125,6 +126,8 @@ def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.
         raise ValueError("positions must be int32 [B]")
     if new_lens is not None and (new_lens.dtype != torch.int32 or new_lens.shape != (B,)):
         raise ValueError("new_lens must be int32 [B]")
+    if lens_out is not None and (lens_out.dtype != torch.int32 or lens_out.shape != (B,)):
+        raise ValueError("lens_out must be int32 [B]")
     if q_out is None:
         q_out = torch.empty(B, Hq, T, D, dtype=q.dtype, device=q.device)
     _check_lastdim("q_out", q_out, 4)
@@ -132,7 +135,7 @@ def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.
     common = [
         _ptr(q), _lib.strides(*q.stride()[:3]), _ptr(k), _lib.strides(*k.stride()[:3]),
         _ptr(v), _lib.strides(*v.stride()[:3]), _ptr(q_out), _lib.strides(*q_out.stride()[:3]),
-        _ptr(table), table.shape[0], _ptr(positions), _ptr(new_lens),
+        _ptr(table), table.shape[0], _ptr(positions), _ptr(new_lens), _ptr(lens_out),
         _ptr(layout.page_table), layout.max_pages, layout.num_pages,
         _ptr(layout.k), _ptr(layout.v),
     ]
