@@ -51,7 +51,77 @@ def parse_args():
     p.add_argument("--split-tokens", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of timed CPU-baseline work")
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end greedy decode (config 5)")
+    p.add_argument("--e2e-steps", type=int, default=256)
     return p.parse_args()
+
+
+C5 = dict(num_layer=24, hidden_size=2048, num_attention_heads=32, num_key_value_heads=8, vocab_size=32000,
+          intermediate_size=6144, init_std=0.02, batch=64, lo=64, hi=2048, page=16)
+
+
+def e2e_c5(args, torch):
+    """Greedy decode through the engine, tokens/s as
+    engine.py:236-243 defines it, plus the reference op sequence on the host
+    for a bounded sample of the same batch."""
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT, ModelConfig
+
+    steps = args.e2e_steps
+    g = torch.Generator().manual_seed(args.seed)
+    B = C5["batch"]
+    lens = torch.randint(C5["lo"], C5["hi"] + 1, (B,), generator=g).tolist()
+    prompt = torch.randint(0, C5["vocab_size"], (B, max(lens)), generator=g)
+    cfg = ModelConfig(num_layer=C5["num_layer"], hidden_size=C5["hidden_size"],
+                      num_attention_heads=C5["num_attention_heads"], num_key_value_heads=C5["num_key_value_heads"],
+                      vocab_size=C5["vocab_size"], intermediate_size=C5["intermediate_size"], init_std=C5["init_std"],
+                      block_size=max(lens) + steps, seed=args.seed)
+    model = GPT(cfg, device="cuda", dtype=torch.bfloat16)
+    eng = InferenceEngine(cfg, device="cuda", dtype=torch.bfloat16, kv_cache_page_size=C5["page"], paged_pool=True,
+                          model=model)
+    eng.generate(prompt[:, :16], 4, top_k=1)  # warm kernels and the allocator
+    torch.cuda.synchronize()
+    tokens, stats = eng.generate(prompt, steps, top_k=1, prompt_lens=lens, return_stats=True)
+    tps = stats["decode_tokens_per_sec"]
+    n_params = sum(p.numel() for p in model.parameters())
+    mean_ctx = sum(lens) / B + steps / 2
+    kv_bytes = C5["num_layer"] * 2 * B * mean_ctx * C5["num_key_value_heads"] * (C5["hidden_size"] // C5["num_attention_heads"]) * 2
+    step_bytes = (n_params - C5["vocab_size"] * C5["hidden_size"]) * 2 + C5["vocab_size"] * C5["hidden_size"] * 2 + kv_bytes
+    bound = B / (step_bytes / (PEAK_HBM_GBS * 1e9))
+    out = {
+        "workload": "C5 greedy decode through the engine: 24 L, d 2048, 32/8 heads, D 64, V 32000, bf16 "
+                    "random-init weights, B 64, prompts U[64, 2048], paged KV page 16",
+        "decode_tokens_per_sec": round(tps, 1),
+        "decode_steps": int(stats["decode_tokens"] // B),
+        "prefill_tokens_per_sec": round(stats["prefill_tokens_per_sec"], 1),
+        "params": n_params,
+        "hbm_bound_tokens_per_sec": round(bound, 1),
+        "frac_of_hbm_bound": round(tps / bound, 4),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = e2e_cpu_baseline(model, cfg, prompt, lens, torch)
+    del eng, model
+    torch.cuda.empty_cache()
+    return out
+
+
+def e2e_cpu_baseline(model, cfg, prompt, lens, torch, n_seq=2, n_steps=8):
+    """The reference's op sequence (oracle.ref_model, fp32 on the host, as the
+    reference runs without a GPU) on the n_seq shortest prompts of the batch,
+    timing n_steps greedy decode steps."""
+    from oracle.ref_model import RefGPT
+
+    order = sorted(range(len(lens)), key=lambda b: lens[b])[:n_seq]
+    L = max(lens[b] for b in order)
+    sample = torch.stack([prompt[b, :L] for b in order])  # equal lengths: pad the shorter with its own tokens
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    ref = RefGPT(sd, cfg.num_layer, cfg.num_attention_heads, cfg.num_key_value_heads)
+    threads = torch.get_num_threads()
+    _, tps, _ = ref.generate_greedy(sample, n_steps, L + n_steps + 1, page_size=16)
+    return {"value": round(tps, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"batch {n_seq} (the shortest prompts, {L} tokens), {n_steps} greedy decode steps, fp32 "
+                      "on the host through the reference op sequence; not the batch-64 workload"}
 
 
 def build_workload(cfg, seed, torch, ops):
@@ -303,6 +373,10 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, wl, torch, args.cpu_seconds)
+    if not args.no_e2e:
+        del wl, layout, q_rot, out, ws
+        torch.cuda.empty_cache()
+        result["e2e"] = e2e_c5(args, torch)
     print(json.dumps(result), flush=True)
     return 0
 
