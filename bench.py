@@ -275,6 +275,19 @@ def cpu_baseline(cfg, wl, torch, budget_s):
     }
 
 
+def measured_traffic(config: str):
+    """HBM bytes per decode-attention launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of this workload (copy-calibrated), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"decode_attn_{config}.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(float(line.split(":")[1]))
+    except OSError:
+        return None
+    return None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -365,7 +378,9 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config),
+            "traffic_source": f"profiles/decode_attn_{args.config}.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                              "scaled by a 256 MiB copy)",
             "avg_us": round(attn_ms * 1e3, 2),
             "algorithmic_bytes": attn_bytes,
         },
