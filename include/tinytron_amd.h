@@ -169,7 +169,8 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
  *   H_q / H_kv <= 16; a paged pool has a power-of-two page_size >= 16; the
  *   contiguous store has dense pages (cache_strides[1] == page_size *
  *   head_dim, as the reference's [B, H, pages, P, D] store), any page_size;
- *   q and cache 16-byte aligned, their strides multiples of 8 elements.
+ *   q and cache 16-byte aligned, their strides multiples of 8 elements;
+ *   batch <= 4096 (bf16 / fp8).
  * Physical page numbers read from page_table are clamped into
  *   [0, num_pages) so that a bad table cannot address outside the pool.
  */

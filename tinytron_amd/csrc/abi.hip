@@ -177,6 +177,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
              (long long)cache_strides[1]);
   }
   if (kind != tt::CacheKind::kF32) {
+    TT_CHECK(batch <= 4096, TT_ERR_UNSUPPORTED, "batch %lld > 4096 is not supported (per-sequence split table in LDS)",
+             (long long)batch);
     TT_CHECK(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
              "q and cache pointers must be 16-byte aligned");
     TT_CHECK(q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0, TT_ERR_INVALID_ARGUMENT,

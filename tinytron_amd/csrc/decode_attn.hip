@@ -35,6 +35,8 @@
 // Tokens past a sequence's length are never loaded (predicated loads, zero
 // fill) and their scores are set to -inf, so garbage or NaN in unused cache
 // slots cannot reach the output.
+#include <algorithm>
+
 #include "tt_internal.h"
 #include "tt_numerics.h"
 
@@ -50,6 +52,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kNegInf = -__builtin_huge_valf();
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] in [15:14]).
+constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+constexpr int kLgkmcntZero = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -102,10 +114,10 @@ struct KVTraits<true> {
 template <int D, bool kFP8>
 struct Tile {
   static constexpr int NU = D * KVTraits<kFP8>::kElemBytes / 64;  // 16-byte fragments per lane per row
-  u32x4 k[2][NU];
-  u32x4 v[2][NU];
-  f32x4 ks[2];  // fp8: K scales of this lane's 4 score rows, per 16-token block
+  u32x4 k[2][NU];  // K fragments of the tile's two 16-token blocks (V goes through LDS)
+  f32x4 ks[2];     // fp8: K scales of this lane's 4 score rows, per 16-token block
   f32x4 vs[2];
+  static constexpr int kVBytes = 2 * NU * 1024;  // per-wave LDS bytes of one tile's V
 };
 
 // Element offset of token tb (a multiple of 16) of (b, hk), d = 0; tb must
@@ -127,37 +139,47 @@ __device__ __forceinline__ int64_t token_elem(const DecodeArgs &a, int b, int hk
   return block_elem(a, b, hk, tb, D) + (int64_t)(t - tb) * D;
 }
 
-// Loads one 16-token block whose element offset `elem` was resolved in the
-// prologue. Rows past the sequence end are outside the buffer range
-// (num_records) and read as zero: no branch, no out-of-bounds access, and no
-// garbage (possibly NaN) reaches the MFMAs.
+// Loads of one 16-token block whose element offset `elem` was resolved in
+// the prologue. Rows past the sequence end are outside the buffer range
+// (num_records) and read as zero (or, for LDS loads, leave the LDS slot as
+// it was): no branch, no out-of-bounds access, and no garbage (possibly
+// NaN) from unused cache slots reaches the MFMAs.
 template <int D, bool kFP8>
-__device__ __forceinline__ void load_block(const DecodeArgs &a, int64_t elem, int rows, int lane,
-                                           u32x4 (&k)[Tile<D, kFP8>::NU], u32x4 (&v)[Tile<D, kFP8>::NU],
-                                           f32x4 &ks, f32x4 &vs) {
+__device__ __forceinline__ void load_k_block(const DecodeArgs &a, int64_t elem, int rows, int lane,
+                                             u32x4 (&k)[Tile<D, kFP8>::NU], f32x4 &ks, f32x4 &vs) {
   constexpr int E = KVTraits<kFP8>::kElemBytes;
   constexpr int NU = Tile<D, kFP8>::NU;
   const auto rk = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<char *>(static_cast<const char *>(a.k_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
-  const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
-  const int m = lane & 15;
-  const int g = lane >> 4;
-  const int off = m * D * E + 16 * g;
+  const int off = (lane & 15) * D * E + 16 * (lane >> 4);
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
+  for (int u = 0; u < NU; ++u)
     k[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * u, 0, 0));
-    v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off + 64 * u, 0, 0));
-  }
   if constexpr (kFP8) {
     // this lane's score rows are tokens tb + 4g + r, r = 0..3
     const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + elem / D, (short)0,
                                                        rows * 4, kBufferFlags);
     const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + elem / D, (short)0,
                                                        rows * 4, kBufferFlags);
-    ks = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rks, 16 * g, 0, 0));
-    vs = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvs, 16 * g, 0, 0));
+    ks = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rks, 16 * (lane >> 4), 0, 0));
+    vs = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvs, 16 * (lane >> 4), 0, 0));
   }
+}
+
+// V rows of one 16-token block straight into this wave's LDS slots
+// (buffer_load ... lds: lane i's 16 bytes land at base + 16 i, the layout a
+// register load would have), so the next tile's V costs no VGPRs.
+template <int D, bool kFP8>
+__device__ __forceinline__ void load_v_block_lds(const DecodeArgs &a, int64_t elem, int rows, int lane, char *lds) {
+  constexpr int E = KVTraits<kFP8>::kElemBytes;
+  constexpr int NU = Tile<D, kFP8>::NU;
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
+  const int off = (lane & 15) * D * E + 16 * (lane >> 4);
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(lds + 1024 * u), 16,
+                                             off + 64 * u, 0, 0, 0);
 }
 
 template <int D, bool kFP8>
@@ -169,9 +191,9 @@ struct WaveState {
 };
 
 template <int D, bool kFP8>
-__device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L, int lane, const Tile<D, kFP8> &tile,
-                                             const bf16x8 (&qf)[D / 32], const bf16x8 (&ident16)[2],
-                                             const u32x2 (&ident8)[2], WaveState<D, kFP8> &st) {
+__device__ __forceinline__ void qk_softmax(const DecodeArgs &a, int t0, int L, int lane, const Tile<D, kFP8> &tile,
+                                           const bf16x8 (&qf)[D / 32], WaveState<D, kFP8> &st, bf16x8 &pa_hi,
+                                           bf16x8 &pa_lo) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
   const int g = lane >> 4;
@@ -240,10 +262,16 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
   // so the PV product keeps ~16 mantissa bits of P instead of bf16's 8; the
   // second MFMA per block is free in this memory-bound loop.
   const f32x8 pv = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]};
-  const bf16x8 pa_hi = __builtin_convertvector(pv, bf16x8);
+  pa_hi = __builtin_convertvector(pv, bf16x8);
   const f32x8 p_rem = pv - __builtin_convertvector(pa_hi, f32x8);
-  const bf16x8 pa_lo = __builtin_convertvector(p_rem, bf16x8);
+  pa_lo = __builtin_convertvector(p_rem, bf16x8);
+}
 
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void pv_tile(const u32x4 (&vt)[2][Tile<D, kFP8>::NU], const bf16x8 (&ident16)[2],
+                                        const u32x2 (&ident8)[2], bf16x8 pa_hi, bf16x8 pa_lo, WaveState<D, kFP8> &st) {
+  constexpr int NDB = D / 32;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) {
@@ -253,14 +281,14 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
     if constexpr (kFP8) {
       const int u = c >> 2;
       const int hh = (c >> 1) & 1;
-      const u32x2 v0 = hh ? u32x2{tile.v[0][u][2], tile.v[0][u][3]} : u32x2{tile.v[0][u][0], tile.v[0][u][1]};
-      const u32x2 v1 = hh ? u32x2{tile.v[1][u][2], tile.v[1][u][3]} : u32x2{tile.v[1][u][0], tile.v[1][u][1]};
+      const u32x2 v0 = hh ? u32x2{vt[0][u][2], vt[0][u][3]} : u32x2{vt[0][u][0], vt[0][u][1]};
+      const u32x2 v1 = hh ? u32x2{vt[1][u][2], vt[1][u][3]} : u32x2{vt[1][u][0], vt[1][u][1]};
       t0v = mfma_fp8(v0, ident8[hi], zero);
       t1v = mfma_fp8(v1, ident8[hi], zero);
     } else {
       const int u = c >> 1;
-      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, tile.v[0][u]), ident16[hi], zero);
-      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, tile.v[1][u]), ident16[hi], zero);
+      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[0][u]), ident16[hi], zero);
+      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[1][u]), ident16[hi], zero);
     }
     // lane (n + 16g): V[token t0 + 4g + r][o_col_d(c, n)] (t0v), same for t0 + 16 (t1v)
     const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
@@ -270,7 +298,7 @@ __device__ __forceinline__ void process_tile(const DecodeArgs &a, int t0, int L,
   }
 }
 
-// head_dim index of output column n of PV block c (see process_tile).
+// head_dim index of output column n of PV block c (see pv_tile).
 template <bool kFP8>
 __device__ __forceinline__ int o_col_d(int c, int n) {
   if constexpr (kFP8) {
@@ -308,24 +336,21 @@ __device__ __forceinline__ void make_identity(int lane, bf16x8 (&ident16)[2], u3
   }
 }
 
+// floats of the LDS merge area: [4][G][D] outputs, [4][16] maxima, [4][16] sums
+__host__ __device__ constexpr int merge_floats(int G, int D) { return kWavesPerBlock * G * D + 2 * kWavesPerBlock * 16; }
+
+// One split of one (sequence, KV head): the 4 waves of the workgroup each
+// stream kTiles 32-token tiles, merge their states in LDS and write one
+// partial (unnormalised output, max, sum) to the workspace.
 template <int D, bool kFP8, int kTiles>
-__global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
+__device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, int split, int L, int lane, int wave,
+                                           char *smem_v, float *smem) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
   constexpr int kWaveTokens = kTiles * kTileTokens;
   constexpr int kBlocks = 2 * kTiles;  // 16-token blocks per wave
-  extern __shared__ float smem[];  // [4][G][D] outputs, then [4][16] m, [4][16] l
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // KV heads are the fastest grid dimension: workgroups that run together
-  // read the head blocks of the same physical pages (adjacent in the pool).
-  const int hk = blockIdx.x;
-  const int split = blockIdx.y;
-  const int b = blockIdx.z;
   const int G = a.group;
-  const int L = min(a.seq_lens[b], a.max_len);
   const int s_begin = split * (kWavesPerBlock * kWaveTokens);
-  if (s_begin >= L) return;  // uniform for the block
   const int w_begin = s_begin + wave * kWaveTokens;
   const int n = lane & 15;
   const int g = lane >> 4;
@@ -363,6 +388,12 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
     }
   }
 
+#pragma unroll
+  for (int i = 0; i < kBlocks; ++i) {  // wave-uniform by construction; keep them in SGPRs
+    belem[i] = uniform64(belem[i]);
+    brows[i] = __builtin_amdgcn_readfirstlane(brows[i]);
+  }
+
   // q^T as the B operand: column n = query head hk*G + n (zero for n >= G),
   // k step s holding the head_dim values the K fragments hold.
   bf16x8 qf[NDB];
@@ -386,22 +417,59 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
   st.m = kNegInf;
   st.l = 0.f;
 
-  // kTiles 32-token tiles per wave, fully unrolled, the next tile's loads in
-  // flight while the current one is on the matrix cores. Tiles past the end
-  // of the sequence load nothing (zero-row buffer ranges) and are skipped.
+  // kTiles 32-token tiles per wave, fully unrolled. While tile i is on the
+  // matrix cores, tile i+1's K is in flight to registers and its V to this
+  // wave's LDS slots. Tiles past the end of the sequence are not processed.
+  constexpr int NU = Tile<D, kFP8>::NU;
+  char *vlds = smem_v + wave * Tile<D, kFP8>::kVBytes;
   Tile<D, kFP8> buf[2];
-  load_block<D, kFP8>(a, belem[0], brows[0], lane, buf[0].k[0], buf[0].v[0], buf[0].ks[0], buf[0].vs[0]);
-  load_block<D, kFP8>(a, belem[1], brows[1], lane, buf[0].k[1], buf[0].v[1], buf[0].ks[1], buf[0].vs[1]);
+  load_k_block<D, kFP8>(a, belem[0], brows[0], lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
+  load_k_block<D, kFP8>(a, belem[1], brows[1], lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
+  __builtin_amdgcn_sched_barrier(0);
+  load_v_block_lds<D, kFP8>(a, belem[0], brows[0], lane, vlds);
+  load_v_block_lds<D, kFP8>(a, belem[1], brows[1], lane, vlds + NU * 1024);
+  // Vector-memory issue order, pinned with scheduling barriers so that the
+  // explicit vmcnt waits below count exactly:
+  //   prologue: K(0), V(0);  iteration i: K(i+1) | QK, softmax | wait V(i),
+  //   read V(i) from LDS | V(i+1) | PV.
+  // Loads retire in issue order, so V(i) has landed once at most |K(i+1)|
+  // loads are outstanding.
+  constexpr int kKLoads = 2 * NU + (kFP8 ? 4 : 0);  // per tile: K fragments (+ K, V scales)
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int it = 0; it < kTiles; ++it) {
     const int t0 = w_begin + it * kTileTokens;
+    if (t0 >= L) break;  // uniform; later tiles are past the end too
     if (it + 1 < kTiles) {
       Tile<D, kFP8> &nx = buf[(it + 1) & 1];
-      load_block<D, kFP8>(a, belem[2 * it + 2], brows[2 * it + 2], lane, nx.k[0], nx.v[0], nx.ks[0], nx.vs[0]);
-      load_block<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, nx.k[1], nx.v[1], nx.ks[1], nx.vs[1]);
+      load_k_block<D, kFP8>(a, belem[2 * it + 2], brows[2 * it + 2], lane, nx.k[0], nx.ks[0], nx.vs[0]);
+      load_k_block<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, nx.k[1], nx.ks[1], nx.vs[1]);
     }
-    if (t0 < L) process_tile<D, kFP8>(a, t0, L, lane, buf[it & 1], qf, ident16, ident8, st);
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 pa_hi, pa_lo;
+    qk_softmax<D, kFP8>(a, t0, L, lane, buf[it & 1], qf, st, pa_hi, pa_lo);
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < kTiles)
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    u32x4 vt[2][NU];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+    // the slots are overwritten only after every lane's read has returned
+    __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < kTiles && t0 + kTileTokens < L) {
+      load_v_block_lds<D, kFP8>(a, belem[2 * it + 2], brows[2 * it + 2], lane, vlds);
+      load_v_block_lds<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, vlds + NU * 1024);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    pv_tile<D, kFP8>(vt, ident16, ident8, pa_hi, pa_lo, st);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // no LDS load of this wave is still in flight past the item
 
   // Merge the 4 wave states of the block in LDS.
   float l = st.l;
@@ -442,6 +510,86 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
       a.ws_ml[(item * G + head) * 2 + 0] = M;
       a.ws_ml[(item * G + head) * 2 + 1] = lsum;
     }
+  }
+}
+
+
+// Block-wide exclusive prefix sum of the per-sequence split counts into LDS:
+// prefix[b] = sum_{b' < b} ceil(L_b' / split), prefix[B] = total; lens[b] = L_b.
+__device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int split_tokens, int *lens, int *prefix,
+                                                   int *wave_sums) {
+  const int B = a.batch;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int per = (B + blockDim.x - 1) / blockDim.x;
+  const int first = tid * per;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int b = first + i;
+    if (b < B) {
+      const int L = max(min(a.seq_lens[b], a.max_len), 0);
+      lens[b] = L;
+      local += (L + split_tokens - 1) / split_tokens;
+    }
+  }
+  int v = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(v, off, 64);
+    if (lane >= off) v += t;
+  }
+  if (lane == 63) wave_sums[wave] = v;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wave_sums[w];
+  int run = base + v - local;
+  for (int i = 0; i < per; ++i) {
+    const int b = first + i;
+    if (b < B) {
+      prefix[b] = run;
+      run += (lens[b] + split_tokens - 1) / split_tokens;
+    }
+  }
+  if (tid == blockDim.x - 1) prefix[B] = base + v;
+  __syncthreads();
+}
+
+// Persistent split kernel: a grid of resident workgroups walks the dense list
+// of (sequence, split, KV head) items -- KV heads fastest, so workgroups that
+// run together read the head blocks of the same physical pages -- with no
+// workgroups for splits past a sequence's end.
+template <int D, bool kFP8, int kTiles>
+__global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
+  constexpr int kSplit = kWavesPerBlock * kTiles * kTileTokens;
+  constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
+  extern __shared__ float smem[];  // V slots [4 waves] | merge area | wave sums | lens[B] | prefix[B + 1]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  char *smem_v = reinterpret_cast<char *>(smem);
+  float *merge = reinterpret_cast<float *>(smem_v + kVAll);
+  // V slots start at zero: rows past a sequence's end are never written, so
+  // what P = 0 meets there is a previous tile's finite V or zero.
+  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
+  int *wave_sums = reinterpret_cast<int *>(merge + merge_floats(a.group, D));
+  int *lens = wave_sums + kWavesPerBlock;
+  int *prefix = lens + a.batch;
+  build_split_prefix(a, kSplit, lens, prefix, wave_sums);
+  const int total = __builtin_amdgcn_readfirstlane(prefix[a.batch]) * a.hkv;
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const int hk = item % a.hkv;
+    const int sidx = item / a.hkv;
+    int lo = 0, hi = a.batch;  // largest b with prefix[b] <= sidx
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (prefix[mid] <= sidx) lo = mid; else hi = mid;
+    }
+    const int b = __builtin_amdgcn_readfirstlane(lo);
+    const int split = sidx - __builtin_amdgcn_readfirstlane(prefix[b]);
+    const int L = __builtin_amdgcn_readfirstlane(lens[b]);
+    split_item<D, kFP8, kTiles>(a, b, hk, split, L, lane, wave, smem_v, merge);
+    __syncthreads();  // the merge area is reused by the next item
   }
 }
 
@@ -594,8 +742,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
 }
 
 template <int D, bool kFP8>
-hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds, hipStream_t stream) {
-  const dim3 grid(a.hkv, a.max_splits, a.batch);
+hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStream_t stream) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+  }
+  const int64_t items = (int64_t)a.batch * a.hkv * a.max_splits;  // upper bound of the dense item count
+  const dim3 grid((unsigned)std::min<int64_t>(items, (int64_t)cus * 2));
+  const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + lds_merge +
+                     sizeof(int) * (kWavesPerBlock + 2 * (size_t)a.batch + 1);
   switch (a.split_tokens / (kWavesPerBlock * kTileTokens)) {
     case 2:
       hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 2>), grid, block, lds, stream, a);
