@@ -83,6 +83,11 @@ def e2e_c5(args, torch):
     torch.cuda.synchronize()
     tokens, stats = eng.generate(prompt, steps, top_k=1, prompt_lens=lens, return_stats=True)
     tps = stats["decode_tokens_per_sec"]
+    eng.use_graphs = False
+    eager_tokens, eager_stats = eng.generate(prompt, steps, top_k=1, prompt_lens=lens, return_stats=True)
+    eng.use_graphs = True
+    if not torch.equal(tokens, eager_tokens):
+        raise RuntimeError("graph-replayed decode diverged from the eager decode")
     n_params = sum(p.numel() for p in model.parameters())
     mean_ctx = sum(lens) / B + steps / 2
     kv_bytes = C5["num_layer"] * 2 * B * mean_ctx * C5["num_key_value_heads"] * (C5["hidden_size"] // C5["num_attention_heads"]) * 2
@@ -92,6 +97,8 @@ def e2e_c5(args, torch):
         "workload": "C5 greedy decode through the engine: 24 L, d 2048, 32/8 heads, D 64, V 32000, bf16 "
                     "random-init weights, B 64, prompts U[64, 2048], paged KV page 16",
         "decode_tokens_per_sec": round(tps, 1),
+        "decode_tokens_per_sec_eager": round(eager_stats["decode_tokens_per_sec"], 1),
+        "decode_graphs": "one-token model call replayed from HIP graphs after the first step (capture timed)",
         "decode_steps": int(stats["decode_tokens"] // B),
         "prefill_tokens_per_sec": round(stats["prefill_tokens_per_sec"], 1),
         "params": n_params,

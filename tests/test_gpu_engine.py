@@ -129,3 +129,32 @@ def test_ragged_batch_equals_batch_one(kv_dtype):
             mismatched += 1
     # bf16 GEMMs of different batch shapes round differently; allow a near-tie flip in one sequence
     assert mismatched <= 1, f"{mismatched} of {len(lens)} sequences diverged"
+
+
+@pytest.mark.parametrize("kv_dtype,sync_each_step", [(None, True), ("fp8", False)])
+def test_graph_replay_equals_eager(kv_dtype, sync_each_step):
+    """Decode steps replayed from the two captured graphs give the eager path's
+    tokens and log-probabilities bit for bit, on every replay (ragged batch,
+    paged pool). ``eos_token_id=-1`` never fires but makes the loop synchronise
+    with the host after every step, between replays."""
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=3, block_size=512, vocab_size=4096)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    kvd = torch.float8_e4m3fn if kv_dtype == "fp8" else None
+    g = torch.Generator().manual_seed(11)
+    lens = [3, 40, 77, 128, 129, 200]
+    prompt = torch.randint(0, cfg.vocab_size, (len(lens), max(lens)), generator=g)
+    eos = -1 if sync_each_step else None
+    runs = []
+    for use_graphs in (False, True):
+        eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True,
+                              kv_cache_dtype=kvd, model=model, use_graphs=use_graphs)
+        toks, extra = eng.generate(prompt, 40, top_k=1, prompt_lens=lens, eos_token_id=eos, return_stats=True,
+                                   return_logprobs=True)
+        runs.append((toks.cpu(), extra["token_log_probs"].cpu(), extra["lengths"]))
+    (t0, lp0, n0), (t1, lp1, n1) = runs
+    assert n0 == n1 == [n + 40 for n in lens]
+    assert torch.equal(t0, t1)
+    assert torch.equal(lp0, lp1)

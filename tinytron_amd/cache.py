@@ -67,6 +67,7 @@ class _LayerCacheBase:
         self._host_lens = [0] * batch_size
         self._pending_new_lens = None
         self.workspace = None
+        self.static_max_len = None  # graph capture: launch-size bound fixed at the capacity
 
     # -- lengths ---------------------------------------------------------------
     @property
@@ -133,8 +134,20 @@ class _LayerCacheBase:
         """GQA decode attention of q [B, H_q, D] over every cached token of each sequence."""
         if self.workspace is None:
             self.workspace = ops.Workspace(q.device)
-        return ops.decode_attention(q, self.layout, self.seq_lens, self.current_length, out=out,
-                                    workspace=self.workspace)
+        bound = self.static_max_len if self.static_max_len is not None else self.current_length
+        return ops.decode_attention(q, self.layout, self.seq_lens, bound, out=out, workspace=self.workspace)
+
+    # -- host-state snapshots for graph capture ------------------------------------
+    def host_state(self):
+        return (list(self._host_lens), self._cur)
+
+    def set_host_state(self, state) -> None:
+        self._host_lens, self._cur = list(state[0]), state[1]
+
+    def advance_host(self, n: int = 1) -> None:
+        """Mirror a replayed one-token step: lengths + n, length buffers swapped n times."""
+        self._host_lens = [x + n for x in self._host_lens]
+        self._cur = (self._cur + n) & 1
 
     # -- gathers for the protocol / prefill ----------------------------------------
     def _token_index(self, b: int, length: int) -> torch.Tensor:
@@ -347,3 +360,30 @@ class PagedKVCache:
     def set_pending_new_lens(self, new_lens) -> None:
         for c in self._layer_caches:
             c.set_pending_new_lens(new_lens)
+
+    def host_state(self):
+        return [c.host_state() for c in self._layer_caches]
+
+    def set_host_state(self, states) -> None:
+        for c, st in zip(self._layer_caches, states):
+            c.set_host_state(st)
+
+    def advance_host(self, n: int = 1) -> None:
+        for c in self._layer_caches:
+            c.advance_host(n)
+
+    def set_static_max_len(self, n) -> None:
+        """Fix every layer's attention launch bound (split size, grid, workspace) at n
+        tokens, so one captured step stays valid while lengths grow; None restores
+        bounds taken from the current lengths."""
+        for c in self._layer_caches:
+            c.static_max_len = n
+
+    def parity(self) -> int:
+        """Which of the two device length buffers holds the current lengths (same in every layer)."""
+        return self._layer_caches[0]._cur
+
+    def check_room(self, add: int) -> None:
+        """Raise the reference's overflow error unless every sequence can take ``add`` more tokens."""
+        for c in self._layer_caches:
+            c._check_room([add] * c.batch_size)

@@ -11,6 +11,16 @@ Each step's model call is unchanged: ``model(next[B, 1], use_cache=True,
 past_key_values=cache, position_offset=...)``; positions come from the
 cache's per-sequence lengths, so there is no host synchronisation in the
 loop (the reference syncs once per layer at attn.py:395).
+
+With ``use_graphs`` (default) the one-token model call is captured in HIP
+graphs after the first decode step and replayed for the rest, which removes
+the per-kernel launch cost (a decode step is a few hundred small kernels).
+The caches keep their lengths in two device buffers that swap every step, so
+two graphs are captured, one per buffer parity. The attention launch bound is
+fixed at the largest sequence capacity for the whole decode loop, so the
+captured split size and grid stay valid as lengths grow (the kernels read
+the actual lengths on the device). Sampling and the token write stay outside
+the graphs, so every sampling mode works unchanged.
 """
 from __future__ import annotations
 
@@ -23,11 +33,44 @@ from .model import GPT, ModelConfig
 from .sampler import sample_next_token, sample_next_token_with_log_prob
 
 
+class DecodeGraphs:
+    """Two captured one-token model calls (one per length-buffer parity)."""
+
+    def __init__(self, model: GPT, cache: PagedKVCache, batch_size: int, position: int, uniform: bool,
+                 device: torch.device):
+        self.cache = cache
+        self.static_in = torch.zeros(batch_size, 1, dtype=torch.long, device=device)
+        self.graphs = {}
+        self.logits = {}
+        state = cache.host_state()
+        pool = torch.cuda.graph_pool_handle()
+        try:
+            for k in range(2):
+                parity = cache.parity()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=pool):
+                    logits, _ = model(self.static_in, use_cache=True, past_key_values=cache,
+                                      position_offset=(position + k) if uniform else 0)
+                self.graphs[parity] = g
+                self.logits[parity] = logits
+        finally:
+            cache.set_host_state(state)         # capture ran no kernel: undo its host-side advance
+
+    def step(self, next_token: torch.Tensor) -> torch.Tensor:
+        """One decode model call by replay; returns the logits [B, 1, V] it wrote."""
+        self.cache.check_room(1)
+        parity = self.cache.parity()
+        self.static_in.copy_(next_token.view(-1, 1))
+        self.graphs[parity].replay()
+        self.cache.advance_host(1)
+        return self.logits[parity]
+
+
 class InferenceEngine:
     def __init__(self, model_config: ModelConfig, checkpoint_path: str | None = None, device: str = "cuda",
                  dtype: torch.dtype = torch.bfloat16, use_paged_kv_cache: bool = True, kv_cache_page_size: int = 128,
                  kv_cache_dtype: torch.dtype | None = None, paged_pool: bool = False, page_seed: int = 1337,
-                 model: GPT | None = None):
+                 model: GPT | None = None, use_graphs: bool = True):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("the tinytron_amd engine runs on the GPU (no CPU fallback)")
@@ -43,6 +86,7 @@ class InferenceEngine:
         self.kv_cache_dtype = kv_cache_dtype
         self.paged_pool = paged_pool
         self.page_seed = page_seed
+        self.use_graphs = use_graphs
         self.dtype = dtype
         self.model = model if model is not None else GPT(model_config, device=self.device, dtype=dtype)
         if checkpoint_path:
@@ -91,6 +135,8 @@ class InferenceEngine:
         token_log_probs = []
         cur = lens_t.clone()
         uniform = len(set(lens)) == 1
+        graphs = None
+        cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
         for step in range(max_new_tokens):
             if return_logprobs:
@@ -104,11 +150,17 @@ class InferenceEngine:
             if eos_token_id is not None and torch.all(next_token == eos_token_id):
                 break
             position = (lens[0] + step) if uniform else 0
-            logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
-                                       position_offset=position)
+            if graphs is None and self.use_graphs and step >= 1 and max_new_tokens - step >= 3:
+                graphs = DecodeGraphs(self.model, cache, batch_size, position, uniform, self.device)
+            if graphs is not None:
+                logits = graphs.step(next_token)
+            else:
+                logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
+                                           position_offset=position)
             next_logits = logits[:, -1, :]
         torch.cuda.synchronize(self.device)
         decode_t1 = time.perf_counter()
+        cache.set_static_max_len(None)
 
         out_len = max(lens) + decode_steps
         tokens = tokens[:, :out_len]
