@@ -146,7 +146,7 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
 
 /*
  * GQA decode attention over a ragged batch, bf16 cache, split-K
- * (flash-decoding) with a combine pass.
+ * (flash-decoding) with a merge pass.
  *
  * Replaces, for one new token per sequence (T = 1):
  *   cache.get_kv()                             cache.py:47-51
@@ -161,7 +161,11 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
  * out [B, H_q, D] bf16, strides out_strides = {b, h}. A sequence with
  *   seq_lens[b] <= 0 gets zeros.
  * sm_scale: softmax scale (1/sqrt(D) for the reference's SDPA default).
- * split_tokens: tokens per split: 128, 256, 512 or 1024; 0 = automatic.
+ * split_tokens: 0 = balanced partition: the 32-token tiles of all
+ *   (sequence, KV head) pairs are dealt out in equal contiguous runs to the
+ *   resident waves, whatever the length mix (bf16 and fp8; fp32 uses the
+ *   automatic fixed split); 128, 256, 512 or 1024 = fixed splits of that
+ *   many tokens.
  * workspace: device scratch of at least tt_decode_workspace_bytes(...) bytes
  *   for the same (batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
  *   split_tokens); its contents need no initialisation.
@@ -219,10 +223,11 @@ int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2],
                            int64_t split_tokens, void *workspace, size_t workspace_bytes,
                            tt_stream_t stream);
 
-/* Split size the attention entry points use when split_tokens == 0. */
+/* Fixed split size the fp32 entry point uses when split_tokens == 0. */
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 
-/* Workspace bytes the attention entry points need (split_tokens 0 = auto). */
+/* Workspace bytes the attention entry points need; for split_tokens 0 the
+ * size covers every cache dtype. */
 size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                  int64_t head_dim, int64_t max_seq_len, int64_t split_tokens);
 

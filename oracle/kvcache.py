@@ -57,6 +57,17 @@ class CacheLayout:
             base = int(self.page_table[b, j]) * self.page_stride
         return base + h * self.head_stride + slot * self.head_dim
 
+    def token_offsets(self, b: int, length: int) -> np.ndarray:
+        """token_offset(b, h, t) for every t < length and h, as int64 [length, H]."""
+        t = np.arange(int(length), dtype=np.int64)
+        j, slot = t // self.page_size, t % self.page_size
+        if self.page_table is None:
+            base = b * self.seq_stride + j * self.page_stride
+        else:
+            base = self.page_table[b, j].astype(np.int64) * self.page_stride
+        h = np.arange(self.num_heads, dtype=np.int64)
+        return (base + slot * self.head_dim)[:, None] + h[None, :] * self.head_stride
+
 
 def contiguous_layout(batch: int, num_heads: int, head_dim: int, max_seq_len: int, page_size: int) -> CacheLayout:
     """The reference's [B, H, ceil(S/P), P, D] store (cache.py:27-28)."""

@@ -63,17 +63,16 @@ def fill_cache_values(layout, numel, batch, lengths, rng, fp8=False):
             vq, vsc = quantize_e4m3_rows(vb)
             kb = dequantize_e4m3_rows(kq, ksc)
             vb = dequantize_e4m3_rows(vq, vsc)
-        for t in range(L):
-            for h in range(H):
-                off = layout.token_offset(b, h, t)
-                if fp8:
-                    kc[off:off + D] = kq[t, h]
-                    vc[off:off + D] = vq[t, h]
-                    ks[off // D] = ksc[t, h]
-                    vs[off // D] = vsc[t, h]
-                else:
-                    kc[off:off + D] = f32_to_bf16_bits(kb[t, h])
-                    vc[off:off + D] = f32_to_bf16_bits(vb[t, h])
+        offs = layout.token_offsets(b, L)                                   # [L, H]
+        idx = (offs[..., None] + np.arange(D, dtype=np.int64)).reshape(-1)  # [L * H * D]
+        if fp8:
+            kc[idx] = kq.reshape(-1)
+            vc[idx] = vq.reshape(-1)
+            ks[(offs // D).reshape(-1)] = ksc.reshape(-1)
+            vs[(offs // D).reshape(-1)] = vsc.reshape(-1)
+        else:
+            kc[idx] = f32_to_bf16_bits(kb).reshape(-1)
+            vc[idx] = f32_to_bf16_bits(vb).reshape(-1)
         keys.append(kb)
         values.append(vb)
     out = {"keys": keys, "values": values, "k_store": kc, "v_store": vc}

@@ -27,7 +27,7 @@ def _dev(arr, dtype):
 
 
 def run_case(lengths, Hq=32, Hkv=8, D=128, P=16, paged=False, fp8=False, seed=0, split_tokens=0, f32=False,
-             zero_first=False):
+             zero_first=False, workspace=None):
     from tinytron_amd import ops
 
     rng = np.random.default_rng(seed)
@@ -81,7 +81,7 @@ def run_case(lengths, Hq=32, Hkv=8, D=128, P=16, paged=False, fp8=False, seed=0,
     if zero_first:
         dev_lens[0] = 0
     seq = torch.from_numpy(dev_lens).to(DEV)
-    out = ops.decode_attention(q, kv, seq, max_len, split_tokens=split_tokens)
+    out = ops.decode_attention(q, kv, seq, max_len, split_tokens=split_tokens, workspace=workspace)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     ref = ref_attention(qf, data["keys"], data["values"], Hkv, sm_scale(D))
@@ -159,3 +159,37 @@ def test_zero_length_gives_zeros():
     got, ref, _ = run_case([5, 9, 33], seed=1, zero_first=True)
     assert np.all(got[0] == 0.0)
     assert_close(got[1:], ref[1:])
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_balanced_partition_large(fp8):
+    """Enough tiles that every wave of the balanced partition holds several
+    segments and multi-chunk pieces (W >> resident waves), with sequences of
+    1 token beside long ones; split_tokens 0 and a fixed split agree with the
+    oracle alike."""
+    rng = np.random.default_rng(99)
+    lengths = rng.integers(1, 6000, 40)
+    lengths[:4] = [1, 2, 31, 33]
+    got, ref, _ = run_case(lengths, paged=True, fp8=fp8, seed=50 + fp8)
+    assert_close(got, ref)
+    got_fixed, _, _ = run_case(lengths, paged=True, fp8=fp8, seed=50 + fp8, split_tokens=512)
+    assert_close(got_fixed, ref)
+
+
+def test_balanced_partition_more_waves_than_tiles():
+    """Fewer tiles than resident waves: most waves hold nothing, segments are
+    split across many single-tile pieces."""
+    got, ref, _ = run_case([1, 64, 33, 300], Hq=8, Hkv=1, seed=12)
+    assert_close(got, ref)
+
+
+def test_balanced_workspace_reuse_across_calls():
+    """The balanced partition's arrival counters return to zero after every
+    call: three calls on one workspace with different lengths and batch
+    shapes each match the oracle."""
+    from tinytron_amd import ops
+
+    ws = ops.Workspace(DEV)
+    for seed, lengths in ((31, [500, 20, 1300]), (32, [7, 3000]), (33, [64] * 9), (34, [500, 20, 1300])):
+        got, ref, _ = run_case(lengths, paged=True, seed=seed, workspace=ws)
+        assert_close(got, ref)

@@ -46,6 +46,20 @@ def test_identity_page_table_reproduces_contiguous():
                 assert paged.token_offset(b, h, t) == cont.token_offset(b, h, t)
 
 
+def test_vectorized_offsets_equal_scalar_offsets():
+    rng = np.random.default_rng(5)
+    lens = np.array([1, 16, 17, 100, 33])
+    H, D, P = 3, 8, 16
+    table, n_pages = okv.random_page_table(lens, P, rng, extra_pages=2)
+    for layout in (okv.paged_layout(n_pages, H, D, P, table), okv.contiguous_layout(len(lens), H, D, 112, P)):
+        for b, L in enumerate(lens):
+            offs = layout.token_offsets(b, int(L))
+            assert offs.shape == (L, H)
+            for t in range(L):
+                for h in range(H):
+                    assert offs[t, h] == layout.token_offset(b, h, t)
+
+
 def test_random_page_table_is_injective_and_in_pool():
     rng = np.random.default_rng(0)
     lens = np.array([1, 16, 17, 100, 33])

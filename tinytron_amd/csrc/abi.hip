@@ -140,6 +140,17 @@ size_t workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim,
   return (size_t)(items * head_dim + items * 2) * sizeof(float);
 }
 
+// Balanced partition: the per-sequence tile prefix (padded to 16 bytes), then
+// one partial slot per (segment + wave) index.
+int64_t balanced_slots(int64_t batch, int64_t hkv) { return batch * hkv + tt::kMaxStreamWaves; }
+int64_t balanced_prefix_ints(int64_t batch) { return (batch + 1 + 3) & ~(int64_t)3; }
+
+size_t balanced_workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim) {
+  const int64_t g = hq / (hkv > 0 ? hkv : 1);
+  const int64_t rows = balanced_slots(batch, hkv) * g;
+  return (size_t)balanced_prefix_ints(batch) * sizeof(int32_t) + (size_t)(rows * head_dim + rows * 2) * sizeof(float);
+}
+
 int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2], const void *k_cache,
                   const void *v_cache, const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
                   const int32_t *seq_lens, int64_t max_seq_len, const int32_t *page_table, int64_t max_pages,
@@ -189,12 +200,22 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     TT_CHECK(aligned(q, 4) && aligned(k_cache, 4) && aligned(v_cache, 4) && aligned(out, 4),
              TT_ERR_INVALID_ARGUMENT, "fp32 pointers must be 4-byte aligned");
   }
-  const int64_t split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
-  TT_CHECK(split == 128 || split == 256 || split == 512 || split == 1024, TT_ERR_INVALID_ARGUMENT,
-           "split_tokens must be 0 (auto), 128, 256, 512 or 1024, got %lld", (long long)split_tokens);
-  const int64_t splits = tt::num_splits(max_seq_len, split);
-  TT_CHECK(splits <= 65535, TT_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
-  const size_t need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
+  // split_tokens == 0 on the bf16/fp8 path: balanced partition (equal tiles per wave); otherwise fixed splits
+  const bool balanced = split_tokens == 0 && kind != tt::CacheKind::kF32;
+  int64_t split = 0, splits = 0;
+  size_t need = 0;
+  if (balanced) {
+    TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens) < ((int64_t)1 << 31),
+             TT_ERR_UNSUPPORTED, "batch * max_seq_len is too large for the balanced partition");
+    need = balanced_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
+  } else {
+    split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
+    TT_CHECK(split == 128 || split == 256 || split == 512 || split == 1024, TT_ERR_INVALID_ARGUMENT,
+             "split_tokens must be 0 (auto), 128, 256, 512 or 1024, got %lld", (long long)split_tokens);
+    splits = tt::num_splits(max_seq_len, split);
+    TT_CHECK(splits <= 65535, TT_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
+    need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
+  }
   TT_CHECK(workspace != nullptr && ws_bytes >= need, TT_ERR_WORKSPACE_TOO_SMALL,
            "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
   TT_CHECK(aligned(workspace, 16), TT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
@@ -220,9 +241,11 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.o_sb = out_strides[0];
   a.o_sh = out_strides[1];
   const int64_t g = num_q_heads / num_kv_heads;
-  const int64_t items = batch * num_kv_heads * splits * g;
-  a.ws_o = static_cast<float *>(workspace);
-  a.ws_ml = static_cast<float *>(workspace) + items * head_dim;
+  const int64_t rows = g * (balanced ? balanced_slots(batch, num_kv_heads) : batch * num_kv_heads * splits);
+  a.ws_prefix = balanced ? static_cast<int32_t *>(workspace) : nullptr;
+  a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                     (balanced ? balanced_prefix_ints(batch) * sizeof(int32_t) : 0));
+  a.ws_ml = a.ws_o + rows * head_dim;
   a.batch = (int)batch;
   a.hq = (int)num_q_heads;
   a.hkv = (int)num_kv_heads;
@@ -328,7 +351,11 @@ size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
   const int64_t split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
   if (split <= 0) return 0;
-  return workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
+  const size_t fixed = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
+  if (split_tokens != 0) return fixed;
+  // 0 serves every cache dtype: the balanced layout (bf16, fp8) or the automatic split (fp32)
+  const size_t bal = balanced_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
+  return bal > fixed ? bal : fixed;
 }
 
 }  // extern "C"

@@ -515,7 +515,8 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
 
 
 // Block-wide exclusive prefix sum of the per-sequence split counts into LDS:
-// prefix[b] = sum_{b' < b} ceil(L_b' / split), prefix[B] = total; lens[b] = L_b.
+// prefix[b] = sum_{b' < b} ceil(L_b' / split), prefix[B] = total; lens[b] = L_b
+// (when lens is not null).
 __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int split_tokens, int *lens, int *prefix,
                                                    int *wave_sums) {
   const int B = a.batch;
@@ -529,7 +530,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
     const int b = first + i;
     if (b < B) {
       const int L = max(min(a.seq_lens[b], a.max_len), 0);
-      lens[b] = L;
+      if (lens != nullptr) lens[b] = L;
       local += (L + split_tokens - 1) / split_tokens;
     }
   }
@@ -548,7 +549,8 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
     const int b = first + i;
     if (b < B) {
       prefix[b] = run;
-      run += (lens[b] + split_tokens - 1) / split_tokens;
+      const int L = lens != nullptr ? lens[b] : max(min(a.seq_lens[b], a.max_len), 0);
+      run += (L + split_tokens - 1) / split_tokens;
     }
   }
   if (tid == blockDim.x - 1) prefix[B] = base + v;
@@ -591,6 +593,305 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
     split_item<D, kFP8, kTiles>(a, b, hk, split, L, lane, wave, smem_v, merge);
     __syncthreads();  // the merge area is reused by the next item
   }
+}
+
+// ---------------------------------------------------------------------------
+// Balanced partition ("stream-K" over tiles). The work is the flat list of
+// 32-token tiles of every (sequence, KV head) segment, segments in (b, hk)
+// order, KV heads fastest: W = H_kv * sum_b ceil(L_b / 32) tiles. Wave w of
+// the NW resident waves takes tiles [w W / NW, (w + 1) W / NW), so every wave
+// streams the same number of bytes (within one tile) whatever the length
+// mix, and waves never wait for each other. The piece of a segment that wave
+// w holds goes to workspace slot (segment index + w) -- injective, because
+// walking the line of tiles, each piece boundary advances the segment, the
+// wave, or both -- and a second kernel merges each segment's pieces. (Merging
+// in the kernel itself, by the last wave to finish a segment, needs an
+// agent-scope release per piece -- an L2 write-back on every arrival -- and
+// measured slower than the second launch.)
+
+// Tile range start of wave w.
+__host__ __device__ __forceinline__ int64_t wave_first_tile(int64_t w, int64_t W, int64_t NW) { return w * W / NW; }
+// The wave whose range holds tile t (the largest w with wave_first_tile(w) <= t).
+__host__ __device__ __forceinline__ int64_t wave_of_tile(int64_t t, int64_t W, int64_t NW) {
+  return ((t + 1) * NW - 1) / W;
+}
+
+constexpr int kChunkTiles = 8;  // tiles per page-table fetch and software-pipelined run
+
+// Element offset and valid rows of 16-token block `blk` of (b, hk). Paged:
+// `entry` holds, one per lane, the page-table entries of pages pbase.. (the
+// block's page index relative to pbase is < 64 for every block of the chunk).
+template <int D>
+__device__ __forceinline__ void stream_block_addr(const DecodeArgs &a, int b, int hk, int L, int entry, int pbase,
+                                                  int blk, int64_t &elem, int &rows) {
+  const int tb = 16 * blk;
+  const int tc = min(tb, (L - 1) & ~15);  // blocks past the end keep an in-sequence address and zero rows
+  rows = __builtin_amdgcn_readfirstlane(min(max(L - tb, 0), 16));
+  int64_t e;
+  if (a.page_table != nullptr) {
+    int64_t phys = __builtin_amdgcn_readlane(entry, (tc >> a.page_shift) - pbase);
+    phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
+    e = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & ((1 << a.page_shift) - 1)) * D;
+  } else {
+    e = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)tc * D;
+  }
+  elem = uniform64(e);
+}
+
+// Merge the pieces of segment (b, hk) held by waves w0..w1 (waves with empty
+// ranges hold none) and write its G output rows:
+// out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p, lane = head_dim column.
+// Pieces go kGroup at a time with every load of a group issued before any
+// arithmetic, so a segment of up to kGroup pieces costs one memory round trip.
+template <int D, int kMaxG>
+__device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk, int64_t seg, int64_t w0, int64_t w1,
+                                              int64_t W, int64_t NW, int lane) {
+  constexpr int DPL = D / 64;
+  constexpr int kGroup = 64 / (kMaxG * DPL) > 0 ? 64 / (kMaxG * DPL) : 1;
+  const int G = a.group;  // <= kMaxG
+  float M[kMaxG], Ls[kMaxG], acc[kMaxG][DPL];
+#pragma unroll
+  for (int h = 0; h < kMaxG; ++h) {
+    M[h] = kNegInf;
+    Ls[h] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[h][j] = 0.f;
+  }
+  for (int64_t wb = w0; wb <= w1; wb += kGroup) {
+    bool on[kGroup];
+    float mv[kGroup][kMaxG], lv[kGroup][kMaxG], ov[kGroup][kMaxG][DPL];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int64_t w = wb + u;
+      on[u] = w <= w1 && wave_first_tile(w, W, NW) < wave_first_tile(w + 1, W, NW);  // uniform
+      const int64_t sk = seg + (on[u] ? w : w0);  // slot w0 always holds a piece
+#pragma unroll
+      for (int h = 0; h < kMaxG; ++h) {
+        if (h < G) {
+          mv[u][h] = a.ws_ml[(sk * G + h) * 2];
+          lv[u][h] = a.ws_ml[(sk * G + h) * 2 + 1];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) ov[u][h][j] = a.ws_o[(sk * G + h) * D + lane + 64 * j];
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxG; ++h) {
+      if (h < G) {
+        float m_new = M[h];
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) m_new = on[u] ? fmaxf(m_new, mv[u][h]) : m_new;
+        const float sc = __builtin_amdgcn_exp2f(M[h] - m_new);  // m_new finite: slot w0 is in the first group
+        Ls[h] *= sc;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[h][j] *= sc;
+#pragma unroll
+        for (int u = 0; u < kGroup; ++u) {
+          if (on[u]) {
+            const float e = __builtin_amdgcn_exp2f(mv[u][h] - m_new);
+            Ls[h] += e * lv[u][h];
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[h][j] += e * ov[u][h][j];
+          }
+        }
+        M[h] = m_new;
+      }
+    }
+  }
+  uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * G * a.o_sh;
+#pragma unroll
+  for (int h = 0; h < kMaxG; ++h) {
+    if (h < G) {
+      const float inv = Ls[h] > 0.f ? 1.0f / Ls[h] : 0.f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) out[(int64_t)h * a.o_sh + lane + 64 * j] = f32_to_bf16_bits(acc[h][j] * inv);
+    }
+  }
+}
+
+// Tiles [j0, j1) of segment (b, hk) (L tokens) by wave w: one partial to workspace slot (segment + w).
+template <int D, bool kFP8>
+__device__ __forceinline__ void stream_piece(const DecodeArgs &a, int b, int hk, int L, int j0, int j1, int64_t w,
+                                             int lane, char *vlds, const bf16x8 (&ident16)[2],
+                                             const u32x2 (&ident8)[2]) {
+  using TR = KVTraits<kFP8>;
+  constexpr int NDB = D / 32;
+  const int G = a.group;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+
+  bf16x8 qf[NDB];
+  {
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + n) * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < NDB; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (n < G) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
+      qf[s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  WaveState<D, kFP8> st;
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = kNegInf;
+  st.l = 0.f;
+
+  constexpr int NU = Tile<D, kFP8>::NU;
+  constexpr int kKLoads = 2 * NU + (kFP8 ? 4 : 0);  // per tile: K fragments (+ K, V scales)
+  // Chunks of kChunkTiles tiles, each fully unrolled so the two K buffers
+  // alternate with static indices. Vector-memory issue order, pinned with
+  // scheduling barriers so that the explicit vmcnt waits count exactly:
+  //   chunk start: page entries, K(0), V(0);  tile k: K(k+1) | QK, softmax |
+  //   wait V(k), read V(k) from LDS | V(k+1) | PV.
+  // Loads retire in issue order, so V(k) has landed once at most |K(k+1)|
+  // loads are outstanding. K(k+1) is issued for every k + 1 < kChunkTiles
+  // (rows past the end read nothing), so no buffer is conditionally written.
+  for (int c0 = j0; c0 < j1; c0 += kChunkTiles) {
+    const int c1 = min(j1, c0 + kChunkTiles);
+    int entry = 0, pbase = 0;
+    if (a.page_table != nullptr) {
+      pbase = (kTileTokens * c0) >> a.page_shift;
+      const int last = (L - 1) >> a.page_shift;
+      entry = a.page_table[(int64_t)b * a.max_pages + min(pbase + lane, last)];
+    }
+    Tile<D, kFP8> buf[2];
+    int64_t e0, e1;
+    int r0, r1;
+    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0, e0, r0);
+    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0 + 1, e1, r1);
+    load_k_block<D, kFP8>(a, e0, r0, lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
+    load_k_block<D, kFP8>(a, e1, r1, lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
+    load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kChunkTiles; ++k) {
+      const int it = c0 + k;
+      if (it >= c1) break;  // uniform
+      if (k + 1 < kChunkTiles) {
+        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 2, e0, r0);
+        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 3, e1, r1);
+        Tile<D, kFP8> &nx = buf[(k + 1) & 1];
+        load_k_block<D, kFP8>(a, e0, r0, lane, nx.k[0], nx.ks[0], nx.vs[0]);
+        load_k_block<D, kFP8>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      bf16x8 pa_hi, pa_lo;
+      qk_softmax<D, kFP8>(a, kTileTokens * it, L, lane, buf[k & 1], qf, st, pa_hi, pa_lo);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 1 < kChunkTiles)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      u32x4 vt[2][NU];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+      // the slots are overwritten only after every lane's read has returned
+      __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 1 < kChunkTiles && it + 1 < c1) {
+        load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
+        load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      pv_tile<D, kFP8>(vt, ident16, ident8, pa_hi, pa_lo, st);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // nothing of this chunk still in flight
+  }
+
+  float l = st.l;  // lane-partial sums -> the head's sum in all 4 lanes of the head
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const int64_t slot = (int64_t)b * a.hkv + hk + w;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int head = 4 * g + r;
+    if (head < G) {
+#pragma unroll
+      for (int c = 0; c < 2 * NDB; ++c) a.ws_o[(slot * G + head) * D + o_col_d<kFP8>(c, n)] = st.o[c][r];
+    }
+  }
+  if (g == 0 && n < G) {
+    a.ws_ml[(slot * G + n) * 2 + 0] = st.m;
+    a.ws_ml[(slot * G + n) * 2 + 1] = l;
+  }
+}
+
+// Persistent balanced kernel: NW = gridDim.x * 4 waves, all resident
+// (kStreamOcc workgroups per CU).
+constexpr int kStreamOcc = 2;
+
+template <int D, bool kFP8>
+__global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeArgs a) {
+  constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
+  extern __shared__ float smem[];  // V slots [4 waves] | wave sums [4] | prefix[B + 1]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  char *smem_v = reinterpret_cast<char *>(smem);
+  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
+  int *wave_sums = reinterpret_cast<int *>(smem_v + kVAll);
+  int *prefix = wave_sums + kWavesPerBlock;
+  build_split_prefix(a, kTileTokens, nullptr, prefix, wave_sums);  // ends with a block barrier
+  if (blockIdx.x == 0)  // for the merge kernel
+    for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.ws_prefix[i] = prefix[i];
+  const int64_t W = (int64_t)__builtin_amdgcn_readfirstlane(prefix[a.batch]) * a.hkv;
+  const int64_t NW = a.stream_waves;
+  const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  int64_t t = uniform64(wave_first_tile(w, W, NW));
+  const int64_t t_end = uniform64(wave_first_tile(w + 1, W, NW));
+  bf16x8 ident16[2];
+  u32x2 ident8[2];
+  make_identity(lane, ident16, ident8);
+  char *vlds = smem_v + wave * Tile<D, kFP8>::kVBytes;
+  while (t < t_end) {
+    int lo = 0, hi = a.batch;  // largest b with hkv * prefix[b] <= t
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if ((int64_t)prefix[mid] * a.hkv <= t) lo = mid; else hi = mid;
+    }
+    const int b = __builtin_amdgcn_readfirstlane(lo);
+    const int pb = __builtin_amdgcn_readfirstlane(prefix[b]);
+    const int nb = __builtin_amdgcn_readfirstlane(prefix[b + 1]) - pb;  // > 0: tile t lies in sequence b
+    const int64_t local = t - (int64_t)pb * a.hkv;
+    const int hk = (int)(local / nb);
+    const int j0 = (int)(local - (int64_t)hk * nb);
+    const int64_t seg_end = (int64_t)pb * a.hkv + (int64_t)(hk + 1) * nb;
+    const int64_t stop = seg_end < t_end ? seg_end : t_end;
+    const int j1 = j0 + (int)(stop - t);
+    const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b], a.max_len));
+    stream_piece<D, kFP8>(a, b, hk, L, j0, j1, w, lane, vlds, ident16, ident8);
+    t = stop;
+  }
+}
+
+// One wave per segment (b, KV head): merge its pieces into the G output rows
+// (zeros for a sequence with nothing cached). kMaxG bounds the group size.
+template <int D, int kMaxG>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 64;
+  const int64_t seg = blockIdx.x;
+  const int b = (int)(seg / a.hkv);
+  const int hk = (int)(seg - (int64_t)b * a.hkv);
+  const int lane = threadIdx.x;
+  const int pb = a.ws_prefix[b];
+  const int nb = a.ws_prefix[b + 1] - pb;
+  if (nb <= 0) {
+    uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * a.group * a.o_sh;
+    for (int h = 0; h < a.group; ++h)
+      for (int j = 0; j < DPL; ++j) out[(int64_t)h * a.o_sh + lane + 64 * j] = 0;
+    return;
+  }
+  const int64_t W = (int64_t)a.ws_prefix[a.batch] * a.hkv;
+  const int64_t NW = a.stream_waves;
+  const int64_t start = (int64_t)pb * a.hkv + (int64_t)hk * nb;
+  merge_segment<D, kMaxG>(a, b, hk, seg, wave_of_tile(start, W, NW), wave_of_tile(start + nb - 1, W, NW), W, NW,
+                          lane);
 }
 
 // fp32 cache and activations: VALU path (small models run in fp32, e.g. the
@@ -769,8 +1070,37 @@ hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStr
   return hipGetLastError();
 }
 
+template <int D, bool kFP8>
+hipError_t launch_stream(const DecodeArgs &a0, hipStream_t stream) {
+  DecodeArgs a = a0;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+  }
+  // kStreamOcc resident workgroups of 4 waves per CU; no more waves than the longest-case tile count
+  const int64_t tiles_bound = (int64_t)a.batch * a.hkv * ((a.max_len + kTileTokens - 1) / kTileTokens);
+  int64_t blocks = std::min<int64_t>((int64_t)cus * kStreamOcc, kMaxStreamBlocks);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (tiles_bound + kWavesPerBlock - 1) / kWavesPerBlock));
+  a.stream_waves = (int)(blocks * kWavesPerBlock);
+  const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + sizeof(int) * (kWavesPerBlock + (size_t)a.batch + 1);
+  hipLaunchKernelGGL((decode_stream_kernel<D, kFP8>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock), lds, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const dim3 mgrid((unsigned)((int64_t)a.batch * a.hkv));
+  if (a.group <= 4)
+    hipLaunchKernelGGL((decode_merge_kernel<D, 4>), mgrid, dim3(64), 0, stream, a);
+  else if (a.group <= 8)
+    hipLaunchKernelGGL((decode_merge_kernel<D, 8>), mgrid, dim3(64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_merge_kernel<D, 16>), mgrid, dim3(64), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int D>
 hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
+  if (kind != CacheKind::kF32 && a.split_tokens == 0)
+    return kind == CacheKind::kFP8 ? launch_stream<D, true>(a, stream) : launch_stream<D, false>(a, stream);
   const dim3 grid(a.max_splits, a.hkv, a.batch);
   const dim3 block(64 * kWavesPerBlock);
   const size_t lds = sizeof(float) * (kWavesPerBlock * a.group * D + 2 * kWavesPerBlock * 16);

@@ -50,6 +50,9 @@ struct DecodeArgs {
   int64_t o_sb, o_sh;
   float *ws_o;   // [B][H_kv][max_splits][G][D] unnormalised partial outputs
   float *ws_ml;  // [B][H_kv][max_splits][G][2] (running max in log2 units, sum)
+                 // balanced partition (split_tokens == 0): [B * H_kv + kMaxStreamWaves][G][D] and [..][G][2]
+  int32_t *ws_prefix;  // balanced partition: per-sequence tile prefix [B + 1], written by the split kernel
+  int stream_waves;    // balanced partition: waves of the split kernel's grid (set by the launcher)
   int batch, hq, hkv, group, split_tokens, max_splits;
   int page_shift;    // paged pools: log2(page_size); the contiguous store is addressed linearly
   float scale_log2;  // sm_scale * log2(e)
@@ -66,5 +69,7 @@ inline int64_t num_splits(int64_t max_len, int64_t split_tokens) {
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kTileTokens = 32;  // tokens per wave iteration (two 16-row MFMA blocks)
+constexpr int kMaxStreamBlocks = 1024;  // balanced partition: grid cap (>= 3 workgroups on each of 256 CUs)
+constexpr int kMaxStreamWaves = kMaxStreamBlocks * kWavesPerBlock;
 
 }  // namespace tt
