@@ -231,6 +231,48 @@ int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_
 size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                  int64_t head_dim, int64_t max_seq_len, int64_t split_tokens);
 
+/*
+ * Decode-step layer operations: the dense work of a decode step around the
+ * attention path (projections, residual adds, RMSNorm, SwiGLU), for M rows
+ * (one token per sequence). bf16 activations and weights, fp32 accumulation
+ * and residual stream. Deterministic: split-K partials are summed in a fixed
+ * order by the operation that consumes them.
+ */
+
+/*
+ * partials[s][m][n] = sum over k in [s * k_chunk, (s + 1) * k_chunk) of
+ * x[m][k] * weight[n][k], s < K / k_chunk (fp32, [K / k_chunk, M, N]).
+ * Replaces nn.Linear(bias=False) under bf16 autocast for the projections
+ * q/k/v/c_proj (attn.py:141-145, 420-430), gate/up/down (mlp.py:24-26,
+ * 44-45); the rows of several projections of one input may be stacked into
+ * one weight (q|k|v, gate|up). x bf16 [M, K] (row stride ldx), weight bf16
+ * [N, K] (row stride ldw). Requirements: N % 64 == 0, K % k_chunk == 0,
+ * k_chunk in {256, 512}, 16-byte aligned pointers, strides multiples of 8.
+ */
+int tt_linear_splitk_bf16(const void *x, int64_t ldx, const void *weight, int64_t ldw, float *partials, int64_t m,
+                          int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream);
+
+/* y[m][n] = bf16(sum_s partials[s][m][n]) (the projection's bf16 output). */
+int tt_splitk_reduce_bf16(const float *partials, int64_t splits, int64_t m, int64_t n, void *y, tt_stream_t stream);
+
+/*
+ * Residual add + RMSNorm (gpt.py:40-41 + norm.py:6-19, eps as given):
+ * with partials (a projection's split-K output for this residual stream),
+ * x[m] += bf16(sum_s partials[s][m]) first; then
+ * y[m] = bf16(weight * (x[m] * rsqrt(mean(x[m]^2) + eps))), the normalised
+ * row as the next projection's bf16 input. partials may be NULL (plain
+ * RMSNorm). x, weight fp32; C % 1024 == 0, 1024 <= C <= 8192.
+ */
+int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const float *weight, float eps, void *y,
+                        int64_t m, int64_t c, tt_stream_t stream);
+
+/*
+ * SwiGLU of a stacked gate|up projection (mlp.py:44-45): with g, u the bf16
+ * sums of the partials of columns [0, I) and [I, 2I),
+ * y[m][i] = bf16(bf16(silu(g)) * u). partials [splits, M, 2I] fp32.
+ */
+int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t inter, void *y, tt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -158,3 +158,37 @@ def test_graph_replay_equals_eager(kv_dtype, sync_each_step):
     assert n0 == n1 == [n + 40 for n in lens]
     assert torch.equal(t0, t1)
     assert torch.equal(lp0, lp1)
+
+
+def test_fused_decode_step_matches_module_path():
+    """GPT.forward's fused bf16 decode step (stacked q|k|v and gate|up GEMMs,
+    fused residual add + RMSNorm, SwiGLU) against the module path on the same
+    caches: the appended K/V rows are identical in both caches when the
+    projections agree, and the logits agree to bf16 GEMM rounding."""
+    from tinytron_amd.cache import PagedKVCache
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=4,
+                     intermediate_size=2048, vocab_size=4096, block_size=256)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(17)
+    B, T = 3, 40
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(DEV)
+    nxt = torch.randint(0, cfg.vocab_size, (B, 1), generator=g).to(DEV)
+    outs = []
+    for fused in (False, True):
+        model.fused_decode = fused
+        cache = PagedKVCache.from_model_config(cfg, B, 16, DEV, torch.bfloat16, paged_pool=True, seq_capacity=[64] * B)
+        with torch.no_grad():
+            model(prompt, use_cache=True, past_key_values=cache, position_offset=0)
+            logits, _ = model(nxt, use_cache=True, past_key_values=cache, position_offset=T)
+        k, v = cache.get_layer_cache(1).gather(0, T + 1, torch.float32)
+        outs.append((logits.float().cpu(), k.cpu(), cache.get_layer_cache(0).seq_lens_host))
+    model.fused_decode = True
+    (l0, k0, n0), (l1, k1, n1) = outs
+    assert n0 == n1 == [T + 1] * B
+    assert torch.equal(k0[:, :, :T], k1[:, :, :T])           # prefill rows: same path
+    assert torch.allclose(k0[:, :, T], k1[:, :, T], rtol=2e-2, atol=2e-2)  # decode row: bf16 GEMMs of two libraries
+    scale = float(l0.abs().max())
+    assert float((l0 - l1).abs().max()) <= 0.05 * scale
+    assert torch.equal(l0.argmax(-1), l1.argmax(-1)) or float((l0 - l1).abs().max()) < 1e-2

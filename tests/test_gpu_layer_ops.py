@@ -1,0 +1,112 @@
+"""GPU: decode-step layer operations (skinny split-K GEMM, partial
+reductions, residual add + RMSNorm, SwiGLU) against fp64 / torch CPU
+references of the same math.
+
+* linear_partials: the sum of the partials equals x @ W^T up to fp32
+  accumulation error, bounded elementwise by 1e-5 * (|x| @ |W|^T) (K <= 6144
+  terms, fp32 epsilon 6e-8).
+* splitk_reduce_bf16 / the partial sums inside add_rmsnorm and silu_mul add
+  the splits in order 0, 1, ..., S-1 in fp32; the references do the same, so
+  those sums are compared bit for bit.
+* RMSNorm and SiLU outputs agree within one bf16 ulp (the rsqrt / exp of the
+  device and of the host may differ in the last fp32 bit).
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _seq_sum(P: torch.Tensor) -> torch.Tensor:
+    acc = P[0].clone()
+    for s in range(1, P.shape[0]):
+        acc = acc + P[s]
+    return acc
+
+
+def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> int:
+    ai = a.view(torch.int16).to(torch.int32)
+    bi = b.view(torch.int16).to(torch.int32)
+    return int((ai - bi).abs().max())
+
+
+@pytest.mark.parametrize("M,N,K,kc", [(1, 64, 512, 256), (7, 3072, 2048, 512), (64, 2048, 6144, 512),
+                                      (100, 128, 1024, 256), (64, 12288, 2048, 512)])
+def test_linear_partials(M, N, K, kc):
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(M + N + K)
+    x_full = torch.randn(M, K + 8, generator=g).to(torch.bfloat16)
+    x = x_full[:, :K]
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    x_dev = x_full.to(DEV)[:, :K]  # row stride K + 8
+    assert x_dev.stride(0) == K + 8
+    P = ops.linear_partials(x_dev, w.to(DEV), k_chunk=kc)
+    torch.cuda.synchronize()
+    assert P.shape == (K // kc, M, N)
+    got = P.double().sum(0).cpu()
+    xd, wd = x.double(), w.double()
+    ref = xd @ wd.T
+    bound = 1e-5 * (xd.abs() @ wd.abs().T) + 1e-30
+    assert torch.all((got - ref).abs() <= bound), float(((got - ref).abs() / bound).max())
+    # each split is the product over its own k chunk
+    s = K // kc - 1
+    ref_s = xd[:, s * kc:(s + 1) * kc] @ wd[:, s * kc:(s + 1) * kc].T
+    bound_s = 1e-5 * (xd[:, s * kc:(s + 1) * kc].abs() @ wd[:, s * kc:(s + 1) * kc].abs().T) + 1e-30
+    assert torch.all((P[s].double().cpu() - ref_s).abs() <= bound_s)
+
+
+def test_splitk_reduce_bit_exact():
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(3)
+    P = torch.randn(5, 33, 192, generator=g) * 10
+    got = ops.splitk_reduce_bf16(P.to(DEV)).cpu()
+    ref = _seq_sum(P).to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("C,with_partials", [(2048, True), (1024, False), (3072, True)])
+def test_add_rmsnorm(C, with_partials):
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(C)
+    M, S, eps = 37, 4, 1e-6
+    x = torch.randn(M, C, generator=g) * 3
+    w = torch.rand(C, generator=g) + 0.5
+    P = torch.randn(S, M, C, generator=g) if with_partials else None
+    xd = x.to(DEV)
+    y = ops.add_rmsnorm(xd, w.to(DEV), eps, partials=P.to(DEV) if with_partials else None).cpu()
+    x_ref = x + _seq_sum(P).to(torch.bfloat16).float() if with_partials else x
+    assert torch.equal(xd.cpu(), x_ref)  # the residual update is exact
+    xr = x_ref.double()
+    y_ref = (w.double() * (xr / torch.sqrt((xr * xr).mean(-1, keepdim=True) + eps))).float().to(torch.bfloat16)
+    assert _bf16_ulps(y, y_ref) <= 1
+
+
+def test_silu_mul():
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(5)
+    S, M, I = 3, 19, 6144
+    P = torch.randn(S, M, 2 * I, generator=g) * 2
+    got = ops.silu_mul(P.to(DEV)).cpu()
+    tot = _seq_sum(P)
+    gate = tot[:, :I].to(torch.bfloat16)
+    up = tot[:, I:].to(torch.bfloat16)
+    ref = (torch.nn.functional.silu(gate.float()).to(torch.bfloat16).float() * up.float()).to(torch.bfloat16)
+    assert _bf16_ulps(got, ref) <= 1
+
+
+def test_layer_ops_reject_bad_shapes():
+    from tinytron_amd import ops
+
+    x = torch.zeros(4, 100, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(64, 100, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        ops.linear_partials(x, w, k_chunk=256)  # K not a multiple of the chunk
+    with pytest.raises(ValueError):
+        ops.add_rmsnorm(torch.zeros(2, 1000, device=DEV), torch.ones(1000, device=DEV), 1e-6)

@@ -358,4 +358,71 @@ size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num
   return bal > fixed ? bal : fixed;
 }
 
+int tt_linear_splitk_bf16(const void *x, int64_t ldx, const void *weight, int64_t ldw, float *partials, int64_t m,
+                          int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream) {
+  TT_CHECK(x && weight && partials, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(m >= 0 && m <= 65535 * 64 && n > 0 && k > 0, TT_ERR_INVALID_ARGUMENT, "bad GEMM shape");
+  TT_CHECK(k_chunk == 256 || k_chunk == 512, TT_ERR_INVALID_ARGUMENT, "k_chunk must be 256 or 512, got %lld",
+           (long long)k_chunk);
+  TT_CHECK(n % 64 == 0 && k % k_chunk == 0, TT_ERR_UNSUPPORTED,
+           "N must be a multiple of 64 and K of k_chunk (N %lld, K %lld, k_chunk %lld)", (long long)n, (long long)k,
+           (long long)k_chunk);
+  TT_CHECK(n < ((int64_t)1 << 31) && k < ((int64_t)1 << 31), TT_ERR_UNSUPPORTED, "GEMM dimension too large");
+  TT_CHECK(ldx >= k && ldw >= k && ldx % 8 == 0 && ldw % 8 == 0, TT_ERR_INVALID_ARGUMENT,
+           "row strides must be >= K and multiples of 8 elements");
+  TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(partials, 16), TT_ERR_INVALID_ARGUMENT,
+           "x, weight and partials must be 16-byte aligned");
+  if (m == 0) return ok();
+  tt::SkinnyGemmArgs a{};
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = ldx;
+  a.w = static_cast<const uint16_t *>(weight);
+  a.ldw = ldw;
+  a.part = partials;
+  a.M = (int)m;
+  a.N = (int)n;
+  a.K = (int)k;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_skinny_gemm(a, (int)k_chunk, (hipStream_t)stream), "linear launch");
+}
+
+int tt_splitk_reduce_bf16(const float *partials, int64_t splits, int64_t m, int64_t n, void *y, tt_stream_t stream) {
+  TT_CHECK(partials && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(splits >= 1 && splits <= 4096 && m >= 0 && n > 0, TT_ERR_INVALID_ARGUMENT, "bad reduce shape");
+  TT_CHECK((m * n) % 4 == 0, TT_ERR_UNSUPPORTED, "M * N must be a multiple of 4");
+  TT_CHECK(aligned(partials, 16) && aligned(y, 8), TT_ERR_INVALID_ARGUMENT, "partials / y misaligned");
+  if (m == 0) return ok();
+  (void)hipGetLastError();
+  return from_hip(tt::launch_reduce_bf16(partials, (int)splits, m * n, static_cast<uint16_t *>(y), (hipStream_t)stream),
+                  "reduce launch");
+}
+
+int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const float *weight, float eps, void *y,
+                        int64_t m, int64_t c, tt_stream_t stream) {
+  TT_CHECK(x && weight && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(m >= 0 && m <= 0x7fffffff, TT_ERR_INVALID_ARGUMENT, "bad row count");
+  TT_CHECK(c % 1024 == 0 && c >= 1024 && c <= 8192, TT_ERR_UNSUPPORTED,
+           "hidden size must be a multiple of 1024 in [1024, 8192], got %lld", (long long)c);
+  TT_CHECK(partials == nullptr || (splits >= 1 && splits <= 4096), TT_ERR_INVALID_ARGUMENT, "bad split count");
+  TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(y, 8) && (partials == nullptr || aligned(partials, 16)),
+           TT_ERR_INVALID_ARGUMENT, "x / weight / partials must be 16-byte aligned, y 8-byte aligned");
+  if (m == 0) return ok();
+  (void)hipGetLastError();
+  return from_hip(tt::launch_add_rmsnorm(x, partials, partials ? (int)splits : 0, (int)m, (int)c, weight, eps,
+                                         static_cast<uint16_t *>(y), (hipStream_t)stream),
+                  "add_rmsnorm launch");
+}
+
+int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t inter, void *y, tt_stream_t stream) {
+  TT_CHECK(partials && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(splits >= 1 && splits <= 4096 && m >= 0 && inter > 0, TT_ERR_INVALID_ARGUMENT, "bad shape");
+  TT_CHECK(inter % 4 == 0 && inter < ((int64_t)1 << 30), TT_ERR_UNSUPPORTED, "intermediate size must be a multiple of 4");
+  TT_CHECK(aligned(partials, 16) && aligned(y, 8), TT_ERR_INVALID_ARGUMENT, "partials / y misaligned");
+  if (m == 0) return ok();
+  (void)hipGetLastError();
+  return from_hip(tt::launch_silu_mul(partials, (int)splits, (int)m, (int)inter, static_cast<uint16_t *>(y),
+                                      (hipStream_t)stream),
+                  "silu_mul launch");
+}
+
 }  // extern "C"

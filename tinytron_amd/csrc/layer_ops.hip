@@ -1,0 +1,214 @@
+// Decode-step layer kernels for gfx950: the dense work around the attention
+// path of one decode step (one token per sequence, M = batch rows).
+//
+//   skinny GEMM   P[s][m][n] = sum_{k in chunk s} x[m][k] * W[n][k]
+//                 (nn.Linear without bias, weights [N, K] bf16; the reference's
+//                 projections attn.py:141-145, mlp.py:24-26, gpt.py:62-63)
+//   reductions    the split-K partials are summed in a fixed order by the
+//                 kernel that consumes them, so results do not depend on
+//                 scheduling:
+//     reduce_bf16   y = bf16(sum_s P[s])                    (q/k/v projection)
+//     add_rmsnorm   x += bf16(sum_s P[s]); y = bf16(w * x * rsqrt(mean(x^2) + eps))
+//                   (residual add gpt.py:40-41 + RMSNorm norm.py:6-19)
+//     silu_mul      y = bf16(bf16(silu(bf16(sum_s P_gate))) * bf16(sum_s P_up))
+//                   (SwiGLU, mlp.py:44-45, with the bf16 rounding points of
+//                   the reference under autocast)
+//
+// The GEMM is weight-bandwidth bound (M <= 64 rows against K x N weights), so
+// it is organised around streaming W exactly once: a workgroup owns 64
+// output columns and one KC-wide chunk of K; each of its 4 waves loads its 16
+// weight rows x KC columns in one burst (all loads in flight together), while
+// the workgroup stages the x chunk (64 rows x KC) in LDS. The product runs on
+// v_mfma_f32_16x16x32_bf16 with W as the A operand (16 rows = output
+// columns) and x^T as the B operand (16 columns = batch rows).
+#include <algorithm>
+
+#include "tt_internal.h"
+#include "tt_numerics.h"
+
+namespace tt {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int KC>
+__global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(SkinnyGemmArgs a) {
+  constexpr int KSTEPS = KC / 32;
+  constexpr int ROW = KC + 8;  // padded LDS row (elements): 16 consecutive rows hit distinct banks
+  __shared__ __attribute__((aligned(16))) uint16_t xs[64 * ROW];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * 64 + wave * 16;
+  const int64_t k0 = (int64_t)blockIdx.y * KC;
+  const int m0 = blockIdx.z * 64;
+
+  // This wave's weight fragments for the whole chunk: lane (i + 16g) holds
+  // W[n0 + i][k0 + 32 s + 8 g .. + 8] for k step s.
+  const uint16_t *wrow = a.w + (int64_t)(n0 + (lane & 15)) * a.ldw + k0 + 8 * (lane >> 4);
+  u32x4 wf[KSTEPS];
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) wf[s] = *reinterpret_cast<const u32x4 *>(wrow + 32 * s);
+
+  // x rows m0 .. m0 + 63 of the chunk into LDS (rows past M are zero).
+  for (int i = threadIdx.x; i < 64 * (KC / 8); i += blockDim.x) {
+    const int r = i / (KC / 8);
+    const int c = i - r * (KC / 8);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (m0 + r < a.M) v = *reinterpret_cast<const u32x4 *>(a.x + (int64_t)(m0 + r) * a.ldx + k0 + 8 * c);
+    *reinterpret_cast<u32x4 *>(xs + r * ROW + 8 * c) = v;
+  }
+  __syncthreads();
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) {
+    const bf16x8 af = __builtin_bit_cast(bf16x8, wf[s]);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const bf16x8 bfr =
+          *reinterpret_cast<const bf16x8 *>(xs + (mb * 16 + (lane & 15)) * ROW + 32 * s + 8 * (lane >> 4));
+      acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, acc[mb], 0, 0, 0);
+    }
+  }
+
+  // acc[mb]: lane (j + 16g) holds out column n0 + 4g + r (r = 0..3) of batch row m0 + 16 mb + j.
+  float *P = a.part + (int64_t)blockIdx.y * a.M * a.N;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int m = m0 + mb * 16 + (lane & 15);
+    if (m < a.M) *reinterpret_cast<f32x4 *>(P + (int64_t)m * a.N + n0 + 4 * (lane >> 4)) = acc[mb];
+  }
+}
+
+// y[i] = bf16(sum_s P[s][i]), four elements per thread.
+__global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *P, int S, int64_t MN, uint16_t *y) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= MN) return;
+  f32x4 acc = *reinterpret_cast<const f32x4 *>(P + i);
+  for (int s = 1; s < S; ++s) acc += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN + i);
+  uint32_t lo = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
+  uint32_t hi = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
+  *reinterpret_cast<uint2 *>(y + i) = make_uint2(lo, hi);
+}
+
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float t = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return t;
+}
+
+// One workgroup per row m. With P != null the residual row first takes the
+// bf16-rounded sum of the partials (the projection's autocast output).
+template <int PER>  // float4 groups per thread: C = 1024 * PER
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float *P, int S, int64_t MN,
+                                                          const float *w, float eps, uint16_t *y, int C) {
+  __shared__ float red[4];
+  const int64_t row = (int64_t)blockIdx.x * C;
+  f32x4 v[PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = 4 * (threadIdx.x + 256 * j);
+    v[j] = *reinterpret_cast<const f32x4 *>(x + row + c);
+    if (P != nullptr) {
+      f32x4 d = *reinterpret_cast<const f32x4 *>(P + row + c);
+      for (int s = 1; s < S; ++s) d += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN + row + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[j][e] += round_bf16(d[e]);
+      *reinterpret_cast<f32x4 *>(x + row + c) = v[j];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += v[j][e] * v[j][e];
+  }
+  const float var = block_sum_256(ss, red) / (float)C;
+  const float r = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = 4 * (threadIdx.x + 256 * j);
+    const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
+    uint32_t lo = f32_to_bf16_bits(wv[0] * (v[j][0] * r)) | ((uint32_t)f32_to_bf16_bits(wv[1] * (v[j][1] * r)) << 16);
+    uint32_t hi = f32_to_bf16_bits(wv[2] * (v[j][2] * r)) | ((uint32_t)f32_to_bf16_bits(wv[3] * (v[j][3] * r)) << 16);
+    *reinterpret_cast<uint2 *>(y + row + c) = make_uint2(lo, hi);
+  }
+}
+
+// Partials of the fused gate|up projection: columns [0, I) gate, [I, 2I) up.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, int64_t MN2, int I, int M,
+                                                       uint16_t *y) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;  // index into [M, I]
+  if (i >= (int64_t)M * I) return;
+  const int64_t m = i / I;
+  const int64_t c = i - m * I;
+  const int64_t gi = m * 2 * I + c;
+  f32x4 g = *reinterpret_cast<const f32x4 *>(P + gi);
+  f32x4 u = *reinterpret_cast<const f32x4 *>(P + gi + I);
+  for (int s = 1; s < S; ++s) {
+    g += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN2 + gi);
+    u += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN2 + gi + I);
+  }
+  uint16_t out[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float gb = round_bf16(g[e]);
+    const float act = round_bf16(gb / (1.0f + expf(-gb)));
+    out[e] = f32_to_bf16_bits(act * round_bf16(u[e]));
+  }
+  *reinterpret_cast<uint2 *>(y + i) = make_uint2(out[0] | ((uint32_t)out[1] << 16), out[2] | ((uint32_t)out[3] << 16));
+}
+
+}  // namespace
+
+hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream) {
+  const dim3 grid((unsigned)(a.N / 64), (unsigned)(a.K / kc), (unsigned)((a.M + 63) / 64));
+  if (kc == 256)
+    hipLaunchKernelGGL((skinny_gemm_kernel<256>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<512>), grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_bf16(const float *P, int S, int64_t MN, uint16_t *y, hipStream_t stream) {
+  const int64_t threads = (MN + 3) / 4;
+  hipLaunchKernelGGL(reduce_bf16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, P, S, MN, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, const float *w, float eps, uint16_t *y,
+                              hipStream_t stream) {
+  const int64_t MN = (int64_t)M * C;
+#define TT_ADD_RMSNORM_CASE(n)                                                                           \
+  case n:                                                                                                \
+    hipLaunchKernelGGL((add_rmsnorm_kernel<n>), dim3(M), dim3(256), 0, stream, x, P, S, MN, w, eps, y, C); \
+    break;
+  switch (C / 1024) {  // C in {1024, 2048, ..., 8192}, checked by the caller
+    TT_ADD_RMSNORM_CASE(1)
+    TT_ADD_RMSNORM_CASE(2)
+    TT_ADD_RMSNORM_CASE(3)
+    TT_ADD_RMSNORM_CASE(4)
+    TT_ADD_RMSNORM_CASE(5)
+    TT_ADD_RMSNORM_CASE(6)
+    TT_ADD_RMSNORM_CASE(7)
+    TT_ADD_RMSNORM_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef TT_ADD_RMSNORM_CASE
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hipStream_t stream) {
+  const int64_t threads = ((int64_t)M * I + 3) / 4;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, P, S,
+                     (int64_t)M * 2 * I, I, M, y);
+  return hipGetLastError();
+}
+
+}  // namespace tt

@@ -58,6 +58,22 @@ struct DecodeArgs {
   float scale_log2;  // sm_scale * log2(e)
 };
 
+// Skinny GEMM of the decode step: partials P[K / kc][M][N] (fp32) of x[M, K] . W[N, K]^T.
+struct SkinnyGemmArgs {
+  const uint16_t *x;  // bf16 [M, K], row stride ldx
+  int64_t ldx;
+  const uint16_t *w;  // bf16 [N, K], row stride ldw
+  int64_t ldw;
+  float *part;
+  int M, N, K;
+};
+
+hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream);
+hipError_t launch_reduce_bf16(const float *P, int S, int64_t MN, uint16_t *y, hipStream_t stream);
+hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, const float *w, float eps, uint16_t *y,
+                              hipStream_t stream);
+hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hipStream_t stream);
+
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream);
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
 

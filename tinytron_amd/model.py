@@ -16,6 +16,14 @@ autocast produces from fp32 weights.
 package's caches, a decode step (T = 1) is one fused RoPE + KV-append kernel
 and one split-K GQA attention kernel; prefill (T > 1) writes the cache with
 the same append kernel and attends with SDPA per sequence. No CPU fallback.
+
+``GPT.forward`` runs a bf16 decode step (T = 1) as a fused layer sequence
+when the shapes allow it (``GPT.fused_decode``): per layer, one skinny
+split-K GEMM for the stacked q|k|v projection, its bf16 reduction, the
+RoPE + append and attention kernels, the c_proj GEMM, residual add + RMSNorm
+in one kernel, one GEMM for the stacked gate|up projection, SwiGLU, the
+down GEMM, and the next residual add + RMSNorm -- 11 launches instead of
+about 30, with the same math and bf16 rounding points as the module path.
 """
 from __future__ import annotations
 
@@ -220,6 +228,9 @@ class GPT(nn.Module):
         if not config.tied_lm_head:
             raise ValueError("only the tied lm_head of the reference's default config is supported")
         self._lm_head_weight = None
+        self.fused_decode = True   # bf16 decode steps through the fused layer kernels when shapes allow
+        self._stacked = {}         # layer -> (source key, q|k|v weight, gate|up weight)
+        self._decode_bufs = {}     # (device, rows) -> split-K partial buffer
 
     def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
         # reference checkpoints carry the tied lm_head as its own key (gpt.py:60-62)
@@ -234,6 +245,86 @@ class GPT(nn.Module):
             self._lm_head_weight = w
         return w
 
+    # -- fused bf16 decode step ------------------------------------------------------
+    @staticmethod
+    def _k_chunk(k: int) -> int:
+        return 512 if k % 512 == 0 else (256 if k % 256 == 0 else 0)
+
+    def _fused_decode_ok(self, cache, B: int) -> bool:
+        c = self.config
+        if not self.fused_decode or self.compute_dtype != torch.bfloat16 or not self.wte.weight.is_cuda:
+            return False
+        D = c.hidden_size // c.num_attention_heads
+        n_qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
+        return (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192 and n_qkv % 64 == 0
+                and (2 * c.intermediate_size) % 64 == 0 and self._k_chunk(c.hidden_size) > 0
+                and self._k_chunk(c.intermediate_size) > 0
+                and all(_is_fused_cache(cache.get_layer_cache(i)) for i in range(len(self.blocks))))
+
+    def _stacked_weights(self, i: int):
+        """q|k|v and gate|up weights of layer i stacked row-wise (rebuilt when a source changes)."""
+        blk = self.blocks[i]
+        srcs = (blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight,
+                blk.mlp.gate_proj.weight, blk.mlp.up_proj.weight)
+        key = tuple((t.data_ptr(), t._version) for t in srcs)
+        ent = self._stacked.get(i)
+        if ent is None or ent[0] != key:
+            with torch.no_grad():
+                ent = (key, torch.cat(srcs[:3]).contiguous(), torch.cat(srcs[3:]).contiguous())
+            self._stacked[i] = ent
+        return ent[1], ent[2]
+
+    def _partials(self, device, B: int) -> torch.Tensor:
+        c = self.config
+        D = c.hidden_size // c.num_attention_heads
+        n_qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
+        sizes = [(c.hidden_size // self._k_chunk(c.hidden_size)) * max(n_qkv, 2 * c.intermediate_size),
+                 (c.intermediate_size // self._k_chunk(c.intermediate_size)) * c.hidden_size]
+        need = B * max(sizes)
+        key = (str(device), B)
+        buf = self._decode_bufs.get(key)
+        if buf is None or buf.numel() < need:
+            buf = torch.empty(need, dtype=torch.float32, device=device)
+            self._decode_bufs[key] = buf
+        return buf
+
+    def _decode_step_fused(self, idx: torch.Tensor, cache, position_offset: int) -> torch.Tensor:
+        """One decode step (gpt.py:84-115 with attn.py:378-440, mlp.py:44-45,
+        norm.py:6-19 per layer) through the fused layer kernels; [B, 1, V] logits."""
+        c = self.config
+        B = idx.shape[0]
+        C, Hq, Hkv = c.hidden_size, c.num_attention_heads, c.num_key_value_heads
+        D = C // Hq
+        eps = self.lnf.variance_epsilon
+        kc_c, kc_i = self._k_chunk(C), self._k_chunk(c.intermediate_size)
+        first = cache.get_layer_cache(0)
+        lens = first.seq_lens_host
+        if len(set(lens)) == 1 and lens[0] != position_offset:
+            raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
+        table = rope_table_for(first.max_seq_len + 1, D, c.rope_theta, torch.bfloat16, idx.device)
+        pbuf = self._partials(idx.device, B)
+        x = self.wte(idx).view(B, C).float().contiguous()          # fp32 residual stream
+        h = ops.add_rmsnorm(x, self.blocks[0].ln_1.weight, eps)      # bf16 [B, C]
+        for i, blk in enumerate(self.blocks):
+            layer = cache.get_layer_cache(i)
+            wqkv, wgu = self._stacked_weights(i)
+            P = ops.linear_partials(h, wqkv, partials=pbuf, k_chunk=kc_c)
+            qkv = ops.splitk_reduce_bf16(P)                          # [B, (Hq + 2 Hkv) D]
+            q = qkv[:, :Hq * D].view(B, 1, Hq, D).transpose(1, 2)
+            k = qkv[:, Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D).transpose(1, 2)
+            v = qkv[:, (Hq + Hkv) * D:].view(B, 1, Hkv, D).transpose(1, 2)
+            q_rot = layer.rope_append(q, k, v, table)
+            y = layer.attend(q_rot.view(B, Hq, D))                   # [B, Hq, D]
+            P = ops.linear_partials(y.view(B, C), blk.attn.c_proj.weight, partials=pbuf, k_chunk=kc_c)
+            h = ops.add_rmsnorm(x, blk.ln_2.weight, eps, partials=P)
+            P = ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_c)
+            a = ops.silu_mul(P)                                      # [B, I]
+            P = ops.linear_partials(a, blk.mlp.down_proj.weight, partials=pbuf, k_chunk=kc_i)
+            nxt = self.blocks[i + 1].ln_1.weight if i + 1 < len(self.blocks) else self.lnf.weight
+            h = ops.add_rmsnorm(x, nxt, eps, partials=P)             # residual add + next norm (or lnf)
+        logits = F.linear(h, self.lm_head_weight())
+        return logits.view(B, 1, -1)
+
     def forward(self, idx: torch.Tensor, targets=None, past_key_values=None, use_cache: bool = False,
                 position_offset: int = 0, logits_index: torch.Tensor | None = None):
         """gpt.py:84-115. ``logits_index`` ([B], optional, prefill only)
@@ -241,10 +332,13 @@ class GPT(nn.Module):
         all T."""
         B, T = idx.size()
         assert T <= self.config.block_size, f"Cannot forward sequence of length {T}, block size is only {self.config.block_size}"
-        x = self.wte(idx)
         paged_cache = past_key_values if hasattr(past_key_values, "get_layer_cache") else None
         if paged_cache is None:
             raise TypeError("tinytron_amd.GPT runs with a tinytron_amd PagedKVCache")
+        if T == 1 and logits_index is None and targets is None and self._fused_decode_ok(paged_cache, B):
+            logits = self._decode_step_fused(idx, paged_cache, position_offset)
+            return (logits, paged_cache) if use_cache else logits
+        x = self.wte(idx)
         for layer_idx, block in enumerate(self.blocks):
             x, _, _ = block(x, past_kv=paged_cache.get_layer_cache(layer_idx), use_cache=use_cache,
                             position_offset=position_offset)

@@ -221,3 +221,84 @@ def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, 
         st = lib.tt_gqa_decode_attn_f32(*head, *tail)
     _lib.check(st, "decode_attention")
     return out
+
+
+# -- decode-step layer operations ----------------------------------------------------------
+
+def _rows(t: torch.Tensor, name: str) -> tuple:
+    """(rows, row stride) of a 2-D row-major view (last dim contiguous)."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D view with a contiguous last dimension")
+    return t.shape[0], t.stride(0)
+
+
+def linear_partials(x: torch.Tensor, weight: torch.Tensor, partials: torch.Tensor | None = None,
+                    k_chunk: int = 512) -> torch.Tensor:
+    """Split-K partials [K / k_chunk, M, N] (fp32) of x [M, K] @ weight[N, K]^T (bf16).
+
+    nn.Linear(bias=False) under bf16 autocast (attn.py:141-145, mlp.py:24-26)
+    for M <= a few hundred rows; sum the partials with splitk_reduce_bf16 or
+    a consuming op (add_rmsnorm, silu_mul)."""
+    _require_cuda(x, weight)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("linear_partials takes bf16 x and weight")
+    M, ldx = _rows(x, "x")
+    N, ldw = _rows(weight, "weight")
+    K = x.shape[1]
+    if weight.shape[1] != K:
+        raise ValueError(f"x has K = {K}, weight has {weight.shape[1]}")
+    S = K // k_chunk
+    if partials is None:
+        partials = torch.empty(S, M, N, dtype=torch.float32, device=x.device)
+    elif partials.dtype != torch.float32 or partials.numel() < S * M * N or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 buffer of at least K / k_chunk * M * N elements")
+    _lib.check(_lib.load().tt_linear_splitk_bf16(_ptr(x), ldx, _ptr(weight), ldw, _ptr(partials), M, N, K, k_chunk,
+                                                   _stream(x.device)), "linear_partials")
+    return partials.view(-1)[:S * M * N].view(S, M, N)
+
+
+def splitk_reduce_bf16(partials: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(sum over the first axis) of fp32 partials [S, M, N]."""
+    _require_cuda(partials)
+    S, M, N = partials.shape
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=partials.device)
+    if not out.is_contiguous() or out.shape != (M, N) or out.dtype != torch.bfloat16:
+        raise ValueError("out must be a contiguous bf16 [M, N] tensor")
+    _lib.check(_lib.load().tt_splitk_reduce_bf16(_ptr(partials), S, M, N, _ptr(out), _stream(partials.device)),
+               "splitk_reduce_bf16")
+    return out
+
+
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, partials: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """x += bf16(sum of partials) (in place, if given); returns bf16 RMSNorm(x) [M, C].
+
+    The residual add of Block.forward (gpt.py:40-41) fused with the next
+    RMSNorm (norm.py:6-19)."""
+    _require_cuda(x, weight)
+    if x.dtype != torch.float32 or weight.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("add_rmsnorm takes a contiguous fp32 residual x [M, C] and fp32 weight [C]")
+    M, C = x.shape
+    S = 0
+    if partials is not None:
+        S = partials.shape[0]
+        if partials.shape[1:] != (M, C) or not partials.is_contiguous():
+            raise ValueError("partials must be contiguous [S, M, C]")
+    if out is None:
+        out = torch.empty(M, C, dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().tt_add_rmsnorm_bf16(_ptr(x), _ptr(partials), S, _ptr(weight), float(eps), _ptr(out), M, C,
+                                                 _stream(x.device)), "add_rmsnorm")
+    return out
+
+
+def silu_mul(partials: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(bf16(silu(g)) * u) from partials [S, M, 2I] of a stacked gate|up projection (mlp.py:44-45)."""
+    _require_cuda(partials)
+    S, M, I2 = partials.shape
+    inter = I2 // 2
+    if out is None:
+        out = torch.empty(M, inter, dtype=torch.bfloat16, device=partials.device)
+    _lib.check(_lib.load().tt_silu_mul_bf16(_ptr(partials), S, M, inter, _ptr(out), _stream(partials.device)),
+               "silu_mul")
+    return out
