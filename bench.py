@@ -38,6 +38,9 @@ CONFIGS = {
                lo=128, hi=16384, page=16, paged=True, fp8=False),
     "c4": dict(name="C4 ragged paged fp8-e4m3 GQA decode step", batch=128, hq=32, hkv=8, head_dim=128,
                lo=1024, hi=32768, page=16, paged=True, fp8=True),
+    # one layer's attention of the C5 model mid-decode (prompts U[64, 2048] + 128 generated tokens)
+    "c5a": dict(name="C5 per-layer ragged paged bf16 GQA decode step (D 64)", batch=64, hq=32, hkv=8, head_dim=64,
+                lo=192, hi=2176, page=16, paged=True, fp8=False),
 }
 
 

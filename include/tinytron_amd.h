@@ -247,10 +247,22 @@ size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num
  * 44-45); the rows of several projections of one input may be stacked into
  * one weight (q|k|v, gate|up). x bf16 [M, K] (row stride ldx), weight bf16
  * [N, K] (row stride ldw). Requirements: N % 64 == 0, K % k_chunk == 0,
- * k_chunk in {256, 512}, 16-byte aligned pointers, strides multiples of 8.
+ * k_chunk in {256, 512, 1024}, 16-byte aligned pointers, strides multiples
+ * of 8.
  */
 int tt_linear_splitk_bf16(const void *x, int64_t ldx, const void *weight, int64_t ldw, float *partials, int64_t m,
                           int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream);
+
+/*
+ * As tt_linear_splitk_bf16 with the weight in fragment order: element
+ * W[n][k] at index ((n / 16) * (K / 32) + k / 32) * 512 + ((k % 32) / 8) * 128
+ * + (n % 16) * 8 + k % 8, i.e. W.view(N/16, 16, K/32, 4, 8).permute(0, 2, 3,
+ * 1, 4) made contiguous, so each 32-wide k step of a 16-row block is one
+ * contiguous 1 KB read. (Layout of this library; no counterpart in the
+ * reference.)
+ */
+int tt_linear_splitk_packed_bf16(const void *x, int64_t ldx, const void *weight_packed, float *partials, int64_t m,
+                                 int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream);
 
 /* y[m][n] = bf16(sum_s partials[s][m][n]) (the projection's bf16 output). */
 int tt_splitk_reduce_bf16(const float *partials, int64_t splits, int64_t m, int64_t n, void *y, tt_stream_t stream);

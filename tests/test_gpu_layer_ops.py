@@ -34,7 +34,7 @@ def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> int:
 
 
 @pytest.mark.parametrize("M,N,K,kc", [(1, 64, 512, 256), (7, 3072, 2048, 512), (64, 2048, 6144, 512),
-                                      (100, 128, 1024, 256), (64, 12288, 2048, 512)])
+                                      (100, 128, 1024, 256), (64, 12288, 2048, 512), (64, 3072, 2048, 1024), (37, 2048, 6144, 1024), (100, 128, 1024, 1024)])
 def test_linear_partials(M, N, K, kc):
     from tinytron_amd import ops
 
@@ -57,6 +57,23 @@ def test_linear_partials(M, N, K, kc):
     ref_s = xd[:, s * kc:(s + 1) * kc] @ wd[:, s * kc:(s + 1) * kc].T
     bound_s = 1e-5 * (xd[:, s * kc:(s + 1) * kc].abs() @ wd[:, s * kc:(s + 1) * kc].abs().T) + 1e-30
     assert torch.all((P[s].double().cpu() - ref_s).abs() <= bound_s)
+
+
+@pytest.mark.parametrize("kc", [256, 512, 1024])
+def test_linear_partials_packed_equals_row_major(kc):
+    """The fragment-ordered weight gives the row-major kernel's partials bit
+    for bit (same fragments, same MFMA sequence), and packing round-trips."""
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(kc)
+    M, N, K = 45, 192, 2048
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = torch.randn(N, K, generator=g).to(torch.bfloat16).to(DEV)
+    pw = ops.PackedWeight(w)
+    assert torch.equal(pw.unpack(), w)
+    a = ops.linear_partials(x, w, k_chunk=kc).clone()
+    b = ops.linear_partials(x, pw, k_chunk=kc)
+    assert torch.equal(a, b)
 
 
 def test_splitk_reduce_bit_exact():

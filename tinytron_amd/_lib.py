@@ -61,6 +61,7 @@ SIGNATURES = {
     "tt_decode_split_tokens": ([_i64, _i64, _i64], ctypes.c_int64),
     "tt_decode_workspace_bytes": ([_i64, _i64, _i64, _i64, _i64, _i64], ctypes.c_size_t),
     "tt_linear_splitk_bf16": ([_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp], ctypes.c_int),
+    "tt_linear_splitk_packed_bf16": ([_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp], ctypes.c_int),
     "tt_splitk_reduce_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_add_rmsnorm_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
     "tt_silu_mul_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),

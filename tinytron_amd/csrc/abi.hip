@@ -258,6 +258,34 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   return from_hip(tt::launch_decode_attn(a, kind, (int)head_dim, (hipStream_t)stream), "decode attention launch");
 }
 
+int linear_common(const void *x, int64_t ldx, const void *weight, int64_t ldw, int packed, float *partials,
+                  int64_t m, int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream) {
+  TT_CHECK(x && weight && partials, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(m >= 0 && m <= 65535 * 64 && n > 0 && k > 0, TT_ERR_INVALID_ARGUMENT, "bad GEMM shape");
+  TT_CHECK(k_chunk == 256 || k_chunk == 512 || k_chunk == 1024, TT_ERR_INVALID_ARGUMENT,
+           "k_chunk must be 256, 512 or 1024, got %lld", (long long)k_chunk);
+  TT_CHECK(n % 64 == 0 && k % k_chunk == 0, TT_ERR_UNSUPPORTED,
+           "N must be a multiple of 64 and K of k_chunk (N %lld, K %lld, k_chunk %lld)", (long long)n, (long long)k,
+           (long long)k_chunk);
+  TT_CHECK(n < ((int64_t)1 << 31) && k < ((int64_t)1 << 31), TT_ERR_UNSUPPORTED, "GEMM dimension too large");
+  TT_CHECK(ldx >= k && ldw >= k && ldx % 8 == 0 && ldw % 8 == 0, TT_ERR_INVALID_ARGUMENT,
+           "row strides must be >= K and multiples of 8 elements");
+  TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(partials, 16), TT_ERR_INVALID_ARGUMENT,
+           "x, weight and partials must be 16-byte aligned");
+  if (m == 0) return ok();
+  tt::SkinnyGemmArgs a{};
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = ldx;
+  a.w = static_cast<const uint16_t *>(weight);
+  a.ldw = ldw;
+  a.part = partials;
+  a.M = (int)m;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.packed = packed;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_skinny_gemm(a, (int)k_chunk, (hipStream_t)stream), "linear launch");
+}
 }  // namespace
 
 extern "C" {
@@ -360,31 +388,15 @@ size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num
 
 int tt_linear_splitk_bf16(const void *x, int64_t ldx, const void *weight, int64_t ldw, float *partials, int64_t m,
                           int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream) {
-  TT_CHECK(x && weight && partials, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
-  TT_CHECK(m >= 0 && m <= 65535 * 64 && n > 0 && k > 0, TT_ERR_INVALID_ARGUMENT, "bad GEMM shape");
-  TT_CHECK(k_chunk == 256 || k_chunk == 512, TT_ERR_INVALID_ARGUMENT, "k_chunk must be 256 or 512, got %lld",
-           (long long)k_chunk);
-  TT_CHECK(n % 64 == 0 && k % k_chunk == 0, TT_ERR_UNSUPPORTED,
-           "N must be a multiple of 64 and K of k_chunk (N %lld, K %lld, k_chunk %lld)", (long long)n, (long long)k,
-           (long long)k_chunk);
-  TT_CHECK(n < ((int64_t)1 << 31) && k < ((int64_t)1 << 31), TT_ERR_UNSUPPORTED, "GEMM dimension too large");
-  TT_CHECK(ldx >= k && ldw >= k && ldx % 8 == 0 && ldw % 8 == 0, TT_ERR_INVALID_ARGUMENT,
-           "row strides must be >= K and multiples of 8 elements");
-  TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(partials, 16), TT_ERR_INVALID_ARGUMENT,
-           "x, weight and partials must be 16-byte aligned");
-  if (m == 0) return ok();
-  tt::SkinnyGemmArgs a{};
-  a.x = static_cast<const uint16_t *>(x);
-  a.ldx = ldx;
-  a.w = static_cast<const uint16_t *>(weight);
-  a.ldw = ldw;
-  a.part = partials;
-  a.M = (int)m;
-  a.N = (int)n;
-  a.K = (int)k;
-  (void)hipGetLastError();
-  return from_hip(tt::launch_skinny_gemm(a, (int)k_chunk, (hipStream_t)stream), "linear launch");
+  return linear_common(x, ldx, weight, ldw, 0, partials, m, n, k, k_chunk, stream);
 }
+
+int tt_linear_splitk_packed_bf16(const void *x, int64_t ldx, const void *weight_packed, float *partials, int64_t m,
+                                 int64_t n, int64_t k, int64_t k_chunk, tt_stream_t stream) {
+  return linear_common(x, ldx, weight_packed, k, 1, partials, m, n, k, k_chunk, stream);
+}
+
+
 
 int tt_splitk_reduce_bf16(const float *partials, int64_t splits, int64_t m, int64_t n, void *y, tt_stream_t stream) {
   TT_CHECK(partials && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");

@@ -657,13 +657,16 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[h][j] = 0.f;
   }
+  // With W >= NW every wave holds at least one tile, so every wave of w0..w1
+  // holds a piece; only otherwise is a wave's range tested (64-bit divisions).
+  const bool every_wave = W >= NW;
   for (int64_t wb = w0; wb <= w1; wb += kGroup) {
     bool on[kGroup];
     float mv[kGroup][kMaxG], lv[kGroup][kMaxG], ov[kGroup][kMaxG][DPL];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
       const int64_t w = wb + u;
-      on[u] = w <= w1 && wave_first_tile(w, W, NW) < wave_first_tile(w + 1, W, NW);  // uniform
+      on[u] = w <= w1 && (every_wave || wave_first_tile(w, W, NW) < wave_first_tile(w + 1, W, NW));  // uniform
       const int64_t sk = seg + (on[u] ? w : w0);  // slot w0 always holds a piece
 #pragma unroll
       for (int h = 0; h < kMaxG; ++h) {

@@ -15,10 +15,11 @@
 //                   the reference under autocast)
 //
 // The GEMM is weight-bandwidth bound (M <= 64 rows against K x N weights), so
-// it is organised around streaming W exactly once: a workgroup owns 64
-// output columns and one KC-wide chunk of K; each of its 4 waves loads its 16
-// weight rows x KC columns in one burst (all loads in flight together), while
-// the workgroup stages the x chunk (64 rows x KC) in LDS. The product runs on
+// it is organised around streaming W exactly once, spread over every CU (a
+// CU alone draws only a few tens of GB/s): a workgroup owns 64 or 128 output
+// columns and one KC-wide chunk of K; each of its waves loads its 16 weight
+// rows x KC columns in one burst (all loads in flight together), while the
+// workgroup stages the x chunk (64 rows x KC) in LDS. The product runs on
 // v_mfma_f32_16x16x32_bf16 with W as the A operand (16 rows = output
 // columns) and x^T as the B operand (16 columns = batch rows).
 #include <algorithm>
@@ -33,23 +34,38 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int KC>
-__global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(SkinnyGemmArgs a) {
+// Weight fragment of k step s of 16-row block nb, starting at column k (a
+// multiple of 32): lane (i + 16g) reads W[16 nb + i][k + 32 s + 8 g .. + 8].
+// Row-major weights: base + 32 s. Packed weights ([N/16][K/32][64 lanes][8],
+// the fragment order) make every k step one contiguous 1 KB: base + 512 s.
+__device__ __forceinline__ const uint16_t *wfrag_base(const SkinnyGemmArgs &a, int nb, int64_t k, int lane,
+                                                      int &step) {
+  if (a.packed) {
+    step = 512;
+    return a.w + (((int64_t)nb * (a.K / 32) + k / 32) * 64 + lane) * 8;
+  }
+  step = 32;
+  return a.w + (int64_t)(nb * 16 + (lane & 15)) * a.ldw + k + 8 * (lane >> 4);
+}
+
+template <int KC, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void skinny_gemm_kernel(SkinnyGemmArgs a) {
   constexpr int KSTEPS = KC / 32;
   constexpr int ROW = KC + 8;  // padded LDS row (elements): 16 consecutive rows hit distinct banks
   __shared__ __attribute__((aligned(16))) uint16_t xs[64 * ROW];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 64 + wave * 16;
+  const int n0 = blockIdx.x * (16 * WAVES) + wave * 16;
   const int64_t k0 = (int64_t)blockIdx.y * KC;
   const int m0 = blockIdx.z * 64;
 
   // This wave's weight fragments for the whole chunk: lane (i + 16g) holds
   // W[n0 + i][k0 + 32 s + 8 g .. + 8] for k step s.
-  const uint16_t *wrow = a.w + (int64_t)(n0 + (lane & 15)) * a.ldw + k0 + 8 * (lane >> 4);
+  int wstep;
+  const uint16_t *wrow = wfrag_base(a, n0 / 16, k0, lane, wstep);
   u32x4 wf[KSTEPS];
 #pragma unroll
-  for (int s = 0; s < KSTEPS; ++s) wf[s] = *reinterpret_cast<const u32x4 *>(wrow + 32 * s);
+  for (int s = 0; s < KSTEPS; ++s) wf[s] = *reinterpret_cast<const u32x4 *>(wrow + wstep * s);
 
   // x rows m0 .. m0 + 63 of the chunk into LDS (rows past M are zero).
   for (int i = threadIdx.x; i < 64 * (KC / 8); i += blockDim.x) {
@@ -84,12 +100,30 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(SkinnyGemmArgs a) {
   }
 }
 
+// sum_{s < S} P[s * stride + i] added in order s = 0, 1, ..., four loads
+// issued ahead of their adds (the order of the additions is unchanged).
+__device__ __forceinline__ f32x4 ordered_sum4(const float *P, int S, int64_t stride, int64_t i) {
+  f32x4 d = *reinterpret_cast<const f32x4 *>(P + i);
+  int s = 1;
+  for (; s + 4 <= S; s += 4) {
+    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(P + (int64_t)s * stride + i);
+    const f32x4 a1 = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s + 1) * stride + i);
+    const f32x4 a2 = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s + 2) * stride + i);
+    const f32x4 a3 = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s + 3) * stride + i);
+    d += a0;
+    d += a1;
+    d += a2;
+    d += a3;
+  }
+  for (; s < S; ++s) d += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * stride + i);
+  return d;
+}
+
 // y[i] = bf16(sum_s P[s][i]), four elements per thread.
 __global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *P, int S, int64_t MN, uint16_t *y) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= MN) return;
-  f32x4 acc = *reinterpret_cast<const f32x4 *>(P + i);
-  for (int s = 1; s < S; ++s) acc += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN + i);
+  const f32x4 acc = ordered_sum4(P, S, MN, i);
   uint32_t lo = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
   uint32_t hi = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
   *reinterpret_cast<uint2 *>(y + i) = make_uint2(lo, hi);
@@ -119,8 +153,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
     const int c = 4 * (threadIdx.x + 256 * j);
     v[j] = *reinterpret_cast<const f32x4 *>(x + row + c);
     if (P != nullptr) {
-      f32x4 d = *reinterpret_cast<const f32x4 *>(P + row + c);
-      for (int s = 1; s < S; ++s) d += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN + row + c);
+      const f32x4 d = ordered_sum4(P, S, MN, row + c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[j][e] += round_bf16(d[e]);
       *reinterpret_cast<f32x4 *>(x + row + c) = v[j];
@@ -148,12 +181,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
   const int64_t m = i / I;
   const int64_t c = i - m * I;
   const int64_t gi = m * 2 * I + c;
-  f32x4 g = *reinterpret_cast<const f32x4 *>(P + gi);
-  f32x4 u = *reinterpret_cast<const f32x4 *>(P + gi + I);
-  for (int s = 1; s < S; ++s) {
-    g += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN2 + gi);
-    u += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN2 + gi + I);
-  }
+  const f32x4 g = ordered_sum4(P, S, MN2, gi);
+  const f32x4 u = ordered_sum4(P, S, MN2, gi + I);
   uint16_t out[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -167,11 +196,25 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
 }  // namespace
 
 hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.N / 64), (unsigned)(a.K / kc), (unsigned)((a.M + 63) / 64));
-  if (kc == 256)
-    hipLaunchKernelGGL((skinny_gemm_kernel<256>), grid, dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((skinny_gemm_kernel<512>), grid, dim3(256), 0, stream, a);
+  // 8 waves (128 weight rows) share one staged x chunk when that still gives
+  // every CU a workgroup; otherwise 4 waves (64 rows)
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+  }
+  const int splits = a.K / kc, mt = (a.M + 63) / 64;
+  const bool wide = a.N % 128 == 0 && (int64_t)(a.N / 128) * splits * mt >= cus;
+  const dim3 grid((unsigned)(a.N / (wide ? 128 : 64)), (unsigned)splits, (unsigned)mt);
+#define TT_GEMM_LAUNCH(KC, W) hipLaunchKernelGGL((skinny_gemm_kernel<KC, W>), grid, dim3(64 * W), 0, stream, a)
+  if (kc == 256) {
+    if (wide) TT_GEMM_LAUNCH(256, 8); else TT_GEMM_LAUNCH(256, 4);
+  } else if (kc == 512) {
+    if (wide) TT_GEMM_LAUNCH(512, 8); else TT_GEMM_LAUNCH(512, 4);
+  } else {
+    if (wide) TT_GEMM_LAUNCH(1024, 8); else TT_GEMM_LAUNCH(1024, 4);
+  }
+#undef TT_GEMM_LAUNCH
   return hipGetLastError();
 }
 

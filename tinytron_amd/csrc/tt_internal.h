@@ -66,6 +66,7 @@ struct SkinnyGemmArgs {
   int64_t ldw;
   float *part;
   int M, N, K;
+  int packed;  // weights in fragment order [N/16][K/32][64][8] (ldw unused)
 };
 
 hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream);

@@ -250,6 +250,11 @@ class GPT(nn.Module):
     def _k_chunk(k: int) -> int:
         return 512 if k % 512 == 0 else (256 if k % 256 == 0 else 0)
 
+    @staticmethod
+    def _k_chunk_small(k: int) -> int:
+        """Split for the square c_proj GEMM: more, shorter splits keep every CU streaming."""
+        return 256 if k % 256 == 0 else 0
+
     def _fused_decode_ok(self, cache, B: int) -> bool:
         c = self.config
         if not self.fused_decode or self.compute_dtype != torch.bfloat16 or not self.wte.weight.is_cuda:
@@ -258,27 +263,31 @@ class GPT(nn.Module):
         n_qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
         return (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192 and n_qkv % 64 == 0
                 and (2 * c.intermediate_size) % 64 == 0 and self._k_chunk(c.hidden_size) > 0
-                and self._k_chunk(c.intermediate_size) > 0
+                and self._k_chunk_small(c.hidden_size) > 0 and self._k_chunk(c.intermediate_size) > 0
                 and all(_is_fused_cache(cache.get_layer_cache(i)) for i in range(len(self.blocks))))
 
     def _stacked_weights(self, i: int):
-        """q|k|v and gate|up weights of layer i stacked row-wise (rebuilt when a source changes)."""
+        """Layer i's decode GEMM weights in the kernels' fragment order: q|k|v
+        and gate|up stacked row-wise, c_proj, down (rebuilt when a source
+        parameter changes: its storage or its in-place version counter)."""
         blk = self.blocks[i]
-        srcs = (blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight,
-                blk.mlp.gate_proj.weight, blk.mlp.up_proj.weight)
+        srcs = (blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight, blk.attn.c_proj.weight,
+                blk.mlp.gate_proj.weight, blk.mlp.up_proj.weight, blk.mlp.down_proj.weight)
         key = tuple((t.data_ptr(), t._version) for t in srcs)
         ent = self._stacked.get(i)
         if ent is None or ent[0] != key:
             with torch.no_grad():
-                ent = (key, torch.cat(srcs[:3]).contiguous(), torch.cat(srcs[3:]).contiguous())
+                ent = (key, ops.PackedWeight(torch.cat(srcs[:3])), ops.PackedWeight(srcs[3]),
+                       ops.PackedWeight(torch.cat(srcs[4:6])), ops.PackedWeight(srcs[6]))
             self._stacked[i] = ent
-        return ent[1], ent[2]
+        return ent[1:]
 
     def _partials(self, device, B: int) -> torch.Tensor:
         c = self.config
         D = c.hidden_size // c.num_attention_heads
         n_qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
         sizes = [(c.hidden_size // self._k_chunk(c.hidden_size)) * max(n_qkv, 2 * c.intermediate_size),
+                 (c.hidden_size // self._k_chunk_small(c.hidden_size)) * c.hidden_size,
                  (c.intermediate_size // self._k_chunk(c.intermediate_size)) * c.hidden_size]
         need = B * max(sizes)
         key = (str(device), B)
@@ -296,7 +305,7 @@ class GPT(nn.Module):
         C, Hq, Hkv = c.hidden_size, c.num_attention_heads, c.num_key_value_heads
         D = C // Hq
         eps = self.lnf.variance_epsilon
-        kc_c, kc_i = self._k_chunk(C), self._k_chunk(c.intermediate_size)
+        kc_c, kc_i, kc_o = self._k_chunk(C), self._k_chunk(c.intermediate_size), self._k_chunk_small(C)
         first = cache.get_layer_cache(0)
         lens = first.seq_lens_host
         if len(set(lens)) == 1 and lens[0] != position_offset:
@@ -307,7 +316,7 @@ class GPT(nn.Module):
         h = ops.add_rmsnorm(x, self.blocks[0].ln_1.weight, eps)      # bf16 [B, C]
         for i, blk in enumerate(self.blocks):
             layer = cache.get_layer_cache(i)
-            wqkv, wgu = self._stacked_weights(i)
+            wqkv, wo, wgu, wd = self._stacked_weights(i)
             P = ops.linear_partials(h, wqkv, partials=pbuf, k_chunk=kc_c)
             qkv = ops.splitk_reduce_bf16(P)                          # [B, (Hq + 2 Hkv) D]
             q = qkv[:, :Hq * D].view(B, 1, Hq, D).transpose(1, 2)
@@ -315,11 +324,11 @@ class GPT(nn.Module):
             v = qkv[:, (Hq + Hkv) * D:].view(B, 1, Hkv, D).transpose(1, 2)
             q_rot = layer.rope_append(q, k, v, table)
             y = layer.attend(q_rot.view(B, Hq, D))                   # [B, Hq, D]
-            P = ops.linear_partials(y.view(B, C), blk.attn.c_proj.weight, partials=pbuf, k_chunk=kc_c)
+            P = ops.linear_partials(y.view(B, C), wo, partials=pbuf, k_chunk=kc_o)
             h = ops.add_rmsnorm(x, blk.ln_2.weight, eps, partials=P)
             P = ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_c)
             a = ops.silu_mul(P)                                      # [B, I]
-            P = ops.linear_partials(a, blk.mlp.down_proj.weight, partials=pbuf, k_chunk=kc_i)
+            P = ops.linear_partials(a, wd, partials=pbuf, k_chunk=kc_i)
             nxt = self.blocks[i + 1].ln_1.weight if i + 1 < len(self.blocks) else self.lnf.weight
             h = ops.add_rmsnorm(x, nxt, eps, partials=P)             # residual add + next norm (or lnf)
         logits = F.linear(h, self.lm_head_weight())

@@ -232,28 +232,57 @@ def _rows(t: torch.Tensor, name: str) -> tuple:
     return t.shape[0], t.stride(0)
 
 
-def linear_partials(x: torch.Tensor, weight: torch.Tensor, partials: torch.Tensor | None = None,
+class PackedWeight:
+    """A [N, K] bf16 weight in the GEMM's fragment order ([N/16][K/32][64][8])."""
+
+    def __init__(self, weight: torch.Tensor):
+        N, K = weight.shape
+        if N % 16 or K % 32:
+            raise ValueError("packing needs N % 16 == 0 and K % 32 == 0")
+        self.shape = (N, K)
+        self.data = weight.detach().reshape(N // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous()
+
+    def unpack(self) -> torch.Tensor:
+        N, K = self.shape
+        return self.data.permute(0, 3, 1, 2, 4).reshape(N, K)
+
+
+def linear_partials(x: torch.Tensor, weight, partials: torch.Tensor | None = None,
                     k_chunk: int = 512) -> torch.Tensor:
     """Split-K partials [K / k_chunk, M, N] (fp32) of x [M, K] @ weight[N, K]^T (bf16).
 
     nn.Linear(bias=False) under bf16 autocast (attn.py:141-145, mlp.py:24-26)
     for M <= a few hundred rows; sum the partials with splitk_reduce_bf16 or
-    a consuming op (add_rmsnorm, silu_mul)."""
-    _require_cuda(x, weight)
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    a consuming op (add_rmsnorm, silu_mul). ``weight`` is a bf16 tensor or a
+    PackedWeight."""
+    packed = isinstance(weight, PackedWeight)
+    wt = weight.data if packed else weight
+    _require_cuda(x, wt)
+    if x.dtype != torch.bfloat16 or wt.dtype != torch.bfloat16:
         raise ValueError("linear_partials takes bf16 x and weight")
     M, ldx = _rows(x, "x")
-    N, ldw = _rows(weight, "weight")
+    if packed:
+        N, Kw = weight.shape
+        ldw = Kw
+    else:
+        N, ldw = _rows(weight, "weight")
+        Kw = weight.shape[1]
     K = x.shape[1]
-    if weight.shape[1] != K:
-        raise ValueError(f"x has K = {K}, weight has {weight.shape[1]}")
+    if Kw != K:
+        raise ValueError(f"x has K = {K}, weight has {Kw}")
     S = K // k_chunk
     if partials is None:
         partials = torch.empty(S, M, N, dtype=torch.float32, device=x.device)
     elif partials.dtype != torch.float32 or partials.numel() < S * M * N or not partials.is_contiguous():
         raise ValueError("partials must be a contiguous fp32 buffer of at least K / k_chunk * M * N elements")
-    _lib.check(_lib.load().tt_linear_splitk_bf16(_ptr(x), ldx, _ptr(weight), ldw, _ptr(partials), M, N, K, k_chunk,
-                                                   _stream(x.device)), "linear_partials")
+    lib = _lib.load()
+    if packed:
+        st = lib.tt_linear_splitk_packed_bf16(_ptr(x), ldx, _ptr(wt), _ptr(partials), M, N, K, k_chunk,
+                                              _stream(x.device))
+    else:
+        st = lib.tt_linear_splitk_bf16(_ptr(x), ldx, _ptr(wt), ldw, _ptr(partials), M, N, K, k_chunk,
+                                       _stream(x.device))
+    _lib.check(st, "linear_partials")
     return partials.view(-1)[:S * M * N].view(S, M, N)
 
 
