@@ -638,16 +638,29 @@ __device__ __forceinline__ void stream_block_addr(const DecodeArgs &a, int b, in
   elem = uniform64(e);
 }
 
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
 // Merge the pieces of segment (b, hk) held by waves w0..w1 (waves with empty
 // ranges hold none) and write its G output rows:
-// out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p, lane = head_dim column.
-// Pieces go kGroup at a time with every load of a group issued before any
-// arithmetic, so a segment of up to kGroup pieces costs one memory round trip.
+// out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p.
+// Up to 64 pieces at a time: lane k loads piece k's maxima and sums for every
+// head (one vector load each, all in flight together), the batch maximum and
+// weighted sum come from wave reductions, and the partial rows are summed with
+// lane = head_dim column, four pieces' loads issued ahead of their adds.
 template <int D, int kMaxG>
 __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk, int64_t seg, int64_t w0, int64_t w1,
                                               int64_t W, int64_t NW, int lane) {
   constexpr int DPL = D / 64;
-  constexpr int kGroup = 64 / (kMaxG * DPL) > 0 ? 64 / (kMaxG * DPL) : 1;
   const int G = a.group;  // <= kMaxG
   float M[kMaxG], Ls[kMaxG], acc[kMaxG][DPL];
 #pragma unroll
@@ -660,44 +673,51 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
   // With W >= NW every wave holds at least one tile, so every wave of w0..w1
   // holds a piece; only otherwise is a wave's range tested (64-bit divisions).
   const bool every_wave = W >= NW;
-  for (int64_t wb = w0; wb <= w1; wb += kGroup) {
-    bool on[kGroup];
-    float mv[kGroup][kMaxG], lv[kGroup][kMaxG], ov[kGroup][kMaxG][DPL];
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      const int64_t w = wb + u;
-      on[u] = w <= w1 && (every_wave || wave_first_tile(w, W, NW) < wave_first_tile(w + 1, W, NW));  // uniform
-      const int64_t sk = seg + (on[u] ? w : w0);  // slot w0 always holds a piece
-#pragma unroll
-      for (int h = 0; h < kMaxG; ++h) {
-        if (h < G) {
-          mv[u][h] = a.ws_ml[(sk * G + h) * 2];
-          lv[u][h] = a.ws_ml[(sk * G + h) * 2 + 1];
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) ov[u][h][j] = a.ws_o[(sk * G + h) * D + lane + 64 * j];
-        }
-      }
-    }
+  for (int64_t wb = w0; wb <= w1; wb += 64) {
+    const int64_t w = wb + lane;
+    const bool valid = w <= w1 && (every_wave || wave_first_tile(w, W, NW) < wave_first_tile(w + 1, W, NW));
+    const int64_t slot = seg + (valid ? w : w0);  // slot w0 always holds a piece
+    float e[kMaxG];
 #pragma unroll
     for (int h = 0; h < kMaxG; ++h) {
+      e[h] = 0.f;
       if (h < G) {
-        float m_new = M[h];
-#pragma unroll
-        for (int u = 0; u < kGroup; ++u) m_new = on[u] ? fmaxf(m_new, mv[u][h]) : m_new;
-        const float sc = __builtin_amdgcn_exp2f(M[h] - m_new);  // m_new finite: slot w0 is in the first group
-        Ls[h] *= sc;
+        const float m = valid ? a.ws_ml[(slot * G + h) * 2] : kNegInf;
+        const float l = a.ws_ml[(slot * G + h) * 2 + 1];
+        const float m_new = fmaxf(M[h], wave_max(m));  // finite: wave w0 holds a piece
+        const float sc = __builtin_amdgcn_exp2f(M[h] - m_new);
+        e[h] = valid ? __builtin_amdgcn_exp2f(m - m_new) : 0.f;
+        Ls[h] = Ls[h] * sc + wave_sum(valid ? e[h] * l : 0.f);
 #pragma unroll
         for (int j = 0; j < DPL; ++j) acc[h][j] *= sc;
+        M[h] = m_new;
+      }
+    }
+    const int nk = (int)(w1 - wb + 1 < 64 ? w1 - wb + 1 : 64);
+    for (int k0 = 0; k0 < nk; k0 += 4) {
+      float ov[4][kMaxG][DPL];
 #pragma unroll
-        for (int u = 0; u < kGroup; ++u) {
-          if (on[u]) {
-            const float e = __builtin_amdgcn_exp2f(mv[u][h] - m_new);
-            Ls[h] += e * lv[u][h];
+      for (int u = 0; u < 4; ++u) {
+        const int k = k0 + u < nk ? k0 + u : nk - 1;  // repeats are read with weight 0 below
+        const int64_t sk = seg + __builtin_amdgcn_readlane((int)(slot - seg), k);
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) acc[h][j] += e * ov[u][h][j];
+        for (int h = 0; h < kMaxG; ++h)
+          if (h < G)
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) ov[u][h][j] = a.ws_o[(sk * G + h) * D + lane + 64 * j];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (k0 + u < nk) {  // uniform
+#pragma unroll
+          for (int h = 0; h < kMaxG; ++h) {
+            if (h < G) {
+              const float ek = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e[h]), k0 + u));
+#pragma unroll
+              for (int j = 0; j < DPL; ++j) acc[h][j] += ek * ov[u][h][j];
+            }
           }
         }
-        M[h] = m_new;
       }
     }
   }
