@@ -145,6 +145,42 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
                        int64_t page_size, tt_stream_t stream);
 
 /*
+ * As tt_rope_append_bf16 / tt_rope_append_fp8, with q, k and v read from the
+ * fp32 split-K partials of their projection (tt_linear_splitk*_bf16): each
+ * input element is bf16(sum over s < splits of in[s * split_stride + i]),
+ * added in order -- the projection's bf16 output, so the cache bytes equal
+ * those of tt_splitk_reduce_bf16 followed by tt_rope_append_*. Strides are
+ * in fp32 elements within one split. (Fuses the projection's reduction into
+ * the append; no counterpart in the reference.)
+ */
+int tt_rope_append_partials_bf16(const float *q_in, const int64_t q_in_strides[3],
+                                 const float *k_in, const int64_t k_in_strides[3],
+                                 const float *v_in, const int64_t v_in_strides[3],
+                                 int64_t splits, int64_t split_stride,
+                                 void *q_out, const int64_t q_out_strides[3],
+                                 const void *rope_table, int64_t rope_table_len,
+                                 const int32_t *positions, const int32_t *new_lens, int32_t *lens_out,
+                                 const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                                 void *k_cache, void *v_cache, const int64_t cache_strides[3],
+                                 int64_t capacity, int64_t batch, int64_t num_new,
+                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t page_size, tt_stream_t stream);
+
+int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3],
+                                const float *k_in, const int64_t k_in_strides[3],
+                                const float *v_in, const int64_t v_in_strides[3],
+                                int64_t splits, int64_t split_stride,
+                                void *q_out, const int64_t q_out_strides[3],
+                                const void *rope_table, int64_t rope_table_len,
+                                const int32_t *positions, const int32_t *new_lens, int32_t *lens_out,
+                                const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                                void *k_cache, void *v_cache, float *k_scale, float *v_scale,
+                                const int64_t cache_strides[3],
+                                int64_t capacity, int64_t batch, int64_t num_new,
+                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                int64_t page_size, tt_stream_t stream);
+
+/*
  * GQA decode attention over a ragged batch, bf16 cache, split-K
  * (flash-decoding) with a merge pass.
  *

@@ -28,7 +28,7 @@ def _bits(t: "torch.Tensor") -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False):
+def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False, from_partials=False):
     from tinytron_amd import ops
 
     rng = np.random.default_rng(seed)
@@ -56,6 +56,17 @@ def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False):
     else:
         q, k, v = _to_dev_bf16(qb), _to_dev_bf16(kb), _to_dev_bf16(vb)
     q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    if from_partials:
+        # q|k|v as 3 fp32 split-K partials [S, B, (Hq + 2 Hkv) D]; the inputs the
+        # oracle sees are bf16(partial 0 + partial 1 + partial 2), added in order
+        assert T == 1 and kind != "f32"
+        N = (Hq + 2 * Hkv) * D
+        parts = (rng.standard_normal((3, B, N)) * 1.5).astype(np.float32)
+        tot = (parts[0] + parts[1]) + parts[2]
+        proj = bf16_bits_to_f32(f32_to_bf16_bits(tot)).reshape(B, 1, N)
+        qf = proj[:, :, :Hq * D].reshape(B, 1, Hq, D)
+        kf = proj[:, :, Hq * D:(Hq + Hkv) * D].reshape(B, 1, Hkv, D)
+        vf = proj[:, :, (Hq + Hkv) * D:].reshape(B, 1, Hkv, D)
     table = ops.build_rope_table(128, D, dtype=act, device=DEV)
     table_np = table.float().cpu().numpy()
 
@@ -82,7 +93,10 @@ def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False):
     )
     pos_t = torch.from_numpy(positions).to(DEV)
     nl_t = torch.from_numpy(new_lens).to(DEV) if ragged_new else None
-    q_out = ops.rope_append(q, k, v, table, pos_t, kv, new_lens=nl_t)
+    if from_partials:
+        q_out = ops.rope_append_partials(torch.from_numpy(parts).to(DEV), Hq, table, pos_t, kv)
+    else:
+        q_out = ops.rope_append(q, k, v, table, pos_t, kv, new_lens=nl_t)
     torch.cuda.synchronize()
 
     # ---- oracle ----
@@ -139,6 +153,16 @@ def test_rope_append_decode(kind, paged, D):
 @pytest.mark.parametrize("paged", [False, True])
 def test_rope_append_prefill_ragged(kind, paged):
     _case(kind, paged, 128, T=9, seed=5, ragged_new=True)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_append_from_split_k_partials(kind, paged, D):
+    """q|k|v taken from the stacked projection's fp32 split-K partials: the
+    kernel's in-order sum rounded to bf16 gives the same rotated q and cache
+    bytes as the oracle on those rounded values."""
+    _case(kind, paged, D, 1, seed=300 + D + paged, from_partials=True)
 
 
 def test_rope_table_matches_closed_form():

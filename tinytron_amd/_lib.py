@@ -37,6 +37,16 @@ _ROPE_TAIL = [
     _vp,                                             # stream
 ]
 
+_ROPE_PART_HEAD = [
+    _vp, _i64p, _vp, _i64p, _vp, _i64p,              # q_in, k_in, v_in partials (+ strides)
+    _i64, _i64,                                      # splits, split_stride
+    _vp, _i64p,                                      # q_out (+ strides)
+    _vp, _i64,                                       # rope_table, rope_table_len
+    _i32p, _i32p, _i32p,                             # positions, new_lens, lens_out
+    _i32p, _i64, _i64,                               # page_table, max_pages, num_pages
+    _vp, _vp,                                        # k_cache, v_cache
+]
+
 _ATTN_HEAD = [_vp, _i64p, _vp, _vp]                  # q, q_strides, k_cache, v_cache
 _ATTN_TAIL = [
     _i64p,                                           # cache_strides
@@ -55,6 +65,8 @@ SIGNATURES = {
     "tt_rope_append_bf16": (_ROPE_COMMON + _ROPE_TAIL, ctypes.c_int),
     "tt_rope_append_f32": (_ROPE_COMMON + _ROPE_TAIL, ctypes.c_int),
     "tt_rope_append_fp8": (_ROPE_COMMON + [_vp, _vp] + _ROPE_TAIL, ctypes.c_int),
+    "tt_rope_append_partials_bf16": (_ROPE_PART_HEAD + _ROPE_TAIL, ctypes.c_int),
+    "tt_rope_append_partials_fp8": (_ROPE_PART_HEAD + [_vp, _vp] + _ROPE_TAIL, ctypes.c_int),
     "tt_gqa_decode_attn_bf16": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
     "tt_gqa_decode_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ATTN_TAIL, ctypes.c_int),
     "tt_gqa_decode_attn_f32": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),

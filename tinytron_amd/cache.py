@@ -130,6 +130,17 @@ class _LayerCacheBase:
         self._host_lens = [a + b for a, b in zip(self._host_lens, adds)]
         return q_rot
 
+    def rope_append_partials(self, partials: torch.Tensor, num_q_heads: int, rope_table: torch.Tensor) -> torch.Tensor:
+        """One-token rope_append whose q|k|v are the split-K partials [S, B, N]
+        of the stacked q|k|v projection (summed and rounded inside the kernel)."""
+        self._check_room([1] * self.batch_size)
+        nxt = 1 - self._cur
+        q_rot = ops.rope_append_partials(partials, num_q_heads, rope_table, self._lens_dev[self._cur], self.layout,
+                                         lens_out=self._lens_dev[nxt])
+        self._cur = nxt
+        self._host_lens = [a + 1 for a in self._host_lens]
+        return q_rot
+
     def attend(self, q: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """GQA decode attention of q [B, H_q, D] over every cached token of each sequence."""
         if self.workspace is None:

@@ -64,9 +64,13 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
                        int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
                        float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
                        int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                       int64_t page_size, tt_stream_t stream) {
+                       int64_t page_size, tt_stream_t stream, int64_t part_splits = 0, int64_t part_stride = 0) {
   TT_CHECK(q_in && k_in && v_in && q_out && rope_table && positions && k_cache && v_cache, TT_ERR_INVALID_ARGUMENT,
            "a required pointer is NULL");
+  TT_CHECK(part_splits >= 0 && part_splits <= 4096 && (part_splits == 0 || part_stride > 0), TT_ERR_INVALID_ARGUMENT,
+           "bad split-K partial description");
+  TT_CHECK(part_splits == 0 || kind != tt::CacheKind::kF32, TT_ERR_UNSUPPORTED,
+           "split-K partial inputs are for bf16 activations");
   TT_CHECK(q_in_strides && k_in_strides && v_in_strides && q_out_strides, TT_ERR_INVALID_ARGUMENT,
            "a stride array is NULL");
   TT_CHECK(batch >= 0 && num_new >= 0, TT_ERR_INVALID_ARGUMENT, "batch and num_new must be >= 0");
@@ -125,6 +129,8 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
   a.hkv = (int)num_kv_heads;
   a.head_dim = (int)head_dim;
   a.page_size = (int)page_size;
+  a.part_splits = (int)part_splits;
+  a.part_stride = part_stride;
   (void)hipGetLastError();
   return from_hip(tt::launch_rope_append(a, kind, (hipStream_t)stream), "rope_append launch");
 }
@@ -334,6 +340,38 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3], const vo
                             q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table, max_pages,
                             num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch, num_new,
                             num_q_heads, num_kv_heads, head_dim, page_size, stream);
+}
+
+int tt_rope_append_partials_bf16(const float *q_in, const int64_t q_in_strides[3], const float *k_in,
+                                 const int64_t k_in_strides[3], const float *v_in, const int64_t v_in_strides[3],
+                                 int64_t splits, int64_t split_stride, void *q_out, const int64_t q_out_strides[3],
+                                 const void *rope_table, int64_t rope_table_len, const int32_t *positions,
+                                 const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table,
+                                 int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache,
+                                 const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
+                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                 tt_stream_t stream) {
+  TT_CHECK(splits >= 1, TT_ERR_INVALID_ARGUMENT, "splits must be >= 1");
+  return rope_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table,
+                            max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides, capacity, batch,
+                            num_new, num_q_heads, num_kv_heads, head_dim, page_size, stream, splits, split_stride);
+}
+
+int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3], const float *k_in,
+                                const int64_t k_in_strides[3], const float *v_in, const int64_t v_in_strides[3],
+                                int64_t splits, int64_t split_stride, void *q_out, const int64_t q_out_strides[3],
+                                const void *rope_table, int64_t rope_table_len, const int32_t *positions,
+                                const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table,
+                                int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
+                                float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
+                                int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                int64_t page_size, tt_stream_t stream) {
+  TT_CHECK(splits >= 1, TT_ERR_INVALID_ARGUMENT, "splits must be >= 1");
+  return rope_append_common(tt::CacheKind::kFP8, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides, q_out,
+                            q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table,
+                            max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch,
+                            num_new, num_q_heads, num_kv_heads, head_dim, page_size, stream, splits, split_stride);
 }
 
 int tt_gqa_decode_attn_bf16(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,

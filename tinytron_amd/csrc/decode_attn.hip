@@ -654,13 +654,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 // ranges hold none) and write its G output rows:
 // out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p.
 // Up to 64 pieces at a time: lane k loads piece k's maxima and sums for every
-// head (one vector load each, all in flight together), the batch maximum and
-// weighted sum come from wave reductions, and the partial rows are summed with
-// lane = head_dim column, four pieces' loads issued ahead of their adds.
+// head (one vector load each), the batch maximum and weighted sum come from
+// wave reductions, and the partial rows are summed with lane = head_dim
+// column, kBatch pieces' loads ahead of their adds. The first row batch is
+// loaded together with the maxima and sums, so a segment of up to kBatch
+// pieces costs one memory round trip after the prefix.
 template <int D, int kMaxG>
 __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk, int64_t seg, int64_t w0, int64_t w1,
                                               int64_t W, int64_t NW, int lane) {
   constexpr int DPL = D / 64;
+  constexpr int kBatch = 64 / (kMaxG * DPL) < 2 ? 2 : (64 / (kMaxG * DPL) > 16 ? 16 : 64 / (kMaxG * DPL));
   const int G = a.group;  // <= kMaxG
   float M[kMaxG], Ls[kMaxG], acc[kMaxG][DPL];
 #pragma unroll
@@ -676,7 +679,23 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
   for (int64_t wb = w0; wb <= w1; wb += 64) {
     const int64_t w = wb + lane;
     const bool valid = w <= w1 && (every_wave || wave_first_tile(w, W, NW) < wave_first_tile(w + 1, W, NW));
-    const int64_t slot = seg + (valid ? w : w0);  // slot w0 always holds a piece
+    const int slot_rel = (int)(valid ? w - w0 : 0);  // slot = seg + w0 + slot_rel; slot w0 always holds a piece
+    const int nk = (int)(w1 - wb + 1 < 64 ? w1 - wb + 1 : 64);
+    float ov[kBatch][kMaxG][DPL];
+    auto load_rows = [&](int k0) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int k = k0 + u < nk ? k0 + u : nk - 1;  // repeats are added with weight 0 below
+        const int64_t sk = seg + w0 + __builtin_amdgcn_readlane(slot_rel, k);
+#pragma unroll
+        for (int h = 0; h < kMaxG; ++h)
+          if (h < G)
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) ov[u][h][j] = a.ws_o[(sk * G + h) * D + lane + 64 * j];
+      }
+    };
+    load_rows(0);
+    const int64_t slot = seg + w0 + slot_rel;
     float e[kMaxG];
 #pragma unroll
     for (int h = 0; h < kMaxG; ++h) {
@@ -693,21 +712,10 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
         M[h] = m_new;
       }
     }
-    const int nk = (int)(w1 - wb + 1 < 64 ? w1 - wb + 1 : 64);
-    for (int k0 = 0; k0 < nk; k0 += 4) {
-      float ov[4][kMaxG][DPL];
+    for (int k0 = 0; k0 < nk; k0 += kBatch) {
+      if (k0 > 0) load_rows(k0);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = k0 + u < nk ? k0 + u : nk - 1;  // repeats are read with weight 0 below
-        const int64_t sk = seg + __builtin_amdgcn_readlane((int)(slot - seg), k);
-#pragma unroll
-        for (int h = 0; h < kMaxG; ++h)
-          if (h < G)
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) ov[u][h][j] = a.ws_o[(sk * G + h) * D + lane + 64 * j];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kBatch; ++u) {
         if (k0 + u < nk) {  // uniform
 #pragma unroll
           for (int h = 0; h < kMaxG; ++h) {

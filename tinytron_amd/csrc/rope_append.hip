@@ -81,7 +81,21 @@ __device__ __forceinline__ int64_t slot_offset(const RopeAppendArgs &a, int b, i
   return base + (int64_t)hk * a.c_head + slot * a.head_dim;
 }
 
-template <typename A, bool kFP8>
+// An input element: the activation at p[i], or with split-K partials the
+// activation-typed sum of the splits added in order (the projection's output).
+template <typename A, bool kPart>
+__device__ __forceinline__ float load_in(const RopeAppendArgs &a, const void *p, int64_t i) {
+  if constexpr (kPart) {
+    const float *f = static_cast<const float *>(p);
+    float acc = f[i];
+    for (int s = 1; s < a.part_splits; ++s) acc += f[(int64_t)s * a.part_stride + i];
+    return Elem<A>::rnd(acc);
+  } else {
+    return Elem<A>::load(p, i);
+  }
+}
+
+template <typename A, bool kFP8, bool kPart>
 __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const int row = blockIdx.x;
   const int t = blockIdx.y;
@@ -105,8 +119,8 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   if (row < a.hq) {
     if (!active) return;
     const int64_t src = (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st;
-    const float x1 = Elem<A>::load(a.q_in, src + i);
-    const float x2 = Elem<A>::load(a.q_in, src + half + i);
+    const float x1 = load_in<A, kPart>(a, a.q_in, src + i);
+    const float x2 = load_in<A, kPart>(a, a.q_in, src + half + i);
     float o1, o2;
     rotate_pair<A>(x1, x2, c, s, o1, o2);
     const int64_t dst = (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh + (int64_t)t * a.qo_st;
@@ -123,9 +137,9 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   if (active) {
     const int64_t ks = (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
     const int64_t vs = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh + (int64_t)t * a.vi_st;
-    rotate_pair<A>(Elem<A>::load(a.k_in, ks + i), Elem<A>::load(a.k_in, ks + half + i), c, s, k1, k2);
-    v1 = Elem<A>::load(a.v_in, vs + i);
-    v2 = Elem<A>::load(a.v_in, vs + half + i);
+    rotate_pair<A>(load_in<A, kPart>(a, a.k_in, ks + i), load_in<A, kPart>(a, a.k_in, ks + half + i), c, s, k1, k2);
+    v1 = load_in<A, kPart>(a, a.v_in, vs + i);
+    v2 = load_in<A, kPart>(a, a.v_in, vs + half + i);
   }
 
   if constexpr (!kFP8) {
@@ -161,15 +175,22 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
   const dim3 grid(a.hq + a.hkv, a.num_new > 0 ? a.num_new : 1, a.batch);
   const dim3 block(64);
+  const bool part = a.part_splits > 0;  // bf16 activations only (checked by the caller)
   switch (kind) {
     case CacheKind::kBF16:
-      hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false>), grid, block, 0, stream, a);
+      if (part)
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, false>), grid, block, 0, stream, a);
       break;
     case CacheKind::kF32:
-      hipLaunchKernelGGL((rope_append_kernel<float, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((rope_append_kernel<float, false, false>), grid, block, 0, stream, a);
       break;
     case CacheKind::kFP8:
-      hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true>), grid, block, 0, stream, a);
+      if (part)
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, false>), grid, block, 0, stream, a);
       break;
   }
   return hipGetLastError();

@@ -32,6 +32,10 @@ struct RopeAppendArgs {
   int64_t c_seq, c_page, c_head;
   int64_t capacity;
   int batch, num_new, hq, hkv, head_dim, page_size;
+  // q_in / k_in / v_in point into fp32 split-K partials (split stride part_stride
+  // elements) when part_splits > 0: each input is bf16(sum of the splits, in order)
+  int part_splits;
+  int64_t part_stride;
 };
 
 struct DecodeArgs {

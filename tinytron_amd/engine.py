@@ -12,9 +12,12 @@ past_key_values=cache, position_offset=...)``; positions come from the
 cache's per-sequence lengths, so there is no host synchronisation in the
 loop (the reference syncs once per layer at attn.py:395).
 
-With ``use_graphs`` (default) the one-token model call is captured in HIP
-graphs after the first decode step and replayed for the rest, which removes
-the per-kernel launch cost (a decode step is a few hundred small kernels).
+With ``use_graphs`` the one-token model call is captured in HIP graphs
+after the first decode step and replayed for the rest, which removes the
+per-kernel launch cost. By default (``None``) graphs are used only when the
+model runs its module-by-module decode step (about 30 launches per layer);
+the fused bf16 step (10 per layer) keeps the GPU busy from the host alone,
+and replay measured no faster than eager launches there.
 The caches keep their lengths in two device buffers that swap every step, so
 two graphs are captured, one per buffer parity. The attention launch bound is
 fixed at the largest sequence capacity for the whole decode loop, so the
@@ -70,7 +73,7 @@ class InferenceEngine:
     def __init__(self, model_config: ModelConfig, checkpoint_path: str | None = None, device: str = "cuda",
                  dtype: torch.dtype = torch.bfloat16, use_paged_kv_cache: bool = True, kv_cache_page_size: int = 128,
                  kv_cache_dtype: torch.dtype | None = None, paged_pool: bool = False, page_seed: int = 1337,
-                 model: GPT | None = None, use_graphs: bool = True):
+                 model: GPT | None = None, use_graphs: bool | None = None):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("the tinytron_amd engine runs on the GPU (no CPU fallback)")
@@ -136,6 +139,9 @@ class InferenceEngine:
         cur = lens_t.clone()
         uniform = len(set(lens)) == 1
         graphs = None
+        use_graphs = self.use_graphs
+        if use_graphs is None:
+            use_graphs = not (hasattr(self.model, "_fused_decode_ok") and self.model._fused_decode_ok(cache, batch_size))
         cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
         for step in range(max_new_tokens):
@@ -150,7 +156,7 @@ class InferenceEngine:
             if eos_token_id is not None and torch.all(next_token == eos_token_id):
                 break
             position = (lens[0] + step) if uniform else 0
-            if graphs is None and self.use_graphs and step >= 1 and max_new_tokens - step >= 3:
+            if graphs is None and use_graphs and step >= 1 and max_new_tokens - step >= 3:
                 graphs = DecodeGraphs(self.model, cache, batch_size, position, uniform, self.device)
             if graphs is not None:
                 logits = graphs.step(next_token)

@@ -19,11 +19,12 @@ the same append kernel and attends with SDPA per sequence. No CPU fallback.
 
 ``GPT.forward`` runs a bf16 decode step (T = 1) as a fused layer sequence
 when the shapes allow it (``GPT.fused_decode``): per layer, one skinny
-split-K GEMM for the stacked q|k|v projection, its bf16 reduction, the
-RoPE + append and attention kernels, the c_proj GEMM, residual add + RMSNorm
-in one kernel, one GEMM for the stacked gate|up projection, SwiGLU, the
-down GEMM, and the next residual add + RMSNorm -- 11 launches instead of
-about 30, with the same math and bf16 rounding points as the module path.
+split-K GEMM for the stacked q|k|v projection, the
+RoPE + append kernel (which sums those partials itself), the attention
+kernels, the c_proj GEMM, residual add + RMSNorm in one kernel, one GEMM for
+the stacked gate|up projection, SwiGLU, the down GEMM, and the next residual
+add + RMSNorm -- 10 launches instead of about 30, with the same math and
+bf16 rounding points as the module path.
 """
 from __future__ import annotations
 
@@ -318,11 +319,7 @@ class GPT(nn.Module):
             layer = cache.get_layer_cache(i)
             wqkv, wo, wgu, wd = self._stacked_weights(i)
             P = ops.linear_partials(h, wqkv, partials=pbuf, k_chunk=kc_c)
-            qkv = ops.splitk_reduce_bf16(P)                          # [B, (Hq + 2 Hkv) D]
-            q = qkv[:, :Hq * D].view(B, 1, Hq, D).transpose(1, 2)
-            k = qkv[:, Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D).transpose(1, 2)
-            v = qkv[:, (Hq + Hkv) * D:].view(B, 1, Hkv, D).transpose(1, 2)
-            q_rot = layer.rope_append(q, k, v, table)
+            q_rot = layer.rope_append_partials(P, Hq, table)         # sums the q|k|v partials itself
             y = layer.attend(q_rot.view(B, Hq, D))                   # [B, Hq, D]
             P = ops.linear_partials(y.view(B, C), wo, partials=pbuf, k_chunk=kc_o)
             h = ops.add_rmsnorm(x, blk.ln_2.weight, eps, partials=P)

@@ -151,6 +151,48 @@ def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.
     return q_out
 
 
+def rope_append_partials(partials: torch.Tensor, num_q_heads: int, table: torch.Tensor, positions: torch.Tensor,
+                         layout: KVLayout, q_out: torch.Tensor | None = None,
+                         lens_out: torch.Tensor | None = None) -> torch.Tensor:
+    """rope_append for one new token per sequence whose q|k|v come as the fp32
+    split-K partials [S, B, (H_q + 2 H_kv) D] of the stacked projection: the
+    kernel sums the splits in order and rounds to bf16 (the projection's
+    output) before RoPE + append. Returns rotated q [B, H_q, 1, D] (bf16)."""
+    _require_cuda(partials, table, positions, layout.k, layout.v)
+    if partials.dtype != torch.float32 or partials.dim() != 3 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 [S, B, N] tensor")
+    S, B, N = partials.shape
+    Hkv, D = layout.num_heads, layout.head_dim
+    if N != (num_q_heads + 2 * Hkv) * D:
+        raise ValueError(f"partials have {N} columns, expected (H_q + 2 H_kv) * D = {(num_q_heads + 2 * Hkv) * D}")
+    if table.dtype != torch.bfloat16 or table.dim() != 2 or table.shape[1] != D or not table.is_contiguous():
+        raise ValueError("rope table must be a contiguous bf16 [positions, head_dim] tensor")
+    if layout.kind not in ("bf16", "fp8"):
+        raise ValueError("split-K partial inputs are for bf16 activations (bf16 or fp8 cache)")
+    if positions.dtype != torch.int32 or positions.shape != (B,):
+        raise ValueError("positions must be int32 [B]")
+    if lens_out is not None and (lens_out.dtype != torch.int32 or lens_out.shape != (B,)):
+        raise ValueError("lens_out must be int32 [B]")
+    if q_out is None:
+        q_out = torch.empty(B, num_q_heads, 1, D, dtype=torch.bfloat16, device=partials.device)
+    _check_lastdim("q_out", q_out, 4)
+    base = partials.data_ptr()
+    in_strides = _lib.strides(N, D, N)  # [B, H, T = 1, D] views of one split
+    lib = _lib.load()
+    head = [base, in_strides, base + num_q_heads * D * 4, in_strides, base + (num_q_heads + Hkv) * D * 4, in_strides,
+            S, B * N, _ptr(q_out), _lib.strides(*q_out.stride()[:3]),
+            _ptr(table), table.shape[0], _ptr(positions), None, _ptr(lens_out),
+            _ptr(layout.page_table), layout.max_pages, layout.num_pages, _ptr(layout.k), _ptr(layout.v)]
+    tail = [_lib.strides(*layout.strides), layout.capacity, B, 1, num_q_heads, Hkv, D, layout.page_size,
+            _stream(partials.device)]
+    if layout.kind == "fp8":
+        st = lib.tt_rope_append_partials_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
+    else:
+        st = lib.tt_rope_append_partials_bf16(*head, *tail)
+    _lib.check(st, "rope_append_partials")
+    return q_out
+
+
 class Workspace:
     """Grow-only device scratch for the split-K partials of one stream."""
 
