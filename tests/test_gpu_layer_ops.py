@@ -86,12 +86,13 @@ def test_splitk_reduce_bit_exact():
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("C,with_partials", [(2048, True), (1024, False), (3072, True)])
-def test_add_rmsnorm(C, with_partials):
+@pytest.mark.parametrize("C,with_partials,S", [(2048, True, 4), (1024, False, 0), (3072, True, 8), (2048, True, 12),
+                                               (2048, True, 20), (4096, True, 6)])
+def test_add_rmsnorm(C, with_partials, S):
     from tinytron_amd import ops
 
-    g = torch.Generator().manual_seed(C)
-    M, S, eps = 37, 4, 1e-6
+    g = torch.Generator().manual_seed(C + S)
+    M, eps = 37, 1e-6
     x = torch.randn(M, C, generator=g) * 3
     w = torch.rand(C, generator=g) + 0.5
     P = torch.randn(S, M, C, generator=g) if with_partials else None

@@ -140,20 +140,36 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 }
 
 // One workgroup per row m. With P != null the residual row first takes the
-// bf16-rounded sum of the partials (the projection's autocast output).
-template <int PER>  // float4 groups per thread: C = 1024 * PER
+// bf16-rounded sum of the partials (the projection's autocast output). Every
+// load of the row (x and up to SMAX splits) is issued before the first add,
+// so the row costs one memory round trip; the splits are added in order.
+template <int PER, int SMAX>  // PER float4 groups per thread (C = 1024 * PER); SMAX splits loaded at once
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float *P, int S, int64_t MN,
                                                           const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
   const int64_t row = (int64_t)blockIdx.x * C;
   f32x4 v[PER];
-  float ss = 0.f;
+  f32x4 pv[PER][SMAX];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
     v[j] = *reinterpret_cast<const f32x4 *>(x + row + c);
     if (P != nullptr) {
-      const f32x4 d = ordered_sum4(P, S, MN, row + c);
+#pragma unroll
+      for (int s = 0; s < SMAX; ++s)  // splits past S reload split 0 and are not added
+        pv[j][s] = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s < S ? s : 0) * MN + row + c);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = 4 * (threadIdx.x + 256 * j);
+    if (P != nullptr) {
+      f32x4 d = pv[j][0];
+#pragma unroll
+      for (int s = 1; s < SMAX; ++s)
+        if (s < S) d += pv[j][s];
+      for (int s = SMAX; s < S; ++s) d += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * MN + row + c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[j][e] += round_bf16(d[e]);
       *reinterpret_cast<f32x4 *>(x + row + c) = v[j];
@@ -227,9 +243,16 @@ hipError_t launch_reduce_bf16(const float *P, int S, int64_t MN, uint16_t *y, hi
 hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, const float *w, float eps, uint16_t *y,
                               hipStream_t stream) {
   const int64_t MN = (int64_t)M * C;
-#define TT_ADD_RMSNORM_CASE(n)                                                                           \
-  case n:                                                                                                \
-    hipLaunchKernelGGL((add_rmsnorm_kernel<n>), dim3(M), dim3(256), 0, stream, x, P, S, MN, w, eps, y, C); \
+#define TT_ADD_RMSNORM_LAUNCH(n, smax) \
+  hipLaunchKernelGGL((add_rmsnorm_kernel<n, smax>), dim3(M), dim3(256), 0, stream, x, P, S, MN, w, eps, y, C)
+#define TT_ADD_RMSNORM_CASE(n)                  \
+  case n:                                       \
+    if (S <= 4)                                 \
+      TT_ADD_RMSNORM_LAUNCH(n, 4);              \
+    else if (S <= 8 && n <= 4)                  \
+      TT_ADD_RMSNORM_LAUNCH(n, (n <= 4 ? 8 : 4)); \
+    else                                        \
+      TT_ADD_RMSNORM_LAUNCH(n, (n <= 2 ? 16 : 4)); \
     break;
   switch (C / 1024) {  // C in {1024, 2048, ..., 8192}, checked by the caller
     TT_ADD_RMSNORM_CASE(1)
@@ -244,6 +267,7 @@ hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, con
       return hipErrorInvalidValue;
   }
 #undef TT_ADD_RMSNORM_CASE
+#undef TT_ADD_RMSNORM_LAUNCH
   return hipGetLastError();
 }
 
