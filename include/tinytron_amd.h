@@ -259,6 +259,43 @@ int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2],
                            int64_t split_tokens, void *workspace, size_t workspace_bytes,
                            tt_stream_t stream);
 
+/*
+ * Prefill attention: causal GQA attention of T new tokens per sequence over
+ * the sequence's cache, after tt_rope_append_* has appended them.
+ *
+ * Replaces the prefill branch of the reference's attention (attn.py:321-341:
+ * cache append + get_kv, then F.scaled_dot_product_attention with
+ * is_causal=True at past_len 0, or the mask key_pos <= past_len + query_pos,
+ * attn.py:86-95) for a ragged batch.
+ *
+ * q   [B, H_q, T, D] bf16 (rotated), strides q_strides = {b, h, t}
+ * positions [B] int32: tokens cached before the new ones (the new token t of
+ *   sequence b is at position positions[b] + t and attends keys 0 .. that).
+ * new_lens [B] int32 or NULL: new tokens of sequence b (<= T; NULL = T);
+ *   output rows t >= new_lens[b] are left untouched.
+ * max_seq_len: host-side bound of positions[b] + new_lens[b] (the keys read
+ *   are clamped to it).
+ * out [B, T, H_q, D] bf16, strides out_strides = {b, t, h}.
+ * Requirements as tt_gqa_decode_attn_bf16 (head_dim 64/128, G <= 16, ...).
+ */
+int tt_prefill_attn_bf16(const void *q, const int64_t q_strides[3],
+                         const void *k_cache, const void *v_cache, const int64_t cache_strides[3],
+                         const int32_t *positions, const int32_t *new_lens, int64_t max_seq_len,
+                         const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                         void *out, const int64_t out_strides[3],
+                         int64_t batch, int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads,
+                         int64_t head_dim, int64_t page_size, float sm_scale, tt_stream_t stream);
+
+/* As tt_prefill_attn_bf16 with an fp8-e4m3fn cache and per-(token, head) scales. */
+int tt_prefill_attn_fp8(const void *q, const int64_t q_strides[3],
+                        const void *k_cache, const void *v_cache,
+                        const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                        const int32_t *positions, const int32_t *new_lens, int64_t max_seq_len,
+                        const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                        void *out, const int64_t out_strides[3],
+                        int64_t batch, int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads,
+                        int64_t head_dim, int64_t page_size, float sm_scale, tt_stream_t stream);
+
 /* Fixed split size the fp32 entry point uses when split_tokens == 0. */
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 

@@ -62,6 +62,31 @@ def decode_attention(q: np.ndarray, keys: list, values: list, num_kv_heads: int,
     return out
 
 
+def prefill_attention(q: np.ndarray, keys: list, values: list, positions, new_lens, num_kv_heads: int,
+                      sm_scale: float | None = None) -> np.ndarray:
+    """Causal attention of a prompt chunk over each sequence's cache (attn.py:321-341).
+
+    q [B, H_q, T, D]: query t of sequence b sits at position positions[b] + t
+    and exists for t < new_lens[b]; keys[b] / values[b] [>= positions[b] +
+    new_lens[b], H_kv, D] hold the cache after the chunk was appended. Query
+    (b, t) attends keys 0 .. positions[b] + t (the reference's mask
+    key_pos <= past_len + query_pos; is_causal when past_len = 0).
+    Returns [B, T, H_q, D] in fp64, zero for t >= new_lens[b]."""
+    B, Hq, T, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / np.sqrt(D)
+    hmap = gqa_head_map(Hq, num_kv_heads)
+    out = np.zeros((B, T, Hq, D), dtype=np.float64)
+    for b in range(B):
+        kb = np.asarray(keys[b], np.float64)
+        vb = np.asarray(values[b], np.float64)
+        for t in range(int(new_lens[b])):
+            p = int(positions[b]) + t
+            for h in range(Hq):
+                out[b, t, h] = attend_one(q[b, h, t], kb[:p + 1, hmap[h]], vb[:p + 1, hmap[h]], sm_scale)
+    return out
+
+
 def partial_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, sm_scale: float):
     """(m, l, o) of one split in fp64, natural-log domain."""
     s = (np.asarray(k, np.float64) @ np.asarray(q, np.float64)) * sm_scale

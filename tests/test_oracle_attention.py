@@ -106,3 +106,41 @@ def test_reference_decode_step_matches_oracle():
     ref = oat.decode_attention(qr[:, :, 0].numpy(), keys, vals, Hkv)
     assert np.allclose(y[:, :, 0].numpy(), ref, rtol=1e-5, atol=1e-5)
     assert cache.current_length == L + 1
+
+
+@pytest.mark.parametrize("past", [0, 5])
+def test_prefill_matches_torch_sdpa_fp64(past):
+    """prefill_attention == the reference's prefill call (attn.py:321-341):
+    SDPA with is_causal=True at past_len 0, the key_pos <= past_len + query_pos
+    mask (build_cache_causal_mask) otherwise; GQA by repeat_interleave."""
+    rng = np.random.default_rng(11 + past)
+    B, Hq, Hkv, D, T = 2, 8, 2, 32, 7
+    q = rng.standard_normal((B, Hq, T, D))
+    keys = [rng.standard_normal((past + T, Hkv, D)) for _ in range(B)]
+    vals = [rng.standard_normal((past + T, Hkv, D)) for _ in range(B)]
+    ours = oat.prefill_attention(q, keys, vals, [past] * B, [T] * B, Hkv)
+    for b in range(B):
+        K = torch.from_numpy(keys[b]).permute(1, 0, 2)[None]
+        V = torch.from_numpy(vals[b]).permute(1, 0, 2)[None]
+        K, V = ref_path.gqa_impl(K, V, Hkv, Hq)
+        qb = torch.from_numpy(q[b])[None]
+        if past == 0:
+            y = F.scaled_dot_product_attention(qb, K, V, is_causal=True)
+        else:
+            mask = ref_path.build_cache_causal_mask(T, past + T, past, "cpu")
+            y = F.scaled_dot_product_attention(qb, K, V, attn_mask=mask)
+        assert np.allclose(ours[b], y[0].permute(1, 0, 2).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_single_token_equals_decode_and_ragged_rows_are_zero():
+    rng = np.random.default_rng(4)
+    B, Hq, Hkv, D = 3, 4, 2, 16
+    past = [3, 0, 9]
+    q = rng.standard_normal((B, Hq, 2, D))
+    keys = [rng.standard_normal((p + 2, Hkv, D)) for p in past]
+    vals = [rng.standard_normal((p + 2, Hkv, D)) for p in past]
+    out = oat.prefill_attention(q, keys, vals, past, [1, 2, 1], Hkv)
+    dec = oat.decode_attention(q[:, :, 0], [k[:p + 1] for k, p in zip(keys, past)],
+                               [v[:p + 1] for v, p in zip(vals, past)], Hkv)
+    assert np.allclose(out[:, 0], dec, rtol=1e-13, atol=1e-13)
+    assert np.all(out[0, 1] == 0) and np.all(out[2, 1] == 0) and np.any(out[1, 1] != 0)

@@ -47,6 +47,14 @@ _ROPE_PART_HEAD = [
     _vp, _vp,                                        # k_cache, v_cache
 ]
 
+_PREFILL_TAIL = [
+    _i32p, _i32p, _i64,                              # positions, new_lens, max_seq_len
+    _i32p, _i64, _i64,                               # page_table, max_pages, num_pages
+    _vp, _i64p,                                      # out, out_strides {b, t, h}
+    _i64, _i64, _i64, _i64, _i64, _i64,              # batch, num_new, hq, hkv, head_dim, page_size
+    _f32, _vp,                                       # sm_scale, stream
+]
+
 _ATTN_HEAD = [_vp, _i64p, _vp, _vp]                  # q, q_strides, k_cache, v_cache
 _ATTN_TAIL = [
     _i64p,                                           # cache_strides
@@ -72,6 +80,8 @@ SIGNATURES = {
     "tt_gqa_decode_attn_f32": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
     "tt_decode_split_tokens": ([_i64, _i64, _i64], ctypes.c_int64),
     "tt_decode_workspace_bytes": ([_i64, _i64, _i64, _i64, _i64, _i64], ctypes.c_size_t),
+    "tt_prefill_attn_bf16": ([_vp, _i64p, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),
+    "tt_prefill_attn_fp8": ([_vp, _i64p, _vp, _vp, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),
     "tt_linear_splitk_bf16": ([_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp], ctypes.c_int),
     "tt_linear_splitk_packed_bf16": ([_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp], ctypes.c_int),
     "tt_splitk_reduce_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),

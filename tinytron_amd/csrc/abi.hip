@@ -292,6 +292,86 @@ int linear_common(const void *x, int64_t ldx, const void *weight, int64_t ldw, i
   (void)hipGetLastError();
   return from_hip(tt::launch_skinny_gemm(a, (int)k_chunk, (hipStream_t)stream), "linear launch");
 }
+int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3], const void *k_cache,
+                   const void *v_cache, const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                   const int32_t *positions, const int32_t *new_lens, int64_t max_seq_len, const int32_t *page_table,
+                   int64_t max_pages, int64_t num_pages, void *out, const int64_t out_strides[3], int64_t batch,
+                   int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                   float sm_scale, tt_stream_t stream) {
+  TT_CHECK(q && k_cache && v_cache && positions && out, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(q_strides && out_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
+  TT_CHECK(batch >= 0 && num_new >= 0, TT_ERR_INVALID_ARGUMENT, "batch and num_new must be >= 0");
+  TT_CHECK(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, TT_ERR_INVALID_ARGUMENT,
+           "num_attention_heads must be divisible by num_key_value_heads");
+  const int64_t g = num_q_heads / num_kv_heads;
+  TT_CHECK(g <= 16, TT_ERR_UNSUPPORTED, "GQA group size %lld > 16 is not supported", (long long)g);
+  TT_CHECK(head_dim == 64 || head_dim == 128, TT_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld",
+           (long long)head_dim);
+  TT_CHECK(max_seq_len >= 0 && max_seq_len < ((int64_t)1 << 30), TT_ERR_INVALID_ARGUMENT, "max_seq_len out of range");
+  TT_CHECK(batch * num_kv_heads < ((int64_t)1 << 26) && num_new < ((int64_t)1 << 24), TT_ERR_UNSUPPORTED,
+           "grid too large");
+  if (kind == tt::CacheKind::kFP8) {
+    TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+  }
+  int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
+  if (rc != TT_OK) return rc;
+  int page_shift = 0;
+  if (page_table != nullptr) {
+    while (page_shift < 30 && ((int64_t)1 << page_shift) < page_size) ++page_shift;
+    TT_CHECK(page_size >= 16 && ((int64_t)1 << page_shift) == page_size, TT_ERR_UNSUPPORTED,
+             "paged pools need a power-of-two page_size >= 16, got %lld", (long long)page_size);
+    TT_CHECK(max_seq_len <= max_pages * page_size, TT_ERR_INVALID_ARGUMENT,
+             "max_seq_len %lld exceeds the page table's %lld pages of %lld tokens", (long long)max_seq_len,
+             (long long)max_pages, (long long)page_size);
+  } else {
+    TT_CHECK(cache_strides[1] == page_size * head_dim, TT_ERR_UNSUPPORTED,
+             "the contiguous store needs dense pages (page stride %lld != page_size * head_dim)",
+             (long long)cache_strides[1]);
+  }
+  TT_CHECK(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
+           "q and cache pointers must be 16-byte aligned");
+  TT_CHECK(q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 && q_strides[2] % 8 == 0, TT_ERR_INVALID_ARGUMENT,
+           "q strides must be multiples of 8 elements");
+  TT_CHECK(cache_strides[0] % 8 == 0 && cache_strides[1] % 8 == 0 && cache_strides[2] % 8 == 0,
+           TT_ERR_INVALID_ARGUMENT, "cache strides must be multiples of 8 elements");
+  if (batch == 0 || num_new == 0) return ok();
+
+  tt::PrefillArgs a{};
+  a.q = q;
+  a.q_sb = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.q_st = q_strides[2];
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.c_seq = cache_strides[0];
+  a.c_page = cache_strides[1];
+  a.c_head = cache_strides[2];
+  a.max_len = (int)max_seq_len;
+  a.page_table = page_table;
+  a.max_pages = max_pages;
+  a.num_pages = num_pages;
+  a.out = out;
+  a.o_sb = out_strides[0];
+  a.o_st = out_strides[1];
+  a.o_sh = out_strides[2];
+  a.batch = (int)batch;
+  a.hq = (int)num_q_heads;
+  a.hkv = (int)num_kv_heads;
+  a.group = (int)g;
+  a.page_shift = page_shift;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.positions = positions;
+  a.new_lens = new_lens;
+  a.num_new = (int)num_new;
+  a.qt = (int)(16 / g);
+  a.nq = (int)((num_new + a.qt - 1) / a.qt);
+  a.wg_per_pair = (a.nq + tt::kWavesPerBlock - 1) / tt::kWavesPerBlock;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_prefill_attn(a, kind, (int)head_dim, (hipStream_t)stream), "prefill attention launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -372,6 +452,29 @@ int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3]
                             q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table,
                             max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch,
                             num_new, num_q_heads, num_kv_heads, head_dim, page_size, stream, splits, split_stride);
+}
+
+int tt_prefill_attn_bf16(const void *q, const int64_t q_strides[3], const void *k_cache, const void *v_cache,
+                         const int64_t cache_strides[3], const int32_t *positions, const int32_t *new_lens,
+                         int64_t max_seq_len, const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                         void *out, const int64_t out_strides[3], int64_t batch, int64_t num_new,
+                         int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                         float sm_scale, tt_stream_t stream) {
+  return prefill_common(tt::CacheKind::kBF16, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides,
+                        positions, new_lens, max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch,
+                        num_new, num_q_heads, num_kv_heads, head_dim, page_size, sm_scale, stream);
+}
+
+int tt_prefill_attn_fp8(const void *q, const int64_t q_strides[3], const void *k_cache, const void *v_cache,
+                        const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                        const int32_t *positions, const int32_t *new_lens, int64_t max_seq_len,
+                        const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *out,
+                        const int64_t out_strides[3], int64_t batch, int64_t num_new, int64_t num_q_heads,
+                        int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale,
+                        tt_stream_t stream) {
+  return prefill_common(tt::CacheKind::kFP8, q, q_strides, k_cache, v_cache, k_scale, v_scale, cache_strides,
+                        positions, new_lens, max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch,
+                        num_new, num_q_heads, num_kv_heads, head_dim, page_size, sm_scale, stream);
 }
 
 int tt_gqa_decode_attn_bf16(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,

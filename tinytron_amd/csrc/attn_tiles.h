@@ -1,0 +1,344 @@
+// Tile-level building blocks shared by the decode and prefill attention
+// kernels (gfx950): 16-byte K/V fragment loads through raw buffer resources
+// (rows past a length read nothing), V staged straight into LDS, the QK^T /
+// online-softmax step and the PV step on v_mfma_f32_16x16x32_{bf16,fp8}
+// (V transposed across lanes by an exact 0/1 selection MFMA), and paged
+// block addressing. Everything is in an unnamed namespace: each kernel file
+// gets its own copy.
+#pragma once
+
+#include "tt_internal.h"
+#include "tt_numerics.h"
+
+namespace tt {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] in [15:14]).
+constexpr int vmcnt_only(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+constexpr int kLgkmcntZero = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma_fp8(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0,
+                                                    0, 0);
+}
+
+// 8 e4m3fn codes -> 8 bf16 (exact).
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(u32x2 v) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+constexpr int kBufferFlags = 0x00020000;  // gfx9 raw buffer: dword data format, no swizzle
+
+// Every lane loads 16 bytes per load: lane (m + 16g) reads row (token) m of a
+// 16-token block at byte offset 16g + 64u, u < D*E/64. For bf16 a 16-byte
+// fragment is one 32-wide k step of a 16x16x32 MFMA (d = 32u + 8g + i); for
+// fp8 it is two k steps (hh = 0, 1: d = 64u + 16g + 8hh + i). The query
+// operand is loaded in the same d order, so Q.K^T is unchanged.
+template <bool kFP8>
+struct KVTraits;
+
+template <>
+struct KVTraits<false> {
+  static constexpr int kElemBytes = 2;
+  static constexpr int kStepsPerFrag = 1;
+  static __device__ __forceinline__ bf16x8 step(u32x4 f, int) { return __builtin_bit_cast(bf16x8, f); }
+  // d of k-slot (g, i) of k step s
+  static __device__ __forceinline__ int q_offset(int s, int g) { return 32 * s + 8 * g; }
+};
+
+template <>
+struct KVTraits<true> {
+  static constexpr int kElemBytes = 1;
+  static constexpr int kStepsPerFrag = 2;
+  static __device__ __forceinline__ bf16x8 step(u32x4 f, int hh) {
+    return hh == 0 ? fp8x8_to_bf16x8(u32x2{f[0], f[1]}) : fp8x8_to_bf16x8(u32x2{f[2], f[3]});
+  }
+  static __device__ __forceinline__ int q_offset(int s, int g) { return 64 * (s >> 1) + 16 * g + 8 * (s & 1); }
+};
+
+template <int D, bool kFP8>
+struct Tile {
+  static constexpr int NU = D * KVTraits<kFP8>::kElemBytes / 64;  // 16-byte fragments per lane per row
+  u32x4 k[2][NU];  // K fragments of the tile's two 16-token blocks (V goes through LDS)
+  f32x4 ks[2];     // fp8: K scales of this lane's 4 score rows, per 16-token block
+  f32x4 vs[2];
+  static constexpr int kVBytes = 2 * NU * 1024;  // per-wave LDS bytes of one tile's V
+};
+
+// Element offset of token tb (a multiple of 16) of (b, hk), d = 0; tb must
+// lie in a page the sequence owns. A 16-token block never straddles a page:
+// paged pools have power-of-two pages of >= 16 tokens, and the contiguous
+// store is addressed linearly (its pages are dense, page stride = P * D).
+__device__ __forceinline__ int64_t block_elem(const DecodeArgs &a, int b, int hk, int tb, int D) {
+  if (a.page_table != nullptr) {
+    int64_t phys = a.page_table[(int64_t)b * a.max_pages + (tb >> a.page_shift)];
+    phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
+    return phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tb & ((1 << a.page_shift) - 1)) * D;
+  }
+  return (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)tb * D;
+}
+
+// Element offset of any token t < length of (b, hk), d = 0.
+__device__ __forceinline__ int64_t token_elem(const DecodeArgs &a, int b, int hk, int t, int D) {
+  const int tb = t & ~15;
+  return block_elem(a, b, hk, tb, D) + (int64_t)(t - tb) * D;
+}
+
+// Loads of one 16-token block whose element offset `elem` was resolved in
+// the prologue. Rows past the sequence end are outside the buffer range
+// (num_records) and read as zero (or, for LDS loads, leave the LDS slot as
+// it was): no branch, no out-of-bounds access, and no garbage (possibly
+// NaN) from unused cache slots reaches the MFMAs.
+template <int D, bool kFP8>
+__device__ __forceinline__ void load_k_block(const DecodeArgs &a, int64_t elem, int rows, int lane,
+                                             u32x4 (&k)[Tile<D, kFP8>::NU], f32x4 &ks, f32x4 &vs) {
+  constexpr int E = KVTraits<kFP8>::kElemBytes;
+  constexpr int NU = Tile<D, kFP8>::NU;
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(static_cast<const char *>(a.k_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
+  const int off = (lane & 15) * D * E + 16 * (lane >> 4);
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+    k[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * u, 0, 0));
+  if constexpr (kFP8) {
+    // this lane's score rows are tokens tb + 4g + r, r = 0..3
+    const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + elem / D, (short)0,
+                                                       rows * 4, kBufferFlags);
+    const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + elem / D, (short)0,
+                                                       rows * 4, kBufferFlags);
+    ks = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rks, 16 * (lane >> 4), 0, 0));
+    vs = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvs, 16 * (lane >> 4), 0, 0));
+  }
+}
+
+// V rows of one 16-token block straight into this wave's LDS slots
+// (buffer_load ... lds: lane i's 16 bytes land at base + 16 i, the layout a
+// register load would have), so the next tile's V costs no VGPRs.
+template <int D, bool kFP8>
+__device__ __forceinline__ void load_v_block_lds(const DecodeArgs &a, int64_t elem, int rows, int lane, char *lds) {
+  constexpr int E = KVTraits<kFP8>::kElemBytes;
+  constexpr int NU = Tile<D, kFP8>::NU;
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
+  const int off = (lane & 15) * D * E + 16 * (lane >> 4);
+#pragma unroll
+  for (int u = 0; u < NU; ++u)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(lds + 1024 * u), 16,
+                                             off + 64 * u, 0, 0, 0);
+}
+
+template <int D, bool kFP8>
+struct WaveState {
+  static constexpr int NDB = D / 32;
+  f32x4 o[2 * NDB];  // PV accumulators: d block c (16 columns), rows = heads 4g..4g+3
+  float m;           // running max of this lane's head (log2 units)
+  float l;           // running sum (lane-partial: this lane's tokens only)
+};
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void qk_softmax(float scale_log2, int t0, int lim, int lane, const Tile<D, kFP8> &tile,
+                                           const bf16x8 (&qf)[D / 32], WaveState<D, kFP8> &st, bf16x8 &pa_hi,
+                                           bf16x8 &pa_lo) {
+  using TR = KVTraits<kFP8>;
+  constexpr int NDB = D / 32;
+  const int g = lane >> 4;
+
+  // S^T[token][head]: lane (n + 16g), reg r = token t0 + 16*tt + 4g + r, head n.
+  f32x4 S[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    S[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NDB; ++s) {
+      const int u = s / TR::kStepsPerFrag;
+      S[tt] = mfma_bf16(TR::step(tile.k[tt][u], s % TR::kStepsPerFrag), qf[s], S[tt]);
+    }
+  }
+
+  float s[8];
+  bool valid[8];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = t0 + 16 * tt + 4 * g + r;
+      float x = S[tt][r];
+      if constexpr (kFP8) x *= tile.ks[tt][r];
+      valid[tt * 4 + r] = tok < lim;
+      s[tt * 4 + r] = tok < lim ? x * scale_log2 : kNegInf;
+    }
+  }
+  float mx = s[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(st.m, mx);  // finite: every column has key t0 = 0 valid from its first tile on
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  float p[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
+    psum += p[i];
+  }
+  st.l = st.l * alpha + psum;
+  st.m = m_new;
+  if constexpr (kFP8) {
+    // fold the per-token V scale into P; masked tokens stay exactly 0 (select,
+    // not multiply, in case a scale slot past the end holds a non-finite value)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = valid[r] ? p[r] * tile.vs[0][r] : 0.f;
+      p[4 + r] = valid[4 + r] ? p[4 + r] * tile.vs[1][r] : 0.f;
+    }
+  }
+
+  // Rescale O rows (heads 4g + r) by their head's alpha, held by lane 4g + r.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+    for (int c = 0; c < 2 * NDB; ++c) st.o[c][r] *= ar;
+  }
+
+  // P as the A operand: row = head (lane % 16), k slots = this lane's 8 tokens.
+  // P = P_hi + P_lo with both halves bf16 (P_lo = P - P_hi is exact in fp32),
+  // so the PV product keeps ~16 mantissa bits of P instead of bf16's 8; the
+  // second MFMA per block is free in this memory-bound loop.
+  const f32x8 pv = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]};
+  pa_hi = __builtin_convertvector(pv, bf16x8);
+  const f32x8 p_rem = pv - __builtin_convertvector(pa_hi, f32x8);
+  pa_lo = __builtin_convertvector(p_rem, bf16x8);
+}
+
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void pv_tile(const u32x4 (&vt)[2][Tile<D, kFP8>::NU], const bf16x8 (&ident16)[2],
+                                        const u32x2 (&ident8)[2], bf16x8 pa_hi, bf16x8 pa_lo, WaveState<D, kFP8> &st) {
+  constexpr int NDB = D / 32;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) {
+    // block c: bf16 c = 2u + hi; fp8 c = 4u + 2hh + hi (column order in o_col_d)
+    const int hi = c & 1;
+    f32x4 t0v, t1v;
+    if constexpr (kFP8) {
+      const int u = c >> 2;
+      const int hh = (c >> 1) & 1;
+      const u32x2 v0 = hh ? u32x2{vt[0][u][2], vt[0][u][3]} : u32x2{vt[0][u][0], vt[0][u][1]};
+      const u32x2 v1 = hh ? u32x2{vt[1][u][2], vt[1][u][3]} : u32x2{vt[1][u][0], vt[1][u][1]};
+      t0v = mfma_fp8(v0, ident8[hi], zero);
+      t1v = mfma_fp8(v1, ident8[hi], zero);
+    } else {
+      const int u = c >> 1;
+      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[0][u]), ident16[hi], zero);
+      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[1][u]), ident16[hi], zero);
+    }
+    // lane (n + 16g): V[token t0 + 4g + r][o_col_d(c, n)] (t0v), same for t0 + 16 (t1v)
+    const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
+    const bf16x8 vb = __builtin_convertvector(vv, bf16x8);
+    st.o[c] = mfma_bf16(pa_hi, vb, st.o[c]);
+    st.o[c] = mfma_bf16(pa_lo, vb, st.o[c]);
+  }
+}
+
+// head_dim index of output column n of PV block c (see pv_tile).
+template <bool kFP8>
+__device__ __forceinline__ int o_col_d(int c, int n) {
+  if constexpr (kFP8) {
+    const int u = c >> 2, hh = (c >> 1) & 1, hi = c & 1;
+    return 64 * u + 16 * (2 * hi + (n >> 3)) + 8 * hh + (n & 7);
+  } else {
+    return 16 * c + n;
+  }
+}
+
+// Selection matrices for the V transpose: B[k][n] = 1 iff k == n (+16 for
+// the upper half), expressed in the (lane group, slot) coordinates in which
+// the A operand was loaded, so the result does not depend on how the
+// hardware orders the K index inside a lane.
+__device__ __forceinline__ void make_identity(int lane, bf16x8 (&ident16)[2], u32x2 (&ident8)[2]) {
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  uint32_t w8[2][2] = {{0u, 0u}, {0u, 0u}};
+  uint32_t w16[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (8 * g + i == n) {
+      w8[0][i >> 2] |= 0x38u << (8 * (i & 3));        // e4m3fn 1.0
+      w16[0][i >> 1] |= 0x3f80u << (16 * (i & 1));    // bf16 1.0
+    }
+    if (8 * g + i == n + 16) {
+      w8[1][i >> 2] |= 0x38u << (8 * (i & 3));
+      w16[1][i >> 1] |= 0x3f80u << (16 * (i & 1));
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    ident8[h] = u32x2{w8[h][0], w8[h][1]};
+    ident16[h] = __builtin_bit_cast(bf16x8, u32x4{w16[h][0], w16[h][1], w16[h][2], w16[h][3]});
+  }
+}
+
+constexpr int kChunkTiles = 8;  // tiles per page-table fetch and software-pipelined run
+
+// Element offset and valid rows of 16-token block `blk` of (b, hk). Paged:
+// `entry` holds, one per lane, the page-table entries of pages pbase.. (the
+// block's page index relative to pbase is < 64 for every block of the chunk).
+template <int D>
+__device__ __forceinline__ void stream_block_addr(const DecodeArgs &a, int b, int hk, int L, int entry, int pbase,
+                                                  int blk, int64_t &elem, int &rows) {
+  const int tb = 16 * blk;
+  const int tc = min(tb, (L - 1) & ~15);  // blocks past the end keep an in-sequence address and zero rows
+  rows = __builtin_amdgcn_readfirstlane(min(max(L - tb, 0), 16));
+  int64_t e;
+  if (a.page_table != nullptr) {
+    int64_t phys = __builtin_amdgcn_readlane(entry, (tc >> a.page_shift) - pbase);
+    phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
+    e = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & ((1 << a.page_shift) - 1)) * D;
+  } else {
+    e = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)tc * D;
+  }
+  elem = uniform64(e);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+}  // namespace
+}  // namespace tt

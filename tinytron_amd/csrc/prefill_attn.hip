@@ -1,0 +1,192 @@
+// Prefill GQA attention for gfx950: T new tokens per sequence attend causally
+// to their sequence's cached keys (the prompt chunk's own K/V already
+// appended by rope_append), over the reference's contiguous store or the
+// paged pool, bf16 or fp8-e4m3 cache.
+//
+// Replaces the prefill branch of the reference's attention (attn.py:321-341:
+// append, get_kv, then SDPA with is_causal=True at past_len 0 or the mask
+// key_pos <= past_len + query_pos otherwise) for a ragged batch.
+//
+// One wave per (sequence b, KV head hk, block of qt = 16 / G query tokens):
+// the 16 columns of the MFMA B operand are the (token, head) pairs
+// n = tq * G + head of the block, so each streamed K/V tile serves G heads x
+// qt tokens. The key loop is the decode kernel's tile pipeline (K fragments
+// in registers, V through LDS, QK^T and PV on the matrix cores, online
+// softmax per column); column n masks the keys after its own position
+// (position 0 is valid for every column, so no row is ever empty).
+//
+// Workgroups are laid out so that all query blocks of one (sequence, KV
+// head) go to the same XCD (workgroup i runs on XCD i mod 8): the pair's
+// K/V, re-read by each of its blocks, stays in that XCD's L2.
+#include <algorithm>
+
+#include "attn_tiles.h"
+#include "tt_internal.h"
+#include "tt_numerics.h"
+
+namespace tt {
+namespace {
+
+constexpr int kXcds = 8;
+
+template <int D, bool kFP8>
+__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
+  using TR = KVTraits<kFP8>;
+  constexpr int NDB = D / 32;
+  constexpr int NU = Tile<D, kFP8>::NU;
+  constexpr int kKLoads = 2 * NU + (kFP8 ? 4 : 0);
+  constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
+  extern __shared__ char smem_v[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+
+  // workgroup -> (XCD, slot on that XCD) -> (pair, its k-th workgroup); the
+  // longest (last) query blocks of a pair go first
+  const int xcd = blockIdx.x % kXcds;
+  const int slot = blockIdx.x / kXcds;
+  const int pair = (slot / a.wg_per_pair) * kXcds + xcd;
+  if (pair >= a.batch * a.hkv) return;
+  const int qblk = a.nq - 1 - ((slot % a.wg_per_pair) * kWavesPerBlock + wave);
+  if (qblk < 0) return;
+  const int b = pair / a.hkv;
+  const int hk = pair - b * a.hkv;
+  const int nb = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
+  const int t_first = qblk * a.qt;
+  if (t_first >= nb) return;
+  const int pos0 = a.positions[b];
+  const int t_end = min(t_first + a.qt, nb);
+  // keys the block needs: 0 .. pos0 + t_end - 1, never past the host's bound (the page table's reach)
+  const int L = __builtin_amdgcn_readfirstlane(min(pos0 + t_end, a.max_len));
+  if (pos0 < 0 || L <= 0) return;
+
+  const int G = a.group;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int tq = n / G;
+  const int head = n - tq * G;
+  const bool col_valid = tq < a.qt && t_first + tq < t_end;
+  const int lim = col_valid ? min(pos0 + t_first + tq + 1, L) : 1;  // keys this column may see
+
+  bf16x8 qf[NDB];
+  {
+    const uint16_t *q = static_cast<const uint16_t *>(a.q);
+    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + head) * a.q_sh + (int64_t)(t_first + tq) * a.q_st;
+#pragma unroll
+    for (int s = 0; s < NDB; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (col_valid) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
+      qf[s] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+  bf16x8 ident16[2];
+  u32x2 ident8[2];
+  make_identity(lane, ident16, ident8);
+  WaveState<D, kFP8> st;
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = kNegInf;
+  st.l = 0.f;
+
+  char *vlds = smem_v + wave * Tile<D, kFP8>::kVBytes;
+  const int ntiles = (L + kTileTokens - 1) / kTileTokens;
+  // Same chunked pipeline as the decode kernel (K(k+1) | QK, softmax |
+  // wait V(k), read V(k) | V(k+1) | PV), with explicit vmcnt counts.
+  for (int c0 = 0; c0 < ntiles; c0 += kChunkTiles) {
+    const int c1 = min(ntiles, c0 + kChunkTiles);
+    int entry = 0, pbase = 0;
+    if (a.page_table != nullptr) {
+      pbase = (kTileTokens * c0) >> a.page_shift;
+      const int last = (L - 1) >> a.page_shift;
+      entry = a.page_table[(int64_t)b * a.max_pages + min(pbase + lane, last)];
+    }
+    Tile<D, kFP8> buf[2];
+    int64_t e0, e1;
+    int r0, r1;
+    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0, e0, r0);
+    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0 + 1, e1, r1);
+    load_k_block<D, kFP8>(a, e0, r0, lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
+    load_k_block<D, kFP8>(a, e1, r1, lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
+    load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kChunkTiles; ++k) {
+      const int it = c0 + k;
+      if (it >= c1) break;  // uniform
+      if (k + 1 < kChunkTiles) {
+        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 2, e0, r0);
+        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 3, e1, r1);
+        Tile<D, kFP8> &nx = buf[(k + 1) & 1];
+        load_k_block<D, kFP8>(a, e0, r0, lane, nx.k[0], nx.ks[0], nx.vs[0]);
+        load_k_block<D, kFP8>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      bf16x8 pa_hi, pa_lo;
+      qk_softmax<D, kFP8>(a.scale_log2, kTileTokens * it, lim, lane, buf[k & 1], qf, st, pa_hi, pa_lo);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 1 < kChunkTiles)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
+      else
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+      u32x4 vt[2][NU];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+          vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+      __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
+      __builtin_amdgcn_sched_barrier(0);
+      if (k + 1 < kChunkTiles && it + 1 < c1) {
+        load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
+        load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      pv_tile<D, kFP8>(vt, ident16, ident8, pa_hi, pa_lo, st);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+
+  // normalise and write: O row r of lane group g is column 4g + r
+  float l = st.l;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  uint16_t *out = static_cast<uint16_t *>(a.out);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int col = 4 * g + r;
+    const float lr = __shfl(l, col, 64);
+    const float inv = lr > 0.f ? 1.0f / lr : 0.f;
+    const int ctq = col / G;
+    const int chead = col - ctq * G;
+    if (ctq < a.qt && t_first + ctq < t_end) {
+      const int64_t orow =
+          (int64_t)b * a.o_sb + (int64_t)(t_first + ctq) * a.o_st + (int64_t)(hk * G + chead) * a.o_sh;
+#pragma unroll
+      for (int c = 0; c < 2 * NDB; ++c) out[orow + o_col_d<kFP8>(c, n)] = f32_to_bf16_bits(st.o[c][r] * inv);
+    }
+  }
+}
+
+template <int D, bool kFP8>
+hipError_t launch_d(const PrefillArgs &a, hipStream_t stream) {
+  const int64_t pairs = (int64_t)a.batch * a.hkv;
+  const int64_t slots = (pairs + kXcds - 1) / kXcds * a.wg_per_pair;
+  const int64_t grid = slots * kXcds;
+  const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes;
+  hipLaunchKernelGGL((prefill_attn_kernel<D, kFP8>), dim3((unsigned)grid), dim3(64 * kWavesPerBlock), lds, stream,
+                     a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_prefill_attn(const PrefillArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
+  if (head_dim == 64) return kind == CacheKind::kFP8 ? launch_d<64, true>(a, stream) : launch_d<64, false>(a, stream);
+  return kind == CacheKind::kFP8 ? launch_d<128, true>(a, stream) : launch_d<128, false>(a, stream);
+}
+
+}  // namespace tt

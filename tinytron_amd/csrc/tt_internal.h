@@ -82,6 +82,22 @@ hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hip
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream);
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
 
+// Prefill: T new tokens per sequence (their K/V already in the cache), causal
+// GQA attention over each sequence's cached prefix. The cache fields, q / out
+// pointers and scale come from DecodeArgs (out strides: o_sb = batch, o_sh = head).
+struct PrefillArgs : DecodeArgs {
+  int64_t q_st;                // q token stride
+  int64_t o_st;                // out token stride
+  const int32_t *positions;    // [B] tokens cached before the new ones
+  const int32_t *new_lens;     // [B] new tokens per sequence (<= num_new), or null for all num_new
+  int num_new;                 // T
+  int qt;                      // query tokens per wave (16 / G)
+  int nq;                      // query blocks per sequence: ceil(T / qt)
+  int wg_per_pair;             // workgroups per (sequence, KV head): ceil(nq / 4)
+};
+
+hipError_t launch_prefill_attn(const PrefillArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
+
 // Partition helpers shared by the ABI layer and the launchers.
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);
 inline int64_t num_splits(int64_t max_len, int64_t split_tokens) {

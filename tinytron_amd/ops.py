@@ -373,3 +373,45 @@ def silu_mul(partials: torch.Tensor, out: torch.Tensor | None = None) -> torch.T
     _lib.check(_lib.load().tt_silu_mul_bf16(_ptr(partials), S, M, inter, _ptr(out), _stream(partials.device)),
                "silu_mul")
     return out
+
+
+def prefill_attention(q: torch.Tensor, layout: KVLayout, positions: torch.Tensor, max_seq_len: int,
+                      new_lens: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                      sm_scale: float | None = None) -> torch.Tensor:
+    """Causal GQA attention of T new tokens per sequence over its cache (after rope_append).
+
+    q [B, H_q, T, D] bf16 (rotated; any strides with D contiguous),
+    positions int32 [B] = tokens cached before the new ones, new_lens int32
+    [B] (optional) = new tokens per sequence; returns out [B, T, H_q, D]
+    (rows t >= new_lens[b] untouched). Restates the prefill branch of the
+    reference attention (attn.py:321-341) for a ragged batch."""
+    _require_cuda(q, layout.k, layout.v, positions)
+    _check_lastdim("q", q, 4)
+    if q.dtype != torch.bfloat16 or layout.kind not in ("bf16", "fp8"):
+        raise ValueError("prefill_attention takes bf16 q with a bf16 or fp8 cache")
+    B, Hq, T, D = q.shape
+    if D != layout.head_dim:
+        raise ValueError(f"head_dim {D} does not match the cache's {layout.head_dim}")
+    if positions.dtype != torch.int32 or positions.shape != (B,):
+        raise ValueError("positions must be int32 [B]")
+    if new_lens is not None and (new_lens.dtype != torch.int32 or new_lens.shape != (B,)):
+        raise ValueError("new_lens must be int32 [B]")
+    if max_seq_len > layout.capacity:
+        raise ValueError(f"max_seq_len {max_seq_len} exceeds the cache capacity {layout.capacity}")
+    if out is None:
+        out = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=q.device)
+    _check_lastdim("out", out, 4)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    lib = _lib.load()
+    head = [_ptr(q), _lib.strides(*q.stride()[:3]), _ptr(layout.k), _ptr(layout.v)]
+    tail = [_lib.strides(*layout.strides), _ptr(positions), _ptr(new_lens), int(max_seq_len),
+            _ptr(layout.page_table), layout.max_pages, layout.num_pages,
+            _ptr(out), _lib.strides(*out.stride()[:3]), B, T, Hq, layout.num_heads, D, layout.page_size,
+            float(sm_scale), _stream(q.device)]
+    if layout.kind == "fp8":
+        st = lib.tt_prefill_attn_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
+    else:
+        st = lib.tt_prefill_attn_bf16(*head, *tail)
+    _lib.check(st, "prefill_attention")
+    return out
