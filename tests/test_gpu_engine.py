@@ -192,3 +192,36 @@ def test_fused_decode_step_matches_module_path():
     scale = float(l0.abs().max())
     assert float((l0 - l1).abs().max()) <= 0.05 * scale
     assert torch.equal(l0.argmax(-1), l1.argmax(-1)) or float((l0 - l1).abs().max()) < 1e-2
+
+
+@pytest.mark.parametrize("kv_dtype", [None, "fp8"])
+def test_prefill_kernel_matches_sdpa_path(kv_dtype):
+    """Attention._prefill through the prefill kernel equals the per-sequence
+    SDPA path on the same (ragged, partly cached) inputs, to bf16 rounding."""
+    from tinytron_amd.cache import PagedKVCache
+    from tinytron_amd.model import Attention
+
+    cfg = _c1_config(num_layer=1, hidden_size=1024, num_attention_heads=16, num_key_value_heads=4, block_size=256)
+    attn = Attention(cfg, 0, device=DEV, dtype=torch.bfloat16)
+    kvd = torch.float8_e4m3fn if kv_dtype == "fp8" else None
+    g = torch.Generator().manual_seed(21)
+    B, T0, T1 = 4, 30, 50
+    x0 = torch.randn(B, T0, 1024, generator=g).to(DEV)
+    x1 = torch.randn(B, T1, 1024, generator=g).to(DEV)
+    first, second = [30, 7, 19, 1], [50, 12, 1, 33]
+    ys = []
+    for use_kernel in (True, False):
+        attn.prefill_kernel = use_kernel
+        cache = PagedKVCache.from_model_config(cfg, B, 16, DEV, torch.bfloat16, kv_cache_dtype=kvd, paged_pool=True,
+                                               seq_capacity=[128] * B)
+        layer = cache.get_layer_cache(0)
+        with torch.no_grad():
+            layer.set_pending_new_lens(first)
+            attn(x0, past_kv=layer, use_cache=True, position_offset=0)
+            layer.set_pending_new_lens(second)
+            y, _ = attn(x1, past_kv=layer, use_cache=True, position_offset=0)
+        ys.append(y.float().cpu())
+    attn.prefill_kernel = True
+    a, b = ys
+    for i, n in enumerate(second):
+        assert torch.allclose(a[i, :n], b[i, :n], rtol=2e-2, atol=2e-2), f"sequence {i}"

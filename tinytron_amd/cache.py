@@ -141,6 +141,14 @@ class _LayerCacheBase:
         self._host_lens = [a + 1 for a in self._host_lens]
         return q_rot
 
+    def prefill_attend(self, q_rot: torch.Tensor, new_lens, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Causal attention of the chunk just appended by rope_append (q_rot
+        [B, H_q, T, D], new_lens[b] tokens of sequence b) over each sequence's
+        cache; returns [B, T, H_q, D], rows past new_lens[b] untouched."""
+        prev = self._lens_dev[1 - self._cur]  # the lengths before the append (the other buffer)
+        nl = torch.tensor([int(n) for n in new_lens], dtype=torch.int32).to(prev.device, non_blocking=True)
+        return ops.prefill_attention(q_rot, self.layout, prev, self.current_length, new_lens=nl, out=out)
+
     def attend(self, q: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """GQA decode attention of q [B, H_q, D] over every cached token of each sequence."""
         if self.workspace is None:

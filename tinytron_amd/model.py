@@ -15,7 +15,8 @@ autocast produces from fp32 weights.
 ``Attention.forward`` is the drop-in of attn.py:378-440: with one of this
 package's caches, a decode step (T = 1) is one fused RoPE + KV-append kernel
 and one split-K GQA attention kernel; prefill (T > 1) writes the cache with
-the same append kernel and attends with SDPA per sequence. No CPU fallback.
+the same append kernel and attends with the prefill kernel (bf16
+activations; SDPA per sequence for fp32). No CPU fallback.
 
 ``GPT.forward`` runs a bf16 decode step (T = 1) as a fused layer sequence
 when the shapes allow it (``GPT.fused_decode``): per layer, one skinny
@@ -94,6 +95,7 @@ class Attention(nn.Module):
         self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.c_proj = nn.Linear(config.hidden_size, config.hidden_size, **kw)
+        self.prefill_kernel = True  # bf16 prefill through the prefill attention kernel (else SDPA per sequence)
         self._init_weights(config.seed, layer_idx)
 
     def _init_weights(self, base_seed: int, layer_idx: int) -> None:
@@ -130,12 +132,17 @@ class Attention(nn.Module):
 
     def _prefill(self, q, k, v, cache, table, lens_before):
         """T > 1: append all (ragged) prompt tokens with the fused kernel, then
-        causal SDPA per sequence over its cached prefix (attn.py:321-341)."""
+        causal attention over each sequence's cached prefix (attn.py:321-341):
+        the prefill kernel for bf16 activations, SDPA per sequence otherwise."""
         B, _, T, D = q.shape
         new = cache._pending_new_lens or [T] * B
         q_rot = cache.rope_append(q, k, v, table, new_lens=new)
-        rep = self.num_attention_heads // self.num_key_value_heads
         y = torch.zeros(B, T, self.n_embd, dtype=q.dtype, device=q.device)
+        if self.prefill_kernel and q.dtype == torch.bfloat16 and cache.layout.kind in ("bf16", "fp8") \
+                and D in (64, 128) and self.num_attention_heads // self.num_key_value_heads <= 16:
+            cache.prefill_attend(q_rot, new, out=y.view(B, T, self.num_attention_heads, D))
+            return y
+        rep = self.num_attention_heads // self.num_key_value_heads
         for b in range(B):
             n = int(new[b])
             if n == 0:
