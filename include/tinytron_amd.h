@@ -358,6 +358,35 @@ int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const f
  */
 int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t inter, void *y, tt_stream_t stream);
 
+/*
+ * Token sampling from logits [M, V] (row stride ld), replacing
+ * filter_logits + sample_next_token / sample_next_token_with_log_prob
+ * (tinytron/inference/sampler.py:6-62; called at engine.py:196-212):
+ * fp32 cast, division by temperature (skipped at 1.0; temperature <= 0 is an
+ * error), top-k when top_k > 0 (keeps values >= the k-th largest, ties
+ * kept), top-p when 0 < top_p < 1 (keeps the shortest descending prefix
+ * whose cumulative probability exceeds top_p, the first token always; equal
+ * values are ordered by index), then one token per row:
+ *   - top_k == 1: the first maximum (the reference draws among exactly tied
+ *     maxima at random);
+ *   - otherwise a draw from softmax(filtered) by inverse CDF in index order,
+ *     driven by a 64-bit uniform from SplitMix64 over (seed, offset, row):
+ *     the distribution of torch.multinomial, not its random stream. The
+ *     same (seed, offset) gives the same tokens.
+ * tokens int64 [M] (required). token_logprob [M] (optional): the chosen
+ * token's log_softmax(filtered) value (sampler.py:56-61). logprobs [M, V]
+ * with row stride ld_logprobs (optional): log_softmax of the filtered logits,
+ * -inf where filtered. V <= 65536 (bf16 logits), 32768 (fp32 logits).
+ */
+int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
+                   float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
+                   float *logprobs, int64_t ld_logprobs, tt_stream_t stream);
+
+/* As tt_sample_bf16 with fp32 logits (fp32 models). */
+int tt_sample_f32(const float *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
+                  float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
+                  float *logprobs, int64_t ld_logprobs, tt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

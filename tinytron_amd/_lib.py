@@ -67,6 +67,14 @@ _ATTN_TAIL = [
     _vp,                                             # stream
 ]
 
+_SAMPLE = [
+    _vp, _i64, _i64, _i64,                           # logits, row stride, rows, vocab
+    _f32, _i64, _f32,                                # temperature, top_k, top_p
+    ctypes.c_uint64, ctypes.c_uint64,                # seed, offset
+    _vp, _vp, _vp, _i64,                             # tokens, token_logprob, logprobs, logprobs row stride
+    _vp,                                             # stream
+]
+
 SIGNATURES = {
     "tt_abi_version": ([], ctypes.c_int),
     "tt_last_error_string": ([], ctypes.c_char_p),
@@ -87,6 +95,8 @@ SIGNATURES = {
     "tt_splitk_reduce_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_add_rmsnorm_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
     "tt_silu_mul_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
+    "tt_sample_bf16": (_SAMPLE, ctypes.c_int),
+    "tt_sample_f32": (_SAMPLE, ctypes.c_int),
 }
 
 _LIB = None

@@ -15,7 +15,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libtinytron_amd.so"
-SOURCES = ["abi.hip", "rope_append.hip", "decode_attn.hip", "prefill_attn.hip", "layer_ops.hip"]
+SOURCES = ["abi.hip", "rope_append.hip", "decode_attn.hip", "prefill_attn.hip", "layer_ops.hip", "sampler.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -372,6 +372,43 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
   return from_hip(tt::launch_prefill_attn(a, kind, (int)head_dim, (hipStream_t)stream), "prefill attention launch");
 }
 
+int sample_common(bool f32, const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature,
+                  int64_t top_k, float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
+                  float *logprobs, int64_t ld_logprobs, tt_stream_t stream) {
+  TT_CHECK(temperature > 0.f, TT_ERR_INVALID_ARGUMENT, "temperature must be > 0");
+  TT_CHECK(m >= 0 && m <= INT32_MAX, TT_ERR_INVALID_ARGUMENT, "rows must be in [0, 2^31)");
+  if (m == 0) return ok();
+  TT_CHECK(logits && tokens, TT_ERR_INVALID_ARGUMENT, "logits and tokens are required");
+  const int64_t vmax = f32 ? tt::kMaxSampleVocabF32 : tt::kMaxSampleVocabBF16;
+  TT_CHECK(vocab >= 1 && vocab <= vmax, TT_ERR_UNSUPPORTED, "vocab size %lld outside [1, %lld]", (long long)vocab,
+           (long long)vmax);
+  TT_CHECK(ld >= vocab, TT_ERR_INVALID_ARGUMENT, "logits row stride %lld < vocab %lld", (long long)ld,
+           (long long)vocab);
+  TT_CHECK(logprobs == nullptr || ld_logprobs >= vocab, TT_ERR_INVALID_ARGUMENT,
+           "logprobs row stride %lld < vocab %lld", (long long)ld_logprobs, (long long)vocab);
+  const int64_t esize = f32 ? 4 : 2;
+  tt::SampleArgs a{};
+  a.logits = logits;
+  a.ld = ld;
+  a.M = (int)m;
+  a.V = (int)vocab;
+  a.vec = aligned(logits, 16) && (ld * esize) % 16 == 0;
+  a.temperature = temperature;
+  a.apply_temp = temperature != 1.0f;
+  a.top_k = top_k > 0 ? (int)(top_k < vocab ? top_k : vocab) : 0;
+  a.top_p = top_p;
+  a.apply_top_p = top_p > 0.f && top_p < 1.0f;
+  a.seed = seed;
+  a.offset = offset;
+  a.tokens = tokens;
+  a.token_logprob = token_logprob;
+  a.logprobs = logprobs;
+  a.ld_lp = ld_logprobs;
+  a.vec_out = logprobs != nullptr && aligned(logprobs, 16) && ld_logprobs % 4 == 0;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_sample(a, f32, (hipStream_t)stream), "sampler launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -576,6 +613,20 @@ int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t i
   return from_hip(tt::launch_silu_mul(partials, (int)splits, (int)m, (int)inter, static_cast<uint16_t *>(y),
                                       (hipStream_t)stream),
                   "silu_mul launch");
+}
+
+int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
+                   float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
+                   float *logprobs, int64_t ld_logprobs, tt_stream_t stream) {
+  return sample_common(false, logits, ld, m, vocab, temperature, top_k, top_p, seed, offset, tokens, token_logprob,
+                       logprobs, ld_logprobs, stream);
+}
+
+int tt_sample_f32(const float *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
+                  float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
+                  float *logprobs, int64_t ld_logprobs, tt_stream_t stream) {
+  return sample_common(true, logits, ld, m, vocab, temperature, top_k, top_p, seed, offset, tokens, token_logprob,
+                       logprobs, ld_logprobs, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,551 @@
+// Token sampling on gfx950: tinytron/inference/sampler.py:6-62 in one launch.
+//
+// One 1024-thread workgroup per row of logits [M, V] (V <= 65536 bf16,
+// 32768 fp32). The row lives in registers (thread t holds the 8-element
+// groups 8 (t + 1024 g) .. + 7, so a group load is one 16- or 32-byte access
+// and the index order is (g, thread, element)). Steps, all inside the
+// workgroup:
+//
+//   y = float(x) / temperature          (sampler.py:16-18; skipped at 1.0)
+//   max, first argmax, tie count        (one block reduction)
+//   top-k  (sampler.py:20-24): keep y >= the k-th largest value, counting
+//          duplicates. The k-th largest is found by an MSB-first radix
+//          select over order-preserving 32-bit keys of y (four 8-bit digit
+//          passes, integer histograms in LDS).
+//   top-p  (sampler.py:26-34): sorted descending, a token is kept when the
+//          cumulative probability up to and including it is <= p, the first
+//          always kept. The masses exp(y - max) are held as 2^-40 fixed
+//          point (exact 64-bit integer sums, so the result does not depend
+//          on summation order); a radix select over the keys weighted by
+//          mass finds the boundary value kb = the largest value whose
+//          cumulative mass exceeds p. Values above kb are kept; of the
+//          tokens equal to kb the first r in index order are kept (the
+//          order a stable descending sort gives), r from the mass above kb.
+//   log_softmax of the filtered logits (sampler.py:56): (y - max) - log(Z),
+//          Z = sum over kept tokens of exp(y - max) in a fixed order.
+//   draw   top_k == 1: the first maximum (the reference draws among exactly
+//          tied maxima at random). Otherwise inverse CDF in index order over
+//          the kept fixed-point masses with a 64-bit uniform from SplitMix64
+//          (Steele, Lea and Flood, 2014) keyed by (seed, offset, row): the same
+//          distribution as torch.multinomial over softmax(filtered), not the
+//          same random stream.
+#include <climits>
+
+#include "tt_internal.h"
+
+namespace tt {
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr float kMassScale = 1099511627776.0f;  // 2^40
+typedef unsigned long long u64;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct SampleShared {
+  u64 hist[256];
+  u64 red[kWaves][8];
+  float fv[kWaves];
+  int iv[kWaves];
+  int cv[kWaves];
+  int nv[kWaves];
+  u64 bc[4];
+};
+
+// Order-preserving key: key(a) < key(b) iff a < b for non-NaN floats
+// (-0 is folded into +0, which compares equal to it).
+__device__ __forceinline__ uint32_t order_key(float y) {
+  const uint32_t b = __float_as_uint(y == 0.f ? 0.f : y);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ u64 splitmix64_mix(u64 z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// 64-bit uniform of (seed, offset, row): three chained SplitMix64 outputs.
+__device__ __forceinline__ u64 draw_u64(u64 seed, u64 offset, u64 row) {
+  constexpr u64 kGamma = 0x9E3779B97F4A7C15ull;
+  u64 h = splitmix64_mix(seed + kGamma);
+  h = splitmix64_mix(h + (offset + 1) * kGamma);
+  return splitmix64_mix(h + (row + 1) * kGamma);
+}
+
+__device__ __forceinline__ u64 mass_of(float y, float m) {
+  return (u64)rintf(expf(y - m) * kMassScale);
+}
+
+__device__ __forceinline__ u64 wave_sum_u64(u64 v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ u64 block_sum_u64(u64 v, SampleShared &sh) {
+  v = wave_sum_u64(v);
+  if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6][0] = v;
+  __syncthreads();
+  u64 t = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += sh.red[w][0];
+  __syncthreads();
+  return t;
+}
+
+// Sum in a fixed order: thread-sequential, xor butterfly, waves ascending.
+__device__ __forceinline__ float block_sum_f32(float v, SampleShared &sh) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) sh.fv[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += sh.fv[w];
+  __syncthreads();
+  return t;
+}
+
+// Wave 0: the largest digit d with sum_{d' >= d} hist[d'] >= need (the caller
+// guarantees the total reaches need); bc[0] = d, bc[1] = sum over d' > d.
+__device__ __forceinline__ void pick_digit(SampleShared &sh, u64 need) {
+  const int lane = threadIdx.x & 63;
+  u64 h[4];
+  u64 s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h[j] = sh.hist[255 - 4 * lane - j];
+    s += h[j];
+  }
+  u64 incl = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const u64 o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  const u64 excl = incl - s;
+  if (incl >= need && excl < need) {
+    u64 c = excl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (c + h[j] >= need) {
+        sh.bc[0] = (u64)(255 - 4 * lane - j);
+        sh.bc[1] = c;
+        break;
+      }
+      c += h[j];
+    }
+  }
+}
+
+// The row as this thread holds it: fp32 values, or (bf16 logits) the raw
+// bf16 pairs, two per register, converted and divided by the temperature at
+// each use (the division is exact-rounded, so every pass sees the same y).
+template <int EPT, bool kF32>
+struct Row {
+  static constexpr int kRegs = kF32 ? EPT : EPT / 2;
+  uint32_t w[kRegs];
+  int t;  // thread index
+  int V;
+  int apply_temp;
+  float temperature;
+  __device__ __forceinline__ int index(int g, int e) const { return 8 * (t + kThreads * g) + e; }
+  __device__ __forceinline__ float val(int j) const {
+    float x;
+    if (kF32)
+      x = __uint_as_float(w[j]);
+    else
+      x = __uint_as_float((j & 1) ? (w[j >> 1] & 0xffff0000u) : (w[j >> 1] << 16));
+    return apply_temp ? x / temperature : x;
+  }
+  // Start of a pass over the row: the values and the thread index count as
+  // redefined here, so the compiler recomputes keys, masses and index
+  // comparisons per pass instead of keeping them all live across passes
+  // (which would not fit in the register budget).
+  __device__ __forceinline__ void pass() {
+#pragma unroll
+    for (int j = 0; j < kRegs; ++j) asm volatile("" : "+v"(w[j]));
+    asm volatile("" : "+v"(t));
+  }
+};
+
+// MSB-first radix select over the keys weighted by wfn(idx, y) (zero for
+// the -inf padding past V): the largest key kb with sum_{key >= kb} weight
+// >= need.
+// above = sum_{key > kb} weight, at = sum_{key == kb} weight.
+template <int EPT, bool kF32, class WeightFn>
+__device__ __forceinline__ uint32_t radix_select(SampleShared &sh, Row<EPT, kF32> &r, u64 need, WeightFn wfn,
+                                                 u64 &above, u64 &at) {
+  uint32_t prefix = 0, mask = 0;
+  above = 0;
+  at = 0;
+#pragma unroll 1
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    if (threadIdx.x < 256) sh.hist[threadIdx.x] = 0;
+    __syncthreads();
+    r.pass();
+#pragma unroll
+    for (int g = 0; g < EPT / 8; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = r.index(g, e);
+        const float v = r.val(8 * g + e);
+        const uint32_t key = order_key(v);
+        if ((key & mask) == prefix) {
+          const u64 w = wfn(idx, v);
+          if (w) atomicAdd(&sh.hist[(key >> shift) & 255u], w);
+        }
+      }
+    __syncthreads();
+    if (threadIdx.x < 64) pick_digit(sh, need);
+    __syncthreads();
+    const uint32_t d = (uint32_t)sh.bc[0];
+    const u64 ab = sh.bc[1];
+    at = sh.hist[d];
+    above += ab;
+    need -= ab;
+    prefix |= d << shift;
+    mask |= 0xFFu << shift;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// First index (in index order) at which the running sum of wfn(idx, y)
+// exceeds target (weights zero for the -inf padding); the caller guarantees
+// target < the total.
+template <int EPT, bool kF32, class WeightFn>
+__device__ __forceinline__ int find_first_exceeding(SampleShared &sh, Row<EPT, kF32> &r, u64 target, WeightFn wfn) {
+  constexpr int G = EPT / 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  u64 s[G];
+  r.pass();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    s[g] = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[g] += wfn(r.index(g, e), r.val(8 * g + e));
+    }
+    const u64 t = wave_sum_u64(s[g]);
+    if (lane == 0) sh.red[wave][g] = t;
+  }
+  __syncthreads();
+  int gs = -1, ws = -1;
+  u64 cum = 0;
+#pragma unroll 1
+  for (int g = 0; g < G && gs < 0; ++g)
+#pragma unroll 1
+    for (int w = 0; w < kWaves; ++w) {
+      const u64 t = sh.red[w][g];
+      if (cum + t > target) {
+        gs = g;
+        ws = w;
+        break;
+      }
+      cum += t;
+    }
+  if (wave == ws) {
+    const u64 rel = target - cum;
+    u64 sv = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (g == gs) sv = s[g];
+    u64 incl = sv;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const u64 o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    const u64 excl = incl - sv;
+    if (incl > rel && excl <= rel) {
+      r.pass();
+      u64 c = excl;
+      int found = -1;
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (g == gs) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int idx = r.index(g, e);
+            const u64 w = wfn(idx, r.val(8 * g + e));
+            if (found < 0 && c + w > rel) found = idx;
+            c += w;
+          }
+        }
+      sh.bc[2] = (u64)found;
+    }
+  }
+  __syncthreads();
+  const int res = (int)sh.bc[2];
+  __syncthreads();
+  return res;
+}
+
+template <int EPT, bool kF32>
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
+  __shared__ SampleShared sh;
+  constexpr int G = EPT / 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = blockIdx.x;
+  Row<EPT, kF32> r;
+  r.t = threadIdx.x;
+  r.V = a.V;
+  r.apply_temp = a.apply_temp;
+  r.temperature = a.temperature;
+
+  // Row into registers; elements past V read nothing and hold -inf.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int base = r.index(g, 0);
+    if (kF32) {
+      const float *src = static_cast<const float *>(a.logits) + (int64_t)row * a.ld + base;
+      if (a.vec && base + 8 <= a.V) {
+        const u32x4 lo = *reinterpret_cast<const u32x4 *>(src);
+        const u32x4 hi = *reinterpret_cast<const u32x4 *>(src + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          r.w[8 * g + e] = lo[e];
+          r.w[8 * g + 4 + e] = hi[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r.w[8 * g + e] = base + e < a.V ? __float_as_uint(src[e]) : 0xff800000u;
+      }
+    } else {
+      const uint16_t *src = static_cast<const uint16_t *>(a.logits) + (int64_t)row * a.ld + base;
+      if (a.vec && base + 8 <= a.V) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(src);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r.w[4 * g + e] = v[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = base + 2 * e < a.V ? src[2 * e] : 0xff80u;
+          const uint32_t hi = base + 2 * e + 1 < a.V ? src[2 * e + 1] : 0xff80u;
+          r.w[4 * g + e] = lo | (hi << 16);
+        }
+      }
+    }
+  }
+
+  // Maximum, its first index and its multiplicity; the number of finite values.
+  float bm = -INFINITY;
+  int bi = INT_MAX, bcnt = 0, nfin = 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int idx = r.index(g, e);
+      const float v = r.val(8 * g + e);
+      if (idx < a.V) {
+        nfin += v > -INFINITY;
+        if (bi == INT_MAX || v > bm) {
+          bm = v;
+          bi = idx;
+          bcnt = 1;
+        } else if (v == bm) {
+          ++bcnt;
+        }
+      }
+    }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bm, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    const int oc = __shfl_xor(bcnt, off, 64);
+    nfin += __shfl_xor(nfin, off, 64);
+    if (ov > bm || (bi == INT_MAX && oi != INT_MAX)) {
+      bm = ov;
+      bi = oi;
+      bcnt = oc;
+    } else if (ov == bm && oi != INT_MAX) {
+      bi = oi < bi ? oi : bi;
+      bcnt += oc;
+    }
+  }
+  if (lane == 0) {
+    sh.fv[wave] = bm;
+    sh.iv[wave] = bi;
+    sh.cv[wave] = bcnt;
+    sh.nv[wave] = nfin;
+  }
+  __syncthreads();
+  float m = -INFINITY;
+  int amax = INT_MAX, cmax = 0, nfinite = 0;
+#pragma unroll 1
+  for (int w = 0; w < kWaves; ++w) {
+    nfinite += sh.nv[w];
+    const float ov = sh.fv[w];
+    const int oi = sh.iv[w];
+    if (oi == INT_MAX) continue;
+    if (amax == INT_MAX || ov > m) {
+      m = ov;
+      amax = oi;
+      cmax = sh.cv[w];
+    } else if (ov == m) {
+      amax = oi < amax ? oi : amax;
+      cmax += sh.cv[w];
+    }
+  }
+  __syncthreads();
+
+  const bool greedy = a.top_k == 1;
+  const bool do_topk = a.top_k > 0 && a.top_k < a.V;
+  const bool fast = greedy && cmax == 1;
+
+  // top-k threshold key (0 keeps every element). With at most k finite
+  // values the k-th largest is the smallest finite one or -inf, and every
+  // finite value is kept.
+  uint32_t thrk = 0;
+  if (do_topk && !fast) {
+    if (greedy) {
+      thrk = order_key(m);
+    } else if (nfinite > a.top_k) {
+      u64 ab, at;
+      thrk = radix_select(
+          sh, r, (u64)a.top_k, [](int, float v) { return v > -INFINITY ? (u64)1 : (u64)0; }, ab, at);
+    }
+  }
+  auto kept_k = [&](float v) { return order_key(v) >= thrk; };
+
+  // top-p boundary: keys above kb kept, key == kb kept up to index ir.
+  uint32_t kb = 0;
+  int ir = INT_MAX;
+  const bool do_topp = a.apply_top_p && !fast;
+  if (do_topp) {
+    u64 local = 0;
+    r.pass();
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = r.val(8 * g + e);
+        if (kept_k(v)) local += mass_of(v, m);
+      }
+    const u64 etot = block_sum_u64(local, sh);
+    const u64 T = (u64)((double)a.top_p * (double)etot);
+    u64 ab, at;
+    kb = radix_select(
+        sh, r, T + 1, [&](int, float v) { return kept_k(v) ? mass_of(v, m) : (u64)0; }, ab, at);
+    const u64 eb = mass_of(key_value(kb), m);
+    u64 keep_n = eb > 0 && T >= ab ? (T - ab) / eb : 0;
+    if (ab == 0 && keep_n == 0) keep_n = 1;  // the first sorted token is always kept
+    if (keep_n == 0) {
+      ir = -1;
+    } else if (eb > 0 && keep_n < at / eb) {
+      ir = find_first_exceeding(sh, r, keep_n - 1, [&](int, float v) {
+        return (kept_k(v) && order_key(v) == kb) ? (u64)1 : (u64)0;
+      });
+    }
+  }
+  auto keep = [&](int idx, float v) {
+    if (fast) return idx == amax;
+    if (!kept_k(v)) return false;
+    if (!do_topp) return true;
+    const uint32_t k = order_key(v);
+    return k > kb || (k == kb && idx <= ir);
+  };
+
+  // log Z over the kept tokens.
+  float zl = 0.f;
+  if (!fast) {
+    r.pass();
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = r.index(g, e);
+        const float v = r.val(8 * g + e);
+        if (keep(idx, v)) zl += expf(v - m);
+      }
+  }
+  const float logz = fast ? 0.f : logf(block_sum_f32(zl, sh));
+
+  int tok = amax;
+  if (!greedy) {
+    u64 local = 0;
+    r.pass();
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = r.index(g, e);
+        const float v = r.val(8 * g + e);
+        if (keep(idx, v)) local += mass_of(v, m);
+      }
+    const u64 wtot = block_sum_u64(local, sh);
+    const u64 target = __umul64hi(draw_u64(a.seed, a.offset, (u64)row), wtot);
+    tok = find_first_exceeding(sh, r, target, [&](int idx, float v) { return keep(idx, v) ? mass_of(v, m) : (u64)0; });
+  }
+
+  // Outputs: the token (and its log-probability) from the thread holding it,
+  // the full log-probabilities of the filtered logits from every thread.
+  if ((int)threadIdx.x == ((tok >> 3) & (kThreads - 1))) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (r.index(g, e) == tok) {
+          a.tokens[row] = tok;
+          if (a.token_logprob) a.token_logprob[row] = (r.val(8 * g + e) - m) - logz;
+        }
+  }
+  if (a.logprobs) {
+    r.pass();
+    float *dst_row = a.logprobs + (int64_t)row * a.ld_lp;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int base = r.index(g, 0);
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = r.val(8 * g + e);
+        o[e] = keep(base + e, v) ? (v - m) - logz : -INFINITY;
+      }
+      if (a.vec_out && base + 8 <= a.V) {
+        *reinterpret_cast<f32x4 *>(dst_row + base) = f32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<f32x4 *>(dst_row + base + 4) = f32x4{o[4], o[5], o[6], o[7]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (base + e < a.V) dst_row[base + e] = o[e];
+      }
+    }
+  }
+}
+
+template <int EPT, bool kF32>
+hipError_t launch_ept(const SampleArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((sample_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Rows up to 65536 (bf16) / 32768 (fp32) values: fp32 rows of 64 values per
+// thread would not fit in the registers of a 1024-thread workgroup.
+hipError_t launch_sample(const SampleArgs &a, bool f32, hipStream_t stream) {
+  if (a.M == 0) return hipSuccess;
+  if (f32) {
+    if (a.V > kMaxSampleVocabF32) return hipErrorInvalidValue;
+    if (a.V <= 8 * kThreads) return launch_ept<8, true>(a, stream);
+    if (a.V <= 16 * kThreads) return launch_ept<16, true>(a, stream);
+    return launch_ept<32, true>(a, stream);
+  }
+  if (a.V > kMaxSampleVocabBF16) return hipErrorInvalidValue;
+  if (a.V <= 8 * kThreads) return launch_ept<8, false>(a, stream);
+  if (a.V <= 16 * kThreads) return launch_ept<16, false>(a, stream);
+  if (a.V <= 32 * kThreads) return launch_ept<32, false>(a, stream);
+  return launch_ept<64, false>(a, stream);
+}
+
+}  // namespace tt

@@ -98,6 +98,29 @@ struct PrefillArgs : DecodeArgs {
 
 hipError_t launch_prefill_attn(const PrefillArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
 
+// Token sampling: one workgroup per row of logits [M, V] (bf16 or fp32).
+struct SampleArgs {
+  const void *logits;
+  int64_t ld;           // row stride (elements)
+  int M, V;             // V <= kMaxSampleVocabBF16 / kMaxSampleVocabF32
+  int vec;              // rows 16-byte aligned: group loads are vector loads
+  float temperature;
+  int apply_temp;       // temperature != 1
+  int top_k;            // <= 0: no top-k
+  float top_p;
+  int apply_top_p;      // 0 < top_p < 1
+  uint64_t seed, offset;
+  int64_t *tokens;      // [M]
+  float *token_logprob; // [M] or null
+  float *logprobs;      // [M, ld_lp] log-probabilities of the filtered logits, or null
+  int64_t ld_lp;
+  int vec_out;
+};
+
+constexpr int kMaxSampleVocabBF16 = 65536;
+constexpr int kMaxSampleVocabF32 = 32768;
+hipError_t launch_sample(const SampleArgs &a, bool f32, hipStream_t stream);
+
 // Partition helpers shared by the ABI layer and the launchers.
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);
 inline int64_t num_splits(int64_t max_len, int64_t split_tokens) {

@@ -415,3 +415,44 @@ def prefill_attention(q: torch.Tensor, layout: KVLayout, positions: torch.Tensor
         st = lib.tt_prefill_attn_bf16(*head, *tail)
     _lib.check(st, "prefill_attention")
     return out
+
+
+SAMPLE_MAX_VOCAB = {torch.bfloat16: 65536, torch.float32: 32768}
+
+
+def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
+                  top_p: float | None = None, seed: int = 0, offset: int = 0, return_logprob: bool = False,
+                  return_logprobs: bool = False, out: torch.Tensor | None = None):
+    """One token per row of ``logits`` [M, V] (bf16 or fp32, last dim contiguous).
+
+    filter_logits + sample_next_token / sample_next_token_with_log_prob
+    (tinytron/inference/sampler.py:6-62) in one kernel launch: temperature,
+    top-k, top-p, then top_k == 1 takes the first maximum and otherwise a
+    draw from softmax(filtered) keyed by (seed, offset, row). Returns tokens
+    int64 [M]; with ``return_logprob`` also the chosen tokens' log-probabilities
+    [M]; with ``return_logprobs`` also log_softmax of the filtered logits
+    [M, V] (-inf where filtered)."""
+    _require_cuda(logits)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be a 2-D view [M, V] with a contiguous last dimension")
+    if logits.dtype not in SAMPLE_MAX_VOCAB:
+        raise ValueError(f"logits must be bf16 or fp32, got {logits.dtype}")
+    M, V = logits.shape
+    dev = logits.device
+    if out is None:
+        out = torch.empty(M, dtype=torch.int64, device=dev)
+    elif out.dtype != torch.int64 or out.shape != (M,) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int64 [M] tensor")
+    lp = torch.empty(M, dtype=torch.float32, device=dev) if return_logprob else None
+    full = torch.empty(M, V, dtype=torch.float32, device=dev) if return_logprobs else None
+    fn = _lib.load().tt_sample_bf16 if logits.dtype == torch.bfloat16 else _lib.load().tt_sample_f32
+    st = fn(_ptr(logits), logits.stride(0), M, V, float(temperature), int(top_k or 0),
+            1.0 if top_p is None else float(top_p), int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
+            _ptr(out), _ptr(lp), _ptr(full), V, _stream(dev))
+    _lib.check(st, "sample_tokens")
+    res = (out,)
+    if return_logprob:
+        res += (lp,)
+    if return_logprobs:
+        res += (full,)
+    return res[0] if len(res) == 1 else res

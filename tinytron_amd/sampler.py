@@ -1,15 +1,53 @@
 """Token sampling on the device (tinytron/inference/sampler.py:6-62).
 
-Same filtering as the reference: fp32 cast, temperature, top-k keeps values
->= the k-th largest, top-p drops sorted tokens whose cumulative probability
-exceeds p (the first always kept). With top_k == 1 every token but the
-maximum gets probability 0, so sampling is the argmax; that case skips the
-softmax and multinomial draw (identical result except between exactly tied
-maxima, where the reference picks at random and this picks the first).
+``sample_next_token`` and ``sample_next_token_with_log_prob`` keep the
+reference's signatures and run as one kernel launch per call
+(``ops.sample_tokens``): fp32 cast, temperature, top-k (values >= the k-th
+largest, ties kept), top-p (the shortest descending prefix whose cumulative
+probability exceeds p, the first token always kept; equal values ordered by
+index), then the draw. With top_k == 1 every token but the maximum has
+probability 0, so the token is the argmax (the first of exactly tied maxima,
+where the reference picks one at random). Other settings draw from
+softmax(filtered) with a counter-based generator keyed by (seed, offset,
+row): the reference's distribution, not torch.multinomial's random stream.
+Each call takes its seed from torch's default generator (so
+``torch.manual_seed`` makes runs repeatable, as in the reference) unless
+``manual_seed`` here fixes one.
+
+``filter_logits`` restates the reference's op sequence on the device for
+callers that want the filtered logits themselves.
 """
 from __future__ import annotations
 
 import torch
+
+from . import ops
+
+
+class _SamplerState:
+    """Where the device sampler's (seed, offset) come from."""
+
+    def __init__(self):
+        self.seed: int | None = None
+        self.offset = 0
+
+    def next(self) -> tuple[int, int]:
+        if self.seed is None:
+            # one 63-bit draw from torch's default (CPU) generator per call:
+            # torch.manual_seed makes the sequence of calls repeatable
+            return int(torch.randint(0, 2 ** 63 - 1, (1,)).item()), 0
+        off = self.offset
+        self.offset += 1
+        return self.seed, off
+
+
+_STATE = _SamplerState()
+
+
+def manual_seed(seed: int | None) -> None:
+    """Fix the sampler's seed, call n using offset n (None: draw from torch's generator)."""
+    _STATE.seed = None if seed is None else int(seed)
+    _STATE.offset = 0
 
 
 def filter_logits(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
@@ -34,19 +72,29 @@ def filter_logits(logits: torch.Tensor, temperature: float = 1.0, top_k: int | N
     return logits
 
 
+def _rows(logits: torch.Tensor) -> torch.Tensor:
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [B, V], got shape={tuple(logits.shape)}")
+    if logits.dtype not in ops.SAMPLE_MAX_VOCAB:
+        logits = logits.float()
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    return logits
+
+
 def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
                       top_p: float | None = None) -> torch.Tensor:
-    if top_k == 1 and temperature > 0:
-        return torch.argmax(logits, dim=-1)
-    probs = torch.softmax(filter_logits(logits, temperature, top_k, top_p), dim=-1)
-    return torch.multinomial(probs, num_samples=1).squeeze(-1)
+    """sampler.py:39-48: next token ids [B] (int64) from logits [B, V]."""
+    if temperature <= 0:
+        raise ValueError("temperature must be > 0")
+    seed, off = _STATE.next()
+    return ops.sample_tokens(_rows(logits), temperature, top_k, top_p, seed, off)
 
 
 def sample_next_token_with_log_prob(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
                                     top_p: float | None = None):
-    log_probs = torch.log_softmax(filter_logits(logits, temperature, top_k, top_p), dim=-1)
-    if top_k == 1:
-        token = torch.argmax(log_probs, dim=-1)
-    else:
-        token = torch.multinomial(log_probs.exp(), num_samples=1).squeeze(-1)
-    return token, log_probs.gather(-1, token.unsqueeze(-1)).squeeze(-1)
+    """sampler.py:51-62: token ids [B] and their log-probabilities under the filtered distribution."""
+    if temperature <= 0:
+        raise ValueError("temperature must be > 0")
+    seed, off = _STATE.next()
+    return ops.sample_tokens(_rows(logits), temperature, top_k, top_p, seed, off, return_logprob=True)
