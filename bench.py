@@ -107,7 +107,7 @@ def e2e_c5(args, torch):
                     "random-init weights, B 64, prompts U[64, 2048], paged KV page 16",
         "decode_tokens_per_sec": round(tps, 1),
         "decode_tokens_per_sec_graphs": graph_tps,
-        "decode_path": "fused bf16 decode step (10 launches per layer), eager launches; "
+        "decode_path": "fused bf16 decode step (10 launches per layer) + one-launch sampler, eager launches; "
                        "decode_tokens_per_sec_graphs replays it from HIP graphs (capture timed)",
         "decode_steps": int(stats["decode_tokens"] // B),
         "prefill_tokens_per_sec": round(stats["prefill_tokens_per_sec"], 1),
@@ -115,12 +115,48 @@ def e2e_c5(args, torch):
         "hbm_bound_tokens_per_sec": round(bound, 1),
         "frac_of_hbm_bound": round(tps / bound, 4),
         "cpu_baseline": None,
+        "sampler": sampler_timing(torch),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = e2e_cpu_baseline(model, cfg, prompt, lens, torch)
     del eng, model
     torch.cuda.empty_cache()
     return out
+
+
+def sampler_timing(torch, iters=50):
+    """Microseconds per call of the one-launch sampler on C5's logits
+    ([64, 32000] bf16) beside the reference's op sequence on the same device
+    (filter_logits + softmax + multinomial, sampler.py:6-48)."""
+    from tinytron_amd import ops
+    from tinytron_amd.sampler import filter_logits
+
+    g = torch.Generator().manual_seed(0)
+    logits = (torch.randn(C5["batch"], C5["vocab_size"], generator=g) * 3).to(torch.bfloat16).cuda()
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) * 1e3 / iters, 2)
+
+    def ref(t, k, p):
+        return torch.multinomial(torch.softmax(filter_logits(logits, t, k, p), dim=-1), 1)
+
+    return {
+        "logits": "[64, 32000] bf16",
+        "greedy_us": timed(lambda: ops.sample_tokens(logits, top_k=1)),
+        "top_k50_top_p0.9_T0.8_us": timed(lambda: ops.sample_tokens(logits, 0.8, 50, 0.9, 1, 0)),
+        "top_p0.9_logprob_us": timed(lambda: ops.sample_tokens(logits, 1.0, None, 0.9, 1, 0, return_logprob=True)),
+        "reference_ops_greedy_us": timed(lambda: ref(1.0, 1, None)),
+        "reference_ops_top_k50_top_p0.9_T0.8_us": timed(lambda: ref(0.8, 50, 0.9)),
+    }
 
 
 def e2e_cpu_baseline(model, cfg, prompt, lens, torch, n_seq=2, n_steps=8):

@@ -302,31 +302,51 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   r.apply_temp = a.apply_temp;
   r.temperature = a.temperature;
 
-  // Row into registers; elements past V read nothing and hold -inf.
+  // Row into registers; elements past V read nothing and hold -inf. Every
+  // full group's vector load is issued before any is used (a partial or
+  // empty group loads the row's first group instead, always in bounds), so
+  // the row costs one memory round trip; the one partial group of the row
+  // then reads its elements one by one.
+  const char *rowp = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (kF32 ? 4 : 2);
+  if (a.vec) {
+    constexpr int kVec = kF32 ? 2 : 1;  // 16-byte loads per group
+    u32x4 raw[G][kVec];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int base = r.index(g, 0);
+      const char *src = rowp + (base + 8 <= a.V ? base : 0) * (kF32 ? 4 : 2);
+#pragma unroll
+      for (int h = 0; h < kVec; ++h) raw[g][h] = *reinterpret_cast<const u32x4 *>(src + 16 * h);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int base = r.index(g, 0);
+      if (base + 8 <= a.V) {
+#pragma unroll
+        for (int h = 0; h < kVec; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r.w[(kF32 ? 8 : 4) * g + 4 * h + e] = raw[g][h][e];
+      } else {
+#pragma unroll
+        for (int j = 0; j < Row<EPT, kF32>::kRegs / G; ++j) r.w[(Row<EPT, kF32>::kRegs / G) * g + j] = kF32 ? 0xff800000u : 0xff80ff80u;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < Row<EPT, kF32>::kRegs; ++j) r.w[j] = kF32 ? 0xff800000u : 0xff80ff80u;
+  }
+  // The partial group (at most one per row), or every group for rows that
+  // are not 16-byte aligned: element loads.
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int base = r.index(g, 0);
-    if (kF32) {
-      const float *src = static_cast<const float *>(a.logits) + (int64_t)row * a.ld + base;
-      if (a.vec && base + 8 <= a.V) {
-        const u32x4 lo = *reinterpret_cast<const u32x4 *>(src);
-        const u32x4 hi = *reinterpret_cast<const u32x4 *>(src + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          r.w[8 * g + e] = lo[e];
-          r.w[8 * g + 4 + e] = hi[e];
-        }
-      } else {
+    if ((!a.vec && base < a.V) || (base < a.V && base + 8 > a.V)) {
+      if (kF32) {
+        const float *src = reinterpret_cast<const float *>(rowp) + base;
 #pragma unroll
         for (int e = 0; e < 8; ++e) r.w[8 * g + e] = base + e < a.V ? __float_as_uint(src[e]) : 0xff800000u;
-      }
-    } else {
-      const uint16_t *src = static_cast<const uint16_t *>(a.logits) + (int64_t)row * a.ld + base;
-      if (a.vec && base + 8 <= a.V) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(src);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r.w[4 * g + e] = v[e];
       } else {
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(rowp) + base;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t lo = base + 2 * e < a.V ? src[2 * e] : 0xff80u;
