@@ -48,8 +48,21 @@ __device__ __forceinline__ const uint16_t *wfrag_base(const SkinnyGemmArgs &a, i
   return a.w + (int64_t)(nb * 16 + (lane & 15)) * a.ldw + k + 8 * (lane >> 4);
 }
 
+// Workgroups of this shape meant to share a CU (bounded by the x chunk's LDS
+// footprint, 64 x (KC + 8) x 2 bytes), and the waves per SIMD the register
+// allocation must leave room for so that they can.
+constexpr int gemm_wgs_per_cu(int kc, int waves) {
+  return kc == 256 ? (waves <= 4 ? 4 : waves <= 8 ? 2 : 1) : kc == 512 ? (waves <= 8 ? 2 : 1) : 1;
+}
+
 template <int KC, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void skinny_gemm_kernel(SkinnyGemmArgs a) {
+constexpr int gemm_min_waves() {
+  const int w = (WAVES * gemm_wgs_per_cu(KC, WAVES) + 3) / 4;
+  return w < 1 ? 1 : w > 4 ? 4 : w;
+}
+
+template <int KC, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, (gemm_min_waves<KC, WAVES>())) void skinny_gemm_kernel(SkinnyGemmArgs a) {
   constexpr int KSTEPS = KC / 32;
   constexpr int ROW = KC + 8;  // padded LDS row (elements): 16 consecutive rows hit distinct banks
   __shared__ __attribute__((aligned(16))) uint16_t xs[64 * ROW];
@@ -59,6 +72,22 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_gemm_kernel(SkinnyGemmArgs 
   const int64_t k0 = (int64_t)blockIdx.y * KC;
   const int m0 = blockIdx.z * 64;
 
+  // x rows m0 .. m0 + 63 of the chunk (L2-resident, rows past M are zero)
+  // are loaded before the weights: vector loads return in issue order, so
+  // x issued first can go to LDS while the weight stream is still in flight.
+  constexpr int XN = 64 * (KC / 8);                        // 16-byte pieces of the x chunk
+  constexpr int XL = (XN + 64 * WAVES - 1) / (64 * WAVES);  // per thread
+  u32x4 xr[XL];
+#pragma unroll
+  for (int j = 0; j < XL; ++j) {
+    const int i = threadIdx.x + j * 64 * WAVES;
+    const int r = i / (KC / 8);
+    const int c = i - r * (KC / 8);
+    xr[j] = u32x4{0u, 0u, 0u, 0u};
+    if ((XN % (64 * WAVES) == 0 || i < XN) && m0 + r < a.M)
+      xr[j] = *reinterpret_cast<const u32x4 *>(a.x + (int64_t)(m0 + r) * a.ldx + k0 + 8 * c);
+  }
+
   // This wave's weight fragments for the whole chunk: lane (i + 16g) holds
   // W[n0 + i][k0 + 32 s + 8 g .. + 8] for k step s.
   int wstep;
@@ -67,13 +96,12 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_gemm_kernel(SkinnyGemmArgs 
 #pragma unroll
   for (int s = 0; s < KSTEPS; ++s) wf[s] = *reinterpret_cast<const u32x4 *>(wrow + wstep * s);
 
-  // x rows m0 .. m0 + 63 of the chunk into LDS (rows past M are zero).
-  for (int i = threadIdx.x; i < 64 * (KC / 8); i += blockDim.x) {
+#pragma unroll
+  for (int j = 0; j < XL; ++j) {
+    const int i = threadIdx.x + j * 64 * WAVES;
     const int r = i / (KC / 8);
     const int c = i - r * (KC / 8);
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (m0 + r < a.M) v = *reinterpret_cast<const u32x4 *>(a.x + (int64_t)(m0 + r) * a.ldx + k0 + 8 * c);
-    *reinterpret_cast<u32x4 *>(xs + r * ROW + 8 * c) = v;
+    if (XN % (64 * WAVES) == 0 || i < XN) *reinterpret_cast<u32x4 *>(xs + r * ROW + 8 * c) = xr[j];
   }
   __syncthreads();
 
@@ -212,15 +240,17 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
 }  // namespace
 
 hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream) {
-  // 8 waves (128 weight rows) share one staged x chunk when that still gives
-  // every CU a workgroup; otherwise 4 waves (64 rows)
+  // 8 waves (128 weight rows) share one staged x chunk when that still puts
+  // a workgroup on at least 3/4 of the CUs; otherwise 4 waves (64 rows).
+  // (Measured on the decode-step shapes: two 8-wave workgroups on some CUs
+  // beat one 12-wave workgroup on every CU; 6- and 12-wave groups lost.)
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
   }
   const int splits = a.K / kc, mt = (a.M + 63) / 64;
-  const bool wide = a.N % 128 == 0 && (int64_t)(a.N / 128) * splits * mt >= cus;
+  const bool wide = a.N % 128 == 0 && 4 * (int64_t)(a.N / 128) * splits * mt >= 3 * (int64_t)cus;
   const dim3 grid((unsigned)(a.N / (wide ? 128 : 64)), (unsigned)splits, (unsigned)mt);
 #define TT_GEMM_LAUNCH(KC, W) hipLaunchKernelGGL((skinny_gemm_kernel<KC, W>), grid, dim3(64 * W), 0, stream, a)
   if (kc == 256) {
