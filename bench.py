@@ -48,7 +48,10 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--step-path", choices=["auto", "fused", "two"], default="auto",
+                   help="decode step as one launch pair (RoPE + append inside the attention kernel) or as the "
+                        "RoPE + append kernel then attention; auto: fused for bf16 caches, two launches for fp8")
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     p.add_argument("--seed", type=int, default=1337)
     p.add_argument("--split-tokens", type=int, default=0)
@@ -381,7 +384,19 @@ def main():
     calib_dst = torch.empty_like(calib)
     calib_dst.copy_(calib)
 
+    lens_out = torch.empty_like(wl["positions"])
+    fused = args.step_path == "fused" or (args.step_path == "auto" and not cfg["fp8"])
+
     def step():
+        # the fused decode step: RoPE + append of the new token inside the attention launch pair
+        if split or not fused:
+            two_launch_step()
+            return
+        ops.decode_attention_append(wl["rope"], wl["positions"], layout, wl["max_len"], q=wl["q_in"][:, :, 0],
+                                    k=wl["k_in"][:, :, 0], v=wl["v_in"][:, :, 0], lens_out=lens_out, out=out,
+                                    workspace=ws)
+
+    def two_launch_step():
         ops.rope_append(wl["q_in"], wl["k_in"], wl["v_in"], wl["rope"], wl["positions"], layout, q_out=q_rot)
         ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
                              split_tokens=split, workspace=ws)
@@ -402,7 +417,17 @@ def main():
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / max(args.steps, 1)
 
-    # the dominant operator alone, same stream, same events
+    # the same step as two launches (RoPE + append kernel, then attention)
+    ev4 = torch.cuda.Event(enable_timing=True)
+    ev5 = torch.cuda.Event(enable_timing=True)
+    ev4.record()
+    for _ in range(args.steps):
+        two_launch_step()
+    ev5.record()
+    torch.cuda.synchronize()
+    two_ms = ev4.elapsed_time(ev5) / max(args.steps, 1)
+
+    # the dominant operator alone (q rotated by the step above), same stream, same events
     ev2 = torch.cuda.Event(enable_timing=True)
     ev3 = torch.cuda.Event(enable_timing=True)
     ev2.record()
@@ -424,6 +449,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_two_launches": round(two_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -435,6 +461,9 @@ def main():
             "batch": B, "q_heads": hq, "kv_heads": cfg["hkv"], "head_dim": D,
             "context": [cfg["lo"], cfg["hi"]], "page_size": cfg["page"], "paged": cfg["paged"],
             "cached_tokens": tokens, "split_tokens": split_used, "parallelism": "single GPU",
+            "step_path": ("one launch pair: RoPE + append inside the attention split kernel "
+                          "(decode_stream_append_kernel + decode_merge_kernel)" if fused and not split
+                          else "rope_append_kernel, then the attention kernels"),
         },
         "roofline": {
             "bound": "hbm",

@@ -296,6 +296,42 @@ int tt_prefill_attn_fp8(const void *q, const int64_t q_strides[3],
                         int64_t batch, int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads,
                         int64_t head_dim, int64_t page_size, float sm_scale, tt_stream_t stream);
 
+/*
+ * One decode step of attention with this step's RoPE + KV append folded into
+ * the attention launch: the result equals tt_rope_append_bf16 (one new token
+ * per sequence at position positions[b], lens_out = positions + 1) followed
+ * by tt_gqa_decode_attn_bf16 (split_tokens 0) over seq_lens = positions + 1,
+ * without the rotated q being written out. Replaces attn.py:397 (rope_impl),
+ * 308-312 + cache.py:41-44 (append) and attn.py:420-423 (SDPA) for T = 1.
+ * q_in / k_in / v_in are [B, H, D] with element strides {batch, head}: bf16
+ * activations (splits == 0), or with 1 <= splits <= 4 fp32 split-K partials
+ * of the projection (split stride split_stride), each element the bf16 sum of
+ * the splits in order. The wave that reads a segment's last tile writes that
+ * segment's new k / v first, so no other launch is needed. max_seq_len must
+ * bound positions[b] + 1 and the cache capacity. Balanced partition only
+ * (bf16 / fp8 caches); workspace as tt_decode_workspace_bytes(..., 0).
+ */
+int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                               const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                               int64_t splits, int64_t split_stride, const void *rope_table, int64_t rope_table_len,
+                               const int32_t *positions, int32_t *lens_out, int64_t max_seq_len,
+                               const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *k_cache,
+                               void *v_cache, const int64_t cache_strides[3], int64_t capacity, void *out,
+                               const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
+                               size_t workspace_bytes, tt_stream_t stream);
+
+/* As tt_decode_attn_append_bf16 with an fp8-e4m3fn cache (per-(token, head) scales written by the append). */
+int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                              const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                              int64_t splits, int64_t split_stride, const void *rope_table, int64_t rope_table_len,
+                              const int32_t *positions, int32_t *lens_out, int64_t max_seq_len,
+                              const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *k_cache,
+                              void *v_cache, float *k_scale, float *v_scale, const int64_t cache_strides[3],
+                              int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
+                              int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                              float sm_scale, void *workspace, size_t workspace_bytes, tt_stream_t stream);
+
 /* Fixed split size the fp32 entry point uses when split_tokens == 0. */
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 

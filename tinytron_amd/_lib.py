@@ -67,6 +67,21 @@ _ATTN_TAIL = [
     _vp,                                             # stream
 ]
 
+_DECODE_APPEND_HEAD = [
+    _vp, _i64p, _vp, _i64p, _vp, _i64p,             # q_in, k_in, v_in (+ {batch, head} strides)
+    _i64, _i64,                                      # splits, split_stride
+    _vp, _i64,                                       # rope_table, rope_table_len
+    _i32p, _i32p, _i64,                              # positions, lens_out, max_seq_len
+    _i32p, _i64, _i64,                               # page_table, max_pages, num_pages
+    _vp, _vp,                                        # k_cache, v_cache
+]
+_DECODE_APPEND_TAIL = [
+    _i64p, _i64,                                     # cache_strides, capacity
+    _vp, _i64p,                                      # out, out_strides
+    _i64, _i64, _i64, _i64, _i64,                    # batch, H_q, H_kv, head_dim, page_size
+    _f32, _vp, _size, _vp,                           # sm_scale, workspace, workspace_bytes, stream
+]
+
 _SAMPLE = [
     _vp, _i64, _i64, _i64,                           # logits, row stride, rows, vocab
     _f32, _i64, _f32,                                # temperature, top_k, top_p
@@ -95,6 +110,8 @@ SIGNATURES = {
     "tt_splitk_reduce_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_add_rmsnorm_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
     "tt_silu_mul_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
+    "tt_decode_attn_append_bf16": (_DECODE_APPEND_HEAD + _DECODE_APPEND_TAIL, ctypes.c_int),
+    "tt_decode_attn_append_fp8": (_DECODE_APPEND_HEAD + [_vp, _vp] + _DECODE_APPEND_TAIL, ctypes.c_int),
     "tt_sample_bf16": (_SAMPLE, ctypes.c_int),
     "tt_sample_f32": (_SAMPLE, ctypes.c_int),
 }

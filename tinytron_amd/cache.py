@@ -141,6 +141,31 @@ class _LayerCacheBase:
         self._host_lens = [a + 1 for a in self._host_lens]
         return q_rot
 
+    def decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rope_table: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+        """One-token RoPE + append + attention in one launch pair from bf16
+        q [B, H_q, D] and k / v [B, H_kv, D]; returns out [B, H_q, D] (the
+        two-launch rope_append + attend, bit for bit)."""
+        return self._decode_step(rope_table, out, q=q, k=k, v=v)
+
+    def decode_step_partials(self, partials: torch.Tensor, num_q_heads: int, rope_table: torch.Tensor,
+                             out: torch.Tensor | None = None) -> torch.Tensor:
+        """As decode_step with q|k|v given as the split-K partials [S, B, N] of
+        the stacked projection (summed and rounded inside the kernel)."""
+        return self._decode_step(rope_table, out, partials=partials, num_q_heads=num_q_heads)
+
+    def _decode_step(self, rope_table, out, **inputs) -> torch.Tensor:
+        self._check_room([1] * self.batch_size)
+        if self.workspace is None:
+            self.workspace = ops.Workspace(rope_table.device)
+        bound = self.static_max_len if self.static_max_len is not None else self.current_length + 1
+        nxt = 1 - self._cur
+        out = ops.decode_attention_append(rope_table, self._lens_dev[self._cur], self.layout, bound,
+                                          lens_out=self._lens_dev[nxt], out=out, workspace=self.workspace, **inputs)
+        self._cur = nxt
+        self._host_lens = [a + 1 for a in self._host_lens]
+        return out
+
     def prefill_attend(self, q_rot: torch.Tensor, new_lens, out: torch.Tensor | None = None) -> torch.Tensor:
         """Causal attention of the chunk just appended by rope_append (q_rot
         [B, H_q, T, D], new_lens[b] tokens of sequence b) over each sequence's

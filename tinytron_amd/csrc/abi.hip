@@ -162,9 +162,10 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
                   const int32_t *seq_lens, int64_t max_seq_len, const int32_t *page_table, int64_t max_pages,
                   int64_t num_pages, void *out, const int64_t out_strides[2], int64_t batch, int64_t num_q_heads,
                   int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
-                  void *workspace, size_t ws_bytes, tt_stream_t stream) {
-  TT_CHECK(q && k_cache && v_cache && seq_lens && out, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
-  TT_CHECK(q_strides && out_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
+                  void *workspace, size_t ws_bytes, tt_stream_t stream, const tt::DecodeAppend *ap = nullptr) {
+  // ap != null: the fused step (q / k / v from ap, seq_lens = lengths before the step)
+  TT_CHECK((ap || q) && k_cache && v_cache && seq_lens && out, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK((ap || q_strides) && out_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
   TT_CHECK(batch >= 0 && batch <= 65535, TT_ERR_INVALID_ARGUMENT, "batch must be in [0, 65535]");
   TT_CHECK(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, TT_ERR_INVALID_ARGUMENT,
            "num_attention_heads must be divisible by num_key_value_heads");
@@ -196,9 +197,9 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   if (kind != tt::CacheKind::kF32) {
     TT_CHECK(batch <= 4096, TT_ERR_UNSUPPORTED, "batch %lld > 4096 is not supported (per-sequence split table in LDS)",
              (long long)batch);
-    TT_CHECK(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
+    TT_CHECK((ap || aligned(q, 16)) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
              "q and cache pointers must be 16-byte aligned");
-    TT_CHECK(q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0, TT_ERR_INVALID_ARGUMENT,
+    TT_CHECK(ap || (q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0), TT_ERR_INVALID_ARGUMENT,
              "q strides must be multiples of 8 elements");
     TT_CHECK(cache_strides[0] % 8 == 0 && cache_strides[1] % 8 == 0 && cache_strides[2] % 8 == 0,
              TT_ERR_INVALID_ARGUMENT, "cache strides must be multiples of 8 elements");
@@ -229,8 +230,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
 
   tt::DecodeArgs a{};
   a.q = q;
-  a.q_sb = q_strides[0];
-  a.q_sh = q_strides[1];
+  a.q_sb = ap ? 0 : q_strides[0];
+  a.q_sh = ap ? 0 : q_strides[1];
   a.k_cache = k_cache;
   a.v_cache = v_cache;
   a.k_scale = k_scale;
@@ -261,7 +262,59 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.max_splits = (int)splits;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   (void)hipGetLastError();
+  if (ap != nullptr) {
+    tt::DecodeAppendArgs f{};
+    static_cast<tt::DecodeArgs &>(f) = a;
+    f.len_add = 1;
+    f.ap = *ap;
+    return from_hip(tt::launch_decode_attn_append(f, kind, (int)head_dim, (hipStream_t)stream),
+                    "fused decode attention launch");
+  }
   return from_hip(tt::launch_decode_attn(a, kind, (int)head_dim, (hipStream_t)stream), "decode attention launch");
+}
+
+// The fused decode step: RoPE + append of this step's token inside the
+// attention launch (q_in / k_in / v_in: bf16 [B, H, D] views, or with
+// splits > 0 fp32 split-K partials).
+int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                         const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                         int64_t splits, int64_t split_stride, const void *rope_table, int64_t rope_table_len,
+                         const int32_t *positions, int32_t *lens_out, int64_t max_seq_len, const int32_t *page_table,
+                         int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
+                         float *v_scale, const int64_t cache_strides[3], int64_t capacity, void *out,
+                         const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                         int64_t head_dim, int64_t page_size, float sm_scale, void *workspace, size_t ws_bytes,
+                         tt_stream_t stream) {
+  TT_CHECK(q_in && k_in && v_in && rope_table && positions, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(q_in_strides && k_in_strides && v_in_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
+  TT_CHECK(splits >= 0 && (splits == 0 || split_stride > 0), TT_ERR_INVALID_ARGUMENT, "bad split-K partial layout");
+  TT_CHECK(splits <= tt::kMaxApSplits, TT_ERR_UNSUPPORTED, "the fused step sums at most %d split-K partials, got %lld",
+           tt::kMaxApSplits, (long long)splits);
+  TT_CHECK(rope_table_len >= 1 && capacity >= 1, TT_ERR_INVALID_ARGUMENT, "empty RoPE table or cache");
+  TT_CHECK(max_seq_len >= 1 && max_seq_len <= capacity, TT_ERR_INVALID_ARGUMENT,
+           "max_seq_len must bound the lengths after the step (1 .. capacity)");
+  TT_CHECK(lens_out == nullptr || (const void *)lens_out != (const void *)positions, TT_ERR_INVALID_ARGUMENT,
+           "lens_out must not alias positions");
+  tt::DecodeAppend ap{};
+  ap.q_in = q_in;
+  ap.k_in = k_in;
+  ap.v_in = v_in;
+  ap.qi_sb = q_in_strides[0];
+  ap.qi_sh = q_in_strides[1];
+  ap.ki_sb = k_in_strides[0];
+  ap.ki_sh = k_in_strides[1];
+  ap.vi_sb = v_in_strides[0];
+  ap.vi_sh = v_in_strides[1];
+  ap.part_splits = (int)splits;
+  ap.part_stride = split_stride;
+  ap.table = rope_table;
+  ap.table_len = rope_table_len;
+  ap.lens_out = lens_out;
+  ap.capacity = capacity;
+  ap.page_size = page_size;
+  return decode_common(kind, nullptr, nullptr, k_cache, v_cache, k_scale, v_scale, cache_strides, positions,
+                       max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, ws_bytes, stream, &ap);
 }
 
 int linear_common(const void *x, int64_t ldx, const void *weight, int64_t ldw, int packed, float *partials,
@@ -613,6 +666,38 @@ int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t i
   return from_hip(tt::launch_silu_mul(partials, (int)splits, (int)m, (int)inter, static_cast<uint16_t *>(y),
                                       (hipStream_t)stream),
                   "silu_mul launch");
+}
+
+int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                               const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                               int64_t splits, int64_t split_stride, const void *rope_table, int64_t rope_table_len,
+                               const int32_t *positions, int32_t *lens_out, int64_t max_seq_len,
+                               const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *k_cache,
+                               void *v_cache, const int64_t cache_strides[3], int64_t capacity, void *out,
+                               const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
+                               size_t workspace_bytes, tt_stream_t stream) {
+  return decode_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
+                              splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
+                              page_table, max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides,
+                              capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                              sm_scale, workspace, workspace_bytes, stream);
+}
+
+int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                              const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                              int64_t splits, int64_t split_stride, const void *rope_table, int64_t rope_table_len,
+                              const int32_t *positions, int32_t *lens_out, int64_t max_seq_len,
+                              const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *k_cache,
+                              void *v_cache, float *k_scale, float *v_scale, const int64_t cache_strides[3],
+                              int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
+                              int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                              float sm_scale, void *workspace, size_t workspace_bytes, tt_stream_t stream) {
+  return decode_append_common(tt::CacheKind::kFP8, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
+                              splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
+                              page_table, max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides,
+                              capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                              sm_scale, workspace, workspace_bytes, stream);
 }
 
 int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,

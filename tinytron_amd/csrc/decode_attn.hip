@@ -38,6 +38,7 @@
 #include <algorithm>
 
 #include "attn_tiles.h"
+#include "rope_math.h"
 #include "tt_internal.h"
 #include "tt_numerics.h"
 
@@ -237,7 +238,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
   for (int i = 0; i < per; ++i) {
     const int b = first + i;
     if (b < B) {
-      const int L = max(min(a.seq_lens[b], a.max_len), 0);
+      const int L = max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
       if (lens != nullptr) lens[b] = L;
       local += (L + split_tokens - 1) / split_tokens;
     }
@@ -257,7 +258,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
     const int b = first + i;
     if (b < B) {
       prefix[b] = run;
-      const int L = lens != nullptr ? lens[b] : max(min(a.seq_lens[b], a.max_len), 0);
+      const int L = lens != nullptr ? lens[b] : max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
       run += (L + split_tokens - 1) / split_tokens;
     }
   }
@@ -415,9 +416,193 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
 }
 
 // Tiles [j0, j1) of segment (b, hk) (L tokens) by wave w: one partial to workspace slot (segment + w).
-template <int D, bool kFP8>
-__device__ __forceinline__ void stream_piece(const DecodeArgs &a, int b, int hk, int L, int j0, int j1, int64_t w,
-                                             int lane, char *vlds, const bf16x8 (&ident16)[2],
+// ---- fused RoPE + append (decode_stream_append_kernel) ----------------------
+
+// Element i of a q / k / v input row: the bf16 activation, or (kPartIn) the
+// bf16 sum of the split-K partials added in order (the projection's rounded
+// output). Branch-free, so the prologue's loads all go out before any wait:
+// kMaxApSplits loads (indices clamped in bounds; at most that many splits,
+// checked by the host) before the first add.
+
+template <bool kPartIn>
+struct ApRaw {
+  float v[kPartIn ? kMaxApSplits : 1];  // the splits, or the bf16 bits (low half) of the activation
+};
+
+template <bool kPartIn>
+__device__ __forceinline__ void ap_load(const DecodeAppend &ap, const void *p, int64_t i, ApRaw<kPartIn> &r) {
+  if constexpr (kPartIn) {
+    const float *f = static_cast<const float *>(p);
+    const int S = ap.part_splits;
+#pragma unroll
+    for (int s = 0; s < kMaxApSplits; ++s) r.v[s] = f[(int64_t)(s < S ? s : S - 1) * ap.part_stride + i];
+  } else {
+    r.v[0] = __uint_as_float((uint32_t)static_cast<const uint16_t *>(p)[i]);
+  }
+}
+
+template <bool kPartIn>
+__device__ __forceinline__ float ap_value(const DecodeAppend &ap, const ApRaw<kPartIn> &r) {
+  if constexpr (kPartIn) {
+    float acc = r.v[0];
+#pragma unroll
+    for (int s = 1; s < kMaxApSplits; ++s) acc = s < ap.part_splits ? acc + r.v[s] : acc;
+    return round_bf16(acc);
+  } else {
+    return __uint_as_float(__float_as_uint(r.v[0]) << 16);
+  }
+}
+
+// Start of a piece of the fused kernel, issued together with the piece's
+// first page-table load so that all of it costs one memory round trip (the
+// loads are unconditional, with clamped in-bounds addresses, so no wait is
+// forced between them):
+//  - with `append` (the piece holds its segment's last tile, which only this
+//    wave reads): RoPE of this step's k for (b, hk) at position pos and the
+//    append of k and v to the cache slot, with the arithmetic of
+//    rope_append_kernel (lane i < D/2 owns the pair (i, i + D/2)); skipped
+//    when the slot is outside the cache or the table, as that kernel skips it;
+//  - RoPE of the G query rows of (b, hk) into the wave's LDS staging area qs
+//    [G][D] (bf16), then the MFMA B fragments from it.
+template <int D, bool kFP8, bool kPartIn>
+__device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const DecodeAppend &ap, int b, int hk, int pos,
+                                               bool append, int lane, uint16_t *qs, bf16x8 (&qf)[D / 32]) {
+  constexpr int H = D / 2;
+  constexpr int kIt = 4;  // query pairs per lane per round (one round for G * D <= 512)
+  const int G = a.group;
+  const int pairs = G * H;
+  const bool in_table = pos >= 0 && pos < ap.table_len;
+  const int tp = pos < 0 ? 0 : (pos >= ap.table_len ? (int)ap.table_len - 1 : pos);  // in bounds
+  const uint16_t *tab = static_cast<const uint16_t *>(ap.table) + (int64_t)tp * D;
+  const bool active = lane < H;
+  const int li = lane & (H - 1);
+
+  // loads: append inputs and slot (always, in bounds), then the query inputs;
+  // all issued before the scheduling barrier, consumed after it
+  const int64_t ks = (int64_t)b * ap.ki_sb + (int64_t)hk * ap.ki_sh;
+  const int64_t vs = (int64_t)b * ap.vi_sb + (int64_t)hk * ap.vi_sh;
+  ApRaw<kPartIn> kr[4];
+  ap_load<kPartIn>(ap, ap.k_in, ks + li, kr[0]);
+  ap_load<kPartIn>(ap, ap.k_in, ks + H + li, kr[1]);
+  ap_load<kPartIn>(ap, ap.v_in, vs + li, kr[2]);
+  ap_load<kPartIn>(ap, ap.v_in, vs + H + li, kr[3]);
+  const uint32_t kc_raw = tab[li];
+  const uint32_t ks_raw = tab[H + li];
+  const int64_t jp = pos < 0 ? 0 : (int64_t)pos >> a.page_shift;
+  int64_t phys = 0;
+  if (a.page_table != nullptr)
+    phys = a.page_table[(int64_t)b * a.max_pages + (jp < a.max_pages ? jp : a.max_pages - 1)];
+  ApRaw<kPartIn> qr[kIt][2];
+  uint32_t c_raw[kIt], s_raw[kIt];
+  auto load_q = [&](int p0) {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int pr0 = p0 + lane + 64 * it;
+      const int pr = pr0 < pairs ? pr0 : pairs - 1;
+      const int h = pr / H;
+      const int i = pr - h * H;
+      const int64_t src = (int64_t)b * ap.qi_sb + (int64_t)(hk * G + h) * ap.qi_sh;
+      ap_load<kPartIn>(ap, ap.q_in, src + i, qr[it][0]);
+      ap_load<kPartIn>(ap, ap.q_in, src + H + i, qr[it][1]);
+      c_raw[it] = tab[i];
+      s_raw[it] = tab[H + i];
+    }
+  };
+  auto rope_q = [&](int p0) {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int pr = p0 + lane + 64 * it;
+      if (pr < pairs) {
+        const int h = pr / H;
+        const int i = pr - h * H;
+        float o1, o2;
+        rotate_pair<BF16Tag>(ap_value<kPartIn>(ap, qr[it][0]), ap_value<kPartIn>(ap, qr[it][1]),
+                             bf16_bits_to_f32((uint16_t)c_raw[it]), bf16_bits_to_f32((uint16_t)s_raw[it]), o1, o2);
+        qs[h * D + i] = f32_to_bf16_bits(o1);
+        qs[h * D + H + i] = f32_to_bf16_bits(o2);
+      }
+    }
+  };
+  load_q(0);
+  __builtin_amdgcn_sched_barrier(0);
+  const float k1x = ap_value<kPartIn>(ap, kr[0]);
+  const float k2x = ap_value<kPartIn>(ap, kr[1]);
+  const float v1 = ap_value<kPartIn>(ap, kr[2]);
+  const float v2 = ap_value<kPartIn>(ap, kr[3]);
+  const float kc = bf16_bits_to_f32((uint16_t)kc_raw);
+  const float ksn = bf16_bits_to_f32((uint16_t)ks_raw);
+
+  const bool do_append = append && in_table && pos < ap.capacity;
+  // the append
+  if (do_append) {
+    int64_t base = -1;
+    if (a.page_table != nullptr) {
+      phys = __builtin_amdgcn_readfirstlane((int)phys);
+      if (jp < a.max_pages && phys >= 0 && phys < a.num_pages)
+        base = phys * a.c_page + (int64_t)(pos - ((pos >> a.page_shift) << a.page_shift)) * D;
+    } else {
+      const int64_t j = pos / ap.page_size;
+      base = (int64_t)b * a.c_seq + j * a.c_page + (pos - j * ap.page_size) * D;
+    }
+    if (base >= 0) {
+      const int64_t off = base + (int64_t)hk * a.c_head;
+      float k1 = 0.f, k2 = 0.f;
+      if (active) rotate_pair<BF16Tag>(k1x, k2x, kc, ksn, k1, k2);
+      if constexpr (!kFP8) {
+        uint16_t *kcache = static_cast<uint16_t *>(const_cast<void *>(a.k_cache));
+        uint16_t *vcache = static_cast<uint16_t *>(const_cast<void *>(a.v_cache));
+        if (active) {
+          kcache[off + lane] = f32_to_bf16_bits(k1);
+          kcache[off + H + lane] = f32_to_bf16_bits(k2);
+          vcache[off + lane] = f32_to_bf16_bits(v1);
+          vcache[off + H + lane] = f32_to_bf16_bits(v2);
+        }
+      } else {
+        // per-(token, head) symmetric scale: absmax / 448, codes e4m3fn(x / scale)
+        const float kscale = wave_max(fmaxf(fabsf(k1), fabsf(k2))) / 448.0f;
+        const float vscale = wave_max(fmaxf(fabsf(v1), fabsf(v2))) / 448.0f;
+        uint8_t *kcache = static_cast<uint8_t *>(const_cast<void *>(a.k_cache));
+        uint8_t *vcache = static_cast<uint8_t *>(const_cast<void *>(a.v_cache));
+        if (active) {
+          kcache[off + lane] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k1 / kscale);
+          kcache[off + H + lane] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k2 / kscale);
+          vcache[off + lane] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v1 / vscale);
+          vcache[off + H + lane] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v2 / vscale);
+        }
+        if (lane == 0) {
+          const_cast<float *>(a.k_scale)[off / D] = kscale;
+          const_cast<float *>(a.v_scale)[off / D] = vscale;
+        }
+      }
+    }
+  }
+
+  // the query rows (further rounds only for G * D > 512)
+  rope_q(0);
+  for (int p0 = 64 * kIt; p0 < pairs; p0 += 64 * kIt) {
+    load_q(p0);
+    __builtin_amdgcn_sched_barrier(0);
+    rope_q(p0);
+  }
+  __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
+  __builtin_amdgcn_wave_barrier();
+  using TR = KVTraits<kFP8>;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < D / 32; ++s) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (n < G) v = *reinterpret_cast<const u32x4 *>(qs + n * D + TR::q_offset(s, g));
+    qf[s] = __builtin_bit_cast(bf16x8, v);
+  }
+  __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int D, bool kFP8, bool kAppend, bool kPartIn>
+__device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAppend *ap, int b, int hk, int L,
+                                             int j0, int j1, bool append, int64_t w, int lane, char *vlds,
+                                             uint16_t *qs, const bf16x8 (&ident16)[2],
                                              const u32x2 (&ident8)[2]) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
@@ -426,7 +611,19 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, int b, int hk,
   const int g = lane >> 4;
 
   bf16x8 qf[NDB];
-  {
+  int entry0 = 0;
+  if constexpr (kAppend) {
+    // the first chunk's page entries go out with the prologue's loads
+    if (a.page_table != nullptr) {
+      const int pb0 = (kTileTokens * j0) >> a.page_shift;
+      entry0 = a.page_table[(int64_t)b * a.max_pages + min(pb0 + lane, (L - 1) >> a.page_shift)];
+    }
+    piece_prologue<D, kFP8, kPartIn>(a, *ap, b, hk, __builtin_amdgcn_readfirstlane(a.seq_lens[b]), append, lane, qs, qf);
+    // The appended token is in this piece's last tile. Its loads are issued
+    // after the tile loop's first explicit vmcnt wait (which retires the
+    // stores above) unless it is one of the first chunk's first two tiles.
+    if (append && j1 - j0 <= 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+  } else {
     const uint16_t *q = static_cast<const uint16_t *>(a.q);
     const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + n) * a.q_sh;
 #pragma unroll
@@ -458,7 +655,7 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, int b, int hk,
     if (a.page_table != nullptr) {
       pbase = (kTileTokens * c0) >> a.page_shift;
       const int last = (L - 1) >> a.page_shift;
-      entry = a.page_table[(int64_t)b * a.max_pages + min(pbase + lane, last)];
+      entry = (kAppend && c0 == j0) ? entry0 : a.page_table[(int64_t)b * a.max_pages + min(pbase + lane, last)];
     }
     Tile<D, kFP8> buf[2];
     int64_t e0, e1;
@@ -534,10 +731,12 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, int b, int hk,
 constexpr int kStreamOcc = 2;
 constexpr int kStreamBlocksPerCU = 1;
 
-template <int D, bool kFP8>
-__global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeArgs a) {
+// LDS of the split kernel: V slots [4 waves] | wave sums [4] | prefix [B + 1]
+// (| q staging [4 waves][16][D] bf16 for the fused variant).
+template <int D, bool kFP8, bool kAppend, bool kPartIn>
+__device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeAppend *ap) {
   constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
-  extern __shared__ float smem[];  // V slots [4 waves] | wave sums [4] | prefix[B + 1]
+  extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char *smem_v = reinterpret_cast<char *>(smem);
@@ -545,9 +744,17 @@ __global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeAr
     reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
   int *wave_sums = reinterpret_cast<int *>(smem_v + kVAll);
   int *prefix = wave_sums + kWavesPerBlock;
+  uint16_t *qs = nullptr;
+  if constexpr (kAppend)
+    qs = reinterpret_cast<uint16_t *>(smem_v + kVAll + 16 * ((sizeof(int) * (kWavesPerBlock + a.batch + 1) + 15) / 16)) +
+         wave * 16 * D;
   build_split_prefix(a, kTileTokens, nullptr, prefix, wave_sums);  // ends with a block barrier
-  if (blockIdx.x == 0)  // for the merge kernel
+  if (blockIdx.x == 0) {  // for the merge kernel (and the next step's lengths)
     for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.ws_prefix[i] = prefix[i];
+    if constexpr (kAppend)
+      if (ap->lens_out != nullptr)
+        for (int i = threadIdx.x; i < a.batch; i += blockDim.x) ap->lens_out[i] = a.seq_lens[i] + 1;
+  }
   const int64_t W = (int64_t)__builtin_amdgcn_readfirstlane(prefix[a.batch]) * a.hkv;
   const int64_t NW = a.stream_waves;
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wave;
@@ -572,10 +779,25 @@ __global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeAr
     const int64_t seg_end = (int64_t)pb * a.hkv + (int64_t)(hk + 1) * nb;
     const int64_t stop = seg_end < t_end ? seg_end : t_end;
     const int j1 = j0 + (int)(stop - t);
-    const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b], a.max_len));
-    stream_piece<D, kFP8>(a, b, hk, L, j0, j1, w, lane, vlds, ident16, ident8);
+    const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b] + a.len_add, a.max_len));
+    // The segment's last tile holds this step's token: only this wave reads
+    // it, so the fused variant appends it at the start of this piece.
+    stream_piece<D, kFP8, kAppend, kPartIn>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nb, w, lane, vlds, qs, ident16, ident8);
     t = stop;
   }
+}
+
+template <int D, bool kFP8>
+__global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeArgs a) {
+  stream_body<D, kFP8, false, false>(a, nullptr);
+}
+
+// The same split kernel with this step's RoPE + append folded in (q rotated
+// per piece from the projection outputs; k / v written by the wave that
+// reads the segment's last tile).
+template <int D, bool kFP8, bool kPartIn>
+__global__ __launch_bounds__(256, kStreamOcc) void decode_stream_append_kernel(DecodeAppendArgs a) {
+  stream_body<D, kFP8, true, kPartIn>(a, &a.ap);
 }
 
 // One wave per segment (b, KV head): merge its pieces into the G output rows
@@ -779,7 +1001,7 @@ hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStr
 }
 
 template <int D, bool kFP8>
-hipError_t launch_stream(const DecodeArgs &a0, hipStream_t stream) {
+hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream_t stream) {
   DecodeArgs a = a0;
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
@@ -791,8 +1013,23 @@ hipError_t launch_stream(const DecodeArgs &a0, hipStream_t stream) {
   int64_t blocks = std::min<int64_t>((int64_t)cus * kStreamBlocksPerCU, kMaxStreamBlocks);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (tiles_bound + kWavesPerBlock - 1) / kWavesPerBlock));
   a.stream_waves = (int)(blocks * kWavesPerBlock);
-  const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + sizeof(int) * (kWavesPerBlock + (size_t)a.batch + 1);
-  hipLaunchKernelGGL((decode_stream_kernel<D, kFP8>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock), lds, stream, a);
+  const size_t lds_prefix = 16 * ((sizeof(int) * (kWavesPerBlock + (size_t)a.batch + 1) + 15) / 16);
+  size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + lds_prefix;
+  if (ap != nullptr) {
+    lds += (size_t)kWavesPerBlock * 16 * D * sizeof(uint16_t);  // q staging
+    DecodeAppendArgs f;
+    static_cast<DecodeArgs &>(f) = a;
+    f.ap = *ap;
+    if (ap->part_splits > 0)
+      hipLaunchKernelGGL((decode_stream_append_kernel<D, kFP8, true>), dim3((unsigned)blocks),
+                         dim3(64 * kWavesPerBlock), lds, stream, f);
+    else
+      hipLaunchKernelGGL((decode_stream_append_kernel<D, kFP8, false>), dim3((unsigned)blocks),
+                         dim3(64 * kWavesPerBlock), lds, stream, f);
+  } else {
+    hipLaunchKernelGGL((decode_stream_kernel<D, kFP8>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock), lds, stream,
+                       a);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const dim3 mgrid((unsigned)((int64_t)a.batch * a.hkv));
@@ -808,7 +1045,7 @@ hipError_t launch_stream(const DecodeArgs &a0, hipStream_t stream) {
 template <int D>
 hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
   if (kind != CacheKind::kF32 && a.split_tokens == 0)
-    return kind == CacheKind::kFP8 ? launch_stream<D, true>(a, stream) : launch_stream<D, false>(a, stream);
+    return kind == CacheKind::kFP8 ? launch_stream<D, true>(a, nullptr, stream) : launch_stream<D, false>(a, nullptr, stream);
   const dim3 grid(a.max_splits, a.hkv, a.batch);
   const dim3 block(64 * kWavesPerBlock);
   const size_t lds = sizeof(float) * (kWavesPerBlock * a.group * D + 2 * kWavesPerBlock * 16);
@@ -852,6 +1089,13 @@ int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
   if (head_dim == 64) return launch_d<64>(a, kind, stream);
   return launch_d<128>(a, kind, stream);
+}
+
+hipError_t launch_decode_attn_append(const DecodeAppendArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
+  const bool fp8 = kind == CacheKind::kFP8;
+  if (head_dim == 64)
+    return fp8 ? launch_stream<64, true>(a, &a.ap, stream) : launch_stream<64, false>(a, &a.ap, stream);
+  return fp8 ? launch_stream<128, true>(a, &a.ap, stream) : launch_stream<128, false>(a, &a.ap, stream);
 }
 
 }  // namespace tt

@@ -11,51 +11,12 @@
 // role is to produce bytes identical to the reference's rope_impl
 // (attn.py:13-63) and cache append (cache.py:41-42) at the slot given by the
 // per-sequence position.
+#include "rope_math.h"
 #include "tt_internal.h"
 #include "tt_numerics.h"
 
 namespace tt {
 namespace {
-
-template <typename T>
-struct Elem;
-
-template <>
-struct Elem<float> {
-  static __device__ __forceinline__ float load(const void *p, int64_t i) {
-    return static_cast<const float *>(p)[i];
-  }
-  static __device__ __forceinline__ void store(void *p, int64_t i, float v) {
-    static_cast<float *>(p)[i] = v;
-  }
-  static __device__ __forceinline__ float rnd(float v) { return v; }
-};
-
-struct BF16Tag {};
-
-template <>
-struct Elem<BF16Tag> {
-  static __device__ __forceinline__ float load(const void *p, int64_t i) {
-    return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
-  }
-  static __device__ __forceinline__ void store(void *p, int64_t i, float v) {
-    static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
-  }
-  static __device__ __forceinline__ float rnd(float v) { return round_bf16(v); }
-};
-
-// out1 = r(r(x1*c) + r(-x2*s)), out2 = r(r(x2*c) + r(x1*s)), r = rounding to
-// the activation type; the three ops of attn.py:61 in the reference's order.
-template <typename A>
-__device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float &o1, float &o2) {
-#pragma clang fp contract(off)
-  const float a1 = Elem<A>::rnd(x1 * c);
-  const float b1 = Elem<A>::rnd((-x2) * s);
-  const float a2 = Elem<A>::rnd(x2 * c);
-  const float b2 = Elem<A>::rnd(x1 * s);
-  o1 = Elem<A>::rnd(a1 + b1);
-  o2 = Elem<A>::rnd(a2 + b2);
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -101,6 +62,27 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const int t = blockIdx.y;
   const int b = blockIdx.z;
   const int i = threadIdx.x;
+  const int half = a.head_dim >> 1;
+  const bool active = i < half;
+  const bool is_q = row < a.hq;
+  const int hk = row - a.hq;
+  // The inputs do not depend on the position: their loads go out first, so
+  // the position -> (table row, page entry) chain overlaps them.
+  float x1 = 0.f, x2 = 0.f, v1 = 0.f, v2 = 0.f;
+  if (t < a.num_new && active) {
+    if (is_q) {
+      const int64_t src = (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st;
+      x1 = load_in<A, kPart>(a, a.q_in, src + i);
+      x2 = load_in<A, kPart>(a, a.q_in, src + half + i);
+    } else {
+      const int64_t ks = (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
+      const int64_t vs = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh + (int64_t)t * a.vi_st;
+      x1 = load_in<A, kPart>(a, a.k_in, ks + i);
+      x2 = load_in<A, kPart>(a, a.k_in, ks + half + i);
+      v1 = load_in<A, kPart>(a, a.v_in, vs + i);
+      v2 = load_in<A, kPart>(a, a.v_in, vs + half + i);
+    }
+  }
   if (a.lens_out != nullptr && row == 0 && t == 0 && threadIdx.x == 0) {
     const int n = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
     a.lens_out[b] = a.positions[b] + n;
@@ -108,19 +90,14 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   if (t >= a.num_new) return;  // num_new == 0 launches one row only for lens_out
   const int64_t pos = (int64_t)a.positions[b] + t;
   if (pos < 0 || pos >= a.table_len) return;
-  const int half = a.head_dim >> 1;
-  const bool active = i < half;
   float c = 0.f, s = 0.f;
   if (active) {
     c = Elem<A>::load(a.table, pos * a.head_dim + i);
     s = Elem<A>::load(a.table, pos * a.head_dim + half + i);
   }
 
-  if (row < a.hq) {
+  if (is_q) {
     if (!active) return;
-    const int64_t src = (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st;
-    const float x1 = load_in<A, kPart>(a, a.q_in, src + i);
-    const float x2 = load_in<A, kPart>(a, a.q_in, src + half + i);
     float o1, o2;
     rotate_pair<A>(x1, x2, c, s, o1, o2);
     const int64_t dst = (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh + (int64_t)t * a.qo_st;
@@ -130,17 +107,10 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   }
 
   if (a.new_lens != nullptr && t >= a.new_lens[b]) return;  // padding token: no cache write
-  const int hk = row - a.hq;
   const int64_t off = slot_offset(a, b, hk, pos);  // wave-uniform
   if (off < 0) return;
-  float k1 = 0.f, k2 = 0.f, v1 = 0.f, v2 = 0.f;
-  if (active) {
-    const int64_t ks = (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
-    const int64_t vs = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh + (int64_t)t * a.vi_st;
-    rotate_pair<A>(load_in<A, kPart>(a, a.k_in, ks + i), load_in<A, kPart>(a, a.k_in, ks + half + i), c, s, k1, k2);
-    v1 = load_in<A, kPart>(a, a.v_in, vs + i);
-    v2 = load_in<A, kPart>(a, a.v_in, vs + half + i);
-  }
+  float k1 = 0.f, k2 = 0.f;
+  if (active) rotate_pair<A>(x1, x2, c, s, k1, k2);
 
   if constexpr (!kFP8) {
     if (active) {

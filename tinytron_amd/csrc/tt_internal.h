@@ -60,6 +60,29 @@ struct DecodeArgs {
   int batch, hq, hkv, group, split_tokens, max_splits;
   int page_shift;    // paged pools: log2(page_size); the contiguous store is addressed linearly
   float scale_log2;  // sm_scale * log2(e)
+  int len_add;       // added to seq_lens[b] (1 when the kernel appends the step's token itself)
+};
+
+// Fused decode step: the split kernel also applies RoPE to this step's token
+// (q, and k before it is written) and appends k / v to the cache, so that
+// no separate RoPE + append launch precedes it. seq_lens holds the tokens
+// cached before the step (len_add = 1).
+struct DecodeAppend {
+  const void *q_in, *k_in, *v_in;  // bf16 [B, H, D] views, or fp32 split-K partials
+  int64_t qi_sb, qi_sh, ki_sb, ki_sh, vi_sb, vi_sh;
+  int part_splits;  // 0: bf16 inputs; 1 .. kMaxApSplits: sum of the partials (stride part_stride) rounded to bf16
+  int64_t part_stride;
+  const void *table;  // RoPE table [table_len, D] bf16
+  int64_t table_len;
+  int32_t *lens_out;  // [B] lengths after the step, or null
+  int64_t capacity;   // tokens per sequence the cache holds
+  int64_t page_size;  // contiguous store: tokens per page (paged pools: 1 << page_shift)
+};
+
+constexpr int kMaxApSplits = 4;  // split-K partials the fused step sums per input
+
+struct DecodeAppendArgs : DecodeArgs {
+  DecodeAppend ap;
 };
 
 // Skinny GEMM of the decode step: partials P[K / kc][M][N] (fp32) of x[M, K] . W[N, K]^T.
@@ -81,6 +104,7 @@ hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hip
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream);
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
+hipError_t launch_decode_attn_append(const DecodeAppendArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
 
 // Prefill: T new tokens per sequence (their K/V already in the cache), causal
 // GQA attention over each sequence's cached prefix. The cache fields, q / out

@@ -13,19 +13,22 @@ and every projection takes bf16 inputs and returns bf16 -- the values
 autocast produces from fp32 weights.
 
 ``Attention.forward`` is the drop-in of attn.py:378-440: with one of this
-package's caches, a decode step (T = 1) is one fused RoPE + KV-append kernel
-and one split-K GQA attention kernel; prefill (T > 1) writes the cache with
-the same append kernel and attends with the prefill kernel (bf16
-activations; SDPA per sequence for fp32). No CPU fallback.
+package's caches, a decode step (T = 1) is one split-K GQA attention launch
+pair that also applies RoPE to the step's token and appends it to the cache
+(fp8 and fp32 caches: a RoPE + append kernel, then the attention kernels;
+the fused pair measured slower than the two launches on fp8); prefill
+(T > 1) writes the cache with the RoPE + append kernel and attends with the
+prefill kernel (bf16 activations; SDPA per sequence for fp32). No CPU
+fallback.
 
 ``GPT.forward`` runs a bf16 decode step (T = 1) as a fused layer sequence
 when the shapes allow it (``GPT.fused_decode``): per layer, one skinny
-split-K GEMM for the stacked q|k|v projection, the
-RoPE + append kernel (which sums those partials itself), the attention
-kernels, the c_proj GEMM, residual add + RMSNorm in one kernel, one GEMM for
-the stacked gate|up projection, SwiGLU, the down GEMM, and the next residual
-add + RMSNorm -- 10 launches instead of about 30, with the same math and
-bf16 rounding points as the module path.
+split-K GEMM for the stacked q|k|v projection, the attention launch pair
+(which sums those partials, applies RoPE and appends k / v itself), the
+c_proj GEMM, residual add + RMSNorm in one kernel, one GEMM for the stacked
+gate|up projection, SwiGLU, the down GEMM, and the next residual add +
+RMSNorm -- 9 launches instead of about 30 (10 with an fp8 cache), with the
+same math and bf16 rounding points as the module path.
 """
 from __future__ import annotations
 
@@ -121,7 +124,10 @@ class Attention(nn.Module):
         if len(set(lens)) == 1 and lens[0] != position_offset:
             raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
         table = rope_table_for(past_kv.max_seq_len + T, self.head_dim, self.config.rope_theta, act, x.device)
-        if T == 1:
+        if T == 1 and act == torch.bfloat16 and past_kv.layout.kind == "bf16":
+            y = past_kv.decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], table)  # RoPE + append + attention
+            y = y.view(B, 1, C)
+        elif T == 1:
             q_rot = past_kv.rope_append(q, k, v, table)                     # [B, H_q, 1, D]
             y = past_kv.attend(q_rot.view(B, self.num_attention_heads, self.head_dim))
             y = y.view(B, 1, C)
@@ -326,8 +332,11 @@ class GPT(nn.Module):
             layer = cache.get_layer_cache(i)
             wqkv, wo, wgu, wd = self._stacked_weights(i)
             P = ops.linear_partials(h, wqkv, partials=pbuf, k_chunk=kc_c)
-            q_rot = layer.rope_append_partials(P, Hq, table)         # sums the q|k|v partials itself
-            y = layer.attend(q_rot.view(B, Hq, D))                   # [B, Hq, D]
+            if P.shape[0] <= ops.FUSED_STEP_MAX_SPLITS and layer.layout.kind == "bf16":
+                y = layer.decode_step_partials(P, Hq, table)        # RoPE + append + attention, [B, Hq, D]
+            else:
+                q_rot = layer.rope_append_partials(P, Hq, table)     # sums the q|k|v partials itself
+                y = layer.attend(q_rot.view(B, Hq, D))
             P = ops.linear_partials(y.view(B, C), wo, partials=pbuf, k_chunk=kc_o)
             h = ops.add_rmsnorm(x, blk.ln_2.weight, eps, partials=P)
             P = ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_c)

@@ -265,6 +265,80 @@ def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, 
     return out
 
 
+FUSED_STEP_MAX_SPLITS = 4  # split-K partials decode_attention_append sums per input
+
+
+def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout: KVLayout, max_seq_len: int,
+                            q: torch.Tensor | None = None, k: torch.Tensor | None = None, v: torch.Tensor | None = None,
+                            partials: torch.Tensor | None = None, num_q_heads: int | None = None,
+                            lens_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                            sm_scale: float | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """One decode step in one launch pair: RoPE of this step's q and k at
+    positions[b], append of k / v at that slot, and GQA attention over the
+    positions[b] + 1 cached tokens (rope_append followed by decode_attention,
+    without writing the rotated q). Inputs: bf16 q [B, H_q, D] and k / v
+    [B, H_kv, D] (strided views, head_dim contiguous), or ``partials`` fp32
+    [S, B, (H_q + 2 H_kv) D] of the stacked q|k|v projection with
+    ``num_q_heads``. ``max_seq_len`` bounds positions + 1. Returns out
+    [B, H_q, D] bf16."""
+    _require_cuda(table, positions, layout.k, layout.v)
+    if layout.kind not in ("bf16", "fp8"):
+        raise ValueError("the fused decode step takes a bf16 or fp8 cache")
+    Hkv, D = layout.num_heads, layout.head_dim
+    if partials is not None:
+        _require_cuda(partials)
+        if partials.dtype != torch.float32 or partials.dim() != 3 or not partials.is_contiguous():
+            raise ValueError("partials must be a contiguous fp32 [S, B, N] tensor")
+        S, B, N = partials.shape
+        if S > FUSED_STEP_MAX_SPLITS:
+            raise ValueError(f"the fused step sums at most {FUSED_STEP_MAX_SPLITS} split-K partials, got {S}")
+        Hq = int(num_q_heads)
+        if N != (Hq + 2 * Hkv) * D:
+            raise ValueError(f"partials have {N} columns, expected (H_q + 2 H_kv) * D = {(Hq + 2 * Hkv) * D}")
+        base = partials.data_ptr()
+        st_in = _lib.strides(N, D)
+        ins = [base, st_in, base + Hq * D * 4, st_in, base + (Hq + Hkv) * D * 4, st_in, S, B * N]
+        dev = partials.device
+    else:
+        _require_cuda(q, k, v)
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            _check_lastdim(name, t, 3)
+            if t.dtype != torch.bfloat16:
+                raise ValueError("the fused decode step takes bf16 q / k / v")
+        B, Hq, Dq = q.shape
+        if Dq != D or k.shape != (B, Hkv, D) or v.shape != k.shape:
+            raise ValueError(f"q {tuple(q.shape)} / k {tuple(k.shape)} / v {tuple(v.shape)} do not match the cache")
+        ins = [_ptr(q), _lib.strides(*q.stride()[:2]), _ptr(k), _lib.strides(*k.stride()[:2]),
+               _ptr(v), _lib.strides(*v.stride()[:2]), 0, 0]
+        dev = q.device
+    if table.dtype != torch.bfloat16 or table.dim() != 2 or table.shape[1] != D or not table.is_contiguous():
+        raise ValueError("rope table must be a contiguous bf16 [positions, head_dim] tensor")
+    if positions.dtype != torch.int32 or positions.shape != (B,):
+        raise ValueError("positions must be int32 [B]")
+    if lens_out is not None and (lens_out.dtype != torch.int32 or lens_out.shape != (B,)):
+        raise ValueError("lens_out must be int32 [B]")
+    if not 1 <= max_seq_len <= layout.capacity:
+        raise ValueError(f"max_seq_len {max_seq_len} must be in [1, capacity {layout.capacity}]")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=dev)
+    _check_lastdim("out", out, 3)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    need = workspace_bytes(B, Hq, Hkv, D, max_seq_len, 0)
+    ws = (workspace or Workspace(dev)).get(need)
+    lib = _lib.load()
+    head = ins + [_ptr(table), table.shape[0], _ptr(positions), _ptr(lens_out), int(max_seq_len),
+                  _ptr(layout.page_table), layout.max_pages, layout.num_pages, _ptr(layout.k), _ptr(layout.v)]
+    tail = [_lib.strides(*layout.strides), layout.capacity, _ptr(out), _lib.strides(*out.stride()[:2]),
+            B, Hq, Hkv, D, layout.page_size, float(sm_scale), _ptr(ws), ws.numel(), _stream(dev)]
+    if layout.kind == "fp8":
+        st = lib.tt_decode_attn_append_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
+    else:
+        st = lib.tt_decode_attn_append_bf16(*head, *tail)
+    _lib.check(st, "decode_attention_append")
+    return out
+
+
 # -- decode-step layer operations ----------------------------------------------------------
 
 def _rows(t: torch.Tensor, name: str) -> tuple:
