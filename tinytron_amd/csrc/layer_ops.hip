@@ -128,30 +128,44 @@ __global__ __launch_bounds__(64 * WAVES, (gemm_min_waves<KC, WAVES>())) void ski
   }
 }
 
-// sum_{s < S} P[s * stride + i] added in order s = 0, 1, ..., four loads
-// issued ahead of their adds (the order of the additions is unchanged).
-__device__ __forceinline__ f32x4 ordered_sum4(const float *P, int S, int64_t stride, int64_t i) {
-  f32x4 d = *reinterpret_cast<const f32x4 *>(P + i);
-  int s = 1;
-  for (; s + 4 <= S; s += 4) {
-    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(P + (int64_t)s * stride + i);
-    const f32x4 a1 = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s + 1) * stride + i);
-    const f32x4 a2 = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s + 2) * stride + i);
-    const f32x4 a3 = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s + 3) * stride + i);
-    d += a0;
-    d += a1;
-    d += a2;
-    d += a3;
+// sum_{s < S} P[s * stride + i] added in order s = 0, 1, ..., for n rows i[r]
+// at once: the splits go in batches of four whose loads (addresses clamped to
+// a valid split, so no branch separates them) are all issued before the
+// batch's adds, so S <= 4 costs one memory round trip for every row together.
+// Additions past S are selected away; the order of the additions is s = 0,
+// 1, ..., S - 1.
+template <int n>
+__device__ __forceinline__ void ordered_sums(const float *P, int S, int64_t stride, const int64_t (&i)[n],
+                                             f32x4 (&d)[n]) {
+  for (int s0 = 0; s0 < S; s0 += 4) {
+    f32x4 v[n][4];
+#pragma unroll
+    for (int r = 0; r < n; ++r)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = s0 + u < S ? s0 + u : S - 1;
+        v[r][u] = *reinterpret_cast<const f32x4 *>(P + (int64_t)s * stride + i[r]);
+      }
+#pragma unroll
+    for (int r = 0; r < n; ++r)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (s0 + u == 0)
+          d[r] = v[r][0];
+        else
+          d[r] = s0 + u < S ? d[r] + v[r][u] : d[r];
+      }
   }
-  for (; s < S; ++s) d += *reinterpret_cast<const f32x4 *>(P + (int64_t)s * stride + i);
-  return d;
 }
 
 // y[i] = bf16(sum_s P[s][i]), four elements per thread.
 __global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *P, int S, int64_t MN, uint16_t *y) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= MN) return;
-  const f32x4 acc = ordered_sum4(P, S, MN, i);
+  const int64_t ix[1] = {i};
+  f32x4 sum[1];
+  ordered_sums<1>(P, S, MN, ix, sum);
+  const f32x4 acc = sum[0];
   uint32_t lo = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
   uint32_t hi = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
   *reinterpret_cast<uint2 *>(y + i) = make_uint2(lo, hi);
@@ -225,8 +239,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
   const int64_t m = i / I;
   const int64_t c = i - m * I;
   const int64_t gi = m * 2 * I + c;
-  const f32x4 g = ordered_sum4(P, S, MN2, gi);
-  const f32x4 u = ordered_sum4(P, S, MN2, gi + I);
+  const int64_t ix[2] = {gi, gi + I};
+  f32x4 sum[2];
+  ordered_sums<2>(P, S, MN2, ix, sum);
+  const f32x4 g = sum[0];
+  const f32x4 u = sum[1];
   uint16_t out[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {

@@ -42,21 +42,31 @@ __device__ __forceinline__ int64_t slot_offset(const RopeAppendArgs &a, int b, i
   return base + (int64_t)hk * a.c_head + slot * a.head_dim;
 }
 
-// An input element: the activation at p[i], or with split-K partials the
-// activation-typed sum of the splits added in order (the projection's output).
-template <typename A, bool kPart>
+// An input element: the activation at p[i] (kPart 0), or with split-K
+// partials the activation-typed sum of the splits added in order (the
+// projection's output), in batches of four loads (addresses clamped to a
+// valid split, additions past S selected away). kPart 1 (at most four
+// splits) loads a wave's inputs inline instead, all before the first add.
+template <typename A, int kPart>
 __device__ __forceinline__ float load_in(const RopeAppendArgs &a, const void *p, int64_t i) {
-  if constexpr (kPart) {
-    const float *f = static_cast<const float *>(p);
-    float acc = f[i];
-    for (int s = 1; s < a.part_splits; ++s) acc += f[(int64_t)s * a.part_stride + i];
-    return Elem<A>::rnd(acc);
-  } else {
+  if constexpr (kPart == 0) {
     return Elem<A>::load(p, i);
+  } else {
+    const float *f = static_cast<const float *>(p);
+    const int S = a.part_splits;
+    float acc = 0.f;
+    for (int s0 = 0; s0 < (kPart == 1 ? 1 : S); s0 += 4) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = f[(int64_t)(s0 + u < S ? s0 + u : S - 1) * a.part_stride + i];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = s0 + u == 0 ? v[0] : (s0 + u < S ? acc + v[u] : acc);
+    }
+    return Elem<A>::rnd(acc);
   }
 }
 
-template <typename A, bool kFP8, bool kPart>
+template <typename A, bool kFP8, int kPart>
 __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const int row = blockIdx.x;
   const int t = blockIdx.y;
@@ -66,29 +76,60 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const bool active = i < half;
   const bool is_q = row < a.hq;
   const int hk = row - a.hq;
-  // The inputs do not depend on the position: their loads go out first, so
-  // the position -> (table row, page entry) chain overlaps them.
+  // The inputs do not depend on the position: their loads go out first (all
+  // of them, then a scheduling barrier, then the sums), so the position ->
+  // (table row, page entry) chain overlaps them. Lanes past D/2 load lane
+  // i mod D/2 and drop it, which keeps the loads free of branches.
+  const int pos0 = a.positions[b];  // issued with the input loads below
   float x1 = 0.f, x2 = 0.f, v1 = 0.f, v2 = 0.f;
-  if (t < a.num_new && active) {
-    if (is_q) {
-      const int64_t src = (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st;
-      x1 = load_in<A, kPart>(a, a.q_in, src + i);
-      x2 = load_in<A, kPart>(a, a.q_in, src + half + i);
+  if (t < a.num_new) {
+    const int li = i & (half - 1);
+    const void *p1 = is_q ? a.q_in : a.k_in;
+    const int64_t o1 = is_q ? (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st
+                            : (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
+    const int64_t o2 = is_q ? o1 : (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh + (int64_t)t * a.vi_st;
+    const void *p2 = is_q ? a.q_in : a.v_in;  // q rows load their own row twice; the second copy is unused
+    if constexpr (kPart == 1) {
+      const float *f1 = static_cast<const float *>(p1);
+      const float *f2 = static_cast<const float *>(p2);
+      const int S = a.part_splits;
+      float r[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t so = (int64_t)(u < S ? u : S - 1) * a.part_stride;
+        r[0][u] = f1[so + o1 + li];
+        r[1][u] = f1[so + o1 + half + li];
+        r[2][u] = f2[so + o2 + li];
+        r[3][u] = f2[so + o2 + half + li];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      float acc[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[k] = r[k][0];
+#pragma unroll
+        for (int u = 1; u < 4; ++u) acc[k] = u < S ? acc[k] + r[k][u] : acc[k];
+        acc[k] = Elem<A>::rnd(acc[k]);
+      }
+      x1 = acc[0];
+      x2 = acc[1];
+      v1 = acc[2];
+      v2 = acc[3];
     } else {
-      const int64_t ks = (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
-      const int64_t vs = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh + (int64_t)t * a.vi_st;
-      x1 = load_in<A, kPart>(a, a.k_in, ks + i);
-      x2 = load_in<A, kPart>(a, a.k_in, ks + half + i);
-      v1 = load_in<A, kPart>(a, a.v_in, vs + i);
-      v2 = load_in<A, kPart>(a, a.v_in, vs + half + i);
+      x1 = load_in<A, kPart>(a, p1, o1 + li);
+      x2 = load_in<A, kPart>(a, p1, o1 + half + li);
+      if (!is_q) {
+        v1 = load_in<A, kPart>(a, p2, o2 + li);
+        v2 = load_in<A, kPart>(a, p2, o2 + half + li);
+      }
     }
   }
   if (a.lens_out != nullptr && row == 0 && t == 0 && threadIdx.x == 0) {
     const int n = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
-    a.lens_out[b] = a.positions[b] + n;
+    a.lens_out[b] = pos0 + n;
   }
   if (t >= a.num_new) return;  // num_new == 0 launches one row only for lens_out
-  const int64_t pos = (int64_t)a.positions[b] + t;
+  const int64_t pos = (int64_t)pos0 + t;
   if (pos < 0 || pos >= a.table_len) return;
   float c = 0.f, s = 0.f;
   if (active) {
@@ -145,22 +186,27 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
   const dim3 grid(a.hq + a.hkv, a.num_new > 0 ? a.num_new : 1, a.batch);
   const dim3 block(64);
-  const bool part = a.part_splits > 0;  // bf16 activations only (checked by the caller)
+  // split-K partial inputs: bf16 activations only (checked by the caller)
+  const int part = a.part_splits <= 0 ? 0 : (a.part_splits <= 4 ? 1 : 2);
   switch (kind) {
     case CacheKind::kBF16:
-      if (part)
-        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, true>), grid, block, 0, stream, a);
+      if (part == 1)
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, 1>), grid, block, 0, stream, a);
+      else if (part == 2)
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, 2>), grid, block, 0, stream, a);
       else
-        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, false, 0>), grid, block, 0, stream, a);
       break;
     case CacheKind::kF32:
-      hipLaunchKernelGGL((rope_append_kernel<float, false, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((rope_append_kernel<float, false, 0>), grid, block, 0, stream, a);
       break;
     case CacheKind::kFP8:
-      if (part)
-        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, true>), grid, block, 0, stream, a);
+      if (part == 1)
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, 1>), grid, block, 0, stream, a);
+      else if (part == 2)
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, 2>), grid, block, 0, stream, a);
       else
-        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((rope_append_kernel<BF16Tag, true, 0>), grid, block, 0, stream, a);
       break;
   }
   return hipGetLastError();
