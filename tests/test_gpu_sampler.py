@@ -204,3 +204,23 @@ def test_sampler_manual_seed_counts_calls():
     sampler.manual_seed(None)
     assert torch.equal(a[0], ops.sample_tokens(x, top_k=50, seed=5, offset=0))
     assert torch.equal(a[1], ops.sample_tokens(x, top_k=50, seed=5, offset=1))
+
+
+@pytest.mark.parametrize("top_p", [None, 0.5, 0.1, 0.99])
+def test_greedy_kernel_matches_full_sampler_on_ties(top_p):
+    # top_k = 1 without full log-prob rows runs the greedy kernel; with them,
+    # the general kernel: same token and token log-probability, ties included
+    from tinytron_amd import ops
+
+    x = _logits(8, 5000, torch.bfloat16, seed=11)
+    x[:, 100] = x[:, 900] = x[:, 1300] = x[:, 4000] = x[:, 4999] = 60.0  # five tied maxima
+    x[3, 2000] = 70.0  # a single maximum in row 3
+    xd = x.to(DEV)
+    t1, l1 = ops.sample_tokens(xd, top_k=1, top_p=top_p, return_logprob=True)
+    t2, l2, full = ops.sample_tokens(xd, top_k=1, top_p=top_p, return_logprob=True, return_logprobs=True)
+    assert torch.equal(t1, t2) and torch.equal(l1, l2)
+    kept = 5 if top_p is None else max(1, int(top_p * 5))
+    want = torch.full((8,), -math.log(kept))
+    want[3] = 0.0
+    assert torch.allclose(l1.cpu(), want, atol=1e-6)
+    assert int(t1[0]) == 100 and int(t1[3]) == 2000

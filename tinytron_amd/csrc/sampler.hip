@@ -289,24 +289,18 @@ __device__ __forceinline__ int find_first_exceeding(SampleShared &sh, Row<EPT, k
   return res;
 }
 
+// The row into registers; elements past V read nothing and hold -inf. Every
+// full group's vector load is issued before any is used (a partial or empty
+// group loads the row's first group instead, always in bounds), so the row
+// costs one memory round trip; the one partial group of the row then reads
+// its elements one by one.
 template <int EPT, bool kF32>
-__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
-  __shared__ SampleShared sh;
+__device__ __forceinline__ void load_row(const SampleArgs &a, int row, Row<EPT, kF32> &r) {
   constexpr int G = EPT / 8;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row = blockIdx.x;
-  Row<EPT, kF32> r;
   r.t = threadIdx.x;
   r.V = a.V;
   r.apply_temp = a.apply_temp;
   r.temperature = a.temperature;
-
-  // Row into registers; elements past V read nothing and hold -inf. Every
-  // full group's vector load is issued before any is used (a partial or
-  // empty group loads the row's first group instead, always in bounds), so
-  // the row costs one memory round trip; the one partial group of the row
-  // then reads its elements one by one.
   const char *rowp = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (kF32 ? 4 : 2);
   if (a.vec) {
     constexpr int kVec = kF32 ? 2 : 1;  // 16-byte loads per group
@@ -356,8 +350,21 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
       }
     }
   }
+}
 
-  // Maximum, its first index and its multiplicity; the number of finite values.
+struct RowMax {
+  float m;      // maximum
+  int amax;     // its first index
+  int cmax;     // its multiplicity
+  int nfinite;  // finite values in the row
+};
+
+// Block reduction of the row's maximum, first argmax and tie count.
+template <int EPT, bool kF32>
+__device__ __forceinline__ RowMax row_max(const SampleArgs &a, const Row<EPT, kF32> &r, SampleShared &sh) {
+  constexpr int G = EPT / 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   float bm = -INFINITY;
   int bi = INT_MAX, bcnt = 0, nfin = 0;
 #pragma unroll
@@ -417,6 +424,19 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
     }
   }
   __syncthreads();
+  return RowMax{m, amax, cmax, nfinite};
+}
+
+template <int EPT, bool kF32>
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
+  __shared__ SampleShared sh;
+  constexpr int G = EPT / 8;
+  const int row = blockIdx.x;
+  Row<EPT, kF32> r;
+  load_row<EPT, kF32>(a, row, r);
+  const RowMax mx = row_max<EPT, kF32>(a, r, sh);
+  const float m = mx.m;
+  const int amax = mx.amax, cmax = mx.cmax, nfinite = mx.nfinite;
 
   const bool greedy = a.top_k == 1;
   const bool do_topk = a.top_k > 0 && a.top_k < a.V;
@@ -543,9 +563,36 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   }
 }
 
+// top_k == 1 without the full log-probability rows: the first maximum and
+// its log-probability -log(r), r the tied maxima top-p keeps (one, or all of
+// them without top-p), exactly what sample_kernel computes for this case; a
+// kernel of its own so that the engine's greedy step runs only this code.
+template <int EPT, bool kF32>
+__global__ __launch_bounds__(kThreads) void greedy_kernel(SampleArgs a) {
+  __shared__ SampleShared sh;
+  const int row = blockIdx.x;
+  Row<EPT, kF32> r;
+  load_row<EPT, kF32>(a, row, r);
+  const RowMax mx = row_max<EPT, kF32>(a, r, sh);
+  if (threadIdx.x == 0) {
+    a.tokens[row] = mx.amax;
+    if (a.token_logprob) {
+      u64 kept = (u64)mx.cmax;
+      if (a.apply_top_p) {  // equal masses 2^40: the first max(1, floor(p * c)) ties stay
+        const u64 t = (u64)((double)a.top_p * (double)(kept << 40));
+        kept = (t >> 40) > 0 ? (t >> 40) : 1;
+      }
+      a.token_logprob[row] = 0.f - logf((float)kept);
+    }
+  }
+}
+
 template <int EPT, bool kF32>
 hipError_t launch_ept(const SampleArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((sample_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
+  if (a.top_k == 1 && a.logprobs == nullptr)
+    hipLaunchKernelGGL((greedy_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((sample_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
