@@ -225,3 +225,33 @@ def test_prefill_kernel_matches_sdpa_path(kv_dtype):
     a, b = ys
     for i, n in enumerate(second):
         assert torch.allclose(a[i, :n], b[i, :n], rtol=2e-2, atol=2e-2), f"sequence {i}"
+
+
+def test_sampled_generation_is_seeded_and_graph_invariant():
+    """Non-greedy generation (temperature / top-k / top-p through the device
+    sampler, log-probs returned): repeatable under torch.manual_seed, equal
+    between eager launches and graph replay, log-probs finite and <= 0."""
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=2, block_size=256, vocab_size=4096, hidden_size=1024, num_attention_heads=16,
+                     num_key_value_heads=4)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(3)
+    lens = [5, 60, 33, 17]
+    prompt = torch.randint(0, cfg.vocab_size, (len(lens), max(lens)), generator=g)
+    runs = []
+    for use_graphs in (False, False, True):
+        eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True,
+                              model=model, use_graphs=use_graphs)
+        torch.manual_seed(5)
+        toks, extra = eng.generate(prompt, 24, temperature=0.8, top_k=50, top_p=0.9, prompt_lens=lens,
+                                   return_logprobs=True)
+        runs.append((toks.cpu(), extra["token_log_probs"].cpu()))
+    for toks, lp in runs[1:]:
+        assert torch.equal(toks, runs[0][0])
+        assert torch.equal(lp, runs[0][1])
+    toks, lp = runs[0]
+    assert lp.shape == (len(lens), 24) and bool(torch.isfinite(lp).all()) and bool((lp <= 0).all())
+    assert int(toks.max()) < cfg.vocab_size
+    assert len({tuple(r.tolist()) for r in toks}) > 1
