@@ -7,12 +7,13 @@
 // append, get_kv, then SDPA with is_causal=True at past_len 0 or the mask
 // key_pos <= past_len + query_pos otherwise) for a ragged batch.
 //
-// One wave per (sequence b, KV head hk, block of qt = 16 / G query tokens):
-// the 16 columns of the MFMA B operand are the (token, head) pairs
-// n = tq * G + head of the block, so each streamed K/V tile serves G heads x
-// qt tokens. The key loop is the decode kernel's tile pipeline (K fragments
-// in registers, V through LDS, QK^T and PV on the matrix cores, online
-// softmax per column); column n masks the keys after its own position
+// One wave per (sequence b, KV head hk, NB consecutive blocks of qt = 16 / G
+// query tokens): the 16 columns of a block's MFMA B operand are the (token,
+// head) pairs n = tq * G + head, so each streamed K/V tile serves G heads x
+// NB * qt tokens (the tile's K fragments and its transposed V are reused by
+// all NB blocks). The key loop is the decode kernel's tile pipeline (K
+// fragments in registers, V through LDS, QK^T and PV on the matrix cores,
+// online softmax per column); column n masks the keys after its own position
 // (position 0 is valid for every column, so no row is ever empty).
 //
 // Workgroups are laid out so that all query blocks of one (sequence, KV
@@ -29,7 +30,41 @@ namespace {
 
 constexpr int kXcds = 8;
 
-template <int D, bool kFP8>
+// PV of one tile for NB column blocks: V is transposed once (identity MFMA)
+// and multiplied by each block's P = P_hi + P_lo (see pv_tile).
+template <int D, bool kFP8, int NB>
+__device__ __forceinline__ void pv_tile_nb(const u32x4 (&vt)[2][Tile<D, kFP8>::NU], const bf16x8 (&ident16)[2],
+                                           const u32x2 (&ident8)[2], const bf16x8 (&pa_hi)[NB],
+                                           const bf16x8 (&pa_lo)[NB], WaveState<D, kFP8> (&st)[NB]) {
+  constexpr int NDB = D / 32;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) {
+    const int hi = c & 1;
+    f32x4 t0v, t1v;
+    if constexpr (kFP8) {
+      const int u = c >> 2;
+      const int hh = (c >> 1) & 1;
+      const u32x2 v0 = hh ? u32x2{vt[0][u][2], vt[0][u][3]} : u32x2{vt[0][u][0], vt[0][u][1]};
+      const u32x2 v1 = hh ? u32x2{vt[1][u][2], vt[1][u][3]} : u32x2{vt[1][u][0], vt[1][u][1]};
+      t0v = mfma_fp8(v0, ident8[hi], zero);
+      t1v = mfma_fp8(v1, ident8[hi], zero);
+    } else {
+      const int u = c >> 1;
+      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[0][u]), ident16[hi], zero);
+      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[1][u]), ident16[hi], zero);
+    }
+    const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
+    const bf16x8 vb = __builtin_convertvector(vv, bf16x8);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      st[j].o[c] = mfma_bf16(pa_hi[j], vb, st[j].o[c]);
+      st[j].o[c] = mfma_bf16(pa_lo[j], vb, st[j].o[c]);
+    }
+  }
+}
+
+template <int D, bool kFP8, int NB>
 __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
@@ -44,21 +79,22 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   __syncthreads();
 
   // workgroup -> (XCD, slot on that XCD) -> (pair, its k-th workgroup); the
-  // longest (last) query blocks of a pair go first
+  // longest (last) query blocks of a pair go first. a.nq counts groups of NB
+  // blocks here.
   const int xcd = blockIdx.x % kXcds;
   const int slot = blockIdx.x / kXcds;
   const int pair = (slot / a.wg_per_pair) * kXcds + xcd;
   if (pair >= a.batch * a.hkv) return;
-  const int qblk = a.nq - 1 - ((slot % a.wg_per_pair) * kWavesPerBlock + wave);
-  if (qblk < 0) return;
+  const int qgrp = a.nq - 1 - ((slot % a.wg_per_pair) * kWavesPerBlock + wave);
+  if (qgrp < 0) return;
   const int b = pair / a.hkv;
   const int hk = pair - b * a.hkv;
   const int nb = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
-  const int t_first = qblk * a.qt;
+  const int t_first = qgrp * a.qt * NB;
   if (t_first >= nb) return;
   const int pos0 = a.positions[b];
-  const int t_end = min(t_first + a.qt, nb);
-  // keys the block needs: 0 .. pos0 + t_end - 1, never past the host's bound (the page table's reach)
+  const int t_end = min(t_first + a.qt * NB, nb);
+  // keys the group needs: 0 .. pos0 + t_end - 1, never past the host's bound (the page table's reach)
   const int L = __builtin_amdgcn_readfirstlane(min(pos0 + t_end, a.max_len));
   if (pos0 < 0 || L <= 0) return;
 
@@ -67,28 +103,33 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   const int g = lane >> 4;
   const int tq = n / G;
   const int head = n - tq * G;
-  const bool col_valid = tq < a.qt && t_first + tq < t_end;
-  const int lim = col_valid ? min(pos0 + t_first + tq + 1, L) : 1;  // keys this column may see
-
-  bf16x8 qf[NDB];
-  {
-    const uint16_t *q = static_cast<const uint16_t *>(a.q);
-    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + head) * a.q_sh + (int64_t)(t_first + tq) * a.q_st;
+  int lim[NB];
+  bf16x8 qf[NB][NDB];
+  const uint16_t *q = static_cast<const uint16_t *>(a.q);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int tb = t_first + j * a.qt;
+    const bool col_valid = tq < a.qt && tb + tq < t_end;
+    lim[j] = col_valid ? min(pos0 + tb + tq + 1, L) : 1;  // keys this column may see
+    const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + head) * a.q_sh + (int64_t)(tb + tq) * a.q_st;
 #pragma unroll
     for (int s = 0; s < NDB; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (col_valid) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
-      qf[s] = __builtin_bit_cast(bf16x8, v);
+      qf[j][s] = __builtin_bit_cast(bf16x8, v);
     }
   }
   bf16x8 ident16[2];
   u32x2 ident8[2];
   make_identity(lane, ident16, ident8);
-  WaveState<D, kFP8> st;
+  WaveState<D, kFP8> st[NB];
 #pragma unroll
-  for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  st.m = kNegInf;
-  st.l = 0.f;
+  for (int j = 0; j < NB; ++j) {
+#pragma unroll
+    for (int c = 0; c < 2 * NDB; ++c) st[j].o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[j].m = kNegInf;
+    st[j].l = 0.f;
+  }
 
   char *vlds = smem_v + wave * Tile<D, kFP8>::kVBytes;
   const int ntiles = (L + kTileTokens - 1) / kTileTokens;
@@ -125,8 +166,11 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         load_k_block<D, kFP8>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      bf16x8 pa_hi, pa_lo;
-      qk_softmax<D, kFP8>(a.scale_log2, kTileTokens * it, lim, lane, buf[k & 1], qf, st, pa_hi, pa_lo);
+      bf16x8 pa_hi[NB], pa_lo[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        qk_softmax<D, kFP8>(a.scale_log2, kTileTokens * it, lim[j], lane, buf[k & 1], qf[j], st[j], pa_hi[j],
+                            pa_lo[j]);
       __builtin_amdgcn_sched_barrier(0);
       if (k + 1 < kChunkTiles)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
@@ -145,39 +189,53 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
-      pv_tile<D, kFP8>(vt, ident16, ident8, pa_hi, pa_lo, st);
+      pv_tile_nb<D, kFP8, NB>(vt, ident16, ident8, pa_hi, pa_lo, st);
     }
     __builtin_amdgcn_s_waitcnt(0);
   }
 
   // normalise and write: O row r of lane group g is column 4g + r
-  float l = st.l;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
   uint16_t *out = static_cast<uint16_t *>(a.out);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int col = 4 * g + r;
-    const float lr = __shfl(l, col, 64);
-    const float inv = lr > 0.f ? 1.0f / lr : 0.f;
-    const int ctq = col / G;
-    const int chead = col - ctq * G;
-    if (ctq < a.qt && t_first + ctq < t_end) {
-      const int64_t orow =
-          (int64_t)b * a.o_sb + (int64_t)(t_first + ctq) * a.o_st + (int64_t)(hk * G + chead) * a.o_sh;
+  for (int j = 0; j < NB; ++j) {
+    const int tb = t_first + j * a.qt;
+    float l = st[j].l;
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
 #pragma unroll
-      for (int c = 0; c < 2 * NDB; ++c) out[orow + o_col_d<kFP8>(c, n)] = f32_to_bf16_bits(st.o[c][r] * inv);
+    for (int r = 0; r < 4; ++r) {
+      const int col = 4 * g + r;
+      const float lr = __shfl(l, col, 64);
+      const float inv = lr > 0.f ? 1.0f / lr : 0.f;
+      const int ctq = col / G;
+      const int chead = col - ctq * G;
+      if (ctq < a.qt && tb + ctq < t_end) {
+        const int64_t orow =
+            (int64_t)b * a.o_sb + (int64_t)(tb + ctq) * a.o_st + (int64_t)(hk * G + chead) * a.o_sh;
+#pragma unroll
+        for (int c = 0; c < 2 * NDB; ++c) out[orow + o_col_d<kFP8>(c, n)] = f32_to_bf16_bits(st[j].o[c][r] * inv);
+      }
     }
   }
 }
 
+// Column blocks per wave: 4 at head_dim 64, 2 at 128 (the register budget).
+template <int D>
+constexpr int prefill_blocks() {
+  return D == 64 ? 4 : 2;
+}
+
 template <int D, bool kFP8>
-hipError_t launch_d(const PrefillArgs &a, hipStream_t stream) {
+hipError_t launch_d(const PrefillArgs &a0, hipStream_t stream) {
+  constexpr int NB = prefill_blocks<D>();
+  PrefillArgs a = a0;
+  a.nq = (a0.nq + NB - 1) / NB;  // groups of NB query blocks
+  a.wg_per_pair = (a.nq + kWavesPerBlock - 1) / kWavesPerBlock;
   const int64_t pairs = (int64_t)a.batch * a.hkv;
   const int64_t slots = (pairs + kXcds - 1) / kXcds * a.wg_per_pair;
   const int64_t grid = slots * kXcds;
   const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes;
-  hipLaunchKernelGGL((prefill_attn_kernel<D, kFP8>), dim3((unsigned)grid), dim3(64 * kWavesPerBlock), lds, stream,
+  hipLaunchKernelGGL((prefill_attn_kernel<D, kFP8, NB>), dim3((unsigned)grid), dim3(64 * kWavesPerBlock), lds, stream,
                      a);
   return hipGetLastError();
 }
