@@ -66,6 +66,56 @@ __device__ __forceinline__ float load_in(const RopeAppendArgs &a, const void *p,
   }
 }
 
+// The rest of one (row, token) after its inputs and table entries are in:
+// the rotated q row to q_out, or the rotated k and v into the token's cache
+// slot (fp8: codes and the per-(token, head) scales). `off` is the slot's
+// element offset (from the page entry `phys` of the paged pool).
+template <typename A, bool kFP8>
+__device__ __forceinline__ void finish_token(const RopeAppendArgs &a, int b, int row, int t, int64_t off, bool is_q,
+                                             int i, int half, bool active, float x1, float x2, float v1, float v2,
+                                             float c, float s) {
+  if (is_q) {
+    if (!active) return;
+    float o1, o2;
+    rotate_pair<A>(x1, x2, c, s, o1, o2);
+    const int64_t dst = (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh + (int64_t)t * a.qo_st;
+    Elem<A>::store(a.q_out, dst + i, o1);
+    Elem<A>::store(a.q_out, dst + half + i, o2);
+    return;
+  }
+
+  if (off < 0) return;
+  float k1 = 0.f, k2 = 0.f;
+  if (active) rotate_pair<A>(x1, x2, c, s, k1, k2);
+
+  if constexpr (!kFP8) {
+    if (active) {
+      Elem<A>::store(a.k_cache, off + i, k1);
+      Elem<A>::store(a.k_cache, off + half + i, k2);
+      Elem<A>::store(a.v_cache, off + i, v1);
+      Elem<A>::store(a.v_cache, off + half + i, v2);
+    }
+  } else {
+    // Per-(token, head) symmetric scale: absmax / 448, codes e4m3fn(x / scale).
+    const float kmax = wave_max(fmaxf(fabsf(k1), fabsf(k2)));
+    const float vmax = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
+    const float kscale = kmax / 448.0f;
+    const float vscale = vmax / 448.0f;
+    if (active) {
+      uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
+      uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
+      kc[off + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k1 / kscale);
+      kc[off + half + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k2 / kscale);
+      vc[off + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v1 / vscale);
+      vc[off + half + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v2 / vscale);
+    }
+    if (i == 0) {
+      a.k_scale[off / a.head_dim] = kscale;
+      a.v_scale[off / a.head_dim] = vscale;
+    }
+  }
+}
+
 template <typename A, bool kFP8, int kPart>
 __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const int row = blockIdx.x;
@@ -138,52 +188,97 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   }
 
   if (is_q) {
-    if (!active) return;
-    float o1, o2;
-    rotate_pair<A>(x1, x2, c, s, o1, o2);
-    const int64_t dst = (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh + (int64_t)t * a.qo_st;
-    Elem<A>::store(a.q_out, dst + i, o1);
-    Elem<A>::store(a.q_out, dst + half + i, o2);
+    finish_token<A, kFP8>(a, b, row, t, 0, true, i, half, active, x1, x2, v1, v2, c, s);
     return;
   }
-
   if (a.new_lens != nullptr && t >= a.new_lens[b]) return;  // padding token: no cache write
-  const int64_t off = slot_offset(a, b, hk, pos);  // wave-uniform
-  if (off < 0) return;
-  float k1 = 0.f, k2 = 0.f;
-  if (active) rotate_pair<A>(x1, x2, c, s, k1, k2);
+  finish_token<A, kFP8>(a, b, row, t, slot_offset(a, b, hk, pos), false, i, half, active, x1, x2, v1, v2, c, s);
+}
 
-  if constexpr (!kFP8) {
-    if (active) {
-      Elem<A>::store(a.k_cache, off + i, k1);
-      Elem<A>::store(a.k_cache, off + half + i, k2);
-      Elem<A>::store(a.v_cache, off + i, v1);
-      Elem<A>::store(a.v_cache, off + half + i, v2);
+// Prompt chunks (num_new > 1, activations as inputs): one wave per (row,
+// group of kChunkTok tokens, sequence). Every token's inputs, table entries
+// and (KV rows) page entry are loaded before the first is used, so a wave
+// costs about one memory round trip for its kChunkTok tokens instead of two
+// per token; the per-token arithmetic is finish_token's.
+constexpr int kChunkTok = 8;
+
+template <typename A, bool kFP8>
+__global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a) {
+  const int row = blockIdx.x;
+  const int tb = blockIdx.y * kChunkTok;
+  const int b = blockIdx.z;
+  const int i = threadIdx.x;
+  const int half = a.head_dim >> 1;
+  const bool active = i < half;
+  const int li = i & (half - 1);  // in bounds for any half; lanes past half drop their values
+  const bool is_q = row < a.hq;
+  const int hk = row - a.hq;
+  const int pos0 = a.positions[b];
+  const int nlen = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
+  const void *p1 = is_q ? a.q_in : a.k_in;
+  const int64_t o1 = is_q ? (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh : (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh;
+  const int64_t st1 = is_q ? a.qi_st : a.ki_st;
+  const int64_t o2 = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh;
+  float x1[kChunkTok], x2[kChunkTok], v1[kChunkTok], v2[kChunkTok], c[kChunkTok], sn[kChunkTok];
+  int64_t phys[kChunkTok];
+#pragma unroll
+  for (int u = 0; u < kChunkTok; ++u) {
+    const int t = min(tb + u, a.num_new - 1);
+    const int64_t pos = (int64_t)pos0 + t;
+    const int64_t tp = pos < 0 ? 0 : (pos >= a.table_len ? a.table_len - 1 : pos);
+    x1[u] = Elem<A>::load(p1, o1 + t * st1 + li);
+    x2[u] = Elem<A>::load(p1, o1 + t * st1 + half + li);
+    v1[u] = is_q ? 0.f : Elem<A>::load(a.v_in, o2 + t * a.vi_st + li);
+    v2[u] = is_q ? 0.f : Elem<A>::load(a.v_in, o2 + t * a.vi_st + half + li);
+    c[u] = Elem<A>::load(a.table, tp * a.head_dim + li);
+    sn[u] = Elem<A>::load(a.table, tp * a.head_dim + half + li);
+    int64_t j = pos < 0 ? 0 : pos / a.page_size;
+    j = j < a.max_pages ? j : a.max_pages - 1;
+    phys[u] = (a.page_table != nullptr && !is_q) ? a.page_table[(int64_t)b * a.max_pages + j] : 0;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (a.lens_out != nullptr && row == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.lens_out[b] = pos0 + nlen;
+#pragma unroll
+  for (int u = 0; u < kChunkTok; ++u) {
+    const int t = tb + u;
+    const int64_t pos = (int64_t)pos0 + t;
+    if (t >= a.num_new || pos < 0 || pos >= a.table_len) continue;  // uniform
+    if (is_q) {
+      finish_token<A, kFP8>(a, b, row, t, 0, true, i, half, active, x1[u], x2[u], 0.f, 0.f, c[u], sn[u]);
+      continue;
     }
-  } else {
-    // Per-(token, head) symmetric scale: absmax / 448, codes e4m3fn(x / scale).
-    const float kmax = wave_max(fmaxf(fabsf(k1), fabsf(k2)));
-    const float vmax = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
-    const float kscale = kmax / 448.0f;
-    const float vscale = vmax / 448.0f;
-    if (active) {
-      uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
-      uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
-      kc[off + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k1 / kscale);
-      kc[off + half + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k2 / kscale);
-      vc[off + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v1 / vscale);
-      vc[off + half + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v2 / vscale);
+    if (t >= nlen) continue;  // padding token: no cache write
+    int64_t off = -1;        // slot_offset, from the page entry loaded above
+    if (pos < a.capacity) {
+      const int64_t j = pos / a.page_size;
+      const int64_t slot = pos - j * a.page_size;
+      if (a.page_table == nullptr)
+        off = (int64_t)b * a.c_seq + j * a.c_page + (int64_t)hk * a.c_head + slot * a.head_dim;
+      else if (j < a.max_pages && phys[u] >= 0 && phys[u] < a.num_pages)
+        off = phys[u] * a.c_page + (int64_t)hk * a.c_head + slot * a.head_dim;
     }
-    if (i == 0) {
-      a.k_scale[off / a.head_dim] = kscale;
-      a.v_scale[off / a.head_dim] = vscale;
-    }
+    finish_token<A, kFP8>(a, b, row, t, off, false, i, half, active, x1[u], x2[u], v1[u], v2[u], c[u], sn[u]);
   }
 }
 
 }  // namespace
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
+  if (a.num_new > 1 && a.part_splits <= 0) {
+    const dim3 cgrid(a.hq + a.hkv, (a.num_new + kChunkTok - 1) / kChunkTok, a.batch);
+    switch (kind) {
+      case CacheKind::kBF16:
+        hipLaunchKernelGGL((rope_append_chunk_kernel<BF16Tag, false>), cgrid, dim3(64), 0, stream, a);
+        break;
+      case CacheKind::kF32:
+        hipLaunchKernelGGL((rope_append_chunk_kernel<float, false>), cgrid, dim3(64), 0, stream, a);
+        break;
+      case CacheKind::kFP8:
+        hipLaunchKernelGGL((rope_append_chunk_kernel<BF16Tag, true>), cgrid, dim3(64), 0, stream, a);
+        break;
+    }
+    return hipGetLastError();
+  }
   const dim3 grid(a.hq + a.hkv, a.num_new > 0 ? a.num_new : 1, a.batch);
   const dim3 block(64);
   // split-K partial inputs: bf16 activations only (checked by the caller)
