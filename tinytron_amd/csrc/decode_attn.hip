@@ -725,11 +725,14 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
 }
 
 // Persistent balanced kernel: NW = gridDim.x * 4 waves, all resident. The
-// code is compiled for kStreamOcc workgroups per CU (register budget) but
-// launched with kStreamBlocksPerCU: four streaming waves per CU measured
-// best (fewer, longer runs per wave and fewer partials; C2 -6 %, C4 -1 %).
+// code is compiled for kStreamOcc workgroups per CU (register budget) and
+// launched with stream_blocks_per_cu(D) of them: at head_dim 128 four
+// streaming waves per CU measured best (fewer, longer runs per wave and
+// fewer partials; C2 -10 %, C3 -1 % against eight); at head_dim 64 a tile is
+// half the bytes, four waves keep too little in flight, and eight measured
+// better (C5 step -5 %, end to end +2 %).
 constexpr int kStreamOcc = 2;
-constexpr int kStreamBlocksPerCU = 1;
+constexpr int stream_blocks_per_cu(int head_dim) { return head_dim == 64 ? 2 : 1; }
 
 // LDS of the split kernel: V slots [4 waves] | wave sums [4] | prefix [B + 1]
 // (| q staging [4 waves][16][D] bf16 for the fused variant).
@@ -1008,9 +1011,9 @@ hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
   }
-  // kStreamBlocksPerCU resident workgroups of 4 waves per CU; no more waves than the longest-case tile count
+  // stream_blocks_per_cu(D) resident workgroups of 4 waves per CU; no more waves than the longest-case tile count
   const int64_t tiles_bound = (int64_t)a.batch * a.hkv * ((a.max_len + kTileTokens - 1) / kTileTokens);
-  int64_t blocks = std::min<int64_t>((int64_t)cus * kStreamBlocksPerCU, kMaxStreamBlocks);
+  int64_t blocks = std::min<int64_t>((int64_t)cus * stream_blocks_per_cu(D), kMaxStreamBlocks);
   blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (tiles_bound + kWavesPerBlock - 1) / kWavesPerBlock));
   a.stream_waves = (int)(blocks * kWavesPerBlock);
   const size_t lds_prefix = 16 * ((sizeof(int) * (kWavesPerBlock + (size_t)a.batch + 1) + 15) / 16);
