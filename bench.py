@@ -1,20 +1,23 @@
 #!/usr/bin/env python
 """Decode-step benchmark on one MI355X.
 
-A step is one pass of the hot path over one batch: fused RoPE + KV append of
-one new token per sequence (tt_rope_append_*) followed by GQA split-K decode
-attention over each sequence's L_b + 1 cached tokens (tt_gqa_decode_attn_*).
+A step is one pass of the hot path over one batch: RoPE + KV append of one new
+token per sequence and GQA split-K decode attention over each sequence's
+L_b + 1 cached tokens. bf16 caches run it as one fused launch pair
+(tt_decode_attn_append_*); fp8 caches (and --step-path two) as
+tt_rope_append_* followed by tt_gqa_decode_attn_*.
 Inputs are synthetic (seed 1337) and resident in HBM before the timed region.
 
-Default workload (the metric's batch-64 case):
+Default workload (config C3, the headline metric's batch-64 case):
 ragged paged bf16 decode attention, B = 64, 32 q heads / 8 KV heads, D = 128,
 L_b ~ U[128, 16384], page size 16, page table = seeded random permutation of
-the physical pages. --config c2 / c4 select configs 2 and 4.
+the physical pages. --config c2 / c4 / c5a select the other configs (c5a:
+one layer's attention of the C5 model mid-decode); --e2e-only runs C5 end to end.
 
 value = algorithmic bytes per step / time per step (GB/s, 1 GB = 1e9 B), with
 algorithmic bytes = unique K/V bytes read (+ fp8 scales) + q/out/new-token/page
 table I/O. The roofline object covers the decode-attention operator (the
-split kernel and its combine kernel) timed alone with HIP events on the
+balanced stream kernel and its merge kernel) timed alone with HIP events on the
 stream it runs on. The CPU baseline times the reference's own op sequence
 (torch on the host, H_q-expanded cache, per sequence) on a bounded sample of
 the same sequences.
@@ -70,7 +73,7 @@ C5 = dict(num_layer=24, hidden_size=2048, num_attention_heads=32, num_key_value_
 
 
 def e2e_c5(args, torch):
-    """Greedy decode through the engine, tokens/s as
+    """Greedy decode through the engine (config C5: 24 layers, d 2048, batch 64), tokens/s as
     engine.py:236-243 defines it, plus the reference op sequence on the host
     for a bounded sample of the same batch."""
     from tinytron_amd.engine import InferenceEngine
@@ -250,7 +253,8 @@ def build_workload(cfg, seed, torch, ops):
 
 
 def algorithmic_bytes(cfg, total):
-    """Bytes the step must move at minimum (SURVEY 8d accounting)."""
+    """Bytes the step must move at minimum: K/V of every attended token (+ fp8
+    scales), page-table entries, q in / out, lengths, the new token's K/V."""
     B, hq, hkv, D, P = cfg["batch"], cfg["hq"], cfg["hkv"], cfg["head_dim"], cfg["page"]
     e = 1 if cfg["fp8"] else 2
     tokens = int(total.sum())

@@ -109,7 +109,8 @@ def e4m3fn_encode(x) -> np.ndarray:
 
 
 def quantize_e4m3_rows(x_f32: np.ndarray):
-    """Per-row symmetric fp8 quantization (spec D4 of this build).
+    """Per-row symmetric fp8 quantization: this build's fp8-e4m3 cache format
+    (the reference has no fp8 cache; one scale per (token, head) row).
 
     For each row (last axis = head_dim): absmax = max|x| in fp32,
     scale = absmax / 448 (fp32 division, round to nearest), q = e4m3(x / scale)

@@ -1,6 +1,6 @@
 """GPU: the drop-in Attention module, caches and engine end to end.
 
-* C1 (6 layers, d 512, 8/2 heads, D 64, V 32000, fp32,
+* C1 (the reference's CPU-sized model: 6 layers, d 512, 8/2 heads, D 64, V 32000, fp32,
   prompt 128, 64 greedy steps, contiguous cache): greedy tokens of the GPU
   engine equal those of the reference's op sequence restated on the CPU
   (oracle.ref_model), except at a near-tie of the two top logits.

@@ -3,7 +3,7 @@ a ragged prompt chunk was appended) vs the fp64 oracle
 (oracle.attention.prefill_attention, itself pinned to torch SDPA with the
 reference's causal mask).
 
-Tolerance: |out - ref| <= 2e-3 + 2e-2 * |ref|; fp8
+Tolerance (the path's stated target): |out - ref| <= 2e-3 + 2e-2 * |ref|; fp8
 caches against the oracle on the dequantised values. Rows of padding tokens
 (t >= new_lens[b]) must stay untouched.
 """
