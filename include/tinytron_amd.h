@@ -395,6 +395,25 @@ int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const f
 int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t inter, void *y, tt_stream_t stream);
 
 /*
+ * Prefill rows (gpt.py:40-41 + norm.py:6-19 over every prompt token): the
+ * residual add of a projection's bf16 output a [M, C] (row stride lda) into
+ * the fp32 stream x, x[m] += float(a[m]), then y[m] = bf16(weight * (x[m] *
+ * rsqrt(mean(x[m]^2) + eps))). a may be NULL (plain RMSNorm). C as for
+ * tt_add_rmsnorm_bf16; lda % 4 == 0.
+ */
+int tt_add_rmsnorm_rows_bf16(float *x, const void *a, int64_t lda, const float *weight, float eps, void *y, int64_t m,
+                             int64_t c, tt_stream_t stream);
+
+/*
+ * SwiGLU over prompt rows, mlp.py:44-45 under autocast: g and u are the bf16
+ * outputs of the gate and up projections [M, I] (row strides ldg, ldu; a
+ * stacked gate|up output passes u = g + I), y[m][i] = bf16(bf16(silu(g)) * u),
+ * y contiguous [M, I]. I, ldg, ldu multiples of 4.
+ */
+int tt_silu_mul_rows_bf16(const void *g, int64_t ldg, const void *u, int64_t ldu, int64_t m, int64_t inter, void *y,
+                          tt_stream_t stream);
+
+/*
  * Token sampling from logits [M, V] (row stride ld), replacing
  * filter_logits + sample_next_token / sample_next_token_with_log_prob
  * (tinytron/inference/sampler.py:6-62; called at engine.py:196-212):

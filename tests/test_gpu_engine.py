@@ -227,6 +227,52 @@ def test_prefill_kernel_matches_sdpa_path(kv_dtype):
         assert torch.allclose(a[i, :n], b[i, :n], rtol=2e-2, atol=2e-2), f"sequence {i}"
 
 
+@pytest.mark.parametrize("kv_dtype", [None, "fp8"])
+def test_packed_prefill_matches_module_path(kv_dtype):
+    """GPT.forward's packed bf16 prefill (projections, residual add + RMSNorm
+    and SwiGLU over the real prompt tokens only) against the module path on
+    the padded [B, T] grid: same lengths, the cached K of every prompt token
+    and the logits at logits_index agree to bf16 rounding (two GEMM shapes,
+    two norm reductions), and the next greedy decode step agrees."""
+    from tinytron_amd.cache import PagedKVCache
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=4,
+                     intermediate_size=2048, vocab_size=4096, block_size=256)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    kvd = torch.float8_e4m3fn if kv_dtype == "fp8" else None
+    g = torch.Generator().manual_seed(23)
+    B, T = 4, 50
+    lens = [50, 7, 1, 33]
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(DEV)
+    li = (torch.tensor(lens) - 1).to(DEV)
+    outs = []
+    for packed in (False, True):
+        model.fused_prefill = packed
+        cache = PagedKVCache.from_model_config(cfg, B, 16, DEV, torch.bfloat16, kv_cache_dtype=kvd, paged_pool=True,
+                                               seq_capacity=[64] * B)
+        with torch.no_grad():
+            cache.set_pending_new_lens(lens)
+            logits, _ = model(prompt, use_cache=True, past_key_values=cache, position_offset=0, logits_index=li)
+            cache.set_pending_new_lens(None)
+            nxt = logits[:, -1].argmax(-1, keepdim=True)
+            step, _ = model(nxt, use_cache=True, past_key_values=cache, position_offset=0)
+        ks = [cache.get_layer_cache(1).gather(b, lens[b], torch.float32)[0].float().cpu() for b in range(B)]
+        outs.append((logits.float().cpu(), nxt.cpu(), step.float().cpu(), ks,
+                     cache.get_layer_cache(0).seq_lens_host))
+    model.fused_prefill = True
+    (l0, n0, s0, k0, c0), (l1, n1, s1, k1, c1) = outs
+    assert l1.shape == l0.shape == (B, 1, cfg.vocab_size)
+    assert c0 == c1 == [n + 1 for n in lens]
+    tol = 0.1 if kv_dtype == "fp8" else 2e-2
+    for b in range(B):
+        assert torch.allclose(k0[b], k1[b], rtol=tol, atol=tol), f"sequence {b}: cached K differs"
+    for a, c in ((l0, l1), (s0, s1)):
+        scale = float(a.abs().max())
+        assert float((a - c).abs().max()) <= 0.05 * scale
+    assert torch.equal(n0, n1) or float((l0 - l1).abs().max()) < 1e-2
+
+
 def test_sampled_generation_is_seeded_and_graph_invariant():
     """Non-greedy generation (temperature / top-k / top-p through the device
     sampler, log-probs returned): repeatable under torch.manual_seed, equal

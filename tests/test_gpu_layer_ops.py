@@ -119,6 +119,43 @@ def test_silu_mul():
     assert _bf16_ulps(got, ref) <= 1
 
 
+@pytest.mark.parametrize("C,with_addend", [(2048, True), (1024, False), (4096, True)])
+def test_add_rmsnorm_rows(C, with_addend):
+    """Prefill rows: x += float(bf16 addend) exactly (strided addend rows),
+    y within one bf16 ulp of the fp64 RMSNorm."""
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(C + with_addend)
+    M, eps = 3001, 1e-6
+    x = torch.randn(M, C, generator=g) * 3
+    w = torch.rand(C, generator=g) + 0.5
+    wide = (torch.randn(M, C + 64, generator=g) * 2).to(torch.bfloat16)
+    a = wide[:, 32:32 + C] if with_addend else None  # row stride C + 64
+    xd = x.to(DEV)
+    y = ops.add_rmsnorm_rows(xd, w.to(DEV), eps, addend=wide.to(DEV)[:, 32:32 + C] if with_addend else None).cpu()
+    x_ref = x + a.float() if with_addend else x
+    assert torch.equal(xd.cpu(), x_ref)  # the residual update is exact
+    xr = x_ref.double()
+    y_ref = (w.double() * (xr / torch.sqrt((xr * xr).mean(-1, keepdim=True) + eps))).float().to(torch.bfloat16)
+    assert _bf16_ulps(y, y_ref) <= 1
+
+
+def test_silu_mul_rows():
+    """Prefill rows: bf16(bf16(silu(g)) * u) from bf16 gate / up outputs (a
+    stacked gate|up buffer's two column halves), within one bf16 ulp of torch."""
+    from tinytron_amd import ops
+
+    g = torch.Generator().manual_seed(6)
+    M, I = 1003, 6144
+    gu = (torch.randn(M, 2 * I, generator=g) * 2).to(torch.bfloat16)
+    gud = gu.to(DEV)
+    got = ops.silu_mul_rows(gud[:, :I], gud[:, I:]).cpu()
+    ref = (torch.nn.functional.silu(gu[:, :I].float()).to(torch.bfloat16).float() * gu[:, I:].float()).to(torch.bfloat16)
+    assert _bf16_ulps(got, ref) <= 1
+    sep = ops.silu_mul_rows(gud[:, :I].contiguous(), gud[:, I:].contiguous()).cpu()
+    assert torch.equal(sep, got)
+
+
 def test_layer_ops_reject_bad_shapes():
     from tinytron_amd import ops
 

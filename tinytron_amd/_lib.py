@@ -110,6 +110,8 @@ SIGNATURES = {
     "tt_splitk_reduce_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_add_rmsnorm_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
     "tt_silu_mul_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
+    "tt_add_rmsnorm_rows_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
+    "tt_silu_mul_rows_bf16": ([_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_decode_attn_append_bf16": (_DECODE_APPEND_HEAD + _DECODE_APPEND_TAIL, ctypes.c_int),
     "tt_decode_attn_append_fp8": (_DECODE_APPEND_HEAD + [_vp, _vp] + _DECODE_APPEND_TAIL, ctypes.c_int),
     "tt_sample_bf16": (_SAMPLE, ctypes.c_int),

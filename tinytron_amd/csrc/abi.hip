@@ -668,6 +668,37 @@ int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t i
                   "silu_mul launch");
 }
 
+int tt_add_rmsnorm_rows_bf16(float *x, const void *a, int64_t lda, const float *weight, float eps, void *y, int64_t m,
+                             int64_t c, tt_stream_t stream) {
+  TT_CHECK(x && weight && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(m >= 0 && m <= 0x7fffffff, TT_ERR_INVALID_ARGUMENT, "bad row count");
+  TT_CHECK(c % 1024 == 0 && c >= 1024 && c <= 8192, TT_ERR_UNSUPPORTED,
+           "hidden size must be a multiple of 1024 in [1024, 8192], got %lld", (long long)c);
+  TT_CHECK(a == nullptr || (lda >= c && lda % 4 == 0), TT_ERR_INVALID_ARGUMENT, "addend row stride must be >= C and a multiple of 4");
+  TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(y, 8) && (a == nullptr || aligned(a, 8)),
+           TT_ERR_INVALID_ARGUMENT, "x / weight must be 16-byte aligned, y / addend 8-byte aligned");
+  if (m == 0) return ok();
+  (void)hipGetLastError();
+  return from_hip(tt::launch_add_rmsnorm_rows(x, static_cast<const uint16_t *>(a), lda, (int)m, (int)c, weight, eps,
+                                              static_cast<uint16_t *>(y), (hipStream_t)stream),
+                  "add_rmsnorm_rows launch");
+}
+
+int tt_silu_mul_rows_bf16(const void *g, int64_t ldg, const void *u, int64_t ldu, int64_t m, int64_t inter, void *y,
+                          tt_stream_t stream) {
+  TT_CHECK(g && u && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(m >= 0 && inter > 0 && ldg >= inter && ldu >= inter, TT_ERR_INVALID_ARGUMENT, "bad shape");
+  TT_CHECK(inter % 4 == 0 && ldg % 4 == 0 && ldu % 4 == 0 && inter < ((int64_t)1 << 30), TT_ERR_UNSUPPORTED,
+           "intermediate size and row strides must be multiples of 4");
+  TT_CHECK(m * inter < ((int64_t)1 << 40), TT_ERR_UNSUPPORTED, "too many elements");
+  TT_CHECK(aligned(g, 8) && aligned(u, 8) && aligned(y, 8), TT_ERR_INVALID_ARGUMENT, "g / u / y must be 8-byte aligned");
+  if (m == 0) return ok();
+  (void)hipGetLastError();
+  return from_hip(tt::launch_silu_mul_rows(static_cast<const uint16_t *>(g), ldg, static_cast<const uint16_t *>(u), ldu,
+                                           m, (int)inter, static_cast<uint16_t *>(y), (hipStream_t)stream),
+                  "silu_mul_rows launch");
+}
+
 int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
                                const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
                                int64_t splits, int64_t split_stride, const void *rope_table, int64_t rope_table_len,

@@ -254,6 +254,73 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
   *reinterpret_cast<uint2 *>(y + i) = make_uint2(out[0] | ((uint32_t)out[1] << 16), out[2] | ((uint32_t)out[3] << 16));
 }
 
+// Prefill rows (many tokens, bf16 projection outputs from a library GEMM):
+// x += float(a[m]) (a: bf16 [M, C] with row stride lda, the projection's
+// autocast output; a == nullptr skips the add), then
+// y = bf16(w * x * rsqrt(mean(x^2) + eps)) as in add_rmsnorm_kernel.
+template <int PER>
+__global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const uint16_t *a, int64_t lda,
+                                                               const float *w, float eps, uint16_t *y, int C) {
+  __shared__ float red[4];
+  const int64_t row = (int64_t)blockIdx.x * C;
+  f32x4 v[PER];
+  uint2 av[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = 4 * (threadIdx.x + 256 * j);
+    v[j] = *reinterpret_cast<const f32x4 *>(x + row + c);
+    av[j] = make_uint2(0u, 0u);
+    if (a != nullptr) av[j] = *reinterpret_cast<const uint2 *>(a + (int64_t)blockIdx.x * lda + c);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (a != nullptr) {
+      v[j][0] += __builtin_bit_cast(float, av[j].x << 16);
+      v[j][1] += __builtin_bit_cast(float, av[j].x & 0xffff0000u);
+      v[j][2] += __builtin_bit_cast(float, av[j].y << 16);
+      v[j][3] += __builtin_bit_cast(float, av[j].y & 0xffff0000u);
+      *reinterpret_cast<f32x4 *>(x + row + 4 * (threadIdx.x + 256 * j)) = v[j];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += v[j][e] * v[j][e];
+  }
+  const float var = block_sum_256(ss, red) / (float)C;
+  const float r = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = 4 * (threadIdx.x + 256 * j);
+    const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
+    uint32_t lo = f32_to_bf16_bits(wv[0] * (v[j][0] * r)) | ((uint32_t)f32_to_bf16_bits(wv[1] * (v[j][1] * r)) << 16);
+    uint32_t hi = f32_to_bf16_bits(wv[2] * (v[j][2] * r)) | ((uint32_t)f32_to_bf16_bits(wv[3] * (v[j][3] * r)) << 16);
+    *reinterpret_cast<uint2 *>(y + row + c) = make_uint2(lo, hi);
+  }
+}
+
+// SwiGLU of bf16 gate and up projection outputs (rows m of g and u, row
+// strides ldg / ldu): y[m][i] = bf16(bf16(silu(g)) * u), y contiguous
+// [M, I]; four columns per thread.
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *g_in, int64_t ldg, const uint16_t *u_in,
+                                                            int64_t ldu, int I, int64_t MI, uint16_t *y) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;  // index into [M, I]
+  if (i >= MI) return;
+  const int64_t m = i / I;
+  const int64_t c = i - m * I;
+  const uint2 g2 = *reinterpret_cast<const uint2 *>(g_in + m * ldg + c);
+  const uint2 u2 = *reinterpret_cast<const uint2 *>(u_in + m * ldu + c);
+  const float g[4] = {__builtin_bit_cast(float, g2.x << 16), __builtin_bit_cast(float, g2.x & 0xffff0000u),
+                      __builtin_bit_cast(float, g2.y << 16), __builtin_bit_cast(float, g2.y & 0xffff0000u)};
+  const float u[4] = {__builtin_bit_cast(float, u2.x << 16), __builtin_bit_cast(float, u2.x & 0xffff0000u),
+                      __builtin_bit_cast(float, u2.y << 16), __builtin_bit_cast(float, u2.y & 0xffff0000u)};
+  uint16_t out[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float act = round_bf16(g[e] / (1.0f + expf(-g[e])));
+    out[e] = f32_to_bf16_bits(act * u[e]);
+  }
+  *reinterpret_cast<uint2 *>(y + i) = make_uint2(out[0] | ((uint32_t)out[1] << 16), out[2] | ((uint32_t)out[3] << 16));
+}
+
 }  // namespace
 
 hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream) {
@@ -322,6 +389,36 @@ hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hip
   const int64_t threads = ((int64_t)M * I + 3) / 4;
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, P, S,
                      (int64_t)M * 2 * I, I, M, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm_rows(float *x, const uint16_t *a, int64_t lda, int M, int C, const float *w, float eps,
+                                   uint16_t *y, hipStream_t stream) {
+  switch (C / 1024) {  // C in {1024, 2048, ..., 8192}, checked by the caller
+#define TT_ROWS_CASE(n)                                                                                              \
+  case n:                                                                                                            \
+    hipLaunchKernelGGL((add_rmsnorm_rows_kernel<n>), dim3(M), dim3(256), 0, stream, x, a, lda, w, eps, y, C);     \
+    break;
+    TT_ROWS_CASE(1)
+    TT_ROWS_CASE(2)
+    TT_ROWS_CASE(3)
+    TT_ROWS_CASE(4)
+    TT_ROWS_CASE(5)
+    TT_ROWS_CASE(6)
+    TT_ROWS_CASE(7)
+    TT_ROWS_CASE(8)
+#undef TT_ROWS_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_rows(const uint16_t *g, int64_t ldg, const uint16_t *u, int64_t ldu, int64_t M, int I,
+                                uint16_t *y, hipStream_t stream) {
+  const int64_t threads = (M * I + 3) / 4;
+  hipLaunchKernelGGL(silu_mul_rows_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, g, ldg, u,
+                     ldu, I, M * I, y);
   return hipGetLastError();
 }
 

@@ -101,6 +101,10 @@ hipError_t launch_reduce_bf16(const float *P, int S, int64_t MN, uint16_t *y, hi
 hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, const float *w, float eps, uint16_t *y,
                               hipStream_t stream);
 hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hipStream_t stream);
+hipError_t launch_add_rmsnorm_rows(float *x, const uint16_t *a, int64_t lda, int M, int C, const float *w, float eps,
+                                   uint16_t *y, hipStream_t stream);
+hipError_t launch_silu_mul_rows(const uint16_t *g, int64_t ldg, const uint16_t *u, int64_t ldu, int64_t M, int I,
+                                uint16_t *y, hipStream_t stream);
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream);
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream);

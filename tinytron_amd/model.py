@@ -28,7 +28,10 @@ split-K GEMM for the stacked q|k|v projection, the attention launch pair
 c_proj GEMM, residual add + RMSNorm in one kernel, one GEMM for the stacked
 gate|up projection, SwiGLU, the down GEMM, and the next residual add +
 RMSNorm -- 9 launches instead of about 30 (10 with an fp8 cache), with the
-same math and bf16 rounding points as the module path.
+same math and bf16 rounding points as the module path. A bf16 prefill with
+``logits_index`` (the engine's) runs on the packed prompt tokens
+(``GPT.fused_prefill``): the projections, residual add + RMSNorm and SwiGLU
+see only the sum(new_lens) real tokens, not the B x T padded grid.
 """
 from __future__ import annotations
 
@@ -243,6 +246,7 @@ class GPT(nn.Module):
             raise ValueError("only the tied lm_head of the reference's default config is supported")
         self._lm_head_weight = None
         self.fused_decode = True   # bf16 decode steps through the fused layer kernels when shapes allow
+        self.fused_prefill = True  # bf16 ragged prefill over the packed prompt tokens when shapes allow
         self._stacked = {}         # layer -> (source key, q|k|v weight, gate|up weight)
         self._decode_bufs = {}     # (device, rows) -> split-K partial buffer
 
@@ -347,6 +351,71 @@ class GPT(nn.Module):
         logits = F.linear(h, self.lm_head_weight())
         return logits.view(B, 1, -1)
 
+    # -- packed bf16 prefill ---------------------------------------------------------
+    def _fused_prefill_ok(self, cache, idx: torch.Tensor, logits_index: torch.Tensor) -> bool:
+        c = self.config
+        if not self.fused_prefill or self.compute_dtype != torch.bfloat16 or not self.wte.weight.is_cuda:
+            return False
+        D = c.hidden_size // c.num_attention_heads
+        if not (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192 and D in (64, 128)
+                and c.num_attention_heads // c.num_key_value_heads <= 16 and c.intermediate_size % 4 == 0
+                and all(blk.attn.prefill_kernel for blk in self.blocks)
+                and all(_is_fused_cache(cache.get_layer_cache(i))
+                        and cache.get_layer_cache(i).layout.kind in ("bf16", "fp8") for i in range(len(self.blocks)))):
+            return False
+        # every requested logit row must be one of the sequence's new tokens
+        B, T = idx.shape
+        new = cache.get_layer_cache(0)._pending_new_lens or [T] * B
+        li = logits_index.reshape(-1).tolist()
+        return len(li) == B and all(0 <= int(i) < min(int(n), T) for i, n in zip(li, new))
+
+    def _prefill_fused(self, idx: torch.Tensor, cache, position_offset: int, logits_index: torch.Tensor) -> torch.Tensor:
+        """Prefill of a ragged batch (gpt.py:84-115 over T prompt tokens, of
+        which sequence b brings new_lens[b]) on the packed tokens only: the
+        projections and the norm / SwiGLU kernels see sum(new_lens) rows instead
+        of B * T; the RoPE + append and the prefill attention kernels read the
+        q / k / v rows scattered back to the [B, T] grid (padding rows are never
+        read). Same math and bf16 rounding points as the module path; returns
+        the logits at logits_index[b] of each sequence, [B, 1, V]."""
+        c = self.config
+        B, T = idx.shape
+        C, Hq, Hkv = c.hidden_size, c.num_attention_heads, c.num_key_value_heads
+        D = C // Hq
+        dev = idx.device
+        first = cache.get_layer_cache(0)
+        lens = first.seq_lens_host
+        if len(set(lens)) == 1 and lens[0] != position_offset:
+            raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
+        new = [min(int(n), T) for n in (first._pending_new_lens or [T] * B)]
+        cu = [0]
+        for n in new:
+            cu.append(cu[-1] + n)
+        sel = torch.cat([torch.arange(n, dtype=torch.int64) + b * T for b, n in enumerate(new)]).to(dev)
+        rows = torch.tensor(cu[:-1], dtype=torch.int64, device=dev) + logits_index.to(dev, torch.int64)
+        table = rope_table_for(first.max_seq_len + T, D, c.rope_theta, torch.bfloat16, dev)
+        eps = self.lnf.variance_epsilon
+        x = self.wte(idx.reshape(-1).index_select(0, sel)).float().contiguous()  # fp32 residual stream [N, C]
+        h = ops.add_rmsnorm_rows(x, self.blocks[0].ln_1.weight, eps)             # bf16 [N, C]
+        qp = torch.empty(B * T, Hq * D, dtype=torch.bfloat16, device=dev)
+        kp = torch.empty(B * T, Hkv * D, dtype=torch.bfloat16, device=dev)
+        vp = torch.empty(B * T, Hkv * D, dtype=torch.bfloat16, device=dev)
+        y_grid = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
+        for i, blk in enumerate(self.blocks):
+            layer = cache.get_layer_cache(i)
+            att = blk.attn
+            qp.index_copy_(0, sel, F.linear(h, att.q_proj.weight))
+            kp.index_copy_(0, sel, F.linear(h, att.k_proj.weight))
+            vp.index_copy_(0, sel, F.linear(h, att.v_proj.weight))
+            q_rot = layer.rope_append(qp.view(B, T, Hq, D).transpose(1, 2), kp.view(B, T, Hkv, D).transpose(1, 2),
+                                      vp.view(B, T, Hkv, D).transpose(1, 2), table, new_lens=new)
+            layer.prefill_attend(q_rot, new, out=y_grid)
+            y = y_grid.view(B * T, C).index_select(0, sel)
+            h = ops.add_rmsnorm_rows(x, blk.ln_2.weight, eps, addend=F.linear(y, att.c_proj.weight))
+            m = ops.silu_mul_rows(F.linear(h, blk.mlp.gate_proj.weight), F.linear(h, blk.mlp.up_proj.weight))
+            nxt = self.blocks[i + 1].ln_1.weight if i + 1 < len(self.blocks) else self.lnf.weight
+            h = ops.add_rmsnorm_rows(x, nxt, eps, addend=F.linear(m, blk.mlp.down_proj.weight))
+        return F.linear(h.index_select(0, rows), self.lm_head_weight()).unsqueeze(1)
+
     def forward(self, idx: torch.Tensor, targets=None, past_key_values=None, use_cache: bool = False,
                 position_offset: int = 0, logits_index: torch.Tensor | None = None):
         """gpt.py:84-115. ``logits_index`` ([B], optional, prefill only)
@@ -359,6 +428,10 @@ class GPT(nn.Module):
             raise TypeError("tinytron_amd.GPT runs with a tinytron_amd PagedKVCache")
         if T == 1 and logits_index is None and targets is None and self._fused_decode_ok(paged_cache, B):
             logits = self._decode_step_fused(idx, paged_cache, position_offset)
+            return (logits, paged_cache) if use_cache else logits
+        if T > 1 and logits_index is not None and targets is None and self._fused_prefill_ok(paged_cache, idx,
+                                                                                             logits_index):
+            logits = self._prefill_fused(idx, paged_cache, position_offset, logits_index)
             return (logits, paged_cache) if use_cache else logits
         x = self.wte(idx)
         for layer_idx, block in enumerate(self.blocks):

@@ -437,6 +437,44 @@ def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, partials: tor
     return out
 
 
+def add_rmsnorm_rows(x: torch.Tensor, weight: torch.Tensor, eps: float, addend: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """x += float(addend) (in place, if given: a projection's bf16 output [M, C],
+    row stride a multiple of 4); returns bf16 RMSNorm(x) [M, C]. The residual
+    add (gpt.py:40-41) and the next RMSNorm (norm.py:6-19) over prompt rows."""
+    _require_cuda(x, weight)
+    if x.dtype != torch.float32 or weight.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("add_rmsnorm_rows takes a contiguous fp32 residual x [M, C] and fp32 weight [C]")
+    M, C = x.shape
+    lda = 0
+    if addend is not None:
+        if addend.dtype != torch.bfloat16 or addend.shape != (M, C) or addend.stride(1) != 1:
+            raise ValueError("addend must be bf16 [M, C] with unit column stride")
+        lda = addend.stride(0)
+    if out is None:
+        out = torch.empty(M, C, dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().tt_add_rmsnorm_rows_bf16(_ptr(x), _ptr(addend), lda, _ptr(weight), float(eps), _ptr(out),
+                                                      M, C, _stream(x.device)), "add_rmsnorm_rows")
+    return out
+
+
+def silu_mul_rows(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(bf16(silu(g)) * u) from the bf16 gate and up projection outputs
+    [M, I] (unit column stride; mlp.py:44-45 under autocast)."""
+    _require_cuda(gate, up)
+    for name, t in (("gate", gate), ("up", up)):
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"{name} must be bf16 [M, I] with unit column stride")
+    if up.shape != gate.shape:
+        raise ValueError("gate and up must have one shape")
+    M, inter = gate.shape
+    if out is None:
+        out = torch.empty(M, inter, dtype=torch.bfloat16, device=gate.device)
+    _lib.check(_lib.load().tt_silu_mul_rows_bf16(_ptr(gate), gate.stride(0), _ptr(up), up.stride(0), M, inter,
+                                                   _ptr(out), _stream(gate.device)), "silu_mul_rows")
+    return out
+
+
 def silu_mul(partials: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """bf16(bf16(silu(g)) * u) from partials [S, M, 2I] of a stacked gate|up projection (mlp.py:44-45)."""
     _require_cuda(partials)
