@@ -145,6 +145,27 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
                        int64_t page_size, tt_stream_t stream);
 
 /*
+ * As tt_rope_append_bf16 (fp8_cache = 0) / tt_rope_append_fp8 (fp8_cache =
+ * 1; k_scale, v_scale as there, NULL for bf16), for a prompt batch packed
+ * without padding (the reference's prefill, attn.py:378-423, over ragged
+ * prompts): q_in [num_rows, H_q, D], k_in / v_in [num_rows, H_kv, D] with
+ * strides {row, head}; token t < new_lens[b] of sequence b is row
+ * row_offsets[b] + t (int32 device arrays, both required). q_out keeps the
+ * [B, H_q, num_new, D] grid of tt_rope_append_bf16 (strides {b, h, t}); rows
+ * t >= new_lens[b] are not written. Input rows are clamped to [0, num_rows).
+ * (Packing is this library's; the reference pads every prompt to T.)
+ */
+int tt_rope_append_rows_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                             const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                             const int32_t *row_offsets, int64_t num_rows, void *q_out, const int64_t q_out_strides[3],
+                             const void *rope_table, int64_t rope_table_len, const int32_t *positions,
+                             const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table, int64_t max_pages,
+                             int64_t num_pages, void *k_cache, void *v_cache, float *k_scale, float *v_scale,
+                             const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
+                             int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             int fp8_cache, tt_stream_t stream);
+
+/*
  * As tt_rope_append_bf16 / tt_rope_append_fp8, with q, k and v read from the
  * fp32 split-K partials of their projection (tt_linear_splitk*_bf16): each
  * input element is bf16(sum over s < splits of in[s * split_stride + i]),

@@ -165,6 +165,60 @@ def test_rope_append_from_split_k_partials(kind, paged, D):
     _case(kind, paged, D, 1, seed=300 + D + paged, from_partials=True)
 
 
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_append_packed_rows_equal_grid(kind, paged, D):
+    """Packed prompt rows (no padding: token t of sequence b is row
+    row_offsets[b] + t) give the same cache bytes, fp8 scales, lengths and
+    rotated q rows t < new_lens[b] as the [B, H, T, D] grid path pinned to the
+    oracle above; a sequence with no new tokens and sequences with tokens
+    already cached included."""
+    from tinytron_amd import ops
+    from tinytron_amd.cache import PagedKVCache
+    from tinytron_amd.model import ModelConfig
+
+    B, T, Hq, Hkv = 5, 21, 8, 2
+    new = [21, 3, 0, 1, 17]
+    pre = [0, 5, 9, 0, 30]
+    cfg = ModelConfig(num_layer=1, hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hkv, block_size=64)
+    kvd = torch.float8_e4m3fn if kind == "fp8" else None
+    g = torch.Generator().manual_seed(D + 2 * paged)
+    layers = []
+    for _ in range(2):
+        cache = PagedKVCache.from_model_config(cfg, B, 16, DEV, torch.bfloat16, kv_cache_dtype=kvd, paged_pool=paged,
+                                               seq_capacity=[64] * B)
+        layer = cache.get_layer_cache(0)
+        layer.set_lengths(pre)
+        layers.append(layer)
+    lay_a, lay_b = layers[0].layout, layers[1].layout
+    for x, y in ((lay_a.k, lay_b.k), (lay_a.v, lay_b.v)):  # same bytes in the never-written slots
+        r = torch.randint(0, 256, (x.numel() * x.element_size(),), generator=g, dtype=torch.uint8).to(DEV)
+        x.view(torch.uint8).copy_(r)
+        y.view(torch.uint8).copy_(r)
+    if kind == "fp8":
+        for x, y in ((lay_a.k_scale, lay_b.k_scale), (lay_a.v_scale, lay_b.v_scale)):
+            x.fill_(-1.0)
+            y.fill_(-1.0)
+    qg = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    kg = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16).to(DEV)
+    vg = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16).to(DEV)
+    table = ops.build_rope_table(64 + T, D, device=DEV)
+    q_grid = layers[0].rope_append(qg.transpose(1, 2), kg.transpose(1, 2), vg.transpose(1, 2), table, new_lens=new)
+    qp, kp, vp = (torch.cat([t[b, :n] for b, n in enumerate(new)]) for t in (qg, kg, vg))
+    offs = torch.tensor(np.cumsum([0] + new[:-1]), dtype=torch.int32, device=DEV)
+    q_rows = layers[1].rope_append_rows(qp, kp, vp, table, new, offs, T)
+    torch.cuda.synchronize()
+    assert layers[0].seq_lens_host == layers[1].seq_lens_host == [p + n for p, n in zip(pre, new)]
+    assert torch.equal(layers[0].seq_lens, layers[1].seq_lens)
+    for x, y in ((lay_a.k, lay_b.k), (lay_a.v, lay_b.v)):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), "cache bytes differ"
+    if kind == "fp8":
+        assert torch.equal(lay_a.k_scale, lay_b.k_scale) and torch.equal(lay_a.v_scale, lay_b.v_scale)
+    for b, n in enumerate(new):
+        assert torch.equal(q_grid[b, :, :n].view(torch.int16), q_rows[b, :, :n].view(torch.int16)), f"q of sequence {b}"
+
+
 def test_rope_table_matches_closed_form():
     """The table is an input of the bit-exact RoPE; its values follow the
     reference's fp32 op sequence, so they sit within fp32 angle rounding

@@ -96,6 +96,16 @@ SIGNATURES = {
     "tt_rope_append_bf16": (_ROPE_COMMON + _ROPE_TAIL, ctypes.c_int),
     "tt_rope_append_f32": (_ROPE_COMMON + _ROPE_TAIL, ctypes.c_int),
     "tt_rope_append_fp8": (_ROPE_COMMON + [_vp, _vp] + _ROPE_TAIL, ctypes.c_int),
+    "tt_rope_append_rows_bf16": ([
+        _vp, _i64p, _vp, _i64p, _vp, _i64p,         # q_in, k_in, v_in (+ {row, head} strides)
+        _i32p, _i64,                                 # row_offsets, num_rows
+        _vp, _i64p,                                  # q_out, q_out_strides
+        _vp, _i64, _i32p, _i32p, _i32p,              # rope_table, table_len, positions, new_lens, lens_out
+        _i32p, _i64, _i64,                           # page_table, max_pages, num_pages
+        _vp, _vp, _vp, _vp,                          # k_cache, v_cache, k_scale, v_scale
+        _i64p, _i64,                                 # cache_strides, capacity
+        _i64, _i64, _i64, _i64, _i64, _i64,          # batch, num_new, H_q, H_kv, head_dim, page_size
+        ctypes.c_int, _vp], ctypes.c_int),           # fp8_cache, stream
     "tt_rope_append_partials_bf16": (_ROPE_PART_HEAD + _ROPE_TAIL, ctypes.c_int),
     "tt_rope_append_partials_fp8": (_ROPE_PART_HEAD + [_vp, _vp] + _ROPE_TAIL, ctypes.c_int),
     "tt_gqa_decode_attn_bf16": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),

@@ -130,6 +130,21 @@ class _LayerCacheBase:
         self._host_lens = [a + b for a, b in zip(self._host_lens, adds)]
         return q_rot
 
+    def rope_append_rows(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rope_table: torch.Tensor,
+                         new_lens, row_offsets: torch.Tensor, num_new: int) -> torch.Tensor:
+        """rope_append of a packed prompt batch (q [N, H_q, D], k / v [N, H_kv, D];
+        sequence b's new_lens[b] tokens are rows row_offsets[b] ...); returns the
+        rotated q on the [B, H_q, num_new, D] grid."""
+        adds = [int(n) for n in new_lens]
+        self._check_room(adds)
+        nl = torch.tensor(adds, dtype=torch.int32).to(self.seq_lens.device, non_blocking=True)
+        nxt = 1 - self._cur
+        q_rot = ops.rope_append_rows(q, k, v, rope_table, self._lens_dev[self._cur], self.layout, row_offsets, nl,
+                                     num_new, lens_out=self._lens_dev[nxt])
+        self._cur = nxt
+        self._host_lens = [a + b for a, b in zip(self._host_lens, adds)]
+        return q_rot
+
     def rope_append_partials(self, partials: torch.Tensor, num_q_heads: int, rope_table: torch.Tensor) -> torch.Tensor:
         """One-token rope_append whose q|k|v are the split-K partials [S, B, N]
         of the stacked q|k|v projection (summed and rounded inside the kernel)."""

@@ -64,7 +64,8 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
                        int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
                        float *v_scale, const int64_t cache_strides[3], int64_t capacity, int64_t batch,
                        int64_t num_new, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                       int64_t page_size, tt_stream_t stream, int64_t part_splits = 0, int64_t part_stride = 0) {
+                       int64_t page_size, tt_stream_t stream, int64_t part_splits = 0, int64_t part_stride = 0,
+                       const int32_t *in_rows = nullptr, int64_t num_rows = 0) {
   TT_CHECK(q_in && k_in && v_in && q_out && rope_table && positions && k_cache && v_cache, TT_ERR_INVALID_ARGUMENT,
            "a required pointer is NULL");
   TT_CHECK(part_splits >= 0 && part_splits <= 4096 && (part_splits == 0 || part_stride > 0), TT_ERR_INVALID_ARGUMENT,
@@ -131,6 +132,8 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
   a.page_size = (int)page_size;
   a.part_splits = (int)part_splits;
   a.part_stride = part_stride;
+  a.in_rows = in_rows;
+  a.num_rows = num_rows;
   (void)hipGetLastError();
   return from_hip(tt::launch_rope_append(a, kind, (hipStream_t)stream), "rope_append launch");
 }
@@ -510,6 +513,28 @@ int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3], const vo
                             q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table, max_pages,
                             num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch, num_new,
                             num_q_heads, num_kv_heads, head_dim, page_size, stream);
+}
+
+int tt_rope_append_rows_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                             const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                             const int32_t *row_offsets, int64_t num_rows, void *q_out, const int64_t q_out_strides[3],
+                             const void *rope_table, int64_t rope_table_len, const int32_t *positions,
+                             const int32_t *new_lens, int32_t *lens_out, const int32_t *page_table, int64_t max_pages,
+                             int64_t num_pages, void *k_cache, void *v_cache, float *k_scale, float *v_scale,
+                             const int64_t cache_strides[3], int64_t capacity, int64_t batch, int64_t num_new,
+                             int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             int fp8_cache, tt_stream_t stream) {
+  TT_CHECK(row_offsets && new_lens, TT_ERR_INVALID_ARGUMENT, "packed rows need row_offsets and new_lens");
+  TT_CHECK(num_rows >= 1 && num_rows <= INT32_MAX, TT_ERR_INVALID_ARGUMENT, "num_rows must be in [1, 2^31)");
+  TT_CHECK(q_in_strides && k_in_strides && v_in_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
+  const int64_t qs[3] = {0, q_in_strides[1], q_in_strides[0]};
+  const int64_t ks[3] = {0, k_in_strides[1], k_in_strides[0]};
+  const int64_t vs[3] = {0, v_in_strides[1], v_in_strides[0]};
+  return rope_append_common(fp8_cache ? tt::CacheKind::kFP8 : tt::CacheKind::kBF16, q_in, qs, k_in, ks, v_in, vs,
+                            q_out, q_out_strides, rope_table, rope_table_len, positions, new_lens, lens_out, page_table,
+                            max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides, capacity, batch,
+                            num_new, num_q_heads, num_kv_heads, head_dim, page_size, stream, 0, 0, row_offsets,
+                            num_rows);
 }
 
 int tt_rope_append_partials_bf16(const float *q_in, const int64_t q_in_strides[3], const float *k_in,

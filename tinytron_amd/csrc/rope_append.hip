@@ -195,11 +195,13 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   finish_token<A, kFP8>(a, b, row, t, slot_offset(a, b, hk, pos), false, i, half, active, x1, x2, v1, v2, c, s);
 }
 
-// Prompt chunks (num_new > 1, activations as inputs): one wave per (row,
-// group of kChunkTok tokens, sequence). Every token's inputs, table entries
-// and (KV rows) page entry are loaded before the first is used, so a wave
-// costs about one memory round trip for its kChunkTok tokens instead of two
-// per token; the per-token arithmetic is finish_token's.
+// Prompt chunks (num_new > 1, or packed prompt rows; activations as inputs):
+// one wave per (row, group of kChunkTok tokens, sequence). Every token's
+// inputs, table entries and (KV rows) page entry are loaded before the first
+// is used, so a wave costs about one memory round trip for its kChunkTok
+// tokens instead of two per token; the per-token arithmetic is
+// finish_token's. Groups past a sequence's new tokens exit at once (KV rows
+// always, q rows for packed inputs).
 constexpr int kChunkTok = 8;
 
 template <typename A, bool kFP8>
@@ -213,23 +215,32 @@ __global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a)
   const int li = i & (half - 1);  // in bounds for any half; lanes past half drop their values
   const bool is_q = row < a.hq;
   const int hk = row - a.hq;
+  const bool packed = a.in_rows != nullptr;
   const int pos0 = a.positions[b];
   const int nlen = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
+  const int64_t r0 = packed ? a.in_rows[b] : 0;
+  if (a.lens_out != nullptr && row == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.lens_out[b] = pos0 + nlen;
+  // KV rows write only the new tokens; packed inputs have no padding rows at all
+  if (tb >= nlen && (packed || !is_q)) return;  // uniform
+  const int tmax = packed ? nlen - 1 : a.num_new - 1;
   const void *p1 = is_q ? a.q_in : a.k_in;
-  const int64_t o1 = is_q ? (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh : (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh;
+  const int64_t o1 = is_q ? (packed ? 0 : (int64_t)b * a.qi_sb) + (int64_t)row * a.qi_sh
+                          : (packed ? 0 : (int64_t)b * a.ki_sb) + (int64_t)hk * a.ki_sh;
   const int64_t st1 = is_q ? a.qi_st : a.ki_st;
-  const int64_t o2 = (int64_t)b * a.vi_sb + (int64_t)hk * a.vi_sh;
+  const int64_t o2 = (packed ? 0 : (int64_t)b * a.vi_sb) + (int64_t)hk * a.vi_sh;
   float x1[kChunkTok], x2[kChunkTok], v1[kChunkTok], v2[kChunkTok], c[kChunkTok], sn[kChunkTok];
   int64_t phys[kChunkTok];
 #pragma unroll
   for (int u = 0; u < kChunkTok; ++u) {
-    const int t = min(tb + u, a.num_new - 1);
+    const int t = min(tb + u, tmax);
+    // input row of token t: packed rows are clamped to the buffer
+    const int64_t tr = packed ? max(min(r0 + t, a.num_rows - 1), (int64_t)0) : (int64_t)t;
     const int64_t pos = (int64_t)pos0 + t;
     const int64_t tp = pos < 0 ? 0 : (pos >= a.table_len ? a.table_len - 1 : pos);
-    x1[u] = Elem<A>::load(p1, o1 + t * st1 + li);
-    x2[u] = Elem<A>::load(p1, o1 + t * st1 + half + li);
-    v1[u] = is_q ? 0.f : Elem<A>::load(a.v_in, o2 + t * a.vi_st + li);
-    v2[u] = is_q ? 0.f : Elem<A>::load(a.v_in, o2 + t * a.vi_st + half + li);
+    x1[u] = Elem<A>::load(p1, o1 + tr * st1 + li);
+    x2[u] = Elem<A>::load(p1, o1 + tr * st1 + half + li);
+    v1[u] = is_q ? 0.f : Elem<A>::load(a.v_in, o2 + tr * a.vi_st + li);
+    v2[u] = is_q ? 0.f : Elem<A>::load(a.v_in, o2 + tr * a.vi_st + half + li);
     c[u] = Elem<A>::load(a.table, tp * a.head_dim + li);
     sn[u] = Elem<A>::load(a.table, tp * a.head_dim + half + li);
     int64_t j = pos < 0 ? 0 : pos / a.page_size;
@@ -237,13 +248,13 @@ __global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a)
     phys[u] = (a.page_table != nullptr && !is_q) ? a.page_table[(int64_t)b * a.max_pages + j] : 0;
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (a.lens_out != nullptr && row == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.lens_out[b] = pos0 + nlen;
 #pragma unroll
   for (int u = 0; u < kChunkTok; ++u) {
     const int t = tb + u;
     const int64_t pos = (int64_t)pos0 + t;
     if (t >= a.num_new || pos < 0 || pos >= a.table_len) continue;  // uniform
     if (is_q) {
+      if (packed && t >= nlen) continue;  // no such input row
       finish_token<A, kFP8>(a, b, row, t, 0, true, i, half, active, x1[u], x2[u], 0.f, 0.f, c[u], sn[u]);
       continue;
     }
@@ -264,7 +275,7 @@ __global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a)
 }  // namespace
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
-  if (a.num_new > 1 && a.part_splits <= 0) {
+  if ((a.num_new > 1 || a.in_rows != nullptr) && a.part_splits <= 0) {
     const dim3 cgrid(a.hq + a.hkv, (a.num_new + kChunkTok - 1) / kChunkTok, a.batch);
     switch (kind) {
       case CacheKind::kBF16:

@@ -36,6 +36,12 @@ struct RopeAppendArgs {
   // elements) when part_splits > 0: each input is bf16(sum of the splits, in order)
   int part_splits;
   int64_t part_stride;
+  // packed prompt rows (in_rows != nullptr): token t of sequence b is input row
+  // in_rows[b] + t (< num_rows) with row stride *_st and head stride *_sh (the
+  // batch strides are unused); rows t >= new_lens[b] do not exist, so their q
+  // rows are not written either
+  const int32_t *in_rows;
+  int64_t num_rows;
 };
 
 struct DecodeArgs {

@@ -373,10 +373,11 @@ class GPT(nn.Module):
         """Prefill of a ragged batch (gpt.py:84-115 over T prompt tokens, of
         which sequence b brings new_lens[b]) on the packed tokens only: the
         projections and the norm / SwiGLU kernels see sum(new_lens) rows instead
-        of B * T; the RoPE + append and the prefill attention kernels read the
-        q / k / v rows scattered back to the [B, T] grid (padding rows are never
-        read). Same math and bf16 rounding points as the module path; returns
-        the logits at logits_index[b] of each sequence, [B, 1, V]."""
+        of B * T; the RoPE + append kernel reads the packed q / k / v rows and
+        writes the rotated q on the [B, T] grid the prefill attention kernel
+        reads (padding rows are never written or read). Same math and bf16
+        rounding points as the module path; returns the logits at
+        logits_index[b] of each sequence, [B, 1, V]."""
         c = self.config
         B, T = idx.shape
         C, Hq, Hkv = c.hidden_size, c.num_attention_heads, c.num_key_value_heads
@@ -396,18 +397,15 @@ class GPT(nn.Module):
         eps = self.lnf.variance_epsilon
         x = self.wte(idx.reshape(-1).index_select(0, sel)).float().contiguous()  # fp32 residual stream [N, C]
         h = ops.add_rmsnorm_rows(x, self.blocks[0].ln_1.weight, eps)             # bf16 [N, C]
-        qp = torch.empty(B * T, Hq * D, dtype=torch.bfloat16, device=dev)
-        kp = torch.empty(B * T, Hkv * D, dtype=torch.bfloat16, device=dev)
-        vp = torch.empty(B * T, Hkv * D, dtype=torch.bfloat16, device=dev)
+        offs = torch.tensor(cu[:-1], dtype=torch.int32, device=dev)
+        N = cu[-1]
         y_grid = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
         for i, blk in enumerate(self.blocks):
             layer = cache.get_layer_cache(i)
             att = blk.attn
-            qp.index_copy_(0, sel, F.linear(h, att.q_proj.weight))
-            kp.index_copy_(0, sel, F.linear(h, att.k_proj.weight))
-            vp.index_copy_(0, sel, F.linear(h, att.v_proj.weight))
-            q_rot = layer.rope_append(qp.view(B, T, Hq, D).transpose(1, 2), kp.view(B, T, Hkv, D).transpose(1, 2),
-                                      vp.view(B, T, Hkv, D).transpose(1, 2), table, new_lens=new)
+            q_rot = layer.rope_append_rows(F.linear(h, att.q_proj.weight).view(N, Hq, D),
+                                           F.linear(h, att.k_proj.weight).view(N, Hkv, D),
+                                           F.linear(h, att.v_proj.weight).view(N, Hkv, D), table, new, offs, T)
             layer.prefill_attend(q_rot, new, out=y_grid)
             y = y_grid.view(B * T, C).index_select(0, sel)
             h = ops.add_rmsnorm_rows(x, blk.ln_2.weight, eps, addend=F.linear(y, att.c_proj.weight))

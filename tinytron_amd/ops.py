@@ -151,6 +151,51 @@ def rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.
     return q_out
 
 
+def rope_append_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.Tensor,
+                     positions: torch.Tensor, layout: KVLayout, row_offsets: torch.Tensor, new_lens: torch.Tensor,
+                     num_new: int, q_out: torch.Tensor | None = None,
+                     lens_out: torch.Tensor | None = None) -> torch.Tensor:
+    """rope_append for a prompt batch packed without padding: q [N, H_q, D],
+    k / v [N, H_kv, D] (strides {row, head}, head_dim contiguous); token t of
+    sequence b is row row_offsets[b] + t for t < new_lens[b] (int32 [B]).
+    Returns the rotated q on the [B, H_q, num_new, D] grid (rows past
+    new_lens[b] not written); k / v go to each sequence's next slots."""
+    _require_cuda(q, k, v, table, positions, layout.k, layout.v, row_offsets, new_lens)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_lastdim(name, t, 3)
+    N, Hq, D = q.shape
+    B = positions.shape[0]
+    if k.shape != (N, layout.num_heads, D) or v.shape != k.shape:
+        raise ValueError(f"k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)} / cache heads")
+    if D != layout.head_dim:
+        raise ValueError(f"head_dim {D} does not match the cache's {layout.head_dim}")
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype or table.dtype != q.dtype:
+        raise ValueError("packed rows take bf16 q, k, v and rope table")
+    if layout.kind not in ("bf16", "fp8"):
+        raise ValueError("packed rows append to a bf16 or fp8 cache")
+    if table.dim() != 2 or table.shape[1] != D or not table.is_contiguous():
+        raise ValueError("rope table must be a contiguous [positions, head_dim] tensor")
+    for name, t in (("positions", positions), ("row_offsets", row_offsets), ("new_lens", new_lens)):
+        if t.dtype != torch.int32 or t.shape != (B,):
+            raise ValueError(f"{name} must be int32 [B]")
+    if lens_out is not None and (lens_out.dtype != torch.int32 or lens_out.shape != (B,)):
+        raise ValueError("lens_out must be int32 [B]")
+    if q_out is None:
+        q_out = torch.empty(B, Hq, num_new, D, dtype=q.dtype, device=q.device)
+    _check_lastdim("q_out", q_out, 4)
+    fp8 = layout.kind == "fp8"
+    st = _lib.load().tt_rope_append_rows_bf16(
+        _ptr(q), _lib.strides(*q.stride()[:2]), _ptr(k), _lib.strides(*k.stride()[:2]), _ptr(v),
+        _lib.strides(*v.stride()[:2]), _ptr(row_offsets), N, _ptr(q_out), _lib.strides(*q_out.stride()[:3]),
+        _ptr(table), table.shape[0], _ptr(positions), _ptr(new_lens), _ptr(lens_out),
+        _ptr(layout.page_table), layout.max_pages, layout.num_pages, _ptr(layout.k), _ptr(layout.v),
+        _ptr(layout.k_scale) if fp8 else None, _ptr(layout.v_scale) if fp8 else None,
+        _lib.strides(*layout.strides), layout.capacity, B, num_new, Hq, layout.num_heads, D, layout.page_size,
+        1 if fp8 else 0, _stream(q.device))
+    _lib.check(st, "rope_append_rows")
+    return q_out
+
+
 def rope_append_partials(partials: torch.Tensor, num_q_heads: int, table: torch.Tensor, positions: torch.Tensor,
                          layout: KVLayout, q_out: torch.Tensor | None = None,
                          lens_out: torch.Tensor | None = None) -> torch.Tensor:
