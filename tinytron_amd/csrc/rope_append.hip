@@ -272,11 +272,183 @@ __global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a)
   }
 }
 
+// Prompt chunks with bf16 activations and a power-of-two head_dim in
+// [16, 128]: a lane holds four consecutive rotation pairs (i .. i+3 and
+// i+D/2 .. i+D/2+3), D/8 lanes per token, so every input, table and output
+// access is 8 bytes wide (the kernel above moves one 2-byte element per
+// lane). Same tokens per wave, same per-element arithmetic (rotate_pair), same
+// early exits; fp8 scales reduce over the token's D/8 lanes.
+__device__ __forceinline__ void unpack4(uint2 w, float (&f)[4]) {
+  f[0] = __builtin_bit_cast(float, w.x << 16);
+  f[1] = __builtin_bit_cast(float, w.x & 0xffff0000u);
+  f[2] = __builtin_bit_cast(float, w.y << 16);
+  f[3] = __builtin_bit_cast(float, w.y & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
+  return make_uint2(f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16),
+                    f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16));
+}
+
+template <bool kFP8>
+__global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
+  constexpr int kPasses = 2;  // head_dim 128: 16 lanes per token, 4 tokens per pass
+  const int row = blockIdx.x;
+  const int tb = blockIdx.y * kChunkTok;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int D = a.head_dim;
+  const int half = D >> 1;
+  const int lpt = D >> 3;         // lanes per token (power of two, 2 .. 16)
+  const int tpp = 64 / lpt;       // tokens per pass
+  const int sub = lane / lpt;     // this lane's token within a pass
+  const int e0 = 4 * (lane & (lpt - 1));
+  const bool is_q = row < a.hq;
+  const int hk = row - a.hq;
+  const bool packed = a.in_rows != nullptr;
+  const int pos0 = a.positions[b];
+  const int nlen = a.new_lens != nullptr ? min(max(a.new_lens[b], 0), a.num_new) : a.num_new;
+  const int64_t r0 = packed ? a.in_rows[b] : 0;
+  if (a.lens_out != nullptr && row == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.lens_out[b] = pos0 + nlen;
+  if (tb >= nlen && (packed || !is_q)) return;  // uniform
+  const int tmax = packed ? nlen - 1 : a.num_new - 1;
+  const uint16_t *p1 = static_cast<const uint16_t *>(is_q ? a.q_in : a.k_in);
+  const uint16_t *pv = static_cast<const uint16_t *>(a.v_in);
+  const uint16_t *tab = static_cast<const uint16_t *>(a.table);
+  const int64_t o1 = is_q ? (packed ? 0 : (int64_t)b * a.qi_sb) + (int64_t)row * a.qi_sh
+                          : (packed ? 0 : (int64_t)b * a.ki_sb) + (int64_t)hk * a.ki_sh;
+  const int64_t st1 = is_q ? a.qi_st : a.ki_st;
+  const int64_t o2 = (packed ? 0 : (int64_t)b * a.vi_sb) + (int64_t)hk * a.vi_sh;
+  uint2 x1[kPasses], x2[kPasses], v1[kPasses], v2[kPasses], cw[kPasses], sw[kPasses];
+  int64_t phys[kPasses];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int t = min(tb + p * tpp + sub, tmax);
+    const int64_t tr = packed ? max(min(r0 + t, a.num_rows - 1), (int64_t)0) : (int64_t)t;
+    const int64_t pos = (int64_t)pos0 + t;
+    const int64_t tp = pos < 0 ? 0 : (pos >= a.table_len ? a.table_len - 1 : pos);
+    x1[p] = *reinterpret_cast<const uint2 *>(p1 + o1 + tr * st1 + e0);
+    x2[p] = *reinterpret_cast<const uint2 *>(p1 + o1 + tr * st1 + half + e0);
+    v1[p] = make_uint2(0u, 0u);
+    v2[p] = make_uint2(0u, 0u);
+    if (!is_q) {
+      v1[p] = *reinterpret_cast<const uint2 *>(pv + o2 + tr * a.vi_st + e0);
+      v2[p] = *reinterpret_cast<const uint2 *>(pv + o2 + tr * a.vi_st + half + e0);
+    }
+    cw[p] = *reinterpret_cast<const uint2 *>(tab + tp * D + e0);
+    sw[p] = *reinterpret_cast<const uint2 *>(tab + tp * D + half + e0);
+    int64_t j = pos < 0 ? 0 : pos / a.page_size;
+    j = j < a.max_pages ? j : a.max_pages - 1;
+    phys[p] = (a.page_table != nullptr && !is_q) ? a.page_table[(int64_t)b * a.max_pages + j] : 0;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    if (p * tpp >= kChunkTok) break;  // uniform: head_dim <= 64 needs one pass
+    const int t = tb + p * tpp + sub;
+    const int64_t pos = (int64_t)pos0 + t;
+    bool valid = p * tpp + sub < kChunkTok && t < a.num_new && pos >= 0 && pos < a.table_len;
+    valid = valid && (is_q ? (!packed || t < nlen) : t < nlen);
+    float xa[4], xb[4], c[4], sn[4], oa[4], ob[4];
+    unpack4(x1[p], xa);
+    unpack4(x2[p], xb);
+    unpack4(cw[p], c);
+    unpack4(sw[p], sn);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rotate_pair<BF16Tag>(xa[e], xb[e], c[e], sn[e], oa[e], ob[e]);
+    if (is_q) {
+      if (valid) {
+        uint16_t *q = static_cast<uint16_t *>(a.q_out) + (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh +
+                      (int64_t)t * a.qo_st;
+        *reinterpret_cast<uint2 *>(q + e0) = pack4(oa);
+        *reinterpret_cast<uint2 *>(q + half + e0) = pack4(ob);
+      }
+      continue;
+    }
+    int64_t off = -1;  // slot offset, from the page entry loaded above
+    if (valid && pos < a.capacity) {
+      const int64_t j = pos / a.page_size;
+      const int64_t slot = pos - j * a.page_size;
+      if (a.page_table == nullptr)
+        off = (int64_t)b * a.c_seq + j * a.c_page + (int64_t)hk * a.c_head + slot * D;
+      else if (j < a.max_pages && phys[p] >= 0 && phys[p] < a.num_pages)
+        off = phys[p] * a.c_page + (int64_t)hk * a.c_head + slot * D;
+    }
+    if constexpr (!kFP8) {
+      if (off >= 0) {
+        uint16_t *kc = static_cast<uint16_t *>(a.k_cache);
+        uint16_t *vc = static_cast<uint16_t *>(a.v_cache);
+        *reinterpret_cast<uint2 *>(kc + off + e0) = pack4(oa);
+        *reinterpret_cast<uint2 *>(kc + off + half + e0) = pack4(ob);
+        *reinterpret_cast<uint2 *>(vc + off + e0) = v1[p];
+        *reinterpret_cast<uint2 *>(vc + off + half + e0) = v2[p];
+      }
+    } else {
+      // per-(token, head) symmetric scale over the token's lpt lanes
+      float va[4], vb[4];
+      unpack4(v1[p], va);
+      unpack4(v2[p], vb);
+      float km = 0.f, vm = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        km = fmaxf(km, fmaxf(fabsf(oa[e]), fabsf(ob[e])));
+        vm = fmaxf(vm, fmaxf(fabsf(va[e]), fabsf(vb[e])));
+      }
+      for (int m = lpt >> 1; m > 0; m >>= 1) {
+        km = fmaxf(km, __shfl_xor(km, m, 64));
+        vm = fmaxf(vm, __shfl_xor(vm, m, 64));
+      }
+      const float ks = km / 448.0f;
+      const float vs = vm / 448.0f;
+      if (off >= 0) {
+        uint32_t ka = 0, kb = 0, wa = 0, wb = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ka |= (uint32_t)(ks == 0.f ? (uint8_t)0 : f32_to_e4m3fn(oa[e] / ks)) << (8 * e);
+          kb |= (uint32_t)(ks == 0.f ? (uint8_t)0 : f32_to_e4m3fn(ob[e] / ks)) << (8 * e);
+          wa |= (uint32_t)(vs == 0.f ? (uint8_t)0 : f32_to_e4m3fn(va[e] / vs)) << (8 * e);
+          wb |= (uint32_t)(vs == 0.f ? (uint8_t)0 : f32_to_e4m3fn(vb[e] / vs)) << (8 * e);
+        }
+        uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
+        uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
+        *reinterpret_cast<uint32_t *>(kc + off + e0) = ka;
+        *reinterpret_cast<uint32_t *>(kc + off + half + e0) = kb;
+        *reinterpret_cast<uint32_t *>(vc + off + e0) = wa;
+        *reinterpret_cast<uint32_t *>(vc + off + half + e0) = wb;
+        if (e0 == 0) {
+          a.k_scale[off / D] = ks;
+          a.v_scale[off / D] = vs;
+        }
+      }
+    }
+  }
+}
+
+// The vector kernel's access widths: 8-byte bf16 groups (4-byte fp8 codes).
+bool vec_ok(const RopeAppendArgs &a) {
+  const int D = a.head_dim;
+  auto al = [](const void *p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
+  const bool pow2 = D >= 16 && D <= 128 && (D & (D - 1)) == 0;
+  const int64_t st[] = {a.qi_sb, a.qi_sh, a.qi_st, a.ki_sb, a.ki_sh, a.ki_st, a.vi_sb, a.vi_sh, a.vi_st,
+                        a.qo_sb, a.qo_sh, a.qo_st, a.c_seq, a.c_page, a.c_head};
+  bool strides4 = true;
+  for (int64_t x : st) strides4 = strides4 && x % 4 == 0;
+  return pow2 && strides4 && al(a.q_in, 8) && al(a.k_in, 8) && al(a.v_in, 8) && al(a.q_out, 8) && al(a.table, 8) &&
+         al(a.k_cache, 8) && al(a.v_cache, 8);
+}
+
 }  // namespace
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
   if ((a.num_new > 1 || a.in_rows != nullptr) && a.part_splits <= 0) {
     const dim3 cgrid(a.hq + a.hkv, (a.num_new + kChunkTok - 1) / kChunkTok, a.batch);
+    if (kind != CacheKind::kF32 && vec_ok(a)) {
+      if (kind == CacheKind::kFP8)
+        hipLaunchKernelGGL((rope_append_vec_kernel<true>), cgrid, dim3(64), 0, stream, a);
+      else
+        hipLaunchKernelGGL((rope_append_vec_kernel<false>), cgrid, dim3(64), 0, stream, a);
+      return hipGetLastError();
+    }
     switch (kind) {
       case CacheKind::kBF16:
         hipLaunchKernelGGL((rope_append_chunk_kernel<BF16Tag, false>), cgrid, dim3(64), 0, stream, a);
