@@ -247,7 +247,8 @@ class GPT(nn.Module):
         self._lm_head_weight = None
         self.fused_decode = True   # bf16 decode steps through the fused layer kernels when shapes allow
         self.fused_prefill = True  # bf16 ragged prefill over the packed prompt tokens when shapes allow
-        self._stacked = {}         # layer -> (source key, q|k|v weight, gate|up weight)
+        self._stacked = {}         # layer -> (source key, packed q|k|v, c_proj, gate|up, down weights)
+        self._stacked_rows = {}    # layer -> (source key, plain q|k|v weight, plain gate|up weight)
         self._decode_bufs = {}     # (device, rows) -> split-K partial buffer
 
     def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
@@ -298,6 +299,21 @@ class GPT(nn.Module):
                 ent = (key, ops.PackedWeight(torch.cat(srcs[:3])), ops.PackedWeight(srcs[3]),
                        ops.PackedWeight(torch.cat(srcs[4:6])), ops.PackedWeight(srcs[6]))
             self._stacked[i] = ent
+        return ent[1:]
+
+    def _stacked_plain(self, i: int):
+        """Layer i's q|k|v and gate|up weights stacked row-wise (plain bf16) for
+        the prefill GEMMs: one wide product instead of three / two (rebuilt when
+        a source parameter changes)."""
+        blk = self.blocks[i]
+        srcs = (blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight,
+                blk.mlp.gate_proj.weight, blk.mlp.up_proj.weight)
+        key = tuple((t.data_ptr(), t._version) for t in srcs)
+        ent = self._stacked_rows.get(i)
+        if ent is None or ent[0] != key:
+            with torch.no_grad():
+                ent = (key, torch.cat(srcs[:3]).contiguous(), torch.cat(srcs[3:]).contiguous())
+            self._stacked_rows[i] = ent
         return ent[1:]
 
     def _partials(self, device, B: int) -> torch.Tensor:
@@ -400,16 +416,20 @@ class GPT(nn.Module):
         offs = torch.tensor(cu[:-1], dtype=torch.int32, device=dev)
         N = cu[-1]
         y_grid = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
+        I = c.intermediate_size
         for i, blk in enumerate(self.blocks):
             layer = cache.get_layer_cache(i)
             att = blk.attn
-            q_rot = layer.rope_append_rows(F.linear(h, att.q_proj.weight).view(N, Hq, D),
-                                           F.linear(h, att.k_proj.weight).view(N, Hkv, D),
-                                           F.linear(h, att.v_proj.weight).view(N, Hkv, D), table, new, offs, T)
+            wqkv, wgu = self._stacked_plain(i)
+            qkv = F.linear(h, wqkv)                                              # [N, (H_q + 2 H_kv) D]
+            q_rot = layer.rope_append_rows(qkv[:, :Hq * D].view(N, Hq, D),
+                                           qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D),
+                                           qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D), table, new, offs, T)
             layer.prefill_attend(q_rot, new, out=y_grid)
             y = y_grid.view(B * T, C).index_select(0, sel)
             h = ops.add_rmsnorm_rows(x, blk.ln_2.weight, eps, addend=F.linear(y, att.c_proj.weight))
-            m = ops.silu_mul_rows(F.linear(h, blk.mlp.gate_proj.weight), F.linear(h, blk.mlp.up_proj.weight))
+            gu = F.linear(h, wgu)                                                # [N, 2I]
+            m = ops.silu_mul_rows(gu[:, :I], gu[:, I:])
             nxt = self.blocks[i + 1].ln_1.weight if i + 1 < len(self.blocks) else self.lnf.weight
             h = ops.add_rmsnorm_rows(x, nxt, eps, addend=F.linear(m, blk.mlp.down_proj.weight))
         return F.linear(h.index_select(0, rows), self.lm_head_weight()).unsqueeze(1)
