@@ -117,6 +117,34 @@ def test_rope_append_rejects_invalid_arguments():
     assert lib.tt_rope_append_bf16(*common_paged, *tail, 128, 16, None) == _lib.TT_ERR_INVALID_ARGUMENT
 
 
+@pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
+def test_prefill_row_entries_reject_invalid_arguments():
+    lib = _lib.load()
+
+    def err():
+        return lib.tt_last_error_string().decode()
+
+    # residual add + RMSNorm over prompt rows
+    assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 2048, FAKE, 1e-6, FAKE, 10, 1000, None) == _lib.TT_ERR_UNSUPPORTED
+    assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 1024, FAKE, 1e-6, FAKE, 10, 2048, None) == \
+        _lib.TT_ERR_INVALID_ARGUMENT and "row stride" in err()
+    assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 2048, FAKE, 1e-6, FAKE + 2, 10, 2048, None) == \
+        _lib.TT_ERR_INVALID_ARGUMENT and "aligned" in err()
+    assert lib.tt_add_rmsnorm_rows_bf16(None, FAKE, 2048, FAKE, 1e-6, FAKE, 10, 2048, None) == \
+        _lib.TT_ERR_INVALID_ARGUMENT
+    # SwiGLU over prompt rows
+    assert lib.tt_silu_mul_rows_bf16(FAKE, 6144, FAKE, 6144, 10, 6142, FAKE, None) == _lib.TT_ERR_UNSUPPORTED
+    assert lib.tt_silu_mul_rows_bf16(FAKE, 100, FAKE, 6144, 10, 6144, FAKE, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert lib.tt_silu_mul_rows_bf16(FAKE, 6144, None, 6144, 10, 6144, FAKE, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    # RoPE + append from packed rows: offsets and new_lens are required, rows >= 1
+    s2, s3 = _lib.strides(3072, 64), _lib.strides(4096, 64, 1)
+    head = [FAKE, s2, FAKE, s2, FAKE, s2]
+    mid = [FAKE, s3, FAKE, 100, FAKE, FAKE, None, None, 0, 0, FAKE, FAKE, None, None,
+           _lib.strides(0, 2048, 256), 64, 2, 8, 32, 8, 64, 16, 0, None]
+    assert lib.tt_rope_append_rows_bf16(*head, None, 10, *mid) == _lib.TT_ERR_INVALID_ARGUMENT and "row_offsets" in err()
+    assert lib.tt_rope_append_rows_bf16(*head, FAKE, 0, *mid) == _lib.TT_ERR_INVALID_ARGUMENT and "num_rows" in err()
+
+
 def test_status_maps_to_python_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.TT_ERR_INVALID_ARGUMENT, "x")
