@@ -306,7 +306,7 @@ __device__ __forceinline__ void make_identity(int lane, bf16x8 (&ident16)[2], u3
   }
 }
 
-constexpr int kChunkTiles = 8;  // tiles per page-table fetch and software-pipelined run
+constexpr int kChunkTiles = 16;  // tiles per page-table fetch and software-pipelined run (<= 64 pages of 16 tokens)
 
 // Element offset and valid rows of 16-token block `blk` of (b, hk). Paged:
 // `entry` holds, one per lane, the page-table entries of pages pbase.. (the
