@@ -43,8 +43,16 @@ typedef unsigned long long u64;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Radix histograms are replicated kRep times, replica = lane mod kRep: the
+// top digit of the keys of a logit row falls in a handful of bins, and a
+// wave's 64 same-address LDS atomics would serialise; with the replicas at
+// adjacent addresses a wave instruction makes at most 64 / kRep same-address
+// updates. The replicas are summed into hist before a digit is picked.
+constexpr int kRep = 16;
+
 struct SampleShared {
   u64 hist[256];
+  u64 hrep[256 * kRep];  // [bin][replica]
   u64 red[kWaves][8];
   float fv[kWaves];
   int iv[kWaves];
@@ -185,9 +193,10 @@ __device__ __forceinline__ uint32_t radix_select(SampleShared &sh, Row<EPT, kF32
   uint32_t prefix = 0, mask = 0;
   above = 0;
   at = 0;
+  const uint32_t rep = threadIdx.x & (kRep - 1);
 #pragma unroll 1
   for (int shift = 24; shift >= 0; shift -= 8) {
-    if (threadIdx.x < 256) sh.hist[threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < 256 * kRep; i += kThreads) sh.hrep[i] = 0;
     __syncthreads();
     r.pass();
 #pragma unroll
@@ -199,9 +208,16 @@ __device__ __forceinline__ uint32_t radix_select(SampleShared &sh, Row<EPT, kF32
         const uint32_t key = order_key(v);
         if ((key & mask) == prefix) {
           const u64 w = wfn(idx, v);
-          if (w) atomicAdd(&sh.hist[(key >> shift) & 255u], w);
+          if (w) atomicAdd(&sh.hrep[((key >> shift) & 255u) * kRep + rep], w);
         }
       }
+    __syncthreads();
+    if (threadIdx.x < 256) {  // replica sums; the rotated start spreads the reads over the banks
+      u64 t = 0;
+#pragma unroll
+      for (int j = 0; j < kRep; ++j) t += sh.hrep[threadIdx.x * kRep + ((j + threadIdx.x) & (kRep - 1))];
+      sh.hist[threadIdx.x] = t;
+    }
     __syncthreads();
     if (threadIdx.x < 64) pick_digit(sh, need);
     __syncthreads();
