@@ -103,6 +103,15 @@ def e2e_c5(args, torch):
         if not torch.equal(tokens, graph_tokens):
             raise RuntimeError("graph-replayed decode diverged from the eager decode")
         graph_tps = round(graph_stats["decode_tokens_per_sec"], 1)
+    # the same decode with an fp8-e4m3 KV cache (per-(token, head) scales; the
+    # decode step is RoPE + append from the q|k|v partials, then the attention
+    # pair, replayed from HIP graphs by the engine's default)
+    fp8_eng = InferenceEngine(cfg, device="cuda", dtype=torch.bfloat16, kv_cache_page_size=C5["page"], paged_pool=True,
+                              kv_cache_dtype=torch.float8_e4m3fn, model=model)
+    fp8_tokens, fp8_stats = fp8_eng.generate(prompt, steps, top_k=1, prompt_lens=lens, return_stats=True)
+    gen = torch.stack([tokens[b, lens[b]:lens[b] + steps] for b in range(B)])
+    gen8 = torch.stack([fp8_tokens[b, lens[b]:lens[b] + steps] for b in range(B)])
+    del fp8_eng
     n_params = sum(p.numel() for p in model.parameters())
     mean_ctx = sum(lens) / B + steps / 2
     kv_bytes = C5["num_layer"] * 2 * B * mean_ctx * C5["num_key_value_heads"] * (C5["hidden_size"] // C5["num_attention_heads"]) * 2
@@ -117,6 +126,9 @@ def e2e_c5(args, torch):
                        "pair) launched eagerly + one-launch sampler; decode_tokens_per_sec_graphs replays the step "
                        "from HIP graphs (the two captures inside the timed window; same tokens, checked)",
         "decode_steps": int(stats["decode_tokens"] // B),
+        "decode_tokens_per_sec_fp8_kv": round(fp8_stats["decode_tokens_per_sec"], 1),
+        "fp8_kv_first_token_agreement": round(float((gen8[:, 0] == gen[:, 0]).float().mean()), 4),
+        "prefill_tokens_per_sec_fp8_kv": round(fp8_stats["prefill_tokens_per_sec"], 1),
         "prefill_tokens_per_sec": round(stats["prefill_tokens_per_sec"], 1),
         "params": n_params,
         "hbm_bound_tokens_per_sec": round(bound, 1),

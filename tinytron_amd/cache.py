@@ -64,6 +64,7 @@ class _LayerCacheBase:
         self._lens_dev = [torch.zeros(batch_size, dtype=torch.int32, device=device),
                           torch.zeros(batch_size, dtype=torch.int32, device=device)]
         self._cur = 0
+        self._caps = None  # per-sequence capacities, filled on first use
         self._host_lens = [0] * batch_size
         self._pending_new_lens = None
         self.workspace = None
@@ -75,22 +76,46 @@ class _LayerCacheBase:
         """Device int32 [B]: tokens cached per sequence."""
         return self._lens_dev[self._cur]
 
+    # Host lengths are base + shift: a one-token step adds 1 to every sequence
+    # by bumping the shift, so the per-layer bookkeeping of a decode step does
+    # not walk the batch.
+    @property
+    def _host_lens(self) -> list:
+        return [x + self._shift for x in self._base] if self._shift else list(self._base)
+
+    @_host_lens.setter
+    def _host_lens(self, lens) -> None:
+        self._base = [int(x) for x in lens]
+        self._shift = 0
+        self._base_max = max(self._base) if self._base else 0
+        self._room = None  # min over b of capacity - base, recomputed on demand
+
+    def _advance_all(self, n: int) -> None:
+        self._shift += n
+
     @property
     def seq_lens_host(self) -> list:
-        return list(self._host_lens)
+        return self._host_lens
 
     @property
     def current_length(self) -> int:
         """Longest sequence; equals the reference's batch-wide length when lengths are uniform."""
-        return max(self._host_lens) if self._host_lens else 0
+        return self._base_max + self._shift if self._base else 0
 
     def capacity_of(self, b: int) -> int:
         raise NotImplementedError
 
     def _check_room(self, adds) -> None:
+        if self._caps is None:
+            self._caps = [self.capacity_of(b) for b in range(self.batch_size)]
+        if self._room is None:
+            self._room = min((c - x for c, x in zip(self._caps, self._base)), default=0)
+        if adds and min(adds) == max(adds) and int(adds[0]) <= self._room - self._shift:
+            return  # the same add everywhere, and every sequence has room for it
+        lens = self._host_lens
         for b, add in enumerate(adds):
-            end = self._host_lens[b] + int(add)
-            cap = self.capacity_of(b)
+            end = lens[b] + int(add)
+            cap = self._caps[b]
             if end > cap:
                 raise ValueError(f"KV cache overflow: requested sequence length {end}, max supported is {cap}")
 
@@ -153,7 +178,7 @@ class _LayerCacheBase:
         q_rot = ops.rope_append_partials(partials, num_q_heads, rope_table, self._lens_dev[self._cur], self.layout,
                                          lens_out=self._lens_dev[nxt])
         self._cur = nxt
-        self._host_lens = [a + 1 for a in self._host_lens]
+        self._advance_all(1)
         return q_rot
 
     def decode_step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rope_table: torch.Tensor,
@@ -178,7 +203,7 @@ class _LayerCacheBase:
         out = ops.decode_attention_append(rope_table, self._lens_dev[self._cur], self.layout, bound,
                                           lens_out=self._lens_dev[nxt], out=out, workspace=self.workspace, **inputs)
         self._cur = nxt
-        self._host_lens = [a + 1 for a in self._host_lens]
+        self._advance_all(1)
         return out
 
     def prefill_attend(self, q_rot: torch.Tensor, new_lens, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -205,7 +230,7 @@ class _LayerCacheBase:
 
     def advance_host(self, n: int = 1) -> None:
         """Mirror a replayed one-token step: lengths + n, length buffers swapped n times."""
-        self._host_lens = [x + n for x in self._host_lens]
+        self._advance_all(n)
         self._cur = (self._cur + n) & 1
 
     # -- gathers for the protocol / prefill ----------------------------------------

@@ -14,11 +14,14 @@ loop (the reference syncs once per layer at attn.py:395).
 
 With ``use_graphs`` the one-token model call is captured in HIP graphs
 after the first decode step and replayed for the rest, which removes the
-per-kernel launch cost. By default (``None``) graphs are used when the model
-runs its module-by-module decode step (about 30 launches per layer); the
-fused bf16 step (9 launches per layer) keeps the GPU busy from the host
-alone, and there eager launches measured 2 % faster than replay plus the
-two captures (C5, 256 steps).
+per-kernel launch cost. By default (``None``) the fused step with a bf16
+cache (9 launches per layer, one launch pair for RoPE + append + attention)
+runs eagerly: the host keeps the GPU busy on its own, and eager launches
+measured 2 % faster than replay plus the two captures (C5, 256 steps).
+Everything else replays graphs: the module-by-module step (about 30
+launches per layer), and the fused step with an fp8 cache, whose separate
+RoPE + append launch makes the host the bottleneck (C5: 22.8 k tokens/s
+eager, 27.6 k replayed).
 The caches keep their lengths in two device buffers that swap every step, so
 two graphs are captured, one per buffer parity. The attention launch bound is
 fixed at the largest sequence capacity for the whole decode loop, so the
@@ -142,7 +145,8 @@ class InferenceEngine:
         graphs = None
         use_graphs = self.use_graphs
         if use_graphs is None:
-            use_graphs = not (hasattr(self.model, "_fused_decode_ok") and self.model._fused_decode_ok(cache, batch_size))
+            fused = hasattr(self.model, "_fused_decode_ok") and self.model._fused_decode_ok(cache, batch_size)
+            use_graphs = not (fused and cache.get_layer_cache(0).layout.kind == "bf16")
         cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
         for step in range(max_new_tokens):

@@ -66,7 +66,10 @@ class KVLayout:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current stream's handle on the tensor's device (torch's raw-stream
+    accessor: the Python stream object costs microseconds per launch)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def _require_cuda(*tensors: torch.Tensor) -> None:
