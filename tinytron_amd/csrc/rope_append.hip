@@ -133,7 +133,7 @@ __global__ __launch_bounds__(64) void rope_append_kernel(RopeAppendArgs a) {
   const int pos0 = a.positions[b];  // issued with the input loads below
   float x1 = 0.f, x2 = 0.f, v1 = 0.f, v2 = 0.f;
   if (t < a.num_new) {
-    const int li = i & (half - 1);
+    const int li = i % half;  // lane i < D/2 reads its own pair; lanes past D/2 a valid one they drop
     const void *p1 = is_q ? a.q_in : a.k_in;
     const int64_t o1 = is_q ? (int64_t)b * a.qi_sb + (int64_t)row * a.qi_sh + (int64_t)t * a.qi_st
                             : (int64_t)b * a.ki_sb + (int64_t)hk * a.ki_sh + (int64_t)t * a.ki_st;
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a)
   const int i = threadIdx.x;
   const int half = a.head_dim >> 1;
   const bool active = i < half;
-  const int li = i & (half - 1);  // in bounds for any half; lanes past half drop their values
+  const int li = i % half;  // lane i < D/2 reads its own pair; lanes past D/2 a valid one they drop
   const bool is_q = row < a.hq;
   const int hk = row - a.hq;
   const bool packed = a.in_rows != nullptr;
