@@ -174,20 +174,26 @@ def test_rope_append_packed_rows_equal_grid(kind, paged, D):
     rotated q rows t < new_lens[b] as the [B, H, T, D] grid path pinned to the
     oracle above; a sequence with no new tokens and sequences with tokens
     already cached included."""
+    packed_vs_grid(kind, paged, D, Hq=8, Hkv=2, new=[21, 3, 0, 1, 17], pre=[0, 5, 9, 0, 30], seed=D + 2 * paged)
+
+
+def packed_vs_grid(kind, paged, D, Hq, Hkv, new, pre, seed, page=16):
+    """rope_append_rows on packed rows against rope_append on the [B, H, T, D]
+    grid of the same tokens: cache bytes, scales, lengths, rotated q rows."""
     from tinytron_amd import ops
     from tinytron_amd.cache import PagedKVCache
     from tinytron_amd.model import ModelConfig
 
-    B, T, Hq, Hkv = 5, 21, 8, 2
-    new = [21, 3, 0, 1, 17]
-    pre = [0, 5, 9, 0, 30]
-    cfg = ModelConfig(num_layer=1, hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hkv, block_size=64)
+    B, T = len(new), max(max(new), 1)
+    cap = ((max(p + n for p, n in zip(pre, new)) + 8 + page - 1) // page) * page
+    cfg = ModelConfig(num_layer=1, hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                      block_size=cap)
     kvd = torch.float8_e4m3fn if kind == "fp8" else None
-    g = torch.Generator().manual_seed(D + 2 * paged)
+    g = torch.Generator().manual_seed(seed)
     layers = []
     for _ in range(2):
-        cache = PagedKVCache.from_model_config(cfg, B, 16, DEV, torch.bfloat16, kv_cache_dtype=kvd, paged_pool=paged,
-                                               seq_capacity=[64] * B)
+        cache = PagedKVCache.from_model_config(cfg, B, page, DEV, torch.bfloat16, kv_cache_dtype=kvd, paged_pool=paged,
+                                               seq_capacity=[cap] * B)
         layer = cache.get_layer_cache(0)
         layer.set_lengths(pre)
         layers.append(layer)
@@ -203,7 +209,7 @@ def test_rope_append_packed_rows_equal_grid(kind, paged, D):
     qg = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
     kg = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16).to(DEV)
     vg = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16).to(DEV)
-    table = ops.build_rope_table(64 + T, D, device=DEV)
+    table = ops.build_rope_table(cap + T, D, device=DEV)
     q_grid = layers[0].rope_append(qg.transpose(1, 2), kg.transpose(1, 2), vg.transpose(1, 2), table, new_lens=new)
     qp, kp, vp = (torch.cat([t[b, :n] for b, n in enumerate(new)]) for t in (qg, kg, vg))
     offs = torch.tensor(np.cumsum([0] + new[:-1]), dtype=torch.int32, device=DEV)
