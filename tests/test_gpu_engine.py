@@ -227,8 +227,8 @@ def test_prefill_kernel_matches_sdpa_path(kv_dtype):
         assert torch.allclose(a[i, :n], b[i, :n], rtol=2e-2, atol=2e-2), f"sequence {i}"
 
 
-@pytest.mark.parametrize("kv_dtype", [None, "fp8"])
-def test_packed_prefill_matches_module_path(kv_dtype):
+@pytest.mark.parametrize("kv_dtype,D", [(None, 64), ("fp8", 64), (None, 128), ("fp8", 128)])
+def test_packed_prefill_matches_module_path(kv_dtype, D):
     """GPT.forward's packed bf16 prefill (projections, residual add + RMSNorm
     and SwiGLU over the real prompt tokens only) against the module path on
     the padded [B, T] grid: same lengths, the cached K of every prompt token
@@ -237,11 +237,12 @@ def test_packed_prefill_matches_module_path(kv_dtype):
     from tinytron_amd.cache import PagedKVCache
     from tinytron_amd.model import GPT
 
-    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=4,
+    heads = 16 if D == 64 else 8
+    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=heads, num_key_value_heads=heads // 4,
                      intermediate_size=2048, vocab_size=4096, block_size=256)
     model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
     kvd = torch.float8_e4m3fn if kv_dtype == "fp8" else None
-    g = torch.Generator().manual_seed(23)
+    g = torch.Generator().manual_seed(23 + D)
     B, T = 4, 50
     lens = [50, 7, 1, 33]
     prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=g).to(DEV)
