@@ -33,8 +33,72 @@ constexpr int kXcds = 8;
 // slower: NB column blocks per wave already make the unrolled body long).
 constexpr int kPrefillChunkTiles = 8;
 
+// QK^T and the online-softmax step of one 32-token tile for one column block
+// (16 (token, head) columns). Unlike the decode step this loop is bound by
+// VALU issue, so: bf16 scores become y = s * scale - m in one FMA; the causal
+// mask runs only on `edge` tiles (those reaching past the smallest limit of
+// the wave's columns: every other tile is whole for every column); the
+// maximum is the IEEE-754-2019 one (v_maximum3_f32, which needs no NaN
+// quieting of its inputs; no score is NaN). P enters PV as P_hi + P_lo
+// (two bf16 operands, ~16 mantissa bits: a single bf16 P misses the 2e-3
+// absolute bound on short, cancelling rows). The caller rescales O by
+// `alpha` (this column's exp2(m_old - m_new); 0 on the first tile, whose key
+// 0 is valid for every column).
+template <int D, bool kFP8>
+__device__ __forceinline__ void qk_softmax_pf(float scale_log2, const f32x4 (&kc)[2], bool edge, int t0, int lim,
+                                              int lane, const Tile<D, kFP8> &tile, const bf16x8 (&qf)[D / 32],
+                                              WaveState<D, kFP8> &st, float &alpha, bf16x8 &pa_hi, bf16x8 &pa_lo) {
+  using TR = KVTraits<kFP8>;
+  constexpr int NDB = D / 32;
+  const int g = lane >> 4;
+  // S^T[token][column]: lane (n + 16g), reg r = token t0 + 16*tt + 4g + r, column n.
+  f32x4 S[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    S[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NDB; ++s) {
+      const int u = s / TR::kStepsPerFrag;
+      S[tt] = mfma_bf16(TR::step(tile.k[tt][u], s % TR::kStepsPerFrag), qf[s], S[tt]);
+    }
+  }
+  // x: raw scores (bf16) or scores in log2 units (fp8: K scale x softmax scale)
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = kFP8 ? S[i >> 2][i & 3] * kc[i >> 2][i & 3] : S[i >> 2][i & 3];
+  if (edge) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = t0 + 16 * (i >> 2) + 4 * g + (i & 3) < lim ? x[i] : kNegInf;
+  }
+  const auto mx2 = [](float u, float v) { return __builtin_elementwise_maximum(u, v); };
+  float mx = mx2(mx2(mx2(x[0], x[1]), mx2(x[2], x[3])), mx2(mx2(x[4], x[5]), mx2(x[6], x[7])));
+  mx = mx2(mx, __shfl_xor(mx, 16, 64));
+  mx = mx2(mx, __shfl_xor(mx, 32, 64));
+  if constexpr (!kFP8) mx *= scale_log2;  // scale > 0: the maximum commutes with it (-inf stays -inf)
+  const float m_new = mx2(st.m, mx);  // finite from the first tile on
+  alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  st.m = m_new;
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    p[i] = __builtin_amdgcn_exp2f(kFP8 ? x[i] - m_new : __builtin_fmaf(x[i], scale_log2, -m_new));
+  st.l = __builtin_fmaf(st.l, alpha, ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+  if constexpr (kFP8) {
+    // fold the per-token V scale into P; on edge tiles masked tokens stay
+    // exactly 0 (select: a scale slot past the end may hold anything)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float pv = p[i] * tile.vs[i >> 2][i & 3];
+      p[i] = edge ? (p[i] == 0.f ? 0.f : pv) : pv;
+    }
+  }
+  const f32x8 pv = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]};
+  pa_hi = __builtin_convertvector(pv, bf16x8);
+  pa_lo = __builtin_convertvector(pv - __builtin_convertvector(pa_hi, f32x8), bf16x8);  // P - P_hi exact in fp32
+}
+
 // PV of one tile for NB column blocks: V is transposed once (identity MFMA)
-// and multiplied by each block's P = P_hi + P_lo (see pv_tile).
+// and multiplied by each block's P_hi + P_lo.
 template <int D, bool kFP8, int NB>
 __device__ __forceinline__ void pv_tile_nb(const u32x4 (&vt)[2][Tile<D, kFP8>::NU], const bf16x8 (&ident16)[2],
                                            const u32x2 (&ident8)[2], const bf16x8 (&pa_hi)[NB],
@@ -100,6 +164,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   // keys the group needs: 0 .. pos0 + t_end - 1, never past the host's bound (the page table's reach)
   const int L = __builtin_amdgcn_readfirstlane(min(pos0 + t_end, a.max_len));
   if (pos0 < 0 || L <= 0) return;
+  // smallest key limit of the wave's valid columns (its first token's): tiles
+  // below it are whole for every column and skip the mask
+  const int lim_min = __builtin_amdgcn_readfirstlane(min(pos0 + t_first + 1, L));
 
   const int G = a.group;
   const int n = lane & 15;
@@ -169,11 +236,19 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         load_k_block<D, kFP8>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
       }
       __builtin_amdgcn_sched_barrier(0);
+      const int t0 = kTileTokens * it;
+      const bool edge = t0 + kTileTokens > lim_min;  // uniform
+      f32x4 kc[2] = {};
+      if constexpr (kFP8) {
+        kc[0] = buf[k & 1].ks[0] * a.scale_log2;
+        kc[1] = buf[k & 1].ks[1] * a.scale_log2;
+      }
       bf16x8 pa_hi[NB], pa_lo[NB];
+      float alpha[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        qk_softmax<D, kFP8>(a.scale_log2, kTileTokens * it, lim[j], lane, buf[k & 1], qf[j], st[j], pa_hi[j],
-                            pa_lo[j]);
+        qk_softmax_pf<D, kFP8>(a.scale_log2, kc, edge, t0, lim[j], lane, buf[k & 1], qf[j], st[j], alpha[j], pa_hi[j],
+                               pa_lo[j]);
       __builtin_amdgcn_sched_barrier(0);
       if (k + 1 < kPrefillChunkTiles)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
@@ -192,6 +267,15 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
+      // O rows (columns 4g + r) take their column's alpha from lane 4g + r
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha[j], 4 * (lane >> 4) + r, 64);
+#pragma unroll
+          for (int c = 0; c < 2 * NDB; ++c) st[j].o[c][r] *= ar;
+        }
       pv_tile_nb<D, kFP8, NB>(vt, ident16, ident8, pa_hi, pa_lo, st);
     }
     __builtin_amdgcn_s_waitcnt(0);
