@@ -107,3 +107,17 @@ def test_prefill_single_token_equals_decode():
     """T = 1: the prefill kernel computes the decode step (same oracle)."""
     got, ref, new = run_prefill([10, 0, 333], [1, 1, 1], seed=2)
     check(got, ref, new)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("G", [1, 4])
+def test_prefill_mask_edges_at_tile_boundaries(G, fp8):
+    """The causal mask runs only on tiles reaching past the smallest key limit
+    of a wave's columns: limits landing exactly on, just before and just after
+    32-key tile boundaries, prompts ending there, and (G = 1) a wave spanning
+    64 tokens, so up to three edge tiles per wave."""
+    Hkv = 2
+    past = [0, 31, 32, 33, 63, 95, 0, 1, 30, 62]
+    new = [32, 1, 33, 64, 65, 97, 128, 31, 1, 2]  # 30 + 1, 62 + 2: a limit one key short of a tile end
+    got, ref, n = run_prefill(past, new, Hq=Hkv * G, Hkv=Hkv, D=64, fp8=fp8, seed=40 + G + fp8)
+    check(got, ref, n)
