@@ -147,8 +147,8 @@ def sampler_timing(torch, iters=50):
     """Microseconds per call of the one-launch sampler on C5's logits
     ([64, 32000] bf16) beside the reference's op sequence on the same device
     (filter_logits + softmax + multinomial, sampler.py:6-48)."""
+    from oracle.ref_path import filter_logits
     from tinytron_amd import ops
-    from tinytron_amd.sampler import filter_logits
 
     g = torch.Generator().manual_seed(0)
     logits = (torch.randn(C5["batch"], C5["vocab_size"], generator=g) * 3).to(torch.bfloat16).cuda()

@@ -229,7 +229,10 @@ int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3]
  * Requirements: head_dim in {64, 128}; H_q % H_kv == 0 and
  *   H_q / H_kv <= 16; a paged pool has a power-of-two page_size >= 16; the
  *   contiguous store has dense pages (cache_strides[1] == page_size *
- *   head_dim, as the reference's [B, H, pages, P, D] store), any page_size;
+ *   head_dim, as the reference's [B, H, pages, P, D] store), any page_size,
+ *   and holds max_seq_len tokens per (sequence, head): cache_strides[2] >=
+ *   max_seq_len * head_dim when num_kv_heads > 1 and cache_strides[0] >=
+ *   max_seq_len * head_dim when batch > 1;
  *   q and cache 16-byte aligned, their strides multiples of 8 elements;
  *   batch <= 4096 (bf16 / fp8).
  * Physical page numbers read from page_table are clamped into

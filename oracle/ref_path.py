@@ -122,3 +122,25 @@ def decode_attention_step(q, k, v, cache: LayerPagedKVCache, num_kv_heads: int, 
         mask = build_cache_causal_mask(q.size(2), K.size(2), past_len, q.device)
         causal = False
     return F.scaled_dot_product_attention(q, K, V, attn_mask=mask, dropout_p=0.0, is_causal=causal)
+
+
+def filter_logits(logits, temperature: float = 1.0, top_k=None, top_p=None):
+    """sampler.py:6-36 in torch (any device): fp32 cast, temperature, top-k
+    (values below the k-th largest -> -inf), top-p over the descending sort
+    (the first token always kept). bench.py times this op sequence plus
+    softmax + multinomial (sampler.py:39-48) on the GPU as the reference's
+    sampler; the numpy oracle.sampler.filter_logits is the checker."""
+    if temperature <= 0:
+        raise ValueError("temperature must be > 0")
+    x = logits.float()
+    if temperature != 1.0:
+        x = x / temperature
+    if top_k is not None and top_k > 0:
+        kth = torch.topk(x, k=min(top_k, x.size(-1)), dim=-1).values[:, -1:]
+        x = torch.where(x < kth, torch.full_like(x, float("-inf")), x)
+    if top_p is not None and 0 < top_p < 1.0:
+        vals, order = torch.sort(x, descending=True, dim=-1)
+        drop = torch.cumsum(torch.softmax(vals, dim=-1), dim=-1) > top_p
+        drop[..., 0] = False
+        x = torch.full_like(x, float("-inf")).scatter_(-1, order, vals.masked_fill(drop, float("-inf")))
+    return x

@@ -125,6 +125,7 @@ def test_ragged_batch_equals_batch_one(kv_dtype):
         a = batch[b, n:n + steps].cpu()
         s = single[0, n:n + steps].cpu()
         assert torch.equal(batch[b, :n].cpu(), prompt[b, :n])
+        assert not batch[b, n + steps:].any()  # pad 0 after the row's own end, no stale prompt padding
         if not torch.equal(a, s):
             mismatched += 1
     # bf16 GEMMs of different batch shapes round differently; allow a near-tie flip in one sequence

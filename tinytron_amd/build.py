@@ -10,11 +10,13 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libtinytron_amd.so"
+OBJ_DIR = PKG_DIR / "_build"  # per-source objects (git-ignored)
 SOURCES = ["abi.hip", "rope_append.hip", "decode_attn.hip", "prefill_attn.hip", "layer_ops.hip", "sampler.hip"]
 
 HIPCC_FLAGS = [
@@ -22,7 +24,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-fno-gpu-flush-denormals-to-zero",
     # no packed-fp32 VALU ops anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -38,19 +39,28 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(PKG_DIR.parent / "include"),
-           *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
-    if verbose and res.stderr.strip():
-        sys.stderr.write(res.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source into LIB_PATH (always recompiles): one object
+    per source, compiled concurrently, then one link."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    inc = ["-I", str(PKG_DIR.parent / "include")]
+    objs = [OBJ_DIR / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [[hipcc(), *HIPCC_FLAGS, *inc, "-c", str(CSRC / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    jobs = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 16)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        for f in [pool.submit(_run, c, verbose) for c in cmds]:
+            f.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *[str(o) for o in objs], "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

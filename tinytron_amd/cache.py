@@ -239,9 +239,12 @@ class _LayerCacheBase:
         raise NotImplementedError
 
     def gather(self, b: int, length: int, dtype: torch.dtype | None = None):
-        """Dense (K, V) [1, H, length, D] of sequence b (dequantized for fp8)."""
+        """Dense (K, V) [1, H, length, D] of sequence b (dequantized for fp8).
+        ``length`` may not exceed the sequence's capacity (ValueError)."""
         lay = self.layout
         D, H = lay.head_dim, lay.num_heads
+        if length < 0 or length > self.capacity_of(b):
+            raise ValueError(f"cannot gather {length} tokens of sequence {b}: it holds at most {self.capacity_of(b)}")
         base = self._token_index(b, length)                                   # [L]
         idx = base[None, :, None] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None, None] \
             + torch.arange(D, device=base.device)[None, None, :]              # [H, L, D]
@@ -285,9 +288,19 @@ class _LayerCacheBase:
         return previous
 
     def get_kv(self):
-        """cache.py:47-51: (K, V) [B, H, current_length, D] (dense copies for the pool and fp8)."""
+        """cache.py:47-51: (K, V) [B, H, current_length, D] (dense copies for the
+        pool and fp8). With ragged lengths (which the reference's one batch-wide
+        length cannot express) sequence b contributes its own lens[b] tokens and
+        zeros after them; no slot past a sequence's length is read."""
         L = self.current_length
-        ks, vs = zip(*(self.gather(b, L) for b in range(self.batch_size)))
+        ks, vs = [], []
+        for b, n in enumerate(self._host_lens):
+            k, v = self.gather(b, n)
+            if n < L:
+                pad = (0, 0, 0, L - n)
+                k, v = torch.nn.functional.pad(k, pad), torch.nn.functional.pad(v, pad)
+            ks.append(k)
+            vs.append(v)
         return torch.cat(ks, 0), torch.cat(vs, 0)
 
 
@@ -354,7 +367,8 @@ class PagedLayerKVCache(_LayerCacheBase):
         table_cpu = page_table.to(torch.int32).cpu()
         if table_cpu.dim() != 2:
             raise ValueError("page_table must be [B, max_pages]")
-        self._pages_of = [int((row >= 0).sum()) for row in table_cpu]
+        # a sequence owns the leading run of valid entries of its row (its capacity)
+        self._pages_of = [int(torch.cumprod((row >= 0).to(torch.int64), 0).sum()) for row in table_cpu]
         if table_cpu.numel() and int(table_cpu.max()) >= num_pages:
             raise ValueError("page_table refers to pages beyond the pool")
         self.page_table = table_cpu.to(device)
@@ -378,6 +392,8 @@ class PagedLayerKVCache(_LayerCacheBase):
         return self._pages_of[b] * self.page_size
 
     def _token_index(self, b: int, length: int) -> torch.Tensor:
+        if length > self.capacity_of(b):  # beyond the sequence's pages the table holds -1
+            raise ValueError(f"sequence {b} owns {self._pages_of[b]} pages; {length} tokens do not fit")
         lay = self.layout
         t = torch.arange(length, device=lay.k.device)
         phys = self.page_table[b].long()[t // self.page_size]

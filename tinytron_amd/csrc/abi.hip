@@ -57,6 +57,24 @@ int check_layout(const int32_t *page_table, int64_t max_pages, int64_t num_pages
   return TT_OK;
 }
 
+// The contiguous store addresses token t of (b, h) at b * strides[0] +
+// h * strides[2] + t * head_dim: the kernels read tokens below max_seq_len,
+// so each (sequence, head) region must hold that many tokens. A stride whose
+// dimension has more than one entry must be at least max_seq_len * head_dim
+// (the reference's [B, H, pages, P, D] store has c_head = pages * P * D and
+// c_seq = H * c_head).
+int check_contiguous_room(int64_t max_seq_len, int64_t head_dim, const int64_t cache_strides[3], int64_t batch,
+                          int64_t num_kv_heads) {
+  const int64_t need = max_seq_len * head_dim;
+  TT_CHECK(num_kv_heads <= 1 || cache_strides[2] >= need, TT_ERR_INVALID_ARGUMENT,
+           "max_seq_len %lld does not fit the contiguous store: head stride %lld < %lld * head_dim",
+           (long long)max_seq_len, (long long)cache_strides[2], (long long)max_seq_len);
+  TT_CHECK(batch <= 1 || cache_strides[0] >= need, TT_ERR_INVALID_ARGUMENT,
+           "max_seq_len %lld does not fit the contiguous store: sequence stride %lld < %lld * head_dim",
+           (long long)max_seq_len, (long long)cache_strides[0], (long long)max_seq_len);
+  return TT_OK;
+}
+
 int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_strides[3], const void *k_in,
                        const int64_t k_in_strides[3], const void *v_in, const int64_t v_in_strides[3], void *q_out,
                        const int64_t q_out_strides[3], const void *rope_table, int64_t rope_table_len,
@@ -196,6 +214,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     TT_CHECK(cache_strides[1] == page_size * head_dim, TT_ERR_UNSUPPORTED,
              "the contiguous store needs dense pages (page stride %lld != page_size * head_dim)",
              (long long)cache_strides[1]);
+    rc = check_contiguous_room(max_seq_len, head_dim, cache_strides, batch, num_kv_heads);
+    if (rc != TT_OK) return rc;
   }
   if (kind != tt::CacheKind::kF32) {
     TT_CHECK(batch <= 4096, TT_ERR_UNSUPPORTED, "batch %lld > 4096 is not supported (per-sequence split table in LDS)",
@@ -383,6 +403,8 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
     TT_CHECK(cache_strides[1] == page_size * head_dim, TT_ERR_UNSUPPORTED,
              "the contiguous store needs dense pages (page stride %lld != page_size * head_dim)",
              (long long)cache_strides[1]);
+    rc = check_contiguous_room(max_seq_len, head_dim, cache_strides, batch, num_kv_heads);
+    if (rc != TT_OK) return rc;
   }
   TT_CHECK(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
            "q and cache pointers must be 16-byte aligned");

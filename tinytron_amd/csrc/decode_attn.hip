@@ -977,11 +977,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
 
 template <int D, bool kFP8>
 hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStream_t stream) {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
-  }
+  const int cus = device_cu_count();
   const int64_t items = (int64_t)a.batch * a.hkv * a.max_splits;  // upper bound of the dense item count
   const dim3 grid((unsigned)std::min<int64_t>(items, (int64_t)cus * 2));
   const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + lds_merge +
@@ -1006,15 +1002,7 @@ hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStr
 template <int D, bool kFP8>
 hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream_t stream) {
   DecodeArgs a = a0;
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
-  }
-  // stream_blocks_per_cu(D) resident workgroups of 4 waves per CU; no more waves than the longest-case tile count
-  const int64_t tiles_bound = (int64_t)a.batch * a.hkv * ((a.max_len + kTileTokens - 1) / kTileTokens);
-  int64_t blocks = std::min<int64_t>((int64_t)cus * stream_blocks_per_cu(D), kMaxStreamBlocks);
-  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (tiles_bound + kWavesPerBlock - 1) / kWavesPerBlock));
+  const int64_t blocks = balanced_stream_waves(D, a.batch, a.hkv, a.max_len) / kWavesPerBlock;
   a.stream_waves = (int)(blocks * kWavesPerBlock);
   const size_t lds_prefix = 16 * ((sizeof(int) * (kWavesPerBlock + (size_t)a.batch + 1) + 15) / 16);
   size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + lds_prefix;
@@ -1078,6 +1066,14 @@ hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
 }
 
 }  // namespace
+
+int64_t balanced_stream_waves(int head_dim, int64_t batch, int64_t hkv, int64_t max_len) {
+  // stream_blocks_per_cu(D) resident workgroups of 4 waves per CU; no more waves than the longest-case tile count
+  const int64_t tiles_bound = batch * hkv * ((max_len + kTileTokens - 1) / kTileTokens);
+  int64_t blocks = std::min<int64_t>((int64_t)device_cu_count() * stream_blocks_per_cu(head_dim), kMaxStreamBlocks);
+  blocks = std::max<int64_t>(1, std::min<int64_t>(blocks, (tiles_bound + kWavesPerBlock - 1) / kWavesPerBlock));
+  return blocks * kWavesPerBlock;
+}
 
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
   // Aim for >= 8 workgroups per CU (256 CUs) over the longest sequence while

@@ -328,11 +328,7 @@ hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t strea
   // a workgroup on at least 3/4 of the CUs; otherwise 4 waves (64 rows).
   // (Measured on the decode-step shapes: two 8-wave workgroups on some CUs
   // beat one 12-wave workgroup on every CU; 6- and 12-wave groups lost.)
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
-  }
+  const int cus = device_cu_count();
   const int splits = a.K / kc, mt = (a.M + 63) / 64;
   const bool wide = a.N % 128 == 0 && 4 * (int64_t)(a.N / 128) * splits * mt >= 3 * (int64_t)cus;
   const dim3 grid((unsigned)(a.N / (wide ? 128 : 64)), (unsigned)splits, (unsigned)mt);

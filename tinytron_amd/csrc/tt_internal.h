@@ -5,7 +5,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace tt {
+
+// Compute units of the current device, queried once per device (launch
+// sizing reads it on every launch; the attribute query is not free).
+inline int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < kMaxDevices) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < kMaxDevices) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 enum class CacheKind { kBF16, kF32, kFP8 };
 
@@ -157,6 +176,9 @@ hipError_t launch_sample(const SampleArgs &a, bool f32, hipStream_t stream);
 
 // Partition helpers shared by the ABI layer and the launchers.
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);
+// Waves of the balanced stream kernel's grid on the current device (at most
+// kMaxStreamWaves); the partial slots it writes are b * H_kv + hk + wave.
+int64_t balanced_stream_waves(int head_dim, int64_t batch, int64_t hkv, int64_t max_len);
 inline int64_t num_splits(int64_t max_len, int64_t split_tokens) {
   return max_len <= 0 ? 1 : (max_len + split_tokens - 1) / split_tokens;
 }

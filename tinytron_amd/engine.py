@@ -107,7 +107,8 @@ class InferenceEngine:
                  return_stats: bool = False, return_logprobs: bool = False, prompt_lens=None):
         """engine.py:144-261. ``prompt_lens`` (optional, [B]) marks ragged
         prompts inside a right-padded ``input_ids``; the returned tokens are
-        right-padded likewise and ``stats["lengths"]`` gives each length."""
+        right-padded with 0 after each row's own end (prompt_lens[b] + decode
+        steps) and ``stats["lengths"]`` gives each length."""
         if input_ids.dim() != 2:
             raise ValueError(f"input_ids must be [B, T], got shape={tuple(input_ids.shape)}")
         prompt = input_ids.to(self.device)
@@ -175,6 +176,9 @@ class InferenceEngine:
 
         out_len = max(lens) + decode_steps
         tokens = tokens[:, :out_len]
+        if not uniform:  # row b ends at lens[b] + decode_steps; what follows is pad 0, not stale prompt padding
+            ends = (lens_t + decode_steps).unsqueeze(1)
+            tokens.masked_fill_(torch.arange(out_len, device=self.device).unsqueeze(0) >= ends, 0)
         if not return_stats and not return_logprobs:
             return tokens
         extras = {}

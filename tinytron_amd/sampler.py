@@ -13,9 +13,6 @@ row): the reference's distribution, not torch.multinomial's random stream.
 Each call takes its seed from torch's default generator (so
 ``torch.manual_seed`` makes runs repeatable, as in the reference) unless
 ``manual_seed`` here fixes one.
-
-``filter_logits`` restates the reference's op sequence on the device for
-callers that want the filtered logits themselves.
 """
 from __future__ import annotations
 
@@ -48,28 +45,6 @@ def manual_seed(seed: int | None) -> None:
     """Fix the sampler's seed, call n using offset n (None: draw from torch's generator)."""
     _STATE.seed = None if seed is None else int(seed)
     _STATE.offset = 0
-
-
-def filter_logits(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
-                  top_p: float | None = None) -> torch.Tensor:
-    if temperature <= 0:
-        raise ValueError("temperature must be > 0")
-    logits = logits.float()
-    if temperature != 1.0:
-        logits = logits / temperature
-    if top_k is not None and top_k > 0:
-        k = min(top_k, logits.size(-1))
-        v, _ = torch.topk(logits, k=k, dim=-1)
-        min_keep = v[:, -1].unsqueeze(-1)
-        logits = torch.where(logits < min_keep, torch.full_like(logits, float("-inf")), logits)
-    if top_p is not None and 0 < top_p < 1.0:
-        sorted_logits, sorted_indices = torch.sort(logits, descending=True, dim=-1)
-        cum_probs = torch.cumsum(torch.softmax(sorted_logits, dim=-1), dim=-1)
-        sorted_mask = cum_probs > top_p
-        sorted_mask[..., 0] = False
-        keep = sorted_logits.masked_fill(sorted_mask, float("-inf"))
-        logits = torch.full_like(logits, float("-inf")).scatter_(-1, sorted_indices, keep)
-    return logits
 
 
 def _rows(logits: torch.Tensor) -> torch.Tensor:
