@@ -356,6 +356,34 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                               float sm_scale, void *workspace, size_t workspace_bytes, tt_stream_t stream);
 
+/*
+ * tt_decode_attn_append_bf16 without the workspace argument: the attention
+ * workspace is a device array inside the library, TT_NOALLOC_SCRATCH_BYTES
+ * per GPU, held by every GPU the entry point runs on until the process ends.
+ * No counterpart in the reference: this is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid hipMalloc). The call itself allocates nothing; the caller
+ * still passes every input and output. A call whose workspace (tile prefix
+ * plus (B * H_kv + waves of the launched grid) * G * (D + 2) fp32 partials)
+ * exceeds the scratch returns TT_ERR_WORKSPACE_TOO_SMALL before launching.
+ * Every call on one GPU shares that GPU's scratch, which keeps the last
+ * call's contents (nothing in it needs to start at zero): calls that overlap
+ * on one GPU (different streams, or threads) race and must be serialised by
+ * the caller. Results are those of tt_decode_attn_append_bf16, bit for bit.
+ */
+#define TT_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                                       const int64_t k_in_strides[2], const void *v_in,
+                                       const int64_t v_in_strides[2], int64_t splits, int64_t split_stride,
+                                       const void *rope_table, int64_t rope_table_len, const int32_t *positions,
+                                       int32_t *lens_out, int64_t max_seq_len, const int32_t *page_table,
+                                       int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache,
+                                       const int64_t cache_strides[3], int64_t capacity, void *out,
+                                       const int64_t out_strides[2], int64_t batch, int64_t num_q_heads,
+                                       int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale,
+                                       tt_stream_t stream);
+
 /* Fixed split size the fp32 entry point uses when split_tokens == 0. */
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 

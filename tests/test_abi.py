@@ -41,6 +41,11 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
 
 
+def test_noalloc_scratch_size_matches_header():
+    m = re.search(r"#define TT_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", HEADER.read_text())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+
+
 def test_abi_version():
     assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 1
 

@@ -81,6 +81,8 @@ _DECODE_APPEND_TAIL = [
     _i64, _i64, _i64, _i64, _i64,                    # batch, H_q, H_kv, head_dim, page_size
     _f32, _vp, _size, _vp,                           # sm_scale, workspace, workspace_bytes, stream
 ]
+_DECODE_APPEND_TAIL_NOALLOC = _DECODE_APPEND_TAIL[:-4] + [_f32, _vp]  # sm_scale, stream (scratch inside)
+NOALLOC_SCRATCH_BYTES = 32 << 20  # TT_NOALLOC_SCRATCH_BYTES
 
 _SAMPLE = [
     _vp, _i64, _i64, _i64,                           # logits, row stride, rows, vocab
@@ -124,6 +126,7 @@ SIGNATURES = {
     "tt_silu_mul_rows_bf16": ([_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_decode_attn_append_bf16": (_DECODE_APPEND_HEAD + _DECODE_APPEND_TAIL, ctypes.c_int),
     "tt_decode_attn_append_fp8": (_DECODE_APPEND_HEAD + [_vp, _vp] + _DECODE_APPEND_TAIL, ctypes.c_int),
+    "tt_decode_attn_append_bf16_noalloc": (_DECODE_APPEND_HEAD + _DECODE_APPEND_TAIL_NOALLOC, ctypes.c_int),
     "tt_sample_bf16": (_SAMPLE, ctypes.c_int),
     "tt_sample_f32": (_SAMPLE, ctypes.c_int),
 }

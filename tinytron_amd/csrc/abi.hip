@@ -5,12 +5,52 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/tinytron_amd.h"
 #include "tt_internal.h"
 
+// Device scratch of tt_decode_attn_append_bf16_noalloc (the attention
+// workspace: tile prefix, partial outputs, maxima and sums), one copy per
+// GPU, held until the process ends. Its name is a host-side stand-in:
+// kernels get its device address from scratch_address().
+static __device__ __align__(256) unsigned char scratch[TT_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr size_t kScratchBytes = TT_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_mutex;
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int from_hip(hipError_t err, const char *what);
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_address(void **addr) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return from_hip(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(TT_ERR_UNSUPPORTED, "device %d is beyond the %d devices the scratch table covers", dev,
+                kMaxScratchDevices);
+  void *p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+      err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || p == nullptr) return from_hip(err != hipSuccess ? err : hipErrorInvalidSymbol,
+                                                             "hipGetSymbolAddress(scratch)");
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return TT_OK;
+}
 
 thread_local std::string g_last_error;
 
@@ -168,13 +208,17 @@ size_t workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim,
 }
 
 // Balanced partition: the per-sequence tile prefix (padded to 16 bytes), then
-// one partial slot per (segment + wave) index.
-int64_t balanced_slots(int64_t batch, int64_t hkv) { return batch * hkv + tt::kMaxStreamWaves; }
+// one partial slot per (segment + wave) index. Caller-provided workspaces are
+// sized for the largest grid (kMaxStreamWaves waves, so that one size serves
+// every device); the allocation-free entry point sizes its slots for the grid
+// it launches.
+int64_t balanced_slots(int64_t batch, int64_t hkv, int64_t waves) { return batch * hkv + waves; }
 int64_t balanced_prefix_ints(int64_t batch) { return (batch + 1 + 3) & ~(int64_t)3; }
 
-size_t balanced_workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim) {
+size_t balanced_workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim,
+                                int64_t waves = tt::kMaxStreamWaves) {
   const int64_t g = hq / (hkv > 0 ? hkv : 1);
-  const int64_t rows = balanced_slots(batch, hkv) * g;
+  const int64_t rows = balanced_slots(batch, hkv, waves) * g;
   return (size_t)balanced_prefix_ints(batch) * sizeof(int32_t) + (size_t)(rows * head_dim + rows * 2) * sizeof(float);
 }
 
@@ -183,8 +227,10 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
                   const int32_t *seq_lens, int64_t max_seq_len, const int32_t *page_table, int64_t max_pages,
                   int64_t num_pages, void *out, const int64_t out_strides[2], int64_t batch, int64_t num_q_heads,
                   int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
-                  void *workspace, size_t ws_bytes, tt_stream_t stream, const tt::DecodeAppend *ap = nullptr) {
+                  void *workspace, size_t ws_bytes, tt_stream_t stream, const tt::DecodeAppend *ap = nullptr,
+                  bool exact_slots = false) {
   // ap != null: the fused step (q / k / v from ap, seq_lens = lengths before the step)
+  // exact_slots: the balanced workspace holds slots for the launched grid only (allocation-free entry point)
   TT_CHECK((ap || q) && k_cache && v_cache && seq_lens && out, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK((ap || q_strides) && out_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
   TT_CHECK(batch >= 0 && batch <= 65535, TT_ERR_INVALID_ARGUMENT, "batch must be in [0, 65535]");
@@ -234,10 +280,13 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   const bool balanced = split_tokens == 0 && kind != tt::CacheKind::kF32;
   int64_t split = 0, splits = 0;
   size_t need = 0;
+  // partial slots beyond the segments: one per wave of the largest grid, or of the launched one
+  const int64_t ws_waves =
+      exact_slots ? tt::balanced_stream_waves((int)head_dim, batch, num_kv_heads, max_seq_len) : tt::kMaxStreamWaves;
   if (balanced) {
     TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens) < ((int64_t)1 << 31),
              TT_ERR_UNSUPPORTED, "batch * max_seq_len is too large for the balanced partition");
-    need = balanced_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim);
+    need = balanced_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, ws_waves);
   } else {
     split = resolve_split(split_tokens, batch, num_kv_heads, max_seq_len);
     TT_CHECK(split == 128 || split == 256 || split == 512 || split == 1024, TT_ERR_INVALID_ARGUMENT,
@@ -247,7 +296,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
   }
   TT_CHECK(workspace != nullptr && ws_bytes >= need, TT_ERR_WORKSPACE_TOO_SMALL,
-           "workspace of %zu bytes is smaller than the %zu bytes needed", ws_bytes, need);
+           "%s of %zu bytes is smaller than the %zu bytes needed",
+           exact_slots ? "the allocation-free entry point's scratch" : "workspace", ws_bytes, need);
   TT_CHECK(aligned(workspace, 16), TT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   if (batch == 0) return ok();
 
@@ -271,7 +321,7 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.o_sb = out_strides[0];
   a.o_sh = out_strides[1];
   const int64_t g = num_q_heads / num_kv_heads;
-  const int64_t rows = g * (balanced ? balanced_slots(batch, num_kv_heads) : batch * num_kv_heads * splits);
+  const int64_t rows = g * (balanced ? balanced_slots(batch, num_kv_heads, ws_waves) : batch * num_kv_heads * splits);
   a.ws_prefix = balanced ? static_cast<int32_t *>(workspace) : nullptr;
   a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                      (balanced ? balanced_prefix_ints(batch) * sizeof(int32_t) : 0));
@@ -307,7 +357,7 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
                          float *v_scale, const int64_t cache_strides[3], int64_t capacity, void *out,
                          const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                          int64_t head_dim, int64_t page_size, float sm_scale, void *workspace, size_t ws_bytes,
-                         tt_stream_t stream) {
+                         tt_stream_t stream, bool exact_slots = false) {
   TT_CHECK(q_in && k_in && v_in && rope_table && positions, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK(q_in_strides && k_in_strides && v_in_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
   TT_CHECK(splits >= 0 && (splits == 0 || split_stride > 0), TT_ERR_INVALID_ARGUMENT, "bad split-K partial layout");
@@ -337,7 +387,7 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
   ap.page_size = page_size;
   return decode_common(kind, nullptr, nullptr, k_cache, v_cache, k_scale, v_scale, cache_strides, positions,
                        max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
-                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, ws_bytes, stream, &ap);
+                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, ws_bytes, stream, &ap, exact_slots);
 }
 
 int linear_common(const void *x, int64_t ldx, const void *weight, int64_t ldw, int packed, float *partials,
@@ -776,6 +826,25 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               page_table, max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
                               sm_scale, workspace, workspace_bytes, stream);
+}
+
+int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
+                                       const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
+                                       int64_t splits, int64_t split_stride, const void *rope_table,
+                                       int64_t rope_table_len, const int32_t *positions, int32_t *lens_out,
+                                       int64_t max_seq_len, const int32_t *page_table, int64_t max_pages,
+                                       int64_t num_pages, void *k_cache, void *v_cache, const int64_t cache_strides[3],
+                                       int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
+                                       int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                       float sm_scale, tt_stream_t stream) {
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != TT_OK) return rc;
+  return decode_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
+                              splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
+                              page_table, max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides,
+                              capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                              sm_scale, ws, kScratchBytes, stream, /*exact_slots=*/true);
 }
 
 int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,

@@ -320,7 +320,8 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
                             q: torch.Tensor | None = None, k: torch.Tensor | None = None, v: torch.Tensor | None = None,
                             partials: torch.Tensor | None = None, num_q_heads: int | None = None,
                             lens_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                            sm_scale: float | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+                            sm_scale: float | None = None, workspace: Workspace | None = None,
+                            no_alloc: bool = False) -> torch.Tensor:
     """One decode step in one launch pair: RoPE of this step's q and k at
     positions[b], append of k / v at that slot, and GQA attention over the
     positions[b] + 1 cached tokens (rope_append followed by decode_attention,
@@ -328,7 +329,10 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
     [B, H_kv, D] (strided views, head_dim contiguous), or ``partials`` fp32
     [S, B, (H_q + 2 H_kv) D] of the stacked q|k|v projection with
     ``num_q_heads``. ``max_seq_len`` bounds positions + 1. Returns out
-    [B, H_q, D] bf16."""
+    [B, H_q, D] bf16. ``no_alloc`` (bf16 caches) runs the allocation-free
+    entry point, whose workspace is the library's per-GPU scratch
+    (``workspace`` is then unused; pass ``out`` to allocate nothing at all;
+    calls that overlap on one GPU race on that scratch)."""
     _require_cuda(table, positions, layout.k, layout.v)
     if layout.kind not in ("bf16", "fp8"):
         raise ValueError("the fused decode step takes a bf16 or fp8 cache")
@@ -372,13 +376,20 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
     _check_lastdim("out", out, 3)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
-    need = workspace_bytes(B, Hq, Hkv, D, max_seq_len, 0)
-    ws = (workspace or Workspace(dev)).get(need)
     lib = _lib.load()
     head = ins + [_ptr(table), table.shape[0], _ptr(positions), _ptr(lens_out), int(max_seq_len),
                   _ptr(layout.page_table), layout.max_pages, layout.num_pages, _ptr(layout.k), _ptr(layout.v)]
     tail = [_lib.strides(*layout.strides), layout.capacity, _ptr(out), _lib.strides(*out.stride()[:2]),
-            B, Hq, Hkv, D, layout.page_size, float(sm_scale), _ptr(ws), ws.numel(), _stream(dev)]
+            B, Hq, Hkv, D, layout.page_size, float(sm_scale)]
+    if no_alloc:  # the library's own per-GPU scratch: nothing is allocated (HIP graph capture, serving loops)
+        if layout.kind != "bf16":
+            raise ValueError("the allocation-free decode step takes a bf16 cache")
+        st = lib.tt_decode_attn_append_bf16_noalloc(*head, *tail, _stream(dev))
+        _lib.check(st, "decode_attention_append (no allocation)")
+        return out
+    need = workspace_bytes(B, Hq, Hkv, D, max_seq_len, 0)
+    ws = (workspace or Workspace(dev)).get(need)
+    tail += [_ptr(ws), ws.numel(), _stream(dev)]
     if layout.kind == "fp8":
         st = lib.tt_decode_attn_append_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
     else:
