@@ -4,8 +4,22 @@
 Follows tinytron/model/gpt.py:33-115, modules/norm.py:14-19,
 modules/mlp.py:44-45, modules/attn.py:378-440 (local decode path with the
 H_q-expanded LayerPagedKVCache) and inference/engine.py:144-228 (greedy via
-top_k = 1), op for op, in fp32 on the CPU (the reference's CPU path runs
-without autocast, engine.py:180-184). Weights come from a state dict.
+top_k = 1), op for op. Weights come from a state dict.
+
+Two numeric modes:
+
+* fp32 (default): the reference's CPU path, which runs without autocast
+  (engine.py:180-184).
+* ``autocast_bf16=True``: the reference on the GPU under
+  torch.autocast(bfloat16) (engine.py:180-185), with autocast's rounding
+  points made explicit: every projection (F.linear) takes bf16-rounded
+  inputs and weights, accumulates in fp32 and returns bf16; RoPE, the cache
+  and SiLU * up run in bf16; SDPA (an autocast bf16 op) attends over the
+  bf16 q / K / V in fp32 and returns bf16; the embedding, the residual
+  stream and RMSNorm stay fp32 (x + bf16 promotes to fp32; norm.py:14-19
+  computes in fp32 and multiplies by the fp32 weight). Pinned in
+  tests/test_oracle_ref_model.py against the fp32 code run under torch's own
+  CPU autocast, so the rounding points come from torch's autocast policy.
 """
 from __future__ import annotations
 
@@ -16,16 +30,35 @@ import torch.nn.functional as F
 
 from . import ref_path
 
+BF16 = torch.bfloat16
+
 
 class RefGPT:
     def __init__(self, state_dict: dict, num_layer: int, num_attention_heads: int, num_key_value_heads: int,
-                 dtype=torch.float32):
+                 dtype=torch.float32, autocast_bf16: bool = False):
         self.w = {k: v.detach().to("cpu", dtype) for k, v in state_dict.items() if torch.is_tensor(v)}
         self.L = num_layer
         self.hq = num_attention_heads
         self.hkv = num_key_value_heads
         self.C = self.w["wte.weight"].shape[1]
         self.D = self.C // self.hq
+        self.bf16 = autocast_bf16
+        if autocast_bf16:  # bf16 copies of the projection weights (autocast's per-call weight cast)
+            self.wb = {k: v.to(BF16).float() for k, v in self.w.items() if k.endswith("_proj.weight")}
+            self.wb["wte.weight"] = self.w["wte.weight"].to(BF16).float()
+
+    def _lin(self, x, name):
+        """nn.Linear(bias=False): fp32, or autocast's bf16 in / fp32 accumulate / bf16 out."""
+        if not self.bf16:
+            return F.linear(x, self.w[name])
+        return F.linear(x.to(BF16).float(), self.wb[name]).to(BF16)
+
+    def _sdpa(self, q, k, v, mask, causal):
+        if not self.bf16:
+            return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0.0, is_causal=causal)
+        y = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=mask, dropout_p=0.0,
+                                           is_causal=causal)
+        return y.to(BF16)
 
     @staticmethod
     def _rms(x, w):
@@ -36,9 +69,9 @@ class RefGPT:
     def _attn(self, i, x, cache, position_offset):
         B, T, C = x.shape
         p = f"blocks.{i}.attn."
-        q = F.linear(x, self.w[p + "q_proj.weight"]).view(B, T, self.hq, self.D).transpose(-2, -3)
-        k = F.linear(x, self.w[p + "k_proj.weight"]).view(B, T, self.hkv, self.D).transpose(-2, -3)
-        v = F.linear(x, self.w[p + "v_proj.weight"]).view(B, T, self.hkv, self.D).transpose(-2, -3)
+        q = self._lin(x, p + "q_proj.weight").view(B, T, self.hq, self.D).transpose(-2, -3)
+        k = self._lin(x, p + "k_proj.weight").view(B, T, self.hkv, self.D).transpose(-2, -3)
+        v = self._lin(x, p + "v_proj.weight").view(B, T, self.hkv, self.D).transpose(-2, -3)
         pos = torch.arange(position_offset, position_offset + T).unsqueeze(0)
         q, k = ref_path.rope_impl(q, k, pos)
         k, v = ref_path.gqa_impl(k, v, self.hkv, self.hq)
@@ -48,9 +81,9 @@ class RefGPT:
         if past_len > 0:
             mask = ref_path.build_cache_causal_mask(T, k.size(2), past_len, x.device)
             causal = False
-        y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, dropout_p=0.0, is_causal=causal)
+        y = self._sdpa(q, k, v, mask, causal)
         y = y.transpose(-2, -3).reshape(B, T, C)
-        return F.linear(y, self.w[p + "c_proj.weight"])
+        return self._lin(y, p + "c_proj.weight")
 
     def forward(self, idx, caches, position_offset):
         x = F.embedding(idx, self.w["wte.weight"])
@@ -58,11 +91,18 @@ class RefGPT:
             p = f"blocks.{i}."
             x = x + self._attn(i, self._rms(x, self.w[p + "ln_1.weight"]), caches[i], position_offset)
             h = self._rms(x, self.w[p + "ln_2.weight"])
-            m = F.linear(F.silu(F.linear(h, self.w[p + "mlp.gate_proj.weight"])) * F.linear(h, self.w[p + "mlp.up_proj.weight"]),
-                         self.w[p + "mlp.down_proj.weight"])
+            m = self._lin(F.silu(self._lin(h, p + "mlp.gate_proj.weight")) * self._lin(h, p + "mlp.up_proj.weight"),
+                          p + "mlp.down_proj.weight")
             x = x + m
         x = self._rms(x, self.w["lnf.weight"])
-        return F.linear(x, self.w["wte.weight"])
+        if not self.bf16:
+            return F.linear(x, self.w["wte.weight"])
+        return F.linear(x.to(BF16).float(), self.wb["wte.weight"]).to(BF16)  # tied lm_head (gpt.py:61-63)
+
+    def new_caches(self, batch: int, block_size: int, page_size: int = 128):
+        dt = BF16 if self.bf16 else torch.float32
+        return [ref_path.LayerPagedKVCache(batch, self.hq, self.D, block_size, page_size, "cpu", dt)
+                for _ in range(self.L)]
 
     @torch.no_grad()
     def generate_greedy(self, prompt: torch.Tensor, max_new_tokens: int, block_size: int, page_size: int = 128,
@@ -70,8 +110,7 @@ class RefGPT:
         """engine.py:144-228 with temperature 1, top_k 1 (argmax). Returns
         (tokens [B, T + n], decode tokens/s, logits of every step)."""
         B, T = prompt.shape
-        caches = [ref_path.LayerPagedKVCache(B, self.hq, self.D, block_size, page_size, "cpu", torch.float32)
-                  for _ in range(self.L)]
+        caches = self.new_caches(B, block_size, page_size)
         logits = self.forward(prompt, caches, 0)
         tokens = [prompt]
         step_logits = [logits[:, -1].clone()]

@@ -27,6 +27,13 @@ def _c1_config(**kw):
     return ModelConfig(**base)
 
 
+def _ulps_of_row_max(a, c):
+    """Largest |a - c| over logit rows [..., V], in bf16 ulps of the row's largest |logit|."""
+    top = torch.maximum(a.abs(), c.abs()).amax(-1, keepdim=True)
+    ulp = torch.ldexp(torch.ones(()), torch.frexp(top)[1] - 8)
+    return float(((a - c).abs() / ulp).max())
+
+
 def _first_divergence(a, b):
     diff = (a != b).nonzero()
     return None if len(diff) == 0 else tuple(int(x) for x in diff[0])
@@ -190,9 +197,14 @@ def test_fused_decode_step_matches_module_path():
     assert n0 == n1 == [T + 1] * B
     assert torch.equal(k0[:, :, :T], k1[:, :, :T])           # prefill rows: same path
     assert torch.allclose(k0[:, :, T], k1[:, :, T], rtol=2e-2, atol=2e-2)  # decode row: bf16 GEMMs of two libraries
-    scale = float(l0.abs().max())
-    assert float((l0 - l1).abs().max()) <= 0.05 * scale
-    assert torch.equal(l0.argmax(-1), l1.argmax(-1)) or float((l0 - l1).abs().max()) < 1e-2
+    # two bf16 GEMM implementations (and norm summation orders): a flip of one bf16
+    # rounding per layer moves every logit by at most an ulp or two of the row maximum
+    ulps = _ulps_of_row_max(l0, l1)
+    print(f"fused vs module decode step: {ulps:.2f} bf16 ulps of the row maximum", flush=True)
+    assert ulps <= 2.0  # measured 1.0
+    for r in (l0.argmax(-1) != l1.argmax(-1)).nonzero().tolist():
+        row = l0[tuple(r)]
+        assert float(row.max() - row[l1.argmax(-1)[tuple(r)]]) <= 2 * float(row.abs().max()) * 2.0 ** -7
 
 
 @pytest.mark.parametrize("kv_dtype", [None, "fp8"])
@@ -269,10 +281,18 @@ def test_packed_prefill_matches_module_path(kv_dtype, D):
     tol = 0.1 if kv_dtype == "fp8" else 2e-2
     for b in range(B):
         assert torch.allclose(k0[b], k1[b], rtol=tol, atol=tol), f"sequence {b}: cached K differs"
-    for a, c in ((l0, l1), (s0, s1)):
-        scale = float(a.abs().max())
-        assert float((a - c).abs().max()) <= 0.05 * scale
-    assert torch.equal(n0, n1) or float((l0 - l1).abs().max()) < 1e-2
+    # bf16: GEMMs of two shapes, flips of single roundings (one or two ulps of the row
+    # maximum); fp8: a flip in a bf16 k / v element can move its e4m3 code by a step
+    # (1/16 of the value), so the bound is wider
+    bound = 4.0 if kv_dtype == "fp8" else 2.0  # measured: at most 1.0 (bf16), 1.19 (fp8)
+    for what, a, c in (("prefill logits", l0, l1), ("next step", s0, s1)):
+        ulps = _ulps_of_row_max(a, c)
+        print(f"packed vs module ({kv_dtype or 'bf16'}, D {D}) {what}: {ulps:.2f} bf16 ulps of the row maximum",
+              flush=True)
+        assert ulps <= bound, what
+    for r in (n0 != n1).nonzero().tolist():  # a different greedy token is a near-tie
+        row = l0[r[0], 0]
+        assert float(row.max() - row[n1[r[0], 0]]) <= bound * float(row.abs().max()) * 2.0 ** -7
 
 
 def test_sampled_generation_is_seeded_and_graph_invariant():
