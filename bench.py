@@ -8,19 +8,23 @@ L_b + 1 cached tokens. bf16 caches run it as one fused launch pair
 tt_rope_append_* followed by tt_gqa_decode_attn_*.
 Inputs are synthetic (seed 1337) and resident in HBM before the timed region.
 
-Default workload (config C3, the headline metric's batch-64 case):
-ragged paged bf16 decode attention, B = 64, 32 q heads / 8 KV heads, D = 128,
-L_b ~ U[128, 16384], page size 16, page table = seeded random permutation of
-the physical pages. --config c2 / c4 / c5a select the other configs (c5a:
-one layer's attention of the C5 model mid-decode); --e2e-only runs C5 end to end.
+Headline workload (config C3, the metric's batch-64 case): ragged paged bf16
+decode attention, B = 64, 32 q heads / 8 KV heads, D = 128, L_b ~ U[128,
+16384], page size 16, page table = seeded random permutation of the physical
+pages. The same line carries nested records for C2 (uniform contiguous, B
+32, ctx 4096), C4 (fp8-e4m3 cache, B 128, ctx U[1024, 32768]), c5a (one layer
+of the C5 model mid-decode, D 64), C1 (the reference's CPU-sized model,
+greedy decode) and e2e (C5 through the engine). --config selects the
+headline config; --e2e-only runs C5 end to end alone.
 
 value = algorithmic bytes per step / time per step (GB/s, 1 GB = 1e9 B), with
 algorithmic bytes = unique K/V bytes read (+ fp8 scales) + q/out/new-token/page
 table I/O. The roofline object covers the decode-attention operator (the
 balanced stream kernel and its merge kernel) timed alone with HIP events on the
-stream it runs on. The CPU baseline times the reference's own op sequence
-(torch on the host, H_q-expanded cache, per sequence) on a bounded sample of
-the same sequences.
+stream it runs on. CPU baselines time the reference's own op sequence (torch
+on the host: rope_impl, gqa_impl, the H_q-expanded LayerPagedKVCache, mask,
+SDPA; for C1 / C5 the whole model and generate loop) on bounded samples of
+the same workloads, with the host's CPU model and thread count recorded.
 """
 from __future__ import annotations
 
@@ -45,6 +49,9 @@ CONFIGS = {
     "c5a": dict(name="C5 per-layer ragged paged bf16 GQA decode step (D 64)", batch=64, hq=32, hkv=8, head_dim=64,
                 lo=192, hi=2176, page=16, paged=True, fp8=False),
 }
+# CPU-baseline sample per config: all sequences, or a seeded subset where the
+# reference layout (4x the unique K/V) of every sequence would not fit the budget
+CPU_SAMPLE = {"c2": None, "c3": None, "c4": 16, "c5a": None}
 
 
 def parse_args():
@@ -56,10 +63,14 @@ def parse_args():
                    help="decode step as one launch pair (RoPE + append inside the attention kernel) or as the "
                         "RoPE + append kernel then attention; auto: fused for bf16 caches, two launches for fp8")
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    p.add_argument("--nested", default="c2,c4,c5a",
+                   help="comma-separated configs measured after the headline one and reported in nested records "
+                        "('' for none)")
     p.add_argument("--seed", type=int, default=1337)
     p.add_argument("--split-tokens", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of timed CPU-baseline work")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of timed CPU-baseline work per config")
+    p.add_argument("--no-c1", action="store_true", help="skip config C1 (the reference's CPU-sized model)")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end greedy decode (config 5)")
     p.add_argument("--e2e-steps", type=int, default=256)
     p.add_argument("--e2e-only", action="store_true", help="run only the end-to-end decode and print its record")
@@ -68,8 +79,34 @@ def parse_args():
     return p.parse_args()
 
 
+C1 = dict(num_layer=6, hidden_size=512, num_attention_heads=8, num_key_value_heads=2, vocab_size=32000,
+          intermediate_size=2048, init_std=0.02, prompt=128, steps=64, page=128)
 C5 = dict(num_layer=24, hidden_size=2048, num_attention_heads=32, num_key_value_heads=8, vocab_size=32000,
           intermediate_size=6144, init_std=0.02, batch=64, lo=64, hi=2048, page=16)
+
+
+def host_threads(torch) -> int:
+    """Threads for the CPU baselines: the CPUs this process may run on, capped by
+    OMP_NUM_THREADS when set (the GPU box gives a 16-CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        n = min(n, int(env))
+    torch.set_num_threads(n)
+    return n
+
+
+def host_info(torch) -> dict:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "visible_cpus": len(os.sched_getaffinity(0)), "logical_cpus": os.cpu_count(),
+            "threads_used": host_threads(torch)}
 
 
 def e2e_c5(args, torch):
@@ -137,7 +174,7 @@ def e2e_c5(args, torch):
         "sampler": sampler_timing(torch),
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = e2e_cpu_baseline(model, cfg, prompt, lens, torch)
+        out["cpu_baseline"] = e2e_cpu_baseline(model, cfg, prompt, torch)
     del eng, model
     torch.cuda.empty_cache()
     return out
@@ -178,22 +215,75 @@ def sampler_timing(torch, iters=50):
     }
 
 
-def e2e_cpu_baseline(model, cfg, prompt, lens, torch, n_seq=2, n_steps=8):
+def e2e_cpu_baseline(model, cfg, prompt, torch, prompt_cap=32, n_steps=6):
     """The reference's op sequence (oracle.ref_model, fp32 on the host, as the
-    reference runs without a GPU) on the n_seq shortest prompts of the batch,
-    timing n_steps greedy decode steps."""
+    reference runs without a GPU) at C5's batch of 64: every sequence's first
+    prompt_cap tokens (a uniform batch, as the reference's one batch-wide length
+    requires) prefilled untimed, then n_steps greedy decode steps timed."""
     from oracle.ref_model import RefGPT
 
-    order = sorted(range(len(lens)), key=lambda b: lens[b])[:n_seq]
-    L = max(lens[b] for b in order)
-    sample = torch.stack([prompt[b, :L] for b in order])  # equal lengths: pad the shorter with its own tokens
+    threads = host_threads(torch)
+    sample = prompt[:, :prompt_cap].contiguous()
+    B = sample.shape[0]
     sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
     ref = RefGPT(sd, cfg.num_layer, cfg.num_attention_heads, cfg.num_key_value_heads)
-    threads = torch.get_num_threads()
-    _, tps, _ = ref.generate_greedy(sample, n_steps, L + n_steps + 1, page_size=16)
+    t0 = time.perf_counter()
+    _, tps, _ = ref.generate_greedy(sample, n_steps, prompt_cap + n_steps + 1, page_size=16)
+    wall = time.perf_counter() - t0
+    del ref, sd
     return {"value": round(tps, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"batch {n_seq} (the shortest prompts, {L} tokens), {n_steps} greedy decode steps, fp32 "
-                      "on the host through the reference op sequence; not the batch-64 workload"}
+            "sample": f"batch {B} (the C5 batch), each prompt capped at its first {prompt_cap} tokens, {n_steps} "
+                      f"greedy decode steps timed, fp32 on the host through the reference op sequence (H_q-expanded "
+                      f"LayerPagedKVCache); the short context understates the CPU's attention work, so the rate "
+                      f"is an upper bound for the U[64, 2048] prompts",
+            "seconds_including_prefill": round(wall, 2)}
+
+
+def c1_record(args, torch):
+    """Config C1 (the reference's CPU-runnable case: 6 L, d 512, 8/2 heads, V
+    32000, fp32, prompt 128, 64 greedy steps, contiguous cache): the engine on
+    the GPU (fp32, the CPU path's arithmetic) and the reference's op sequence on
+    the host with the paged cache and with the tuple-concat cache."""
+    from oracle.ref_model import RefGPT
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT, ModelConfig
+
+    cfg = ModelConfig(num_layer=C1["num_layer"], hidden_size=C1["hidden_size"],
+                      num_attention_heads=C1["num_attention_heads"], num_key_value_heads=C1["num_key_value_heads"],
+                      vocab_size=C1["vocab_size"], intermediate_size=C1["intermediate_size"], init_std=C1["init_std"],
+                      block_size=C1["prompt"] + C1["steps"], seed=args.seed)
+    model = GPT(cfg, device="cpu", dtype=torch.float32)  # seeded init on the CPU, then moved
+    sd = {k: v.clone() for k, v in model.state_dict().items()}
+    model = model.to("cuda")
+    prompt = torch.randint(0, C1["vocab_size"], (1, C1["prompt"]), generator=torch.Generator().manual_seed(args.seed))
+    eng = InferenceEngine(cfg, device="cuda", dtype=torch.float32, kv_cache_page_size=C1["page"], model=model)
+    eng.generate(prompt, 4, top_k=1)
+    torch.cuda.synchronize()
+    tokens, stats = eng.generate(prompt, C1["steps"], top_k=1, return_stats=True)
+    out = {"workload": "C1: 6 L, d 512, 8/2 heads, D 64, V 32000, fp32 weights ~N(0, 0.02) seed 1337, batch 1, "
+                       "prompt 128, 64 greedy steps, contiguous KV cache",
+           "decode_tokens_per_sec": round(stats["decode_tokens_per_sec"], 1),
+           "decode_path": "module path in fp32 (d 512 takes no fused kernels): RoPE + append + attention in one "
+                          "launch pair per layer, graph-replayed steps"}
+    del eng, model
+    if not args.no_cpu_baseline:
+        threads = host_threads(torch)
+        ref = RefGPT(sd, cfg.num_layer, cfg.num_attention_heads, cfg.num_key_value_heads)
+        res = {}
+        for name, tuple_cache in (("paged", False), ("tuple_concat", True)):
+            ref_tokens, tps, _ = ref.generate_greedy(prompt, 4, cfg.block_size, page_size=C1["page"],
+                                                     tuple_cache=tuple_cache)  # warm-up
+            ref_tokens, tps, _ = ref.generate_greedy(prompt, C1["steps"], cfg.block_size, page_size=C1["page"],
+                                                     tuple_cache=tuple_cache)
+            res[name] = (tps, ref_tokens)
+        out["greedy_tokens_equal_cpu"] = bool(torch.equal(tokens.cpu(), res["paged"][1]))
+        out["cpu_baseline"] = {
+            "value": round(res["paged"][0], 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "value_tuple_concat_cache": round(res["tuple_concat"][0], 2),
+            "sample": "the whole C1 workload: fp32 on the host through the reference op sequence with "
+                      "LayerPagedKVCache (value) and with use_paged_kv_cache=False's concatenated K/V "
+                      "(value_tuple_concat_cache)"}
+    return out
 
 
 def build_workload(cfg, seed, torch, ops):
@@ -280,77 +370,102 @@ def algorithmic_bytes(cfg, total):
     return step_bytes, attn_bytes, tokens
 
 
-def cpu_baseline(cfg, wl, torch, budget_s, max_steps=64):
-    """Reference op sequence on the host, one sequence at a time (the reference
-    has one batch-wide length, so a ragged batch runs as batch-1 caches): per
-    sequence one untimed warm-up step, then consecutive decode steps (each
-    appends a token, as the reference's loop does) until the sequence's share
-    of the time budget is spent."""
+def _gather_sequence(cfg, wl, torch, b):
+    """Sequence b's cached K/V as bf16 [1, H_kv, L, D] on the host (fp8: dequantised)."""
+    layout = wl["layout"]
+    hkv, D, P = cfg["hkv"], cfg["head_dim"], cfg["page"]
+    L = int(wl["ctx"][b])
+    pos = torch.arange(L, device="cuda")
+    if layout.page_table is not None:
+        phys = layout.page_table[b].long()[pos // P]
+        base = phys * layout.strides[1] + (pos % P) * D
+    else:
+        base = b * layout.strides[0] + (pos // P) * layout.strides[1] + (pos % P) * D
+    heads = torch.arange(hkv, device="cuda") * layout.strides[2]
+    idx = base[:, None, None] + heads[None, :, None] + torch.arange(D, device="cuda")[None, None, :]
+    if cfg["fp8"]:
+        sidx = (base[:, None] + heads[None, :]) // D
+        k = (layout.k[idx].view(torch.float8_e4m3fn).float() * layout.k_scale[sidx][..., None]).to(torch.bfloat16)
+        v = (layout.v[idx].view(torch.float8_e4m3fn).float() * layout.v_scale[sidx][..., None]).to(torch.bfloat16)
+    else:
+        k, v = layout.k[idx], layout.v[idx]
+    return k.permute(1, 0, 2).unsqueeze(0).cpu(), v.permute(1, 0, 2).unsqueeze(0).cpu()
+
+
+def cpu_baseline(cfg, wl, torch, budget_s, sample=None, seed=1337, max_steps=64):
+    """Reference op sequence on the host (oracle.ref_path.decode_attention_step:
+    rope_impl, gqa_impl, H_q-expanded LayerPagedKVCache append / get_kv, mask,
+    SDPA) in torch bf16, consecutive decode steps (each appends a token, as the
+    reference's loop does) until the time budget is spent. Uniform lengths run
+    as one batch (the reference's own batch-wide length); ragged batches run one
+    sequence at a time (batch-1 caches), over all sequences or a seeded sample."""
     from oracle import ref_path
 
-    threads = len(os.sched_getaffinity(0))
-    env = os.environ.get("OMP_NUM_THREADS")
-    if env and env.isdigit():
-        threads = min(threads, int(env))
-    torch.set_num_threads(threads)
-    layout = wl["layout"]
+    threads = host_threads(torch)
     hq, hkv, D, P = cfg["hq"], cfg["hkv"], cfg["head_dim"], cfg["page"]
     rep = hq // hkv
-    total_time = 0.0
-    total_bytes = 0
-    n_seq = 0
-    tokens = 0
-    for b in range(cfg["batch"]):
-        L = int(wl["ctx"][b])
-        # gather sequence b's cached K/V (untimed setup): [L, hkv, D]
-        pos = torch.arange(L, device="cuda")
-        if layout.page_table is not None:
-            phys = layout.page_table[b].long()[pos // P]
-            base = phys * layout.strides[1] + (pos % P) * D
-        else:
-            base = b * layout.strides[0] + (pos // P) * layout.strides[1] + (pos % P) * D
-        idx = base[:, None, None] + (torch.arange(hkv, device="cuda") * layout.strides[2])[None, :, None] \
-            + torch.arange(D, device="cuda")[None, None, :]
-        if cfg["fp8"]:
-            sidx = (base[:, None] + (torch.arange(hkv, device="cuda") * layout.strides[2])[None, :]) // D
-            k = (layout.k[idx].view(torch.float8_e4m3fn).float() * layout.k_scale[sidx][..., None]).to(torch.bfloat16)
-            v = (layout.v[idx].view(torch.float8_e4m3fn).float() * layout.v_scale[sidx][..., None]).to(torch.bfloat16)
-        else:
-            k = layout.k[idx]
-            v = layout.v[idx]
-        k = k.permute(1, 0, 2).unsqueeze(0).cpu()  # [1, hkv, L, D]
-        v = v.permute(1, 0, 2).unsqueeze(0).cpu()
-        cache = ref_path.LayerPagedKVCache(1, hq, D, L + 2 + max_steps, P, torch.device("cpu"), torch.bfloat16)
-        cache.append(k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1))
-        q = wl["q_in"][b:b + 1].cpu()
-        kn = wl["k_in"][b:b + 1].cpu()
-        vn = wl["v_in"][b:b + 1].cpu()
-        del k, v
+    e = 1 if cfg["fp8"] else 2
+    B = cfg["batch"]
+    uniform = cfg["lo"] == cfg["hi"]
+    total_time, total_bytes, tokens, steps_run = 0.0, 0, 0, 0
+    if uniform:
+        L = int(wl["ctx"][0])
+        cache = ref_path.LayerPagedKVCache(B, hq, D, L + 2 + max_steps, P, torch.device("cpu"), torch.bfloat16)
+        for b in range(B):  # append sequence by sequence into the batched store (untimed setup)
+            k, v = _gather_sequence(cfg, wl, torch, b)
+            cache._k_flat[b:b + 1, :, :L].copy_(k.repeat_interleave(rep, dim=1))
+            cache._v_flat[b:b + 1, :, :L].copy_(v.repeat_interleave(rep, dim=1))
+        cache.current_length = L
+        q, kn, vn = wl["q_in"].cpu(), wl["k_in"].cpu(), wl["v_in"].cpu()
         ref_path.decode_attention_step(q, kn, vn, cache, hkv, position=L)  # warm-up (appends one token)
-        share = budget_s / cfg["batch"]
-        spent, step = 0.0, 0
-        e = 1 if cfg["fp8"] else 2
-        while step < max_steps and (step == 0 or spent < share):
-            Lt = L + 1 + step
+        while steps_run < max_steps and (steps_run == 0 or total_time < budget_s):
+            Lt = L + 1 + steps_run
             t0 = time.perf_counter()
             y = ref_path.decode_attention_step(q, kn, vn, cache, hkv, position=Lt)
-            spent += time.perf_counter() - t0
-            assert y.shape == (1, hq, 1, D)
-            total_bytes += (Lt + 1) * hkv * D * e * 2 + ((Lt + 1) * hkv * 8 if cfg["fp8"] else 0)
-            tokens += Lt + 1
-            step += 1
-        total_time += spent
-        n_seq += 1
+            total_time += time.perf_counter() - t0
+            assert y.shape == (B, hq, 1, D)
+            total_bytes += B * (Lt + 1) * hkv * D * e * 2
+            tokens += B * (Lt + 1)
+            steps_run += 1
         del cache
+        what = (f"the whole batch of {B} as one reference batch (uniform length), {steps_run} consecutive decode "
+                f"steps")
+    else:
+        seqs = list(range(B))
+        if sample is not None and sample < B:
+            g = torch.Generator().manual_seed(seed)
+            seqs = sorted(torch.randperm(B, generator=g)[:sample].tolist())
+        for b in seqs:
+            L = int(wl["ctx"][b])
+            k, v = _gather_sequence(cfg, wl, torch, b)
+            cache = ref_path.LayerPagedKVCache(1, hq, D, L + 2 + max_steps, P, torch.device("cpu"), torch.bfloat16)
+            cache.append(k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1))
+            del k, v
+            q, kn, vn = wl["q_in"][b:b + 1].cpu(), wl["k_in"][b:b + 1].cpu(), wl["v_in"][b:b + 1].cpu()
+            ref_path.decode_attention_step(q, kn, vn, cache, hkv, position=L)  # warm-up (appends one token)
+            share, spent, step = budget_s / len(seqs), 0.0, 0
+            while step < max_steps and (step == 0 or spent < share):
+                Lt = L + 1 + step
+                t0 = time.perf_counter()
+                y = ref_path.decode_attention_step(q, kn, vn, cache, hkv, position=Lt)
+                spent += time.perf_counter() - t0
+                assert y.shape == (1, hq, 1, D)
+                total_bytes += (Lt + 1) * hkv * D * e * 2 + ((Lt + 1) * hkv * 8 if cfg["fp8"] else 0)
+                tokens += Lt + 1
+                step += 1
+                steps_run += 1
+            total_time += spent
+            del cache
+        what = (f"{len(seqs)} of the {B} sequences" + (" (seeded sample)" if len(seqs) < B else "")
+                + f", one at a time, {steps_run} decode steps in all")
     return {
         "value": round(total_bytes / total_time / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"all {n_seq} sequences of the batch, consecutive decode steps per sequence ({tokens} cached "
-                   f"tokens attended in total) through the reference op sequence (rope_impl, gqa_impl, H_q-expanded "
-                   f"LayerPagedKVCache append/get_kv, mask, SDPA) in torch bf16 on the host; bytes counted as for the "
-                   f"GPU (unique K/V)"
+        "sample": (f"{what} ({tokens} cached tokens attended) through the reference op sequence (rope_impl, gqa_impl, "
+                   f"H_q-expanded LayerPagedKVCache append/get_kv, mask, SDPA) in torch bf16 on the host; bytes "
+                   f"counted as for the GPU (unique K/V)"
                    + ("; fp8 cache dequantised to bf16, the reference has no fp8" if cfg["fp8"] else "")),
         "seconds": round(total_time, 3),
     }
@@ -369,6 +484,99 @@ def measured_traffic(config: str):
     return None
 
 
+def run_config(name, args, torch, ops, with_cpu):
+    """Time one attention config: the decode step (fused launch pair for bf16
+    caches, RoPE + append then attention for fp8), the two-launch step, and the
+    attention operator alone, each over args.steps steps after args.warmup,
+    bracketed by HIP events on the stream the kernels run on."""
+    cfg = CONFIGS[name]
+    wl = build_workload(cfg, args.seed, torch, ops)
+    B, hq, D = cfg["batch"], cfg["hq"], cfg["head_dim"]
+    layout = wl["layout"]
+    q_rot = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(B, hq, D, dtype=torch.bfloat16, device="cuda")
+    ws = ops.Workspace("cuda")
+    split = args.split_tokens
+    lens_out = torch.empty_like(wl["positions"])
+    fused = args.step_path == "fused" or (args.step_path == "auto" and not cfg["fp8"])
+
+    def two_launch_step():
+        ops.rope_append(wl["q_in"], wl["k_in"], wl["v_in"], wl["rope"], wl["positions"], layout, q_out=q_rot)
+        ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
+                             split_tokens=split, workspace=ws)
+
+    def step():
+        # the fused decode step: RoPE + append of the new token inside the attention launch pair
+        if split or not fused:
+            two_launch_step()
+            return
+        ops.decode_attention_append(wl["rope"], wl["positions"], layout, wl["max_len"], q=wl["q_in"][:, :, 0],
+                                    k=wl["k_in"][:, :, 0], v=wl["v_in"][:, :, 0], lens_out=lens_out, out=out,
+                                    workspace=ws)
+
+    def attn_only():
+        ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
+                             split_tokens=split, workspace=ws)
+
+    def timed(fn, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / max(args.steps, 1)
+
+    ms = timed(step, args.warmup)
+    two_ms = timed(two_launch_step, 0)   # the same step as two launches (RoPE + append kernel, then attention)
+    attn_ms = timed(attn_only, 0)        # the dominant operator alone (q rotated by the step above)
+    step_bytes, attn_bytes, tokens = algorithmic_bytes(cfg, wl["total"])
+    value = step_bytes / (ms * 1e-3) / 1e9
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    rec = {
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 5),
+        "ms_per_step_two_launches": round(two_ms, 5),
+        "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
+        "dtype": "fp8-e4m3 cache, bf16 q/out" if cfg["fp8"] else "bf16",
+        "config": {
+            "workload": cfg["name"],
+            "batch": B, "q_heads": hq, "kv_heads": cfg["hkv"], "head_dim": D,
+            "context": [cfg["lo"], cfg["hi"]], "page_size": cfg["page"], "paged": cfg["paged"],
+            "cached_tokens": tokens, "split_tokens": split or "balanced (equal 32-token tiles per wave)",
+            "parallelism": "single GPU",
+            "step_path": ("one launch pair: RoPE + append inside the attention split kernel "
+                          "(decode_stream_append_kernel + decode_merge_kernel)" if fused and not split
+                          else "rope_append_kernel, then the attention kernels"),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": ("decode attention (decode_stream_kernel + decode_merge_kernel)" if not split
+                       else "decode attention (decode_split_kernel + decode_combine_kernel)"),
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic(name),
+            "traffic_source": f"profiles/decode_attn_{name}.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                              "scaled by a 256 MiB copy)",
+            "avg_us": round(attn_ms * 1e3, 2),
+            "algorithmic_bytes": attn_bytes,
+        },
+        "cpu_baseline": None,
+    }
+    if with_cpu:
+        rec["cpu_baseline"] = cpu_baseline(cfg, wl, torch, args.cpu_seconds, sample=CPU_SAMPLE.get(name),
+                                           seed=args.seed)
+    del wl, layout, q_rot, out, ws
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -382,126 +590,43 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (no CPU fallback)", file=sys.stderr)
         return 1
-    cfg = CONFIGS[args.config]
     torch.cuda.set_device(0)
     if args.e2e_only:
         print(json.dumps({"e2e": e2e_c5(args, torch)}), flush=True)
         return 0
-    wl = build_workload(cfg, args.seed, torch, ops)
-    B, hq, D = cfg["batch"], cfg["hq"], cfg["head_dim"]
-    layout = wl["layout"]
-    q_rot = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
-    out = torch.empty(B, hq, D, dtype=torch.bfloat16, device="cuda")
-    ws = ops.Workspace("cuda")
-    split = args.split_tokens
 
     # a plain copy of known size, for scaling rocprof FETCH/WRITE counters
     calib = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")
     calib_dst = torch.empty_like(calib)
     calib_dst.copy_(calib)
+    del calib, calib_dst
 
-    lens_out = torch.empty_like(wl["positions"])
-    fused = args.step_path == "fused" or (args.step_path == "auto" and not cfg["fp8"])
-
-    def step():
-        # the fused decode step: RoPE + append of the new token inside the attention launch pair
-        if split or not fused:
-            two_launch_step()
-            return
-        ops.decode_attention_append(wl["rope"], wl["positions"], layout, wl["max_len"], q=wl["q_in"][:, :, 0],
-                                    k=wl["k_in"][:, :, 0], v=wl["v_in"][:, :, 0], lens_out=lens_out, out=out,
-                                    workspace=ws)
-
-    def two_launch_step():
-        ops.rope_append(wl["q_in"], wl["k_in"], wl["v_in"], wl["rope"], wl["positions"], layout, q_out=q_rot)
-        ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
-                             split_tokens=split, workspace=ws)
-
-    def attn_only():
-        ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
-                             split_tokens=split, workspace=ws)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / max(args.steps, 1)
-
-    # the same step as two launches (RoPE + append kernel, then attention)
-    ev4 = torch.cuda.Event(enable_timing=True)
-    ev5 = torch.cuda.Event(enable_timing=True)
-    ev4.record()
-    for _ in range(args.steps):
-        two_launch_step()
-    ev5.record()
-    torch.cuda.synchronize()
-    two_ms = ev4.elapsed_time(ev5) / max(args.steps, 1)
-
-    # the dominant operator alone (q rotated by the step above), same stream, same events
-    ev2 = torch.cuda.Event(enable_timing=True)
-    ev3 = torch.cuda.Event(enable_timing=True)
-    ev2.record()
-    for _ in range(args.steps):
-        attn_only()
-    ev3.record()
-    torch.cuda.synchronize()
-    attn_ms = ev2.elapsed_time(ev3) / max(args.steps, 1)
-
-    step_bytes, attn_bytes, tokens = algorithmic_bytes(cfg, wl["total"])
-    value = step_bytes / (ms * 1e-3) / 1e9
-    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
-    split_used = split or "balanced (equal 32-token tiles per wave)"
+    head = run_config(args.config, args, torch, ops, not args.no_cpu_baseline)
     result = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": head["value"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "ms_per_step_two_launches": round(two_ms, 5),
+        "ms_per_step": head["ms_per_step"],
+        "ms_per_step_two_launches": head["ms_per_step_two_launches"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8-e4m3 cache, bf16 q/out" if cfg["fp8"] else "bf16",
+        "dtype": head["dtype"],
         "data": "synthetic",
-        "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
-        "config": {
-            "workload": cfg["name"],
-            "batch": B, "q_heads": hq, "kv_heads": cfg["hkv"], "head_dim": D,
-            "context": [cfg["lo"], cfg["hi"]], "page_size": cfg["page"], "paged": cfg["paged"],
-            "cached_tokens": tokens, "split_tokens": split_used, "parallelism": "single GPU",
-            "step_path": ("one launch pair: RoPE + append inside the attention split kernel "
-                          "(decode_stream_append_kernel + decode_merge_kernel)" if fused and not split
-                          else "rope_append_kernel, then the attention kernels"),
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": ("decode attention (decode_stream_kernel + decode_merge_kernel)" if not split
-                       else "decode attention (decode_split_kernel + decode_combine_kernel)"),
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(args.config),
-            "traffic_source": f"profiles/decode_attn_{args.config}.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
-                              "scaled by a 256 MiB copy)",
-            "avg_us": round(attn_ms * 1e3, 2),
-            "algorithmic_bytes": attn_bytes,
-        },
-        "cpu_baseline": None,
+        "pct_of_peak_hbm": head["pct_of_peak_hbm"],
+        "config": head["config"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+        "host": host_info(torch),
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, wl, torch, args.cpu_seconds)
+    for name in [n for n in args.nested.split(",") if n and n != args.config]:
+        result[name] = run_config(name, args, torch, ops, not args.no_cpu_baseline)
+    if not args.no_c1:
+        result["c1"] = c1_record(args, torch)
     if not args.no_e2e:
-        del wl, layout, q_rot, out, ws
-        torch.cuda.empty_cache()
         result["e2e"] = e2e_c5(args, torch)
     print(json.dumps(result), flush=True)
     return 0

@@ -75,8 +75,18 @@ class RefGPT:
         pos = torch.arange(position_offset, position_offset + T).unsqueeze(0)
         q, k = ref_path.rope_impl(q, k, pos)
         k, v = ref_path.gqa_impl(k, v, self.hkv, self.hq)
-        past_len = cache.append(k, v)
-        k, v = cache.get_kv()
+        if isinstance(cache, list):
+            # use_paged_kv_cache=False (engine.py:168-178): cache[0] is None or the
+            # layer's past (K, V); the new tokens are concatenated to it and the
+            # result becomes the layer's past (attn.py:174-186, 330-331, 437-440)
+            past = cache[0]
+            past_len = 0 if past is None else past[0].size(2)
+            if past is not None:
+                k, v = torch.cat([past[0], k], dim=2), torch.cat([past[1], v], dim=2)
+            cache[0] = (k, v)
+        else:
+            past_len = cache.append(k, v)
+            k, v = cache.get_kv()
         mask, causal = None, True
         if past_len > 0:
             mask = ref_path.build_cache_causal_mask(T, k.size(2), past_len, x.device)
@@ -99,18 +109,23 @@ class RefGPT:
             return F.linear(x, self.w["wte.weight"])
         return F.linear(x.to(BF16).float(), self.wb["wte.weight"]).to(BF16)  # tied lm_head (gpt.py:61-63)
 
-    def new_caches(self, batch: int, block_size: int, page_size: int = 128):
+    def new_caches(self, batch: int, block_size: int, page_size: int = 128, tuple_cache: bool = False):
+        """One reference LayerPagedKVCache per layer (cache.py:54-97), or with
+        ``tuple_cache`` one [past] holder per layer for the concatenating path."""
+        if tuple_cache:
+            return [[None] for _ in range(self.L)]
         dt = BF16 if self.bf16 else torch.float32
         return [ref_path.LayerPagedKVCache(batch, self.hq, self.D, block_size, page_size, "cpu", dt)
                 for _ in range(self.L)]
 
     @torch.no_grad()
     def generate_greedy(self, prompt: torch.Tensor, max_new_tokens: int, block_size: int, page_size: int = 128,
-                        max_steps_timed: int | None = None):
-        """engine.py:144-228 with temperature 1, top_k 1 (argmax). Returns
-        (tokens [B, T + n], decode tokens/s, logits of every step)."""
+                        max_steps_timed: int | None = None, tuple_cache: bool = False):
+        """engine.py:144-228 with temperature 1, top_k 1 (argmax); ``tuple_cache``
+        runs use_paged_kv_cache=False. Returns (tokens [B, T + n], decode
+        tokens/s, logits of every step)."""
         B, T = prompt.shape
-        caches = self.new_caches(B, block_size, page_size)
+        caches = self.new_caches(B, block_size, page_size, tuple_cache)
         logits = self.forward(prompt, caches, 0)
         tokens = [prompt]
         step_logits = [logits[:, -1].clone()]

@@ -115,6 +115,19 @@ def test_cached_steps_equal_full_prefill():
             torch.testing.assert_close(step[:, 0], full[:, t], rtol=1e-5, atol=1e-5)
 
 
+def test_tuple_cache_path_equals_paged_cache_path():
+    """use_paged_kv_cache=False (past K/V concatenated each step) gives the
+    paged cache's greedy tokens and logits."""
+    L, C, hq, hkv, ffn, V = 2, 64, 4, 2, 96, 50
+    ref = RefGPT(_state(L, C, hq, hkv, ffn, V, std=0.1, seed=6), L, hq, hkv)
+    idx = torch.randint(0, V, (2, 10), generator=torch.Generator().manual_seed(3))
+    t0, _, l0 = ref.generate_greedy(idx, 6, 32, page_size=4)
+    t1, _, l1 = ref.generate_greedy(idx, 6, 32, tuple_cache=True)
+    assert torch.equal(t0, t1)
+    for a, b in zip(l0, l1):
+        torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+
+
 class _UnroundedSwiGLU(RefGPT):
     """A planted mistake: SiLU(gate) * up computed from fp32 copies, so the
     product skips its bf16 rounding."""
