@@ -530,9 +530,11 @@ def run_config(name, args, torch, ops, with_cpu):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / max(args.steps, 1)
 
+    # each timed region gets its own warm-up: a kernel's first launch loads its code
+    # object (~0.6 ms), which untimed warm-up keeps out of the per-step figures
     ms = timed(step, args.warmup)
-    two_ms = timed(two_launch_step, 0)   # the same step as two launches (RoPE + append kernel, then attention)
-    attn_ms = timed(attn_only, 0)        # the dominant operator alone (q rotated by the step above)
+    two_ms = timed(two_launch_step, args.warmup)  # the same step as two launches (RoPE + append, then attention)
+    attn_ms = timed(attn_only, args.warmup)       # the dominant operator alone (q rotated by the step above)
     step_bytes, attn_bytes, tokens = algorithmic_bytes(cfg, wl["total"])
     value = step_bytes / (ms * 1e-3) / 1e9
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9

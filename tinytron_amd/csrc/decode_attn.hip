@@ -224,10 +224,14 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
 
 
 // Block-wide exclusive prefix sum of the per-sequence split counts into LDS:
-// prefix[b] = sum_{b' < b} ceil(L_b' / split), prefix[B] = total; lens[b] = L_b
-// (when lens is not null).
+// prefix[b] = sum_{b' < b} n(L_b'), prefix[B] = total, with n(L) = ceil(L /
+// split) + extra for L > 0 (0 for L = 0); lens[b] = L_b (when lens is not null).
+__device__ __forceinline__ int split_count(int L, int split_tokens, int extra) {
+  return L > 0 ? (L + split_tokens - 1) / split_tokens + extra : 0;
+}
+
 __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int split_tokens, int *lens, int *prefix,
-                                                   int *wave_sums) {
+                                                   int *wave_sums, int extra = 0) {
   const int B = a.batch;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -240,7 +244,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
     if (b < B) {
       const int L = max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
       if (lens != nullptr) lens[b] = L;
-      local += (L + split_tokens - 1) / split_tokens;
+      local += split_count(L, split_tokens, extra);
     }
   }
   int v = local;
@@ -259,7 +263,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
     if (b < B) {
       prefix[b] = run;
       const int L = lens != nullptr ? lens[b] : max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
-      run += (L + split_tokens - 1) / split_tokens;
+      run += split_count(L, split_tokens, extra);
     }
   }
   if (tid == blockDim.x - 1) prefix[B] = base + v;
@@ -734,6 +738,14 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
 constexpr int kStreamOcc = 2;
 constexpr int stream_blocks_per_cu(int head_dim) { return head_dim == 64 ? 2 : 1; }
 
+// Tiles' worth of time a wave spends starting a segment piece (length and
+// page-table lookups, q fragments, the fused step's RoPE + append): charged to
+// every segment in the balanced partition, so a wave that holds many short
+// segments gets fewer tiles. Measured (fused step, 0 -> 2): C3 406 -> 387 us,
+// C4 802 -> 766 us, C2 113 -> 110 us, C5 layer 39.3 -> 37.8 us; 1, 3 and 4
+// were as good or worse on every config.
+constexpr int stream_seg_cost(int /*head_dim*/) { return 2; }
+
 // LDS of the split kernel: V slots [4 waves] | wave sums [4] | prefix [B + 1]
 // (| q staging [4 waves][16][D] bf16 for the fused variant).
 template <int D, bool kFP8, bool kAppend, bool kPartIn>
@@ -751,7 +763,7 @@ __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeApp
   if constexpr (kAppend)
     qs = reinterpret_cast<uint16_t *>(smem_v + kVAll + 16 * ((sizeof(int) * (kWavesPerBlock + a.batch + 1) + 15) / 16)) +
          wave * 16 * D;
-  build_split_prefix(a, kTileTokens, nullptr, prefix, wave_sums);  // ends with a block barrier
+  build_split_prefix(a, kTileTokens, nullptr, prefix, wave_sums, a.seg_cost);  // ends with a block barrier
   if (blockIdx.x == 0) {  // for the merge kernel (and the next step's lengths)
     for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.ws_prefix[i] = prefix[i];
     if constexpr (kAppend)
@@ -775,17 +787,22 @@ __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeApp
     }
     const int b = __builtin_amdgcn_readfirstlane(lo);
     const int pb = __builtin_amdgcn_readfirstlane(prefix[b]);
-    const int nb = __builtin_amdgcn_readfirstlane(prefix[b + 1]) - pb;  // > 0: tile t lies in sequence b
+    const int nbe = __builtin_amdgcn_readfirstlane(prefix[b + 1]) - pb;  // > 0: tile t lies in sequence b
     const int64_t local = t - (int64_t)pb * a.hkv;
-    const int hk = (int)(local / nb);
-    const int j0 = (int)(local - (int64_t)hk * nb);
-    const int64_t seg_end = (int64_t)pb * a.hkv + (int64_t)(hk + 1) * nb;
+    const int hk = (int)(local / nbe);
+    const int j0e = (int)(local - (int64_t)hk * nbe);
+    const int64_t seg_end = (int64_t)pb * a.hkv + (int64_t)(hk + 1) * nbe;
     const int64_t stop = seg_end < t_end ? seg_end : t_end;
-    const int j1 = j0 + (int)(stop - t);
-    const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b] + a.len_add, a.max_len));
-    // The segment's last tile holds this step's token: only this wave reads
-    // it, so the fused variant appends it at the start of this piece.
-    stream_piece<D, kFP8, kAppend, kPartIn>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nb, w, lane, vlds, qs, ident16, ident8);
+    // real tiles of the piece: the segment's first seg_cost line positions hold none
+    const int j0 = max(j0e - a.seg_cost, 0);
+    const int j1 = j0e + (int)(stop - t) - a.seg_cost;
+    if (j1 > j0) {
+      const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b] + a.len_add, a.max_len));
+      // The segment's last tile holds this step's token: only this wave reads
+      // it, so the fused variant appends it at the start of this piece.
+      stream_piece<D, kFP8, kAppend, kPartIn>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nbe - a.seg_cost, w, lane,
+                                              vlds, qs, ident16, ident8);
+    }
     t = stop;
   }
 }
@@ -822,9 +839,11 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
   }
   const int64_t W = (int64_t)a.ws_prefix[a.batch] * a.hkv;
   const int64_t NW = a.stream_waves;
-  const int64_t start = (int64_t)pb * a.hkv + (int64_t)hk * nb;
-  merge_segment<D, kMaxG>(a, b, hk, seg, wave_of_tile(start, W, NW), wave_of_tile(start + nb - 1, W, NW), W, NW,
-                          lane);
+  // the segment's real tiles sit after its seg_cost empty line positions; every
+  // wave whose range meets them holds a piece
+  const int64_t start = (int64_t)pb * a.hkv + (int64_t)hk * nb + a.seg_cost;
+  const int64_t last = (int64_t)pb * a.hkv + (int64_t)(hk + 1) * nb - 1;
+  merge_segment<D, kMaxG>(a, b, hk, seg, wave_of_tile(start, W, NW), wave_of_tile(last, W, NW), W, NW, lane);
 }
 
 // fp32 cache and activations: VALU path (small models run in fp32, e.g. the
@@ -1004,6 +1023,7 @@ hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream
   DecodeArgs a = a0;
   const int64_t blocks = balanced_stream_waves(D, a.batch, a.hkv, a.max_len) / kWavesPerBlock;
   a.stream_waves = (int)(blocks * kWavesPerBlock);
+  a.seg_cost = stream_seg_cost(D);
   const size_t lds_prefix = 16 * ((sizeof(int) * (kWavesPerBlock + (size_t)a.batch + 1) + 15) / 16);
   size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes + lds_prefix;
   if (ap != nullptr) {
