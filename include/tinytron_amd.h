@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 1
+#define TT_ABI_VERSION 2
 
 #define TT_OK 0
 #define TT_ERR_INVALID_ARGUMENT (-1)
@@ -484,15 +484,27 @@ int tt_silu_mul_rows_bf16(const void *g, int64_t ldg, const void *u, int64_t ldu
  * token's log_softmax(filtered) value (sampler.py:56-61). logprobs [M, V]
  * with row stride ld_logprobs (optional): log_softmax of the filtered logits,
  * -inf where filtered. V <= 65536 (bf16 logits), 32768 (fp32 logits).
+ * workspace (optional, 16-byte aligned, workspace_bytes >=
+ * tt_sample_workspace_bytes(m, vocab, top_k)): with 2 <= top_k <= 64, V >
+ * 8192 and no logprobs rows, every 8192-logit chunk of a row first reduces to
+ * its top-k candidates on a workgroup of its own, and the row is decided from
+ * those (same tokens and log-probabilities as the one-workgroup-per-row path,
+ * which runs when workspace is NULL or a row's candidates cannot decide it).
+ * Calls that share a workspace must not overlap.
  */
 int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
                    float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
-                   float *logprobs, int64_t ld_logprobs, tt_stream_t stream);
+                   float *logprobs, int64_t ld_logprobs, void *workspace, size_t workspace_bytes,
+                   tt_stream_t stream);
 
 /* As tt_sample_bf16 with fp32 logits (fp32 models). */
 int tt_sample_f32(const float *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
                   float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
-                  float *logprobs, int64_t ld_logprobs, tt_stream_t stream);
+                  float *logprobs, int64_t ld_logprobs, void *workspace, size_t workspace_bytes,
+                  tt_stream_t stream);
+
+/* Workspace bytes tt_sample_* uses for m rows of vocab logits at this top_k (0: none). */
+size_t tt_sample_workspace_bytes(int64_t m, int64_t vocab, int64_t top_k);
 
 #ifdef __cplusplus
 }

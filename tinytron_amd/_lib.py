@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TT_OK = 0
 TT_ERR_INVALID_ARGUMENT = -1
@@ -89,6 +89,7 @@ _SAMPLE = [
     _f32, _i64, _f32,                                # temperature, top_k, top_p
     ctypes.c_uint64, ctypes.c_uint64,                # seed, offset
     _vp, _vp, _vp, _i64,                             # tokens, token_logprob, logprobs, logprobs row stride
+    _vp, _size,                                      # workspace, workspace_bytes
     _vp,                                             # stream
 ]
 
@@ -129,6 +130,7 @@ SIGNATURES = {
     "tt_decode_attn_append_bf16_noalloc": (_DECODE_APPEND_HEAD + _DECODE_APPEND_TAIL_NOALLOC, ctypes.c_int),
     "tt_sample_bf16": (_SAMPLE, ctypes.c_int),
     "tt_sample_f32": (_SAMPLE, ctypes.c_int),
+    "tt_sample_workspace_bytes": ([_i64, _i64, _i64], _size),
 }
 
 _LIB = None

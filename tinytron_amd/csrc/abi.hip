@@ -502,7 +502,8 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
 
 int sample_common(bool f32, const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature,
                   int64_t top_k, float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
-                  float *logprobs, int64_t ld_logprobs, tt_stream_t stream) {
+                  float *logprobs, int64_t ld_logprobs, void *workspace, size_t workspace_bytes,
+                  tt_stream_t stream) {
   TT_CHECK(temperature > 0.f, TT_ERR_INVALID_ARGUMENT, "temperature must be > 0");
   TT_CHECK(m >= 0 && m <= INT32_MAX, TT_ERR_INVALID_ARGUMENT, "rows must be in [0, 2^31)");
   if (m == 0) return ok();
@@ -533,6 +534,15 @@ int sample_common(bool f32, const void *logits, int64_t ld, int64_t m, int64_t v
   a.logprobs = logprobs;
   a.ld_lp = ld_logprobs;
   a.vec_out = logprobs != nullptr && aligned(logprobs, 16) && ld_logprobs % 4 == 0;
+  a.cand_chunks = tt::sample_cand_chunks(vocab, a.top_k, logprobs != nullptr);
+  a.cand = nullptr;
+  if (workspace != nullptr && a.cand_chunks > 0) {
+    const size_t need = (size_t)m * a.cand_chunks * sizeof(tt::CandRecord);
+    TT_CHECK(workspace_bytes >= need, TT_ERR_WORKSPACE_TOO_SMALL,
+             "sampler workspace of %zu bytes is smaller than the %zu this call needs", workspace_bytes, need);
+    TT_CHECK(aligned(workspace, 16), TT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    a.cand = workspace;
+  }
   (void)hipGetLastError();
   return from_hip(tt::launch_sample(a, f32, (hipStream_t)stream), "sampler launch");
 }
@@ -847,18 +857,26 @@ int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_stri
                               sm_scale, ws, kScratchBytes, stream, /*exact_slots=*/true);
 }
 
+size_t tt_sample_workspace_bytes(int64_t m, int64_t vocab, int64_t top_k) {
+  if (m <= 0 || vocab <= 0) return 0;
+  const int chunks = tt::sample_cand_chunks(vocab, top_k > 0 && top_k < vocab ? top_k : 0, false);
+  return (size_t)m * chunks * sizeof(tt::CandRecord);
+}
+
 int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
                    float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
-                   float *logprobs, int64_t ld_logprobs, tt_stream_t stream) {
+                   float *logprobs, int64_t ld_logprobs, void *workspace, size_t workspace_bytes,
+                   tt_stream_t stream) {
   return sample_common(false, logits, ld, m, vocab, temperature, top_k, top_p, seed, offset, tokens, token_logprob,
-                       logprobs, ld_logprobs, stream);
+                       logprobs, ld_logprobs, workspace, workspace_bytes, stream);
 }
 
 int tt_sample_f32(const float *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,
                   float top_p, uint64_t seed, uint64_t offset, int64_t *tokens, float *token_logprob,
-                  float *logprobs, int64_t ld_logprobs, tt_stream_t stream) {
+                  float *logprobs, int64_t ld_logprobs, void *workspace, size_t workspace_bytes,
+                  tt_stream_t stream) {
   return sample_common(true, logits, ld, m, vocab, temperature, top_k, top_p, seed, offset, tokens, token_logprob,
-                       logprobs, ld_logprobs, stream);
+                       logprobs, ld_logprobs, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

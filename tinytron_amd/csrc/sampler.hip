@@ -29,6 +29,18 @@
 //          (Steele, Lea and Flood, 2014) keyed by (seed, offset, row): the same
 //          distribution as torch.multinomial over softmax(filtered), not the
 //          same random stream.
+//
+// Candidate path (2 <= top_k <= kCandSlots, no full log-probability rows,
+// V > kCandChunk): one workgroup per row leaves most CUs idle, so the row is
+// first cut into kCandChunk-logit chunks, each reduced on a workgroup of its
+// own to its top-k candidates (topk_candidates_kernel: the values >= the
+// chunk's k-th largest). The row's kept set lies within the union of those
+// (the row's k-th largest is >= every chunk's), so one wave then finishes the
+// row on at most kCandSlots x chunks candidates (candidates_pick) with the
+// same rules and the same fixed-point masses as the whole-row path. A row the
+// candidates cannot decide exactly -- ties at the row's boundary that a chunk
+// had no slots for, more than kCandSlots kept tokens, fewer than k finite
+// logits -- runs the whole-row path in the same launch.
 #include <climits>
 
 #include "tt_internal.h"
@@ -443,11 +455,296 @@ __device__ __forceinline__ RowMax row_max(const SampleArgs &a, const Row<EPT, kF
   return RowMax{m, amax, cmax, nfinite};
 }
 
+// ---- candidate path ----------------------------------------------------------
+
+constexpr int kCandThreads = 256;
+constexpr int kCandEPT = kCandChunk / kCandThreads;  // 32 logits per thread, 8-logit groups
+
+struct CandShared {
+  uint32_t hrep[256 * kRep];  // [bin][replica]
+  uint32_t hist[256];
+  uint32_t bc[2];
+  int cnt;
+};
+
+// Workgroup (chunk c, row): the chunk's logits in registers (thread t holds
+// groups 8 (t + 256 g) .. + 7 of the chunk), the k-th largest order key by
+// MSB-first radix select (integer histograms in LDS, replicated as in
+// radix_select), then the candidates: every value strictly above it (fewer
+// than k of them), then values equal to it while slots remain.
+template <bool kF32>
+__global__ __launch_bounds__(kCandThreads) void topk_candidates_kernel(SampleArgs a) {
+  __shared__ CandShared sh;
+  constexpr int G = kCandEPT / 8;
+  const int c = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
+  const int base = c * kCandChunk;
+  CandRecord *rec = static_cast<CandRecord *>(a.cand) + (int64_t)row * a.cand_chunks + c;
+  const char *rowp = static_cast<const char *>(a.logits) + (int64_t)row * a.ld * (kF32 ? 4 : 2);
+
+  // loads: every full group's vector load issued before any is used; the
+  // partial group (at most one per row) or unaligned rows read element by element
+  constexpr int kVec = kF32 ? 2 : 1;
+  u32x4 raw[G][kVec];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int i0 = base + 8 * (t + kCandThreads * g);
+    const bool full = a.vec && i0 + 8 <= a.V;
+    const char *src = rowp + (int64_t)(full ? i0 : 0) * (kF32 ? 4 : 2);
+#pragma unroll
+    for (int h = 0; h < kVec; ++h) raw[g][h] = full ? *reinterpret_cast<const u32x4 *>(src + 16 * h) : u32x4{0, 0, 0, 0};
+  }
+  float y[kCandEPT];
+  uint32_t key[kCandEPT];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int i0 = base + 8 * (t + kCandThreads * g);
+    const bool full = a.vec && i0 + 8 <= a.V;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x;
+      if (full) {
+        const uint32_t w = raw[g][kF32 ? e / 4 : 0][kF32 ? e % 4 : e / 2];
+        x = kF32 ? __uint_as_float(w) : __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+      } else if (i0 + e < a.V) {
+        x = kF32 ? reinterpret_cast<const float *>(rowp)[i0 + e]
+                 : __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(rowp)[i0 + e] << 16);
+      } else {
+        x = -INFINITY;
+      }
+      y[8 * g + e] = a.apply_temp ? x / a.temperature : x;
+      key[8 * g + e] = i0 + e < a.V ? order_key(y[8 * g + e]) : 0u;  // real keys are >= key(-inf) > 0
+    }
+  }
+
+  const int nvalid = a.V - base < kCandChunk ? a.V - base : kCandChunk;
+  uint32_t kth = 1;  // below every real key: all of a chunk with at most k logits are candidates
+  if (nvalid > a.top_k) {
+    uint32_t prefix = 0, mask = 0, need = (uint32_t)a.top_k;
+    const uint32_t rep = t & (kRep - 1);
+#pragma unroll 1
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = t; i < 256 * kRep; i += kCandThreads) sh.hrep[i] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kCandEPT; ++j)
+        if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&sh.hrep[((key[j] >> shift) & 255u) * kRep + rep], 1u);
+      __syncthreads();
+      {
+        uint32_t h = 0;
+#pragma unroll
+        for (int j = 0; j < kRep; ++j) h += sh.hrep[t * kRep + ((j + t) & (kRep - 1))];
+        sh.hist[t] = h;
+      }
+      __syncthreads();
+      if (t < 64) {  // the largest digit whose suffix count reaches need
+        uint32_t h[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h[j] = sh.hist[255 - 4 * t - j];
+          sum += h[j];
+        }
+        uint32_t incl = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t o = __shfl_up(incl, off, 64);
+          if (t >= off) incl += o;
+        }
+        const uint32_t excl = incl - sum;
+        if (incl >= need && excl < need) {
+          uint32_t cum = excl;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (cum + h[j] >= need) {
+              sh.bc[0] = 255u - 4u * t - j;
+              sh.bc[1] = cum;
+              break;
+            }
+            cum += h[j];
+          }
+        }
+      }
+      __syncthreads();
+      need -= sh.bc[1];
+      prefix |= sh.bc[0] << shift;
+      mask |= 0xFFu << shift;
+      __syncthreads();
+    }
+    kth = prefix;
+  }
+
+  if (t == 0) sh.cnt = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kCandEPT; ++j)
+    if (key[j] > kth) {  // fewer than k <= kCandSlots of these
+      const int slot = atomicAdd(&sh.cnt, 1);
+      rec->val[slot] = y[j];
+      rec->idx[slot] = base + 8 * (t + kCandThreads * (j / 8)) + j % 8;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kCandEPT; ++j)
+    if (key[j] == kth) {
+      const int slot = atomicAdd(&sh.cnt, 1);
+      if (slot < kCandSlots) {
+        rec->val[slot] = y[j];
+        rec->idx[slot] = base + 8 * (t + kCandThreads * (j / 8)) + j % 8;
+      }
+    }
+  __syncthreads();
+  if (t == 0) {
+    rec->count = sh.cnt < kCandSlots ? sh.cnt : kCandSlots;
+    rec->truncated = sh.cnt > kCandSlots;
+    rec->kth_key = kth;
+  }
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Wave 0 of a row's sample_kernel workgroup: the row's result from its
+// chunks' candidates when they decide it exactly (returns false otherwise,
+// writing nothing). Lane l reads slot l of every chunk.
+__device__ __forceinline__ bool candidates_pick(const CandRecord *rec, int P, int k, int apply_top_p, float top_p,
+                                                u64 seed, u64 offset, int row, int64_t *tokens, float *token_logprob,
+                                                SampleShared &sh) {
+  const int lane = threadIdx.x;  // P <= kMaxSampleVocabBF16 / kCandChunk = 8 chunks
+  rec += (int64_t)row * P;
+  constexpr int kMaxChunks = kMaxSampleVocabBF16 / kCandChunk;
+  uint32_t key[kMaxChunks];
+  float val[kMaxChunks];
+  int idx[kMaxChunks];
+  int nvalid = 0;
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    key[c] = 0u;
+    val[c] = -INFINITY;
+    idx[c] = INT_MAX;
+    if (c < P && lane < rec[c].count) {
+      val[c] = rec[c].val[lane];
+      idx[c] = rec[c].idx[lane];
+      key[c] = order_key(val[c]);
+      ++nvalid;
+    }
+  }
+  if (wave_sum_i32(nvalid) < k) return false;
+  // the row's k-th largest key: the largest thr with #(key >= thr) >= k
+  uint32_t thr = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t trial = thr | (1u << bit);
+    int n = 0;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) n += key[c] >= trial;
+    if (wave_sum_i32(n) >= k) thr = trial;
+  }
+  if (thr <= order_key(-INFINITY)) return false;  // fewer than k finite logits
+  for (int c = 0; c < P; ++c)
+    if (rec[c].truncated && rec[c].kth_key == thr) return false;  // kept ties beyond the chunk's slots
+  int nk = 0;
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) nk += key[c] >= thr;
+  int incl = nk;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  const int total = __shfl(incl, 63, 64);
+  if (total > 64) return false;
+
+  // compact the kept candidates to one per lane: (key desc, index asc) as one
+  // 64-bit sort key, and the value
+  u64 *ck = sh.hrep;
+  u64 *cv = sh.hrep + 64;
+  int pos = incl - nk;
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c)
+    if (key[c] >= thr) {
+      ck[pos] = ((u64)key[c] << 32) | (u64)(0xFFFFFFFFu - (uint32_t)idx[c]);
+      cv[pos] = (u64)__float_as_uint(val[c]);
+      ++pos;
+    }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  u64 sk = lane < total ? ck[lane] : 0ull;
+  float v = lane < total ? __uint_as_float((uint32_t)cv[lane]) : -INFINITY;
+  // bitonic sort across the 64 lanes, descending
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      const u64 ok = __shfl_xor(sk, j, 64);
+      const float ov = __shfl_xor(v, j, 64);
+      const bool take_max = ((lane & size) == 0) == ((lane & j) == 0);
+      if (take_max ? ok > sk : ok < sk) {
+        sk = ok;
+        v = ov;
+      }
+    }
+  const bool in = lane < total;
+  const int my_idx = (int)(0xFFFFFFFFu - (uint32_t)sk);
+  const float m = __shfl(v, 0, 64);
+  const u64 mass = in ? mass_of(v, m) : 0ull;
+  bool keep = in;
+  if (apply_top_p) {  // sorted order: keep while the cumulative mass stays <= T; the first always
+    const u64 etot = wave_sum_u64(mass);
+    const u64 T = (u64)((double)top_p * (double)etot);
+    u64 cum = mass;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const u64 o = __shfl_up(cum, off, 64);
+      if (lane >= off) cum += o;
+    }
+    keep = in && (cum <= T || lane == 0);
+  }
+  float z = keep ? expf(v - m) : 0.f;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off, 64);
+  const float logz = logf(z);
+  // inverse CDF in index order over the kept masses
+  const u64 w = keep ? mass : 0ull;
+  const u64 wtot = wave_sum_u64(w);
+  const u64 target = __umul64hi(draw_u64(seed, offset, (u64)row), wtot);
+  u64 below = 0;  // kept mass at indices <= this lane's
+#pragma unroll 1
+  for (int j = 0; j < 64; ++j) {
+    const int oj = __shfl(my_idx, j, 64);
+    const u64 wj = __shfl(w, j, 64);
+    if (oj <= my_idx) below += wj;
+  }
+  int cand = keep && w > 0 && below > target ? my_idx : INT_MAX;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int o = __shfl_xor(cand, off, 64);
+    cand = o < cand ? o : cand;
+  }
+  if (my_idx == cand && keep) {
+    tokens[row] = cand;
+    if (token_logprob) token_logprob[row] = (v - m) - logz;
+  }
+  return true;
+}
+
 template <int EPT, bool kF32>
 __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a) {
   __shared__ SampleShared sh;
   constexpr int G = EPT / 8;
   const int row = blockIdx.x;
+  if (a.cand != nullptr) {
+    if (threadIdx.x < 64) {
+      const bool done = candidates_pick(static_cast<const CandRecord *>(a.cand), a.cand_chunks, a.top_k,
+                                        a.apply_top_p, a.top_p, a.seed, a.offset, row, a.tokens, a.token_logprob, sh);
+      if (threadIdx.x == 0) sh.iv[0] = done;
+    }
+    __syncthreads();
+    const bool done = sh.iv[0] != 0;
+    __syncthreads();
+    if (done) return;
+  }
   Row<EPT, kF32> r;
   load_row<EPT, kF32>(a, row, r);
   const RowMax mx = row_max<EPT, kF32>(a, r, sh);
@@ -604,15 +901,27 @@ __global__ __launch_bounds__(kThreads) void greedy_kernel(SampleArgs a) {
 }
 
 template <int EPT, bool kF32>
-hipError_t launch_ept(const SampleArgs &a, hipStream_t s) {
-  if (a.top_k == 1 && a.logprobs == nullptr)
+hipError_t launch_ept(SampleArgs a, hipStream_t s) {
+  if (a.top_k == 1 && a.logprobs == nullptr) {
     hipLaunchKernelGGL((greedy_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((sample_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+  }
+  if (a.cand != nullptr && a.cand_chunks == sample_cand_chunks(a.V, a.top_k, a.logprobs != nullptr) &&
+      a.cand_chunks > 0) {
+    hipLaunchKernelGGL((topk_candidates_kernel<kF32>), dim3(a.cand_chunks, a.M), dim3(kCandThreads), 0, s, a);
+  } else {
+    a.cand = nullptr;
+  }
+  hipLaunchKernelGGL((sample_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
 }  // namespace
+
+int sample_cand_chunks(int64_t vocab, int64_t top_k, bool logprobs_rows) {
+  if (logprobs_rows || top_k < 2 || top_k > kCandSlots || vocab <= kCandChunk) return 0;
+  return (int)((vocab + kCandChunk - 1) / kCandChunk);
+}
 
 // Rows up to 65536 (bf16) / 32768 (fp32) values: fp32 rows of 64 values per
 // thread would not fit in the registers of a 1024-thread workgroup.

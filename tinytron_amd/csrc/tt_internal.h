@@ -172,11 +172,33 @@ struct SampleArgs {
   float *logprobs;      // [M, ld_lp] log-probabilities of the filtered logits, or null
   int64_t ld_lp;
   int vec_out;
+  // Candidate path (top_k in [2, kCandSlots], no log-probability rows, V >
+  // kCandChunk): workspace of M x cand_chunks CandRecords, or null.
+  void *cand;
+  int cand_chunks;
 };
 
 constexpr int kMaxSampleVocabBF16 = 65536;
 constexpr int kMaxSampleVocabF32 = 32768;
+constexpr int kCandChunk = 8192;  // logits per candidate workgroup
+constexpr int kCandSlots = 64;    // candidates one chunk keeps (the largest top_k of the path)
+
+// One chunk's candidates: its values >= its own k-th largest (all of those
+// strictly above it, then ties in any order up to the slots; truncated when
+// ties did not fit), the k-th largest's order key, and the values (after the
+// temperature) with their row indices.
+struct CandRecord {
+  int count;
+  int truncated;
+  uint32_t kth_key;
+  int pad;
+  float val[kCandSlots];
+  int32_t idx[kCandSlots];
+};
+
 hipError_t launch_sample(const SampleArgs &a, bool f32, hipStream_t stream);
+// chunks of the candidate path for this call (0: the whole-row path runs alone)
+int sample_cand_chunks(int64_t vocab, int64_t top_k, bool logprobs_rows);
 
 // Partition helpers shared by the ABI layer and the launchers.
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);

@@ -591,9 +591,13 @@ def prefill_attention(q: torch.Tensor, layout: KVLayout, positions: torch.Tensor
 SAMPLE_MAX_VOCAB = {torch.bfloat16: 65536, torch.float32: 32768}
 
 
+_SAMPLE_WS = {}  # (device index, stream) -> Workspace of the sampler's candidate path
+
+
 def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
                   top_p: float | None = None, seed: int = 0, offset: int = 0, return_logprob: bool = False,
-                  return_logprobs: bool = False, out: torch.Tensor | None = None):
+                  return_logprobs: bool = False, out: torch.Tensor | None = None,
+                  workspace: Workspace | None = None):
     """One token per row of ``logits`` [M, V] (bf16 or fp32, last dim contiguous).
 
     filter_logits + sample_next_token / sample_next_token_with_log_prob
@@ -602,7 +606,10 @@ def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, top_k: int | N
     draw from softmax(filtered) keyed by (seed, offset, row). Returns tokens
     int64 [M]; with ``return_logprob`` also the chosen tokens' log-probabilities
     [M]; with ``return_logprobs`` also log_softmax of the filtered logits
-    [M, V] (-inf where filtered)."""
+    [M, V] (-inf where filtered). With 2 <= top_k <= 64 over more than 8192
+    logits, each 8192-logit chunk of a row is reduced to its top-k candidates
+    by a workgroup of its own first (``workspace``, by default one per device
+    and stream)."""
     _require_cuda(logits)
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("logits must be a 2-D view [M, V] with a contiguous last dimension")
@@ -616,10 +623,18 @@ def sample_tokens(logits: torch.Tensor, temperature: float = 1.0, top_k: int | N
         raise ValueError("out must be a contiguous int64 [M] tensor")
     lp = torch.empty(M, dtype=torch.float32, device=dev) if return_logprob else None
     full = torch.empty(M, V, dtype=torch.float32, device=dev) if return_logprobs else None
-    fn = _lib.load().tt_sample_bf16 if logits.dtype == torch.bfloat16 else _lib.load().tt_sample_f32
+    lib = _lib.load()
+    stream = _stream(dev)
+    need = 0 if return_logprobs else int(lib.tt_sample_workspace_bytes(M, V, int(top_k or 0)))
+    ws = None
+    if need:
+        if workspace is None:
+            workspace = _SAMPLE_WS.setdefault((dev.index, stream), Workspace(dev))
+        ws = workspace.get(need)
+    fn = lib.tt_sample_bf16 if logits.dtype == torch.bfloat16 else lib.tt_sample_f32
     st = fn(_ptr(logits), logits.stride(0), M, V, float(temperature), int(top_k or 0),
             1.0 if top_p is None else float(top_p), int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 64 - 1),
-            _ptr(out), _ptr(lp), _ptr(full), V, _stream(dev))
+            _ptr(out), _ptr(lp), _ptr(full), V, _ptr(ws), 0 if ws is None else ws.numel(), stream)
     _lib.check(st, "sample_tokens")
     res = (out,)
     if return_logprob:
