@@ -461,9 +461,9 @@ constexpr int kCandThreads = 256;
 constexpr int kCandEPT = kCandChunk / kCandThreads;  // 32 logits per thread, 8-logit groups
 
 struct CandShared {
-  uint32_t hrep[256 * kRep];  // [bin][replica]
+  uint32_t hrep[2][256 * kRep];  // [pass parity][bin][replica]
   uint32_t hist[256];
-  uint32_t bc[2];
+  uint32_t bc[3];
   int cnt;
 };
 
@@ -517,23 +517,31 @@ __global__ __launch_bounds__(kCandThreads) void topk_candidates_kernel(SampleArg
   }
 
   const int nvalid = a.V - base < kCandChunk ? a.V - base : kCandChunk;
+  // kth: the chunk's k-th largest key, or (early) a lower bound of it below
+  // which at most kCandSlots keys lie at or above; the candidates are then all
+  // keys >= it. The select stops after a digit once the keys at or above its
+  // bin fit in the slots (with logit rows this is usually after 16 bits).
   uint32_t kth = 1;  // below every real key: all of a chunk with at most k logits are candidates
+  bool all_fit = true;
   if (nvalid > a.top_k) {
-    uint32_t prefix = 0, mask = 0, need = (uint32_t)a.top_k;
+    uint32_t prefix = 0, mask = 0, need = (uint32_t)a.top_k, above = 0;
     const uint32_t rep = t & (kRep - 1);
+    for (int i = t; i < 256 * kRep; i += kCandThreads) sh.hrep[0][i] = 0;
+    __syncthreads();
 #pragma unroll 1
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = t; i < 256 * kRep; i += kCandThreads) sh.hrep[i] = 0;
-      __syncthreads();
+    for (int shift = 24, pass = 0; shift >= 0; shift -= 8, ++pass) {
+      uint32_t *hr = sh.hrep[pass & 1];
 #pragma unroll
       for (int j = 0; j < kCandEPT; ++j)
-        if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&sh.hrep[((key[j] >> shift) & 255u) * kRep + rep], 1u);
+        if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&hr[((key[j] >> shift) & 255u) * kRep + rep], 1u);
       __syncthreads();
       {
         uint32_t h = 0;
 #pragma unroll
-        for (int j = 0; j < kRep; ++j) h += sh.hrep[t * kRep + ((j + t) & (kRep - 1))];
+        for (int j = 0; j < kRep; ++j) h += hr[t * kRep + ((j + t) & (kRep - 1))];
         sh.hist[t] = h;
+        uint32_t *nx = sh.hrep[(pass + 1) & 1];  // the next pass's histogram, unused since the last barrier
+        for (int i = t; i < 256 * kRep; i += kCandThreads) nx[i] = 0;
       }
       __syncthreads();
       if (t < 64) {  // the largest digit whose suffix count reaches need
@@ -557,6 +565,7 @@ __global__ __launch_bounds__(kCandThreads) void topk_candidates_kernel(SampleArg
             if (cum + h[j] >= need) {
               sh.bc[0] = 255u - 4u * t - j;
               sh.bc[1] = cum;
+              sh.bc[2] = h[j];
               break;
             }
             cum += h[j];
@@ -565,32 +574,44 @@ __global__ __launch_bounds__(kCandThreads) void topk_candidates_kernel(SampleArg
       }
       __syncthreads();
       need -= sh.bc[1];
+      above += sh.bc[1];
       prefix |= sh.bc[0] << shift;
       mask |= 0xFFu << shift;
-      __syncthreads();
+      if (above + sh.bc[2] <= (uint32_t)kCandSlots) break;  // every key >= prefix fits: uniform exit
+      if (shift == 0) all_fit = false;
     }
     kth = prefix;
   }
 
   if (t == 0) sh.cnt = 0;
   __syncthreads();
+  if (all_fit) {  // every real key >= kth, at most kCandSlots of them
 #pragma unroll
-  for (int j = 0; j < kCandEPT; ++j)
-    if (key[j] > kth) {  // fewer than k <= kCandSlots of these
-      const int slot = atomicAdd(&sh.cnt, 1);
-      rec->val[slot] = y[j];
-      rec->idx[slot] = base + 8 * (t + kCandThreads * (j / 8)) + j % 8;
-    }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kCandEPT; ++j)
-    if (key[j] == kth) {
-      const int slot = atomicAdd(&sh.cnt, 1);
-      if (slot < kCandSlots) {
+    for (int j = 0; j < kCandEPT; ++j)
+      if (key[j] != 0u && key[j] >= kth) {
+        const int slot = atomicAdd(&sh.cnt, 1);
         rec->val[slot] = y[j];
         rec->idx[slot] = base + 8 * (t + kCandThreads * (j / 8)) + j % 8;
       }
-    }
+  } else {  // kth is the k-th largest key: the keys above it (fewer than k), then its ties while slots remain
+#pragma unroll
+    for (int j = 0; j < kCandEPT; ++j)
+      if (key[j] > kth) {
+        const int slot = atomicAdd(&sh.cnt, 1);
+        rec->val[slot] = y[j];
+        rec->idx[slot] = base + 8 * (t + kCandThreads * (j / 8)) + j % 8;
+      }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kCandEPT; ++j)
+      if (key[j] == kth) {
+        const int slot = atomicAdd(&sh.cnt, 1);
+        if (slot < kCandSlots) {
+          rec->val[slot] = y[j];
+          rec->idx[slot] = base + 8 * (t + kCandThreads * (j / 8)) + j % 8;
+        }
+      }
+  }
   __syncthreads();
   if (t == 0) {
     rec->count = sh.cnt < kCandSlots ? sh.cnt : kCandSlots;
@@ -599,38 +620,51 @@ __global__ __launch_bounds__(kCandThreads) void topk_candidates_kernel(SampleArg
   }
 }
 
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 // Wave 0 of a row's sample_kernel workgroup: the row's result from its
 // chunks' candidates when they decide it exactly (returns false otherwise,
-// writing nothing). Lane l reads slot l of every chunk.
+// writing nothing). Lane l reads slot l of every chunk. Counting and ranking
+// go through ballots and lane reads (scalar), not LDS shuffles: every step
+// here is a short dependent chain.
+__device__ __forceinline__ u64 lane_u64(u64 v, int j) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, j);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), j);
+  return ((u64)hi << 32) | lo;
+}
+
 __device__ __forceinline__ bool candidates_pick(const CandRecord *rec, int P, int k, int apply_top_p, float top_p,
                                                 u64 seed, u64 offset, int row, int64_t *tokens, float *token_logprob,
                                                 SampleShared &sh) {
   const int lane = threadIdx.x;  // P <= kMaxSampleVocabBF16 / kCandChunk = 8 chunks
   rec += (int64_t)row * P;
   constexpr int kMaxChunks = kMaxSampleVocabBF16 / kCandChunk;
-  uint32_t key[kMaxChunks];
+  // every record's header and slot are loaded at once (chunks past P re-read
+  // chunk 0; slots past a count hold stale data and are masked below): one
+  // memory round trip
+  int cnt[kMaxChunks], trunc[kMaxChunks];
+  uint32_t kthk[kMaxChunks], key[kMaxChunks];
   float val[kMaxChunks];
   int idx[kMaxChunks];
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    const CandRecord &rc = rec[c < P ? c : 0];
+    cnt[c] = rc.count;
+    trunc[c] = rc.truncated;
+    kthk[c] = rc.kth_key;
+    val[c] = rc.val[lane];
+    idx[c] = rc.idx[lane];
+  }
   int nvalid = 0;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
-    key[c] = 0u;
-    val[c] = -INFINITY;
-    idx[c] = INT_MAX;
-    if (c < P && lane < rec[c].count) {
-      val[c] = rec[c].val[lane];
-      idx[c] = rec[c].idx[lane];
-      key[c] = order_key(val[c]);
-      ++nvalid;
+    const bool valid = c < P && lane < cnt[c];
+    key[c] = valid ? order_key(val[c]) : 0u;
+    if (!valid) {
+      val[c] = -INFINITY;
+      idx[c] = INT_MAX;
     }
+    nvalid += __popcll(__ballot(valid));
   }
-  if (wave_sum_i32(nvalid) < k) return false;
+  if (nvalid < k) return false;
   // the row's k-th largest key: the largest thr with #(key >= thr) >= k
   uint32_t thr = 0;
 #pragma unroll 1
@@ -638,84 +672,82 @@ __device__ __forceinline__ bool candidates_pick(const CandRecord *rec, int P, in
     const uint32_t trial = thr | (1u << bit);
     int n = 0;
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) n += key[c] >= trial;
-    if (wave_sum_i32(n) >= k) thr = trial;
+    for (int c = 0; c < kMaxChunks; ++c) n += __popcll(__ballot(key[c] >= trial));
+    if (n >= k) thr = trial;
   }
   if (thr <= order_key(-INFINITY)) return false;  // fewer than k finite logits
-  for (int c = 0; c < P; ++c)
-    if (rec[c].truncated && rec[c].kth_key == thr) return false;  // kept ties beyond the chunk's slots
-  int nk = 0;
+  bool tied_out = false;  // kept ties beyond a chunk's slots
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) nk += key[c] >= thr;
-  int incl = nk;
+  for (int c = 0; c < kMaxChunks; ++c) tied_out |= c < P && trunc[c] && kthk[c] == thr;
+  if (tied_out) return false;
+  u64 kmask[kMaxChunks];
+  int total = 0;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
+  for (int c = 0; c < kMaxChunks; ++c) {
+    kmask[c] = __ballot(key[c] >= thr);
+    total += __popcll(kmask[c]);
   }
-  const int total = __shfl(incl, 63, 64);
   if (total > 64) return false;
 
   // compact the kept candidates to one per lane: (key desc, index asc) as one
   // 64-bit sort key, and the value
   u64 *ck = sh.hrep;
   u64 *cv = sh.hrep + 64;
-  int pos = incl - nk;
+  const u64 below_lane = (1ull << lane) - 1ull;
+  int base = 0;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c)
+  for (int c = 0; c < kMaxChunks; ++c) {
     if (key[c] >= thr) {
+      const int pos = base + __popcll(kmask[c] & below_lane);
       ck[pos] = ((u64)key[c] << 32) | (u64)(0xFFFFFFFFu - (uint32_t)idx[c]);
       cv[pos] = (u64)__float_as_uint(val[c]);
-      ++pos;
     }
+    base += __popcll(kmask[c]);
+  }
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  u64 sk = lane < total ? ck[lane] : 0ull;
-  float v = lane < total ? __uint_as_float((uint32_t)cv[lane]) : -INFINITY;
-  // bitonic sort across the 64 lanes, descending
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-    for (int j = size >> 1; j > 0; j >>= 1) {
-      const u64 ok = __shfl_xor(sk, j, 64);
-      const float ov = __shfl_xor(v, j, 64);
-      const bool take_max = ((lane & size) == 0) == ((lane & j) == 0);
-      if (take_max ? ok > sk : ok < sk) {
-        sk = ok;
-        v = ov;
-      }
-    }
   const bool in = lane < total;
-  const int my_idx = (int)(0xFFFFFFFFu - (uint32_t)sk);
-  const float m = __shfl(v, 0, 64);
+  const u64 sk = in ? ck[lane] : 0ull;
+  const float v = in ? __uint_as_float((uint32_t)cv[lane]) : -INFINITY;
+  const int my_idx = in ? (int)(0xFFFFFFFFu - (uint32_t)sk) : INT_MAX;
+  // rank in (value desc, index asc) order
+  int rank = 0;
+#pragma unroll 1
+  for (int j = 0; j < total; ++j) rank += lane_u64(sk, j) > sk;
+  const int top = __builtin_ctzll(__ballot(in && rank == 0));
+  const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), top));
   const u64 mass = in ? mass_of(v, m) : 0ull;
   bool keep = in;
-  if (apply_top_p) {  // sorted order: keep while the cumulative mass stays <= T; the first always
-    const u64 etot = wave_sum_u64(mass);
-    const u64 T = (u64)((double)top_p * (double)etot);
-    u64 cum = mass;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const u64 o = __shfl_up(cum, off, 64);
-      if (lane >= off) cum += o;
+  if (apply_top_p) {  // in rank order: keep while the cumulative mass stays <= T; the first always
+    u64 etot = 0, cum = 0;
+#pragma unroll 1
+    for (int j = 0; j < total; ++j) {
+      const u64 mj = lane_u64(mass, j);
+      etot += mj;
+      if (__builtin_amdgcn_readlane(rank, j) <= rank) cum += mj;
     }
-    keep = in && (cum <= T || lane == 0);
+    const u64 T = (u64)((double)top_p * (double)etot);
+    keep = in && (cum <= T || rank == 0);
   }
-  float z = keep ? expf(v - m) : 0.f;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off, 64);
+  // log Z in rank order (a fixed order: the slots' order within a chunk is not)
+  const float e = keep ? expf(v - m) : 0.f;
+  float z = 0.f;
+#pragma unroll 1
+  for (int r = 0; r < total; ++r) {
+    const int l = __builtin_ctzll(__ballot(in && rank == r));
+    z += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, e), l));
+  }
   const float logz = logf(z);
   // inverse CDF in index order over the kept masses
   const u64 w = keep ? mass : 0ull;
-  const u64 wtot = wave_sum_u64(w);
-  const u64 target = __umul64hi(draw_u64(seed, offset, (u64)row), wtot);
-  u64 below = 0;  // kept mass at indices <= this lane's
+  u64 wtot = 0, below = 0;  // below: kept mass at indices <= this lane's
 #pragma unroll 1
-  for (int j = 0; j < 64; ++j) {
-    const int oj = __shfl(my_idx, j, 64);
-    const u64 wj = __shfl(w, j, 64);
-    if (oj <= my_idx) below += wj;
+  for (int j = 0; j < total; ++j) {
+    const u64 wj = lane_u64(w, j);
+    wtot += wj;
+    if (__builtin_amdgcn_readlane(my_idx, j) <= my_idx) below += wj;
   }
+  const u64 target = __umul64hi(draw_u64(seed, offset, (u64)row), wtot);
   int cand = keep && w > 0 && below > target ? my_idx : INT_MAX;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
