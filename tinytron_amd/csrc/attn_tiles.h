@@ -238,31 +238,83 @@ __device__ __forceinline__ void qk_softmax(float scale_log2, int t0, int lim, in
 }
 
 
+// A tile's V for the PV product, read from its LDS slot (the two 16-token
+// blocks' fragments at slot + (tt * NU + u) * 1024 + lane * 16, as
+// load_v_block_lds lays them out). fp8 keeps the raw fragments, transposed on
+// the matrix cores inside pv_tile. bf16 reads each 16-column block already
+// transposed with ds_read_b64_tr_b16: in every group of 16 lanes, lane i
+// receives element i % 4 of the 8-byte rows that lanes 4j + i / 4 address,
+// j = 0..3, as its elements j (lane layout measured on gfx950). Lane s =
+// 4j + q of group g addresses token 4g + j, columns 16c + 4q .. + 3, so lane
+// (n + 16g) gets V[16h + 4g + j][16c + n] for j < 4 -- h = 0 its elements
+// 0-3, h = 1 its elements 4-7 -- the PV MFMA's B operand in the token order
+// of the P operand (the same values the selection MFMA produced, with no
+// MFMA and no conversion).
 template <int D, bool kFP8>
-__device__ __forceinline__ void pv_tile(const u32x4 (&vt)[2][Tile<D, kFP8>::NU], const bf16x8 (&ident16)[2],
-                                        const u32x2 (&ident8)[2], bf16x8 pa_hi, bf16x8 pa_lo, WaveState<D, kFP8> &st) {
+struct VRegs;
+template <int D>
+struct VRegs<D, true> {
+  u32x4 vt[2][Tile<D, true>::NU];
+};
+template <int D>
+struct VRegs<D, false> {
+  bf16x8 vb[D / 16];
+};
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void read_v(const char *vlds, int lane, VRegs<D, kFP8> &v) {
+  constexpr int NU = Tile<D, kFP8>::NU;
+  if constexpr (kFP8) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int u = 0; u < NU; ++u) v.vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+  } else {
+    typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
+    const int row = 4 * (lane >> 4) + ((lane >> 2) & 3);  // token 4g + j of each 16-token block
+    const int q = lane & 3;                                  // columns 4q .. 4q + 3 of the 16-column block
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      bf16x4v part[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int byte = (h * NU + (c >> 1)) * 1024 + (row + 16 * (2 * (c & 1) + (q >> 1))) * 16 + 8 * (q & 1);
+        part[h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (__attribute__((address_space(3))) bf16x4v *)(vlds + byte));
+      }
+      v.vb[c] = bf16x8{part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
+    }
+  }
+}
+
+// V^T of block c (16 output columns o_col_d(c, n)): lane (n + 16g) holds
+// V[token t0 + 4g + r][col] (elements r < 4) and V[t0 + 16 + 4g + r][col]
+// (elements 4 + r), as bf16.
+template <int D, bool kFP8>
+__device__ __forceinline__ bf16x8 v_block(const VRegs<D, kFP8> &v, int c, const u32x2 (&ident8)[2]) {
+  if constexpr (kFP8) {
+    // block c = 4u + 2hh + hi (column order in o_col_d): the fp8 fragments
+    // transposed by an exact 0/1 selection MFMA
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const int hi = c & 1, u = c >> 2, hh = (c >> 1) & 1;
+    const u32x2 v0 = hh ? u32x2{v.vt[0][u][2], v.vt[0][u][3]} : u32x2{v.vt[0][u][0], v.vt[0][u][1]};
+    const u32x2 v1 = hh ? u32x2{v.vt[1][u][2], v.vt[1][u][3]} : u32x2{v.vt[1][u][0], v.vt[1][u][1]};
+    const f32x4 t0v = mfma_fp8(v0, ident8[hi], zero);
+    const f32x4 t1v = mfma_fp8(v1, ident8[hi], zero);
+    const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
+    return __builtin_convertvector(vv, bf16x8);
+  } else {
+    return v.vb[c];
+  }
+}
+
+template <int D, bool kFP8>
+__device__ __forceinline__ void pv_tile(const VRegs<D, kFP8> &v, const u32x2 (&ident8)[2], bf16x8 pa_hi,
+                                        bf16x8 pa_lo, WaveState<D, kFP8> &st) {
   constexpr int NDB = D / 32;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) {
-    // block c: bf16 c = 2u + hi; fp8 c = 4u + 2hh + hi (column order in o_col_d)
-    const int hi = c & 1;
-    f32x4 t0v, t1v;
-    if constexpr (kFP8) {
-      const int u = c >> 2;
-      const int hh = (c >> 1) & 1;
-      const u32x2 v0 = hh ? u32x2{vt[0][u][2], vt[0][u][3]} : u32x2{vt[0][u][0], vt[0][u][1]};
-      const u32x2 v1 = hh ? u32x2{vt[1][u][2], vt[1][u][3]} : u32x2{vt[1][u][0], vt[1][u][1]};
-      t0v = mfma_fp8(v0, ident8[hi], zero);
-      t1v = mfma_fp8(v1, ident8[hi], zero);
-    } else {
-      const int u = c >> 1;
-      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[0][u]), ident16[hi], zero);
-      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[1][u]), ident16[hi], zero);
-    }
-    // lane (n + 16g): V[token t0 + 4g + r][o_col_d(c, n)] (t0v), same for t0 + 16 (t1v)
-    const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
-    const bf16x8 vb = __builtin_convertvector(vv, bf16x8);
+    const bf16x8 vb = v_block<D, kFP8>(v, c, ident8);
     st.o[c] = mfma_bf16(pa_hi, vb, st.o[c]);
     st.o[c] = mfma_bf16(pa_lo, vb, st.o[c]);
   }

@@ -162,12 +162,8 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
       __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    u32x4 vt[2][NU];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int u = 0; u < NU; ++u)
-        vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+    VRegs<D, kFP8> vr;
+    read_v<D, kFP8>(vlds, lane, vr);
     // the slots are overwritten only after every lane's read has returned
     __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
     __builtin_amdgcn_sched_barrier(0);
@@ -176,7 +172,7 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
       load_v_block_lds<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, vlds + NU * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
-    pv_tile<D, kFP8>(vt, ident16, ident8, pa_hi, pa_lo, st);
+    pv_tile<D, kFP8>(vr, ident8, pa_hi, pa_lo, st);
   }
   __builtin_amdgcn_s_waitcnt(0);  // no LDS load of this wave is still in flight past the item
 
@@ -691,12 +687,8 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
       else
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-      u32x4 vt[2][NU];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-          vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+      VRegs<D, kFP8> vr;
+      read_v<D, kFP8>(vlds, lane, vr);
       // the slots are overwritten only after every lane's read has returned
       __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
       __builtin_amdgcn_sched_barrier(0);
@@ -705,7 +697,7 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
         load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
-      pv_tile<D, kFP8>(vt, ident16, ident8, pa_hi, pa_lo, st);
+      pv_tile<D, kFP8>(vr, ident8, pa_hi, pa_lo, st);
     }
     __builtin_amdgcn_s_waitcnt(0);  // nothing of this chunk still in flight
   }

@@ -97,32 +97,16 @@ __device__ __forceinline__ void qk_softmax_pf(float scale_log2, const f32x4 (&kc
   pa_lo = __builtin_convertvector(pv - __builtin_convertvector(pa_hi, f32x8), bf16x8);  // P - P_hi exact in fp32
 }
 
-// PV of one tile for NB column blocks: V is transposed once (identity MFMA)
-// and multiplied by each block's P_hi + P_lo.
+// PV of one tile for NB column blocks: each V^T block (see read_v) is
+// multiplied by every block's P_hi + P_lo.
 template <int D, bool kFP8, int NB>
-__device__ __forceinline__ void pv_tile_nb(const u32x4 (&vt)[2][Tile<D, kFP8>::NU], const bf16x8 (&ident16)[2],
-                                           const u32x2 (&ident8)[2], const bf16x8 (&pa_hi)[NB],
-                                           const bf16x8 (&pa_lo)[NB], WaveState<D, kFP8> (&st)[NB]) {
+__device__ __forceinline__ void pv_tile_nb(const VRegs<D, kFP8> &v, const u32x2 (&ident8)[2],
+                                           const bf16x8 (&pa_hi)[NB], const bf16x8 (&pa_lo)[NB],
+                                           WaveState<D, kFP8> (&st)[NB]) {
   constexpr int NDB = D / 32;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) {
-    const int hi = c & 1;
-    f32x4 t0v, t1v;
-    if constexpr (kFP8) {
-      const int u = c >> 2;
-      const int hh = (c >> 1) & 1;
-      const u32x2 v0 = hh ? u32x2{vt[0][u][2], vt[0][u][3]} : u32x2{vt[0][u][0], vt[0][u][1]};
-      const u32x2 v1 = hh ? u32x2{vt[1][u][2], vt[1][u][3]} : u32x2{vt[1][u][0], vt[1][u][1]};
-      t0v = mfma_fp8(v0, ident8[hi], zero);
-      t1v = mfma_fp8(v1, ident8[hi], zero);
-    } else {
-      const int u = c >> 1;
-      t0v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[0][u]), ident16[hi], zero);
-      t1v = mfma_bf16(__builtin_bit_cast(bf16x8, vt[1][u]), ident16[hi], zero);
-    }
-    const f32x8 vv = {t0v[0], t0v[1], t0v[2], t0v[3], t1v[0], t1v[1], t1v[2], t1v[3]};
-    const bf16x8 vb = __builtin_convertvector(vv, bf16x8);
+    const bf16x8 vb = v_block<D, kFP8>(v, c, ident8);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       st[j].o[c] = mfma_bf16(pa_hi[j], vb, st[j].o[c]);
@@ -254,12 +238,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
       else
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-      u32x4 vt[2][NU];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-          vt[tt][u] = *reinterpret_cast<const u32x4 *>(vlds + (tt * NU + u) * 1024 + lane * 16);
+      VRegs<D, kFP8> vr;
+      read_v<D, kFP8>(vlds, lane, vr);
       __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
       __builtin_amdgcn_sched_barrier(0);
       if (k + 1 < kPrefillChunkTiles && it + 1 < c1) {
@@ -276,7 +256,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
 #pragma unroll
           for (int c = 0; c < 2 * NDB; ++c) st[j].o[c][r] *= ar;
         }
-      pv_tile_nb<D, kFP8, NB>(vt, ident16, ident8, pa_hi, pa_lo, st);
+      pv_tile_nb<D, kFP8, NB>(vr, ident8, pa_hi, pa_lo, st);
     }
     __builtin_amdgcn_s_waitcnt(0);
   }
