@@ -145,7 +145,11 @@ __device__ __forceinline__ void load_v_block_lds(const DecodeArgs &a, int64_t el
   constexpr int NU = Tile<D, kFP8>::NU;
   const auto rv = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
-  const int off = (lane & 15) * D * E + 16 * (lane >> 4);
+  // bf16 slots are swizzled for read_v's transposing reads: slot m + 16 g
+  // holds token m ^ (8 (g & 1)) (chunk g), so that the two 8-column chunks
+  // that one read takes from each of 8 tokens fill all 64 banks once
+  const int tok = kFP8 ? (lane & 15) : ((lane & 15) ^ (8 * ((lane >> 4) & 1)));
+  const int off = tok * D * E + 16 * (lane >> 4);
 #pragma unroll
   for (int u = 0; u < NU; ++u)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(lds + 1024 * u), 16,
@@ -273,12 +277,13 @@ __device__ __forceinline__ void read_v(const char *vlds, int lane, VRegs<D, kFP8
     typedef __bf16 bf16x4v __attribute__((ext_vector_type(4)));
     const int row = 4 * (lane >> 4) + ((lane >> 2) & 3);  // token 4g + j of each 16-token block
     const int q = lane & 3;                                  // columns 4q .. 4q + 3 of the 16-column block
+    const int slot = row ^ (8 * (q >> 1));                   // the swizzled slot of load_v_block_lds
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       bf16x4v part[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int byte = (h * NU + (c >> 1)) * 1024 + (row + 16 * (2 * (c & 1) + (q >> 1))) * 16 + 8 * (q & 1);
+        const int byte = (h * NU + (c >> 1)) * 1024 + (slot + 16 * (2 * (c & 1) + (q >> 1))) * 16 + 8 * (q & 1);
         part[h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
             (__attribute__((address_space(3))) bf16x4v *)(vlds + byte));
       }
