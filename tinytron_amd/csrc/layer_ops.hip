@@ -166,8 +166,8 @@ __global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *P, int S,
   f32x4 sum[1];
   ordered_sums<1>(P, S, MN, ix, sum);
   const f32x4 acc = sum[0];
-  uint32_t lo = f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16);
-  uint32_t hi = f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16);
+  uint32_t lo = pack_bf16x2(acc[0], acc[1]);
+  uint32_t hi = pack_bf16x2(acc[2], acc[3]);
   *reinterpret_cast<uint2 *>(y + i) = make_uint2(lo, hi);
 }
 
@@ -225,8 +225,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
     const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
-    uint32_t lo = f32_to_bf16_bits(wv[0] * (v[j][0] * r)) | ((uint32_t)f32_to_bf16_bits(wv[1] * (v[j][1] * r)) << 16);
-    uint32_t hi = f32_to_bf16_bits(wv[2] * (v[j][2] * r)) | ((uint32_t)f32_to_bf16_bits(wv[3] * (v[j][3] * r)) << 16);
+    uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
+    uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
     *reinterpret_cast<uint2 *>(y + row + c) = make_uint2(lo, hi);
   }
 }
@@ -291,8 +291,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
     const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
-    uint32_t lo = f32_to_bf16_bits(wv[0] * (v[j][0] * r)) | ((uint32_t)f32_to_bf16_bits(wv[1] * (v[j][1] * r)) << 16);
-    uint32_t hi = f32_to_bf16_bits(wv[2] * (v[j][2] * r)) | ((uint32_t)f32_to_bf16_bits(wv[3] * (v[j][3] * r)) << 16);
+    uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
+    uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
     *reinterpret_cast<uint2 *>(y + row + c) = make_uint2(lo, hi);
   }
 }

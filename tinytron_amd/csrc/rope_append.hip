@@ -276,8 +276,14 @@ __global__ __launch_bounds__(64) void rope_append_chunk_kernel(RopeAppendArgs a)
 // [16, 128]: a lane holds four consecutive rotation pairs (i .. i+3 and
 // i+D/2 .. i+D/2+3), D/8 lanes per token, so every input, table and output
 // access is 8 bytes wide (the kernel above moves one 2-byte element per
-// lane). Same tokens per wave, same per-element arithmetic (rotate_pair), same
-// early exits; fp8 scales reduce over the token's D/8 lanes.
+// lane). A wave covers kVecTok tokens in D/16 passes of 512/D tokens, every
+// pass's loads (and page entries) issued before the first is used; same
+// per-element arithmetic (rotate_pair) and early exits as the kernel above;
+// fp8 scales reduce over the token's D/8 lanes. The kernel is bound by
+// instruction issue, not bytes: head_dim (kDsh = log2) is a template
+// argument and page_size a power of two, so page, slot and scale indices
+// are shifts (a 64-bit integer division is a long VALU sequence), and the
+// per-wave set-up is spread over 32 tokens.
 __device__ __forceinline__ void unpack4(uint2 w, float (&f)[4]) {
   f[0] = __builtin_bit_cast(float, w.x << 16);
   f[1] = __builtin_bit_cast(float, w.x & 0xffff0000u);
@@ -286,22 +292,26 @@ __device__ __forceinline__ void unpack4(uint2 w, float (&f)[4]) {
 }
 
 __device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
-  return make_uint2(f32_to_bf16_bits(f[0]) | ((uint32_t)f32_to_bf16_bits(f[1]) << 16),
-                    f32_to_bf16_bits(f[2]) | ((uint32_t)f32_to_bf16_bits(f[3]) << 16));
+  return make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
 }
 
-template <bool kFP8>
+constexpr int kVecTok = 32;
+
+template <bool kFP8, int kDsh>
 __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
-  constexpr int kPasses = 2;  // head_dim 128: 16 lanes per token, 4 tokens per pass
+  static_assert(kDsh >= 4 && kDsh <= 7, "head_dim 16 .. 128");
+  constexpr int D = 1 << kDsh;
+  constexpr int dsh = kDsh;
+  constexpr int half = D >> 1;
+  constexpr int lsh = kDsh - 3;           // log2(lanes per token)
+  constexpr int lpt = 1 << lsh;
+  constexpr int tpp = 64 >> lsh;          // tokens per pass
+  constexpr int kPasses = kVecTok / tpp;  // D / 16
   const int row = blockIdx.x;
-  const int tb = blockIdx.y * kChunkTok;
+  const int tb = blockIdx.y * kVecTok;
   const int b = blockIdx.z;
   const int lane = threadIdx.x;
-  const int D = a.head_dim;
-  const int half = D >> 1;
-  const int lpt = D >> 3;         // lanes per token (power of two, 2 .. 16)
-  const int tpp = 64 / lpt;       // tokens per pass
-  const int sub = lane / lpt;     // this lane's token within a pass
+  const int sub = lane >> lsh;  // this lane's token within a pass
   const int e0 = 4 * (lane & (lpt - 1));
   const bool is_q = row < a.hq;
   const int hk = row - a.hq;
@@ -312,6 +322,7 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
   if (a.lens_out != nullptr && row == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.lens_out[b] = pos0 + nlen;
   if (tb >= nlen && (packed || !is_q)) return;  // uniform
   const int tmax = packed ? nlen - 1 : a.num_new - 1;
+  const int psh = __builtin_ctz(a.page_size);  // a power of two (vec_ok)
   const uint16_t *p1 = static_cast<const uint16_t *>(is_q ? a.q_in : a.k_in);
   const uint16_t *pv = static_cast<const uint16_t *>(a.v_in);
   const uint16_t *tab = static_cast<const uint16_t *>(a.table);
@@ -320,10 +331,15 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
   const int64_t st1 = is_q ? a.qi_st : a.ki_st;
   const int64_t o2 = (packed ? 0 : (int64_t)b * a.vi_sb) + (int64_t)hk * a.vi_sh;
   uint2 x1[kPasses], x2[kPasses], v1[kPasses], v2[kPasses], cw[kPasses], sw[kPasses];
-  int64_t phys[kPasses];
+  int64_t jp[kPasses];  // page index of the token's position
+  int32_t phys[kPasses];
+  bool valid[kPasses];
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
-    const int t = min(tb + p * tpp + sub, tmax);
+    const int tu = tb + p * tpp + sub;
+    // loads use the token clamped into the input rows; whenever the token is
+    // valid below, tu <= tmax, so the clamp leaves it unchanged
+    const int t = min(tu, tmax);
     const int64_t tr = packed ? max(min(r0 + t, a.num_rows - 1), (int64_t)0) : (int64_t)t;
     const int64_t pos = (int64_t)pos0 + t;
     const int64_t tp = pos < 0 ? 0 : (pos >= a.table_len ? a.table_len - 1 : pos);
@@ -335,20 +351,20 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
       v1[p] = *reinterpret_cast<const uint2 *>(pv + o2 + tr * a.vi_st + e0);
       v2[p] = *reinterpret_cast<const uint2 *>(pv + o2 + tr * a.vi_st + half + e0);
     }
-    cw[p] = *reinterpret_cast<const uint2 *>(tab + tp * D + e0);
-    sw[p] = *reinterpret_cast<const uint2 *>(tab + tp * D + half + e0);
-    int64_t j = pos < 0 ? 0 : pos / a.page_size;
-    j = j < a.max_pages ? j : a.max_pages - 1;
-    phys[p] = (a.page_table != nullptr && !is_q) ? a.page_table[(int64_t)b * a.max_pages + j] : 0;
+    cw[p] = *reinterpret_cast<const uint2 *>(tab + (tp << dsh) + e0);
+    sw[p] = *reinterpret_cast<const uint2 *>(tab + (tp << dsh) + half + e0);
+    const int64_t j = pos < 0 ? 0 : pos >> psh;
+    jp[p] = j;
+    phys[p] = (a.page_table != nullptr && !is_q)
+                  ? a.page_table[(int64_t)b * a.max_pages + (j < a.max_pages ? j : a.max_pages - 1)]
+                  : 0;
+    bool ok = tu < a.num_new && pos >= 0 && pos < a.table_len;
+    valid[p] = ok && (is_q ? (!packed || tu < nlen) : (tu < nlen && pos < a.capacity));
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
-    if (p * tpp >= kChunkTok) break;  // uniform: head_dim <= 64 needs one pass
     const int t = tb + p * tpp + sub;
-    const int64_t pos = (int64_t)pos0 + t;
-    bool valid = p * tpp + sub < kChunkTok && t < a.num_new && pos >= 0 && pos < a.table_len;
-    valid = valid && (is_q ? (!packed || t < nlen) : t < nlen);
     float xa[4], xb[4], c[4], sn[4], oa[4], ob[4];
     unpack4(x1[p], xa);
     unpack4(x2[p], xb);
@@ -357,7 +373,7 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) rotate_pair<BF16Tag>(xa[e], xb[e], c[e], sn[e], oa[e], ob[e]);
     if (is_q) {
-      if (valid) {
+      if (valid[p]) {
         uint16_t *q = static_cast<uint16_t *>(a.q_out) + (int64_t)b * a.qo_sb + (int64_t)row * a.qo_sh +
                       (int64_t)t * a.qo_st;
         *reinterpret_cast<uint2 *>(q + e0) = pack4(oa);
@@ -366,13 +382,14 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
       continue;
     }
     int64_t off = -1;  // slot offset, from the page entry loaded above
-    if (valid && pos < a.capacity) {
-      const int64_t j = pos / a.page_size;
-      const int64_t slot = pos - j * a.page_size;
+    if (valid[p]) {
+      const int64_t j = jp[p];
+      const int64_t pos = (int64_t)pos0 + t;
+      const int64_t slot = pos - (j << psh);
       if (a.page_table == nullptr)
-        off = (int64_t)b * a.c_seq + j * a.c_page + (int64_t)hk * a.c_head + slot * D;
+        off = (int64_t)b * a.c_seq + j * a.c_page + (int64_t)hk * a.c_head + (slot << dsh);
       else if (j < a.max_pages && phys[p] >= 0 && phys[p] < a.num_pages)
-        off = phys[p] * a.c_page + (int64_t)hk * a.c_head + slot * D;
+        off = (int64_t)phys[p] * a.c_page + (int64_t)hk * a.c_head + (slot << dsh);
     }
     if constexpr (!kFP8) {
       if (off >= 0) {
@@ -394,6 +411,7 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
         km = fmaxf(km, fmaxf(fabsf(oa[e]), fabsf(ob[e])));
         vm = fmaxf(vm, fmaxf(fabsf(va[e]), fabsf(vb[e])));
       }
+#pragma unroll
       for (int m = lpt >> 1; m > 0; m >>= 1) {
         km = fmaxf(km, __shfl_xor(km, m, 64));
         vm = fmaxf(vm, __shfl_xor(vm, m, 64));
@@ -401,14 +419,10 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
       const float ks = km / 448.0f;
       const float vs = vm / 448.0f;
       if (off >= 0) {
-        uint32_t ka = 0, kb = 0, wa = 0, wb = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ka |= (uint32_t)(ks == 0.f ? (uint8_t)0 : f32_to_e4m3fn(oa[e] / ks)) << (8 * e);
-          kb |= (uint32_t)(ks == 0.f ? (uint8_t)0 : f32_to_e4m3fn(ob[e] / ks)) << (8 * e);
-          wa |= (uint32_t)(vs == 0.f ? (uint8_t)0 : f32_to_e4m3fn(va[e] / vs)) << (8 * e);
-          wb |= (uint32_t)(vs == 0.f ? (uint8_t)0 : f32_to_e4m3fn(vb[e] / vs)) << (8 * e);
-        }
+        const uint32_t ka = ks == 0.f ? 0u : pack_e4m3fn_x4(oa[0] / ks, oa[1] / ks, oa[2] / ks, oa[3] / ks);
+        const uint32_t kb = ks == 0.f ? 0u : pack_e4m3fn_x4(ob[0] / ks, ob[1] / ks, ob[2] / ks, ob[3] / ks);
+        const uint32_t wa = vs == 0.f ? 0u : pack_e4m3fn_x4(va[0] / vs, va[1] / vs, va[2] / vs, va[3] / vs);
+        const uint32_t wb = vs == 0.f ? 0u : pack_e4m3fn_x4(vb[0] / vs, vb[1] / vs, vb[2] / vs, vb[3] / vs);
         uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
         uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
         *reinterpret_cast<uint32_t *>(kc + off + e0) = ka;
@@ -416,8 +430,8 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
         *reinterpret_cast<uint32_t *>(vc + off + e0) = wa;
         *reinterpret_cast<uint32_t *>(vc + off + half + e0) = wb;
         if (e0 == 0) {
-          a.k_scale[off / D] = ks;
-          a.v_scale[off / D] = vs;
+          a.k_scale[off >> dsh] = ks;
+          a.v_scale[off >> dsh] = vs;
         }
       }
     }
@@ -428,7 +442,7 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
 bool vec_ok(const RopeAppendArgs &a) {
   const int D = a.head_dim;
   auto al = [](const void *p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
-  const bool pow2 = D >= 16 && D <= 128 && (D & (D - 1)) == 0;
+  const bool pow2 = D >= 16 && D <= 128 && (D & (D - 1)) == 0 && (a.page_size & (a.page_size - 1)) == 0;
   const int64_t st[] = {a.qi_sb, a.qi_sh, a.qi_st, a.ki_sb, a.ki_sh, a.ki_st, a.vi_sb, a.vi_sh, a.vi_st,
                         a.qo_sb, a.qo_sh, a.qo_st, a.c_seq, a.c_page, a.c_head};
   bool strides4 = true;
@@ -437,18 +451,29 @@ bool vec_ok(const RopeAppendArgs &a) {
          al(a.k_cache, 8) && al(a.v_cache, 8);
 }
 
+template <bool kFP8>
+void launch_vec(const RopeAppendArgs &a, dim3 grid, hipStream_t stream) {
+  switch (a.head_dim) {
+    case 16: hipLaunchKernelGGL((rope_append_vec_kernel<kFP8, 4>), grid, dim3(64), 0, stream, a); break;
+    case 32: hipLaunchKernelGGL((rope_append_vec_kernel<kFP8, 5>), grid, dim3(64), 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((rope_append_vec_kernel<kFP8, 6>), grid, dim3(64), 0, stream, a); break;
+    default: hipLaunchKernelGGL((rope_append_vec_kernel<kFP8, 7>), grid, dim3(64), 0, stream, a); break;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, CacheKind kind, hipStream_t stream) {
   if ((a.num_new > 1 || a.in_rows != nullptr) && a.part_splits <= 0) {
-    const dim3 cgrid(a.hq + a.hkv, (a.num_new + kChunkTok - 1) / kChunkTok, a.batch);
     if (kind != CacheKind::kF32 && vec_ok(a)) {
+      const dim3 vgrid(a.hq + a.hkv, (a.num_new + kVecTok - 1) / kVecTok, a.batch);
       if (kind == CacheKind::kFP8)
-        hipLaunchKernelGGL((rope_append_vec_kernel<true>), cgrid, dim3(64), 0, stream, a);
+        launch_vec<true>(a, vgrid, stream);
       else
-        hipLaunchKernelGGL((rope_append_vec_kernel<false>), cgrid, dim3(64), 0, stream, a);
+        launch_vec<false>(a, vgrid, stream);
       return hipGetLastError();
     }
+    const dim3 cgrid(a.hq + a.hkv, (a.num_new + kChunkTok - 1) / kChunkTok, a.batch);
     switch (kind) {
       case CacheKind::kBF16:
         hipLaunchKernelGGL((rope_append_chunk_kernel<BF16Tag, false>), cgrid, dim3(64), 0, stream, a);

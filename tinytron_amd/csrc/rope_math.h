@@ -19,6 +19,7 @@ struct Elem<float> {
     static_cast<float *>(p)[i] = v;
   }
   static __device__ __forceinline__ float rnd(float v) { return v; }
+  static __device__ __forceinline__ void rnd2(float &, float &) {}
 };
 
 struct BF16Tag {};
@@ -32,6 +33,12 @@ struct Elem<BF16Tag> {
     static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
   }
   static __device__ __forceinline__ float rnd(float v) { return round_bf16(v); }
+  // two values rounded in one conversion
+  static __device__ __forceinline__ void rnd2(float &x, float &y) {
+    const uint32_t p = pack_bf16x2(x, y);
+    x = __uint_as_float(p << 16);
+    y = __uint_as_float(p & 0xffff0000u);
+  }
 };
 
 // out1 = r(r(x1*c) + r(-x2*s)), out2 = r(r(x2*c) + r(x1*s)), r = rounding to
@@ -39,12 +46,13 @@ struct Elem<BF16Tag> {
 template <typename A>
 __device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s, float &o1, float &o2) {
 #pragma clang fp contract(off)
-  const float a1 = Elem<A>::rnd(x1 * c);
-  const float b1 = Elem<A>::rnd((-x2) * s);
-  const float a2 = Elem<A>::rnd(x2 * c);
-  const float b2 = Elem<A>::rnd(x1 * s);
-  o1 = Elem<A>::rnd(a1 + b1);
-  o2 = Elem<A>::rnd(a2 + b2);
+  float a1 = x1 * c, a2 = x2 * c;
+  Elem<A>::rnd2(a1, a2);
+  float b1 = (-x2) * s, b2 = x1 * s;
+  Elem<A>::rnd2(b1, b2);
+  o1 = a1 + b1;
+  o2 = a2 + b2;
+  Elem<A>::rnd2(o1, o2);
 }
 
 }  // namespace tt
