@@ -10,7 +10,7 @@ import math
 import numpy as np
 
 from oracle import kvcache as okv
-from oracle.numerics import f32_to_bf16_bits, bf16_bits_to_f32
+from oracle.numerics import f32_to_bf16_bits, bf16_bits_to_f32, round_bf16
 
 
 def bf16_randn(rng: np.random.Generator, shape, scale: float = 1.0):
@@ -35,8 +35,10 @@ def paged_geometry(seq_capacity, num_heads, head_dim, page_size, rng, extra_page
     return layout, numel, table, num_pages
 
 
-def fill_cache_values(layout, numel, batch, lengths, rng, fp8=False):
+def fill_cache_values(layout, numel, batch, lengths, rng, fp8=False, key_gain=None):
     """Random K/V for tokens [0, lengths[b]) of every sequence, NaN elsewhere.
+    key_gain(b, L) -> [L] scales sequence b's keys token by token (then
+    rounded to bf16), to shape how scores grow along a sequence.
 
     Returns dict with fp32 value arrays (bf16-representable, or dequantized fp8),
     and the raw storage (bf16 bits or fp8 codes + scales).
@@ -58,6 +60,8 @@ def fill_cache_values(layout, numel, batch, lengths, rng, fp8=False):
         L = int(lengths[b])
         _, kb = bf16_randn(rng, (L, H, D))
         _, vb = bf16_randn(rng, (L, H, D))
+        if key_gain is not None:
+            kb = round_bf16(kb * np.asarray(key_gain(b, L), np.float32)[:, None, None])
         if fp8:
             kq, ksc = quantize_e4m3_rows(kb)
             vq, vsc = quantize_e4m3_rows(vb)

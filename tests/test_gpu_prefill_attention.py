@@ -24,7 +24,8 @@ def _dev_bf16(bits):
     return torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
 
 
-def run_prefill(past, new, Hq=32, Hkv=8, D=128, P=16, paged=True, fp8=False, seed=0, transposed_q=False):
+def run_prefill(past, new, Hq=32, Hkv=8, D=128, P=16, paged=True, fp8=False, seed=0, transposed_q=False,
+                key_gain=None):
     from tinytron_amd import ops
 
     rng = np.random.default_rng(seed)
@@ -39,7 +40,7 @@ def run_prefill(past, new, Hq=32, Hkv=8, D=128, P=16, paged=True, fp8=False, see
     else:
         cap = ((max_len + P - 1) // P) * P
         layout, numel = contiguous_geometry(B, Hkv, D, cap, P)
-    data = fill_cache_values(layout, numel, B, total, rng, fp8=fp8)
+    data = fill_cache_values(layout, numel, B, total, rng, fp8=fp8, key_gain=key_gain)
     if transposed_q:
         qb, qf = bf16_randn(rng, (B, T, Hq, D))
         q = _dev_bf16(qb).transpose(1, 2)
@@ -121,3 +122,24 @@ def test_prefill_mask_edges_at_tile_boundaries(G, fp8):
     new = [32, 1, 33, 64, 65, 97, 128, 31, 1, 2]  # 30 + 1, 62 + 2: a limit one key short of a tile end
     got, ref, n = run_prefill(past, new, Hq=Hkv * G, Hkv=Hkv, D=64, fp8=fp8, seed=40 + G + fp8)
     check(got, ref, n)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_prefill_growing_scores(fp8):
+    """Scores that keep growing along the sequence: the running maximum
+    climbs past its slack (8 in log2 units) tile after tile in the middle of
+    the key loop, so O and the sums are rescaled while holding mass; between
+    those steps P runs above 1 under a stale maximum. Keys gain a factor 2
+    every 24 tokens, and one sequence has a single spiking key in the middle."""
+    def gain(b, L):
+        t = np.arange(L, dtype=np.float64)
+        g = 2.0 ** (t / 24.0)
+        if b == 2:
+            g = np.ones(L)
+            g[L // 2] = 40.0
+        return np.minimum(g, 2.0 ** 8)
+
+    Hkv = 2
+    got, ref, new = run_prefill([0, 150, 0], [300, 90, 257], Hq=Hkv * 4, Hkv=Hkv, D=64, fp8=fp8, seed=77 + fp8,
+                                key_gain=gain)
+    check(got, ref, new)

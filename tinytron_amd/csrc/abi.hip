@@ -484,6 +484,7 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
   a.o_sb = out_strides[0];
   a.o_st = out_strides[1];
   a.o_sh = out_strides[2];
+  a.vec_out = aligned(out, 8) && out_strides[0] % 4 == 0 && out_strides[1] % 4 == 0 && out_strides[2] % 4 == 0;
   a.batch = (int)batch;
   a.hq = (int)num_q_heads;
   a.hkv = (int)num_kv_heads;

@@ -41,11 +41,17 @@ constexpr int kPrefillChunkTiles = 8;
 // maximum is the IEEE-754-2019 one (v_maximum3_f32, which needs no NaN
 // quieting of its inputs; no score is NaN). P enters PV as P_hi + P_lo
 // (two bf16 operands, ~16 mantissa bits: a single bf16 P misses the 2e-3
-// absolute bound on short, cancelling rows). The caller rescales O by
-// `alpha` (this column's exp2(m_old - m_new); 0 on the first tile, whose key
-// 0 is valid for every column).
+// absolute bound on short, cancelling rows). The running max is lazy: a
+// column's reference max st.m moves only when the tile's max exceeds it by
+// more than kLazyMax (log2 units), so P <= 2^kLazyMax (fp32 O and l and the
+// bf16 P halves have the range) and most tiles need no rescale at all.
+// Returns whether any column of the wave moved its max; then the caller
+// rescales O by `alpha` (this column's exp2(m_old - m_new), 1 for columns
+// that kept theirs, 0 on the first tile, whose key 0 is valid for every
+// column).
+constexpr float kLazyMax = 8.0f;
 template <int D, bool kFP8>
-__device__ __forceinline__ void qk_softmax_pf(float scale_log2, const f32x4 (&kc)[2], bool edge, int t0, int lim,
+__device__ __forceinline__ bool qk_softmax_pf(float scale_log2, const f32x4 (&kc)[2], bool edge, int t0, int lim,
                                               int lane, const Tile<D, kFP8> &tile, const bf16x8 (&qf)[D / 32],
                                               WaveState<D, kFP8> &st, float &alpha, bf16x8 &pa_hi, bf16x8 &pa_lo) {
   using TR = KVTraits<kFP8>;
@@ -71,18 +77,29 @@ __device__ __forceinline__ void qk_softmax_pf(float scale_log2, const f32x4 (&kc
     for (int i = 0; i < 8; ++i) x[i] = t0 + 16 * (i >> 2) + 4 * g + (i & 3) < lim ? x[i] : kNegInf;
   }
   const auto mx2 = [](float u, float v) { return __builtin_elementwise_maximum(u, v); };
-  float mx = mx2(mx2(mx2(x[0], x[1]), mx2(x[2], x[3])), mx2(mx2(x[4], x[5]), mx2(x[6], x[7])));
-  mx = mx2(mx, __shfl_xor(mx, 16, 64));
-  mx = mx2(mx, __shfl_xor(mx, 32, 64));
+  // nested pairs fold into three-input v_maximum3_f32 (four instructions for eight values)
+  float mx = mx2(mx2(mx2(mx2(x[0], x[1]), x[2]), mx2(mx2(x[3], x[4]), x[5])), mx2(x[6], x[7]));
+  // across the four lane groups (lanes n, n+16, n+32, n+48 hold column n)
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+  mx = mx2(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+  mx = mx2(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
   if constexpr (!kFP8) mx *= scale_log2;  // scale > 0: the maximum commutes with it (-inf stays -inf)
-  const float m_new = mx2(st.m, mx);  // finite from the first tile on
-  alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  // move the reference max only past the slack (always on the first tile: st.m = -inf)
+  const bool bump = mx > st.m + kLazyMax;
+  const bool rescale = __builtin_amdgcn_ballot_w64(bump) != 0;  // wave-uniform
+  const float m_new = bump ? mx : st.m;  // finite from the first tile on
+  alpha = 1.0f;
+  if (rescale) alpha = __builtin_amdgcn_exp2f(st.m - m_new);
   st.m = m_new;
   float p[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     p[i] = __builtin_amdgcn_exp2f(kFP8 ? x[i] - m_new : __builtin_fmaf(x[i], scale_log2, -m_new));
-  st.l = __builtin_fmaf(st.l, alpha, ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
+  if constexpr (kFP8) {  // bf16: the column sums come from the matrix cores (see pv_tile_nb)
+    const float psum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    st.l = rescale ? __builtin_fmaf(st.l, alpha, psum) : st.l + psum;
+  }
   if constexpr (kFP8) {
     // fold the per-token V scale into P; on edge tiles masked tokens stay
     // exactly 0 (select: a scale slot past the end may hold anything)
@@ -94,23 +111,49 @@ __device__ __forceinline__ void qk_softmax_pf(float scale_log2, const f32x4 (&kc
   }
   const f32x8 pv = {p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]};
   pa_hi = __builtin_convertvector(pv, bf16x8);
-  pa_lo = __builtin_convertvector(pv - __builtin_convertvector(pa_hi, f32x8), bf16x8);  // P - P_hi exact in fp32
+  // P_hi back in fp32 straight from the packed halves (element 2i is the low half of word i)
+  const u32x4 hw = __builtin_bit_cast(u32x4, pa_hi);
+  f32x8 hf;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hf[2 * i] = __uint_as_float(hw[i] << 16);
+    hf[2 * i + 1] = __uint_as_float(hw[i] & 0xffff0000u);
+  }
+  pa_lo = __builtin_convertvector(pv - hf, bf16x8);  // P - P_hi exact in fp32
+  return rescale;
 }
 
-// PV of one tile for NB column blocks: each V^T block (see read_v) is
-// multiplied by every block's P_hi + P_lo.
+// PV of one tile for NB column blocks, accumulated transposed: O^T = V^T P^T,
+// with the V block (see read_v) as the A operand and P_hi + P_lo as B (the
+// same registers as in P V: lane (n + 16g) holds V[tokens of group g][d n]
+// and P[column n][tokens of group g]). Lane (n + 16g) then holds
+// O^T[d][column n] for d = o_col_d(c, 4g + r): every O value of a lane
+// belongs to its own column, so the rescale by alpha needs no cross-lane
+// traffic, and each block's four values are consecutive head_dim entries.
+// bf16 caches also accumulate the softmax denominators here: an all-ones
+// A block gives every column's sum of P_hi + P_lo in each of its lanes
+// (two MFMAs instead of eight VALU adds per block and tile, in a loop bound by
+// VALU issue; fp8 P carries the V scales, so fp8 sums on the VALU).
 template <int D, bool kFP8, int NB>
 __device__ __forceinline__ void pv_tile_nb(const VRegs<D, kFP8> &v, const u32x2 (&ident8)[2],
                                            const bf16x8 (&pa_hi)[NB], const bf16x8 (&pa_lo)[NB],
-                                           WaveState<D, kFP8> (&st)[NB]) {
+                                           WaveState<D, kFP8> (&st)[NB], f32x4 (&lsum)[NB]) {
   constexpr int NDB = D / 32;
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) {
     const bf16x8 vb = v_block<D, kFP8>(v, c, ident8);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      st[j].o[c] = mfma_bf16(pa_hi[j], vb, st[j].o[c]);
-      st[j].o[c] = mfma_bf16(pa_lo[j], vb, st[j].o[c]);
+      st[j].o[c] = mfma_bf16(vb, pa_hi[j], st[j].o[c]);
+      st[j].o[c] = mfma_bf16(vb, pa_lo[j], st[j].o[c]);
+    }
+  }
+  if constexpr (!kFP8) {
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      lsum[j] = mfma_bf16(ones, pa_hi[j], lsum[j]);
+      lsum[j] = mfma_bf16(ones, pa_lo[j], lsum[j]);
     }
   }
 }
@@ -184,6 +227,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     st[j].m = kNegInf;
     st[j].l = 0.f;
   }
+  f32x4 lsum[NB];  // bf16: every element holds the lane's column sum of P (rescaled with O)
+#pragma unroll
+  for (int j = 0; j < NB; ++j) lsum[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   char *vlds = smem_v + wave * Tile<D, kFP8>::kVBytes;
   const int ntiles = (L + kTileTokens - 1) / kTileTokens;
@@ -229,10 +275,11 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       }
       bf16x8 pa_hi[NB], pa_lo[NB];
       float alpha[NB];
+      bool rescale[NB];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
-        qk_softmax_pf<D, kFP8>(a.scale_log2, kc, edge, t0, lim[j], lane, buf[k & 1], qf[j], st[j], alpha[j], pa_hi[j],
-                               pa_lo[j]);
+        rescale[j] = qk_softmax_pf<D, kFP8>(a.scale_log2, kc, edge, t0, lim[j], lane, buf[k & 1], qf[j], st[j],
+                                            alpha[j], pa_hi[j], pa_lo[j]);
       __builtin_amdgcn_sched_barrier(0);
       if (k + 1 < kPrefillChunkTiles)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(kKLoads));
@@ -247,40 +294,47 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
-      // O rows (columns 4g + r) take their column's alpha from lane 4g + r
+      // every O^T value of a lane is in the lane's own column: its own alpha
 #pragma unroll
       for (int j = 0; j < NB; ++j)
+        if (rescale[j]) {  // uniform
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float ar = __shfl(alpha[j], 4 * (lane >> 4) + r, 64);
-#pragma unroll
-          for (int c = 0; c < 2 * NDB; ++c) st[j].o[c][r] *= ar;
+          for (int c = 0; c < 2 * NDB; ++c) st[j].o[c] *= alpha[j];
+          if constexpr (!kFP8) lsum[j] *= alpha[j];
         }
-      pv_tile_nb<D, kFP8, NB>(vr, ident8, pa_hi, pa_lo, st);
+      pv_tile_nb<D, kFP8, NB>(vr, ident8, pa_hi, pa_lo, st, lsum);
     }
     __builtin_amdgcn_s_waitcnt(0);
   }
 
-  // normalise and write: O row r of lane group g is column 4g + r
+  // normalise and write: lane (n + 16g) holds column n's head_dim entries
+  // o_col_d(c, 4g) .. + 3 of every block c
   uint16_t *out = static_cast<uint16_t *>(a.out);
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int tb = t_first + j * a.qt;
-    float l = st[j].l;
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    float l = lsum[j][0];
+    if constexpr (kFP8) {
+      l = st[j].l;
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    if (tq < a.qt && tb + tq < t_end) {
+      const int64_t orow = (int64_t)b * a.o_sb + (int64_t)(tb + tq) * a.o_st + (int64_t)(hk * G + head) * a.o_sh;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int col = 4 * g + r;
-      const float lr = __shfl(l, col, 64);
-      const float inv = lr > 0.f ? 1.0f / lr : 0.f;
-      const int ctq = col / G;
-      const int chead = col - ctq * G;
-      if (ctq < a.qt && tb + ctq < t_end) {
-        const int64_t orow =
-            (int64_t)b * a.o_sb + (int64_t)(tb + ctq) * a.o_st + (int64_t)(hk * G + chead) * a.o_sh;
-#pragma unroll
-        for (int c = 0; c < 2 * NDB; ++c) out[orow + o_col_d<kFP8>(c, n)] = f32_to_bf16_bits(st[j].o[c][r] * inv);
+      for (int c = 0; c < 2 * NDB; ++c) {
+        const int d0 = o_col_d<kFP8>(c, 4 * g);
+        const uint2 w = make_uint2(pack_bf16x2(st[j].o[c][0] * inv, st[j].o[c][1] * inv),
+                                   pack_bf16x2(st[j].o[c][2] * inv, st[j].o[c][3] * inv));
+        if (a.vec_out) {
+          *reinterpret_cast<uint2 *>(out + orow + d0) = w;
+        } else {
+          out[orow + d0] = (uint16_t)w.x;
+          out[orow + d0 + 1] = (uint16_t)(w.x >> 16);
+          out[orow + d0 + 2] = (uint16_t)w.y;
+          out[orow + d0 + 3] = (uint16_t)(w.y >> 16);
+        }
       }
     }
   }

@@ -151,6 +151,7 @@ struct PrefillArgs : DecodeArgs {
   int qt;                      // query tokens per wave (16 / G)
   int nq;                      // query blocks per sequence: ceil(T / qt)
   int wg_per_pair;             // workgroups per (sequence, KV head): ceil(nq / 4)
+  int vec_out;                 // out 8-byte aligned, strides multiples of 4: 4 head_dim entries per store
 };
 
 hipError_t launch_prefill_attn(const PrefillArgs &a, CacheKind kind, int head_dim, hipStream_t stream);
