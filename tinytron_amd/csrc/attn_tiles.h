@@ -159,7 +159,7 @@ __device__ __forceinline__ void load_v_block_lds(const DecodeArgs &a, int64_t el
 template <int D, bool kFP8>
 struct WaveState {
   static constexpr int NDB = D / 32;
-  f32x4 o[2 * NDB];  // PV accumulators: d block c (16 columns), rows = heads 4g..4g+3
+  f32x4 o[2 * NDB];  // PV accumulators, transposed: block c, lane (n + 16g) = column n, d = o_col_d(c, 4g + r)
   float m;           // running max of this lane's head (log2 units)
   float l;           // running sum (lane-partial: this lane's tokens only)
 };
@@ -197,12 +197,17 @@ __device__ __forceinline__ void qk_softmax(float scale_log2, int t0, int lim, in
       s[tt * 4 + r] = tok < lim ? x * scale_log2 : kNegInf;
     }
   }
-  float mx = s[0];
-#pragma unroll
-  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const float m_new = fmaxf(st.m, mx);  // finite: every column has key t0 = 0 valid from its first tile on
+  // maxima: IEEE-754-2019 maximum (no score is NaN; masked ones are -inf), the
+  // nested pairs folding into v_maximum3_f32; across the four lane groups with
+  // permlane swaps (with both operands x, the two results' maximum is the
+  // maximum of x[lane] and x[lane ^ 16], resp. x[lane ^ 32])
+  const auto mx2 = [](float u, float v) { return __builtin_elementwise_maximum(u, v); };
+  float mx = mx2(mx2(mx2(mx2(s[0], s[1]), s[2]), mx2(mx2(s[3], s[4]), s[5])), mx2(s[6], s[7]));
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+  mx = mx2(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+  mx = mx2(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+  const float m_new = mx2(st.m, mx);  // finite: every column has key t0 = 0 valid from its first tile on
   const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
   float p[8];
   float psum = 0.f;
@@ -223,13 +228,10 @@ __device__ __forceinline__ void qk_softmax(float scale_log2, int t0, int lim, in
     }
   }
 
-  // Rescale O rows (heads 4g + r) by their head's alpha, held by lane 4g + r.
+  // O is held transposed (see pv_tile): every value of a lane is in the
+  // lane's own column, rescaled by its own alpha.
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float ar = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-    for (int c = 0; c < 2 * NDB; ++c) st.o[c][r] *= ar;
-  }
+  for (int c = 0; c < 2 * NDB; ++c) st.o[c] *= alpha;
 
   // P as the A operand: row = head (lane % 16), k slots = this lane's 8 tokens.
   // P = P_hi + P_lo with both halves bf16 (P_lo = P - P_hi is exact in fp32),
@@ -313,6 +315,11 @@ __device__ __forceinline__ bf16x8 v_block(const VRegs<D, kFP8> &v, int c, const 
   }
 }
 
+// PV of one tile, accumulated transposed: O^T = V^T P^T, the V block as the
+// A operand and P_hi / P_lo as B (the registers P V would use, operands
+// swapped). Lane (n + 16g) holds O^T[d][column n] for d = o_col_d(c, 4g + r),
+// r = 0..3: a lane's values all belong to its own column (no cross-lane
+// rescale), four consecutive head_dim entries per block.
 template <int D, bool kFP8>
 __device__ __forceinline__ void pv_tile(const VRegs<D, kFP8> &v, const u32x2 (&ident8)[2], bf16x8 pa_hi,
                                         bf16x8 pa_lo, WaveState<D, kFP8> &st) {
@@ -320,8 +327,8 @@ __device__ __forceinline__ void pv_tile(const VRegs<D, kFP8> &v, const u32x2 (&i
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) {
     const bf16x8 vb = v_block<D, kFP8>(v, c, ident8);
-    st.o[c] = mfma_bf16(pa_hi, vb, st.o[c]);
-    st.o[c] = mfma_bf16(pa_lo, vb, st.o[c]);
+    st.o[c] = mfma_bf16(vb, pa_hi, st.o[c]);
+    st.o[c] = mfma_bf16(vb, pa_lo, st.o[c]);
   }
 }
 
@@ -385,16 +392,36 @@ __device__ __forceinline__ void stream_block_addr(const DecodeArgs &a, int b, in
   elem = uniform64(e);
 }
 
+// Reductions over the wave without LDS round trips: DPP within each row of
+// 16 lanes (neighbour swap quad_perm [1,0,3,2], pair swap [2,3,0,1], then the
+// mirrored half row and the mirrored row, after each of which a lane holds
+// the total of twice as many lanes), then permlane swaps across rows (with
+// both operands x, the two results are x[lane] and x[lane ^ 16], resp. 32).
+// Every lane combines the same two values at each step, so all 64 end with
+// the same bits.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+  x = op(x, dpp_f32<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = op(x, dpp_f32<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = op(x, dpp_f32<0x141>(x));  // row_half_mirror
+  x = op(x, dpp_f32<0x140>(x));  // row_mirror
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = op(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+}
+
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
-  return x;
+  return wave_reduce(x, [](float u, float v) { return fmaxf(u, v); });
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
+  return wave_reduce(x, [](float u, float v) { return u + v; });
 }
 
 }  // namespace

@@ -187,13 +187,10 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
     sm[wave * 16 + n] = st.m;
     sl[wave * 16 + n] = l;
   }
+  if (n < G) {  // lane (n + 16g): head n, four consecutive head_dim entries per block
 #pragma unroll
-  for (int c = 0; c < 2 * NDB; ++c) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int head = 4 * g + r;
-      if (head < G) so[(wave * G + head) * D + o_col_d<kFP8>(c, n)] = st.o[c][r];
-    }
+    for (int c = 0; c < 2 * NDB; ++c)
+      *reinterpret_cast<f32x4 *>(so + (wave * G + n) * D + o_col_d<kFP8>(c, 4 * g)) = st.o[c];
   }
   __syncthreads();
   const int64_t item = ((int64_t)b * a.hkv + hk) * a.max_splits + split;
@@ -706,13 +703,10 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
   const int64_t slot = (int64_t)b * a.hkv + hk + w;
+  if (n < G) {  // lane (n + 16g): head n, four consecutive head_dim entries per block (16-byte stores)
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int head = 4 * g + r;
-    if (head < G) {
-#pragma unroll
-      for (int c = 0; c < 2 * NDB; ++c) a.ws_o[(slot * G + head) * D + o_col_d<kFP8>(c, n)] = st.o[c][r];
-    }
+    for (int c = 0; c < 2 * NDB; ++c)
+      *reinterpret_cast<f32x4 *>(a.ws_o + (slot * G + n) * D + o_col_d<kFP8>(c, 4 * g)) = st.o[c];
   }
   if (g == 0 && n < G) {
     a.ws_ml[(slot * G + n) * 2 + 0] = st.m;
