@@ -26,6 +26,7 @@
 
 #include "tt_internal.h"
 #include "tt_numerics.h"
+#include "wave_reduce.h"
 
 namespace tt {
 namespace {
@@ -172,8 +173,7 @@ __global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *P, int S,
 }
 
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  v = wave_sum(v);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   const float t = red[0] + red[1] + red[2] + red[3];

@@ -14,15 +14,10 @@
 #include "rope_math.h"
 #include "tt_internal.h"
 #include "tt_numerics.h"
+#include "wave_reduce.h"
 
 namespace tt {
 namespace {
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
 
 // Slot element offset of token `pos` of sequence b, KV head hk; -1 if the
 // slot is outside the cache (capacity, page table or pool).
