@@ -96,7 +96,7 @@ __device__ __forceinline__ bool qk_softmax_pf(float scale_log2, const f32x4 (&kc
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     p[i] = __builtin_amdgcn_exp2f(kFP8 ? x[i] - m_new : __builtin_fmaf(x[i], scale_log2, -m_new));
-  if constexpr (kFP8) {  // bf16: the column sums come from the matrix cores (see pv_tile_nb)
+  if constexpr (kFP8) {  // bf16: the column sums come from the matrix cores (see pv_block)
     const float psum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
     st.l = rescale ? __builtin_fmaf(st.l, alpha, psum) : st.l + psum;
   }
@@ -123,38 +123,30 @@ __device__ __forceinline__ bool qk_softmax_pf(float scale_log2, const f32x4 (&kc
   return rescale;
 }
 
-// PV of one tile for NB column blocks, accumulated transposed: O^T = V^T P^T,
-// with the V block (see read_v) as the A operand and P_hi + P_lo as B (the
-// same registers as in P V: lane (n + 16g) holds V[tokens of group g][d n]
-// and P[column n][tokens of group g]). Lane (n + 16g) then holds
-// O^T[d][column n] for d = o_col_d(c, 4g + r): every O value of a lane
-// belongs to its own column, so the rescale by alpha needs no cross-lane
-// traffic, and each block's four values are consecutive head_dim entries.
-// bf16 caches also accumulate the softmax denominators here: an all-ones
-// A block gives every column's sum of P_hi + P_lo in each of its lanes
-// (two MFMAs instead of eight VALU adds per block and tile, in a loop bound by
-// VALU issue; fp8 P carries the V scales, so fp8 sums on the VALU).
-template <int D, bool kFP8, int NB>
-__device__ __forceinline__ void pv_tile_nb(const VRegs<D, kFP8> &v, const u32x2 (&ident8)[2],
-                                           const bf16x8 (&pa_hi)[NB], const bf16x8 (&pa_lo)[NB],
-                                           WaveState<D, kFP8> (&st)[NB], f32x4 (&lsum)[NB]) {
-  constexpr int NDB = D / 32;
+// PV of one tile for one column block, accumulated transposed: Oᵀ = Vᵀ Pᵀ,
+// with the V block as the A operand and P_hi + P_lo as B (the same
+// registers as in P V: lane (n + 16g) holds V[tokens of group g][d n] and
+// P[column n][tokens of group g]). Lane (n + 16g) then holds Oᵀ[d][column n]
+// for d = o_col_d(c, 4g + r): every O value of a lane belongs to its own
+// column, so the rescale by alpha needs no cross-lane traffic, and each
+// block's four values are consecutive head_dim entries. bf16 caches also
+// accumulate the softmax denominators here: an all-ones A block gives every
+// column's sum of P_hi + P_lo in each of its lanes (two MFMAs instead of
+// eight VALU adds per block and tile, in a loop bound by VALU issue; fp8 P
+// carries the V scales, so fp8 sums on the VALU). `vb` are the tile's V
+// blocks (v_block), converted once for all column blocks.
+template <int D, bool kFP8>
+__device__ __forceinline__ void pv_block(const bf16x8 (&vb)[D / 16], bf16x8 pa_hi, bf16x8 pa_lo,
+                                         WaveState<D, kFP8> &st, f32x4 &lsum) {
 #pragma unroll
-  for (int c = 0; c < 2 * NDB; ++c) {
-    const bf16x8 vb = v_block<D, kFP8>(v, c, ident8);
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      st[j].o[c] = mfma_bf16(vb, pa_hi[j], st[j].o[c]);
-      st[j].o[c] = mfma_bf16(vb, pa_lo[j], st[j].o[c]);
-    }
+  for (int c = 0; c < D / 16; ++c) {
+    st.o[c] = mfma_bf16(vb[c], pa_hi, st.o[c]);
+    st.o[c] = mfma_bf16(vb[c], pa_lo, st.o[c]);
   }
   if constexpr (!kFP8) {
     const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      lsum[j] = mfma_bf16(ones, pa_hi[j], lsum[j]);
-      lsum[j] = mfma_bf16(ones, pa_lo[j], lsum[j]);
-    }
+    lsum = mfma_bf16(ones, pa_hi, lsum);
+    lsum = mfma_bf16(ones, pa_lo, lsum);
   }
 }
 
@@ -273,6 +265,11 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         kc[0] = buf[k & 1].ks[0] * a.scale_log2;
         kc[1] = buf[k & 1].ks[1] * a.scale_log2;
       }
+      // Every column block's QKᵀ and softmax go before the wait for V(k) (time
+      // for its DMA to land; moving some blocks after it, to overlap their
+      // softmax with other blocks' PV, measured no faster with a bf16 cache and
+      // far slower with fp8 at head_dim 128). After the V read, each block's
+      // rescale and PV follow with no scheduling barrier between blocks.
       bf16x8 pa_hi[NB], pa_lo[NB];
       float alpha[NB];
       bool rescale[NB];
@@ -294,15 +291,19 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
-      // every O^T value of a lane is in the lane's own column: its own alpha
+      bf16x8 vb[D / 16];
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
+      for (int c = 0; c < D / 16; ++c) vb[c] = v_block<D, kFP8>(vr, c, ident8);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        // every Oᵀ value of a lane is in the lane's own column: its own alpha
         if (rescale[j]) {  // uniform
 #pragma unroll
           for (int c = 0; c < 2 * NDB; ++c) st[j].o[c] *= alpha[j];
           if constexpr (!kFP8) lsum[j] *= alpha[j];
         }
-      pv_tile_nb<D, kFP8, NB>(vr, ident8, pa_hi, pa_lo, st, lsum);
+        pv_block<D, kFP8>(vb, pa_hi[j], pa_lo[j], st[j], lsum[j]);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
   }
