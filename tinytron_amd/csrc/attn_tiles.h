@@ -2,8 +2,9 @@
 // kernels (gfx950): 16-byte K/V fragment loads through raw buffer resources
 // (rows past a length read nothing), V staged straight into LDS, the QK^T /
 // online-softmax step and the PV step on v_mfma_f32_16x16x32_{bf16,fp8}
-// (V transposed across lanes by an exact 0/1 selection MFMA), and paged
-// block addressing. Everything is in an unnamed namespace: each kernel file
+// (bf16 V read back transposed from LDS with ds_read_b64_tr_b16, fp8 V
+// transposed across lanes by an exact 0/1 selection MFMA), and paged block
+// addressing. Everything is in an unnamed namespace: each kernel file
 // gets its own copy.
 #pragma once
 

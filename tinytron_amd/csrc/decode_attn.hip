@@ -13,19 +13,20 @@
 //   The 4 wave states merge in LDS into one partial per split; a second
 //   kernel merges the splits of a (b, q head).
 //
-// Per 32-token tile, all on the matrix cores (v_mfma_f32_16x16x32_bf16):
+// Per 32-token tile, on the matrix cores (v_mfma_f32_16x16x32_bf16):
 //   QK^T: A = 16 K rows (16-byte loads, one token per lane%16), B = q^T with
 //         the group's heads as columns -> S^T[token][head].
 //   V^T : the PV product contracts over tokens, but a 16-byte load gives a
-//         lane 8 head_dim values of one token. Multiplying the loaded V block
-//         by a 0/1 selection matrix on the MFMA (A = V block, B = identity)
-//         returns the block transposed across lanes, exactly (one nonzero
-//         product per output), with no LDS round trip.
-//   PV  : A = P (heads x tokens, as a bf16 hi + lo pair), B = V^T -> O[head][d]
-//         accumulated in fp32.
+//         lane 8 head_dim values of one token. bf16 V goes into LDS by DMA
+//         (buffer_load ... lds) and comes back transposed with
+//         ds_read_b64_tr_b16; fp8 V is transposed on the fp8 MFMA by a 0/1
+//         selection matrix (exact: one nonzero product per output).
+//   PV  : accumulated transposed, O^T = V^T P^T (A = the V^T block, B = P as a
+//         bf16 hi + lo pair), so every O value a lane holds belongs to its own
+//         head and the online-softmax rescale needs no cross-lane traffic.
 // The token order inside a tile is the one the MFMA output layout produces,
-// used consistently for S, P and V^T, so no cross-lane shuffles are needed
-// except the 4-lane max reduction and the per-head rescale broadcast.
+// used consistently for S, P and V^T; the only cross-lane steps are the head
+// max across the four lane groups (permlane swaps) and the final sums.
 //
 // fp8-e4m3fn caches: K codes become bf16 with v_cvt_scalef32_pk_bf16_fp8
 // (exact: every e4m3 value is a bf16 value), the per-token K scale multiplies
