@@ -150,8 +150,24 @@ __device__ __forceinline__ void pv_block(const bf16x8 (&vb)[D / 16], bf16x8 pa_h
   }
 }
 
+// Column blocks per wave and workgroups per CU. bf16 at head_dim 128 runs
+// 4 blocks at one workgroup per CU (up to 512 registers a wave): the K
+// fragments and transposed V of a tile then feed twice the MFMA work per
+// byte read, which pays more than the second workgroup's latency hiding.
+// fp8 keeps 2 blocks at two workgroups per CU at 128: its dequantisation is
+// VALU work that needs the second workgroup to hide.
+template <int D, bool kFP8>
+constexpr int prefill_blocks() {
+  return D == 64 ? 4 : (kFP8 ? 2 : 4);
+}
+
+template <int D, bool kFP8>
+constexpr int prefill_wgs_per_cu() {
+  return (D == 128 && !kFP8) ? 1 : 2;
+}
+
 template <int D, bool kFP8, int NB>
-__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_attn_kernel(PrefillArgs a) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
   constexpr int NU = Tile<D, kFP8>::NU;
@@ -341,15 +357,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   }
 }
 
-// Column blocks per wave: 4 at head_dim 64, 2 at 128 (the register budget).
-template <int D>
-constexpr int prefill_blocks() {
-  return D == 64 ? 4 : 2;
-}
-
 template <int D, bool kFP8>
 hipError_t launch_d(const PrefillArgs &a0, hipStream_t stream) {
-  constexpr int NB = prefill_blocks<D>();
+  constexpr int NB = prefill_blocks<D, kFP8>();
   PrefillArgs a = a0;
   a.nq = (a0.nq + NB - 1) / NB;  // groups of NB query blocks
   a.wg_per_pair = (a.nq + kWavesPerBlock - 1) / kWavesPerBlock;
