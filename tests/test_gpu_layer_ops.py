@@ -34,7 +34,8 @@ def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> int:
 
 
 @pytest.mark.parametrize("M,N,K,kc", [(1, 64, 512, 256), (7, 3072, 2048, 512), (64, 2048, 6144, 512),
-                                      (100, 128, 1024, 256), (64, 12288, 2048, 512), (64, 3072, 2048, 1024), (37, 2048, 6144, 1024), (100, 128, 1024, 1024)])
+                                      (100, 128, 1024, 256), (64, 12288, 2048, 512), (64, 3072, 2048, 1024), (37, 2048, 6144, 1024), (100, 128, 1024, 1024),
+                                      (64, 12288, 2048, 1024), (3, 6144, 4096, 1024)])
 def test_linear_partials(M, N, K, kc):
     from tinytron_amd import ops
 

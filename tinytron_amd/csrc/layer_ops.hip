@@ -324,21 +324,41 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *g_in
 }  // namespace
 
 hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream) {
-  // 8 waves (128 weight rows) share one staged x chunk when that still puts
-  // a workgroup on at least 3/4 of the CUs; otherwise 4 waves (64 rows).
-  // (Measured on the decode-step shapes: two 8-wave workgroups on some CUs
-  // beat one 12-wave workgroup on every CU; 6- and 12-wave groups lost.)
   const int cus = device_cu_count();
   const int splits = a.K / kc, mt = (a.M + 63) / 64;
-  const bool wide = a.N % 128 == 0 && 4 * (int64_t)(a.N / 128) * splits * mt >= 3 * (int64_t)cus;
-  const dim3 grid((unsigned)(a.N / (wide ? 128 : 64)), (unsigned)splits, (unsigned)mt);
+  int waves;
+  if (kc == 1024) {
+    // One workgroup per CU (the x chunk takes 132 KB of LDS): the shape whose
+    // busiest CU streams the fewest weight rows. (gate|up at C5, N 12288 on
+    // 256 CUs: 6 waves, one 192 KB workgroup per CU, 14.7-15.1 us against
+    // 16.1-16.5 us for 8-wave workgroups at 512-wide chunks.)
+    waves = 4;
+    int64_t best = -1;
+    for (int w : {4, 6, 8}) {
+      if (a.N % (16 * w)) continue;
+      const int64_t wgs = (int64_t)(a.N / (16 * w)) * splits * mt;
+      const int64_t rows = (wgs + cus - 1) / cus * w;
+      if (best < 0 || rows < best) {
+        best = rows;
+        waves = w;
+      }
+    }
+  } else {
+    // 8 waves (128 weight rows) share one staged x chunk when that still puts
+    // a workgroup on at least 3/4 of the CUs; otherwise 4 waves (64 rows).
+    // (Measured on the decode-step shapes: two 8-wave workgroups on some CUs
+    // beat one 12-wave workgroup on every CU; 6- and 12-wave groups lost.)
+    const bool wide = a.N % 128 == 0 && 4 * (int64_t)(a.N / 128) * splits * mt >= 3 * (int64_t)cus;
+    waves = wide ? 8 : 4;
+  }
+  const dim3 grid((unsigned)(a.N / (16 * waves)), (unsigned)splits, (unsigned)mt);
 #define TT_GEMM_LAUNCH(KC, W) hipLaunchKernelGGL((skinny_gemm_kernel<KC, W>), grid, dim3(64 * W), 0, stream, a)
   if (kc == 256) {
-    if (wide) TT_GEMM_LAUNCH(256, 8); else TT_GEMM_LAUNCH(256, 4);
+    if (waves == 8) TT_GEMM_LAUNCH(256, 8); else TT_GEMM_LAUNCH(256, 4);
   } else if (kc == 512) {
-    if (wide) TT_GEMM_LAUNCH(512, 8); else TT_GEMM_LAUNCH(512, 4);
+    if (waves == 8) TT_GEMM_LAUNCH(512, 8); else TT_GEMM_LAUNCH(512, 4);
   } else {
-    if (wide) TT_GEMM_LAUNCH(1024, 8); else TT_GEMM_LAUNCH(1024, 4);
+    if (waves == 8) TT_GEMM_LAUNCH(1024, 8); else if (waves == 6) TT_GEMM_LAUNCH(1024, 6); else TT_GEMM_LAUNCH(1024, 4);
   }
 #undef TT_GEMM_LAUNCH
   return hipGetLastError();

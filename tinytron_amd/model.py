@@ -270,6 +270,12 @@ class GPT(nn.Module):
         return 512 if k % 512 == 0 else (256 if k % 256 == 0 else 0)
 
     @staticmethod
+    def _k_chunk_wide(k: int) -> int:
+        """Split for the gate|up GEMM: its N fills every CU at 1024-wide chunks,
+        which halve the partials that SwiGLU reads."""
+        return 1024 if k % 1024 == 0 else GPT._k_chunk(k)
+
+    @staticmethod
     def _k_chunk_small(k: int) -> int:
         """Split for the square c_proj GEMM: more, shorter splits keep every CU streaming."""
         return 256 if k % 256 == 0 else 0
@@ -320,7 +326,8 @@ class GPT(nn.Module):
         c = self.config
         D = c.hidden_size // c.num_attention_heads
         n_qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
-        sizes = [(c.hidden_size // self._k_chunk(c.hidden_size)) * max(n_qkv, 2 * c.intermediate_size),
+        sizes = [(c.hidden_size // self._k_chunk(c.hidden_size)) * n_qkv,
+                 (c.hidden_size // self._k_chunk_wide(c.hidden_size)) * 2 * c.intermediate_size,
                  (c.hidden_size // self._k_chunk_small(c.hidden_size)) * c.hidden_size,
                  (c.intermediate_size // self._k_chunk(c.intermediate_size)) * c.hidden_size]
         need = B * max(sizes)
@@ -340,6 +347,7 @@ class GPT(nn.Module):
         D = C // Hq
         eps = self.lnf.variance_epsilon
         kc_c, kc_i, kc_o = self._k_chunk(C), self._k_chunk(c.intermediate_size), self._k_chunk_small(C)
+        kc_gu = self._k_chunk_wide(C)
         first = cache.get_layer_cache(0)
         lens = first.seq_lens_host
         if len(set(lens)) == 1 and lens[0] != position_offset:
@@ -359,7 +367,7 @@ class GPT(nn.Module):
                 y = layer.attend(q_rot.view(B, Hq, D))
             P = ops.linear_partials(y.view(B, C), wo, partials=pbuf, k_chunk=kc_o)
             h = ops.add_rmsnorm(x, blk.ln_2.weight, eps, partials=P)
-            P = ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_c)
+            P = ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_gu)
             a = ops.silu_mul(P)                                      # [B, I]
             P = ops.linear_partials(a, wd, partials=pbuf, k_chunk=kc_i)
             nxt = self.blocks[i + 1].ln_1.weight if i + 1 < len(self.blocks) else self.lnf.weight
