@@ -447,6 +447,25 @@ int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const f
 int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t inter, void *y, tt_stream_t stream);
 
 /*
+ * The gate and up projections and SwiGLU of one MLP (mlp.py:24-26, 44-45
+ * under bf16 autocast) in one launch, with no split-K partials:
+ * y[m][i] = bf16(bf16(silu(bf16 g)) * bf16 u), g = x[m] . Wg[i], u = x[m] . Wu[i]
+ * summed in fp32 over the whole K. weight_packed is the fragment-ordered
+ * (as tt_linear_splitk_packed_bf16) matrix of 2I rows interleaved by 8:
+ * rows 16j .. 16j+7 are gate rows 8j .. 8j+7, rows 16j+8 .. 16j+15 up rows
+ * 8j .. 8j+7. x bf16 [M, K] (row stride ldx), y bf16 [M, I] (row stride
+ * ldy). Requirements: K == 2048, I % 24 == 0 (tt_swiglu_gemm_supported),
+ * ldx % 8 == 0, ldy % 4 == 0, 16-byte aligned x and weight, 8-byte aligned y.
+ * (Replaces the gate|up tt_linear_splitk_packed_bf16 + tt_silu_mul_bf16 pair;
+ * the interleaved layout is this library's, no counterpart in the reference.)
+ */
+int tt_linear_swiglu_packed_bf16(const void *x, int64_t ldx, const void *weight_packed, void *y, int64_t ldy,
+                                 int64_t m, int64_t inter, int64_t k, tt_stream_t stream);
+
+/* 1 when tt_linear_swiglu_packed_bf16 takes this K and I, else 0. */
+int tt_swiglu_gemm_supported(int64_t k, int64_t inter);
+
+/*
  * Prefill rows (gpt.py:40-41 + norm.py:6-19 over every prompt token): the
  * residual add of a projection's bf16 output a [M, C] (row stride lda) into
  * the fp32 stream x, x[m] += float(a[m]), then y[m] = bf16(weight * (x[m] *

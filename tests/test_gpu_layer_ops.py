@@ -120,6 +120,70 @@ def test_silu_mul():
     assert _bf16_ulps(got, ref) <= 1
 
 
+def _swiglu_ref(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """bf16(bf16(silu(bf16 g)) * bf16 u) from fp64 / fp32 sums (torch CPU)."""
+    gb = g.to(torch.bfloat16)
+    ub = u.to(torch.bfloat16)
+    return (torch.nn.functional.silu(gb.float()).to(torch.bfloat16).float() * ub.float()).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,I", [(1, 24), (7, 6144), (64, 6144), (100, 240), (130, 6144)])
+def test_linear_swiglu(M, I):
+    """Gate|up + SwiGLU in one launch (whole-K fp32 sums, interleaved packed
+    weight) against the fp64 sums taken through the same bf16 chain. The
+    device sums g, u differ from the fp64 ones by at most 1e-5 * (|x| @ |W|^T)
+    (bg, bu); with the bf16 roundings of g, u, SiLU and the product, each
+    output is within |d/dg| (bg + ulp g) + |d/du| (bu + ulp u) + 2 ulp of the
+    reference (d/dg = silu'(g) u, d/du = silu(g), ulp = 2^-8 relative), and
+    nearly all outputs are bit-equal to it and to the split-K partials path.
+    Columns past I of a strided output stay untouched."""
+    from tinytron_amd import ops
+
+    K = 2048
+    g = torch.Generator().manual_seed(M * 7 + I)
+    x_full = torch.randn(M, K + 8, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(I, K, generator=g) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn(I, K, generator=g) * 0.05).to(torch.bfloat16)
+    x = x_full.to(DEV)[:, :K]
+    pw = ops.PackedWeight(ops.interleave_gate_up(wg, wu).to(DEV))
+    out_full = torch.full((M, I + 8), float("nan"), dtype=torch.bfloat16, device=DEV)
+    got = ops.linear_swiglu(x, pw, out=out_full[:, :I])
+    torch.cuda.synchronize()
+    assert torch.isnan(out_full[:, I:].float()).all()
+    got = got.cpu()
+    xd = x_full[:, :K].double()
+    gd, ud = xd @ wg.double().T, xd @ wu.double().T
+    bg, bu = 1e-5 * (xd.abs() @ wg.double().abs().T), 1e-5 * (xd.abs() @ wu.double().abs().T)
+    ref = _swiglu_ref(gd, ud)
+    sig = torch.sigmoid(gd)
+    silu, dsilu = gd * sig, sig * (1 + gd * (1 - sig))
+    u2 = 2.0 ** -8
+    tol = (dsilu * ud).abs() * (bg + u2 * gd.abs()) + silu.abs() * (bu + u2 * ud.abs()) + 2 * u2 * (silu * ud).abs()
+    err = (got.double() - ref.double()).abs()
+    assert torch.all(err <= tol + 1e-30), float((err / (tol + 1e-30)).max())
+    assert float((got.view(torch.int16) == ref.view(torch.int16)).float().mean()) >= 0.95
+    if (2 * I) % 64 == 0:  # the same projection through split-K partials + silu_mul
+        P = ops.linear_partials(x, ops.PackedWeight(torch.cat([wg, wu]).to(DEV)), k_chunk=512)
+        old = ops.silu_mul(P).cpu()
+        assert float((old.view(torch.int16) == got.view(torch.int16)).float().mean()) >= 0.95
+        assert torch.all((old.double() - ref.double()).abs() <= tol + 1e-30)
+
+
+def test_linear_swiglu_rejects_unsupported():
+    from tinytron_amd import ops
+
+    assert ops.swiglu_supported(2048, 6144) and not ops.swiglu_supported(1024, 6144)
+    assert not ops.swiglu_supported(2048, 100)
+    x = torch.zeros(4, 1024, dtype=torch.bfloat16, device=DEV)
+    w = ops.PackedWeight(torch.zeros(48, 1024, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):
+        ops.linear_swiglu(x, w)  # K must be 2048
+    x = torch.zeros(4, 2048, dtype=torch.bfloat16, device=DEV)
+    w = ops.PackedWeight(torch.zeros(32, 2048, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):
+        ops.linear_swiglu(x, w)  # I = 16 is not a multiple of 24
+
+
 @pytest.mark.parametrize("C,with_addend", [(2048, True), (1024, False), (4096, True)])
 def test_add_rmsnorm_rows(C, with_addend):
     """Prefill rows: x += float(bf16 addend) exactly (strided addend rows),

@@ -123,6 +123,8 @@ SIGNATURES = {
     "tt_splitk_reduce_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_add_rmsnorm_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
     "tt_silu_mul_bf16": ([_vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
+    "tt_linear_swiglu_packed_bf16": ([_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp], ctypes.c_int),
+    "tt_swiglu_gemm_supported": ([_i64, _i64], ctypes.c_int),
     "tt_add_rmsnorm_rows_bf16": ([_vp, _vp, _i64, _vp, ctypes.c_float, _vp, _i64, _i64, _vp], ctypes.c_int),
     "tt_silu_mul_rows_bf16": ([_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp], ctypes.c_int),
     "tt_decode_attn_append_bf16": (_DECODE_APPEND_HEAD + _DECODE_APPEND_TAIL, ctypes.c_int),

@@ -776,6 +776,35 @@ int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t i
                   "silu_mul launch");
 }
 
+int tt_swiglu_gemm_supported(int64_t k, int64_t inter) { return tt::swiglu_gemm_supported(k, inter) ? 1 : 0; }
+
+int tt_linear_swiglu_packed_bf16(const void *x, int64_t ldx, const void *weight_packed, void *y, int64_t ldy,
+                                 int64_t m, int64_t inter, int64_t k, tt_stream_t stream) {
+  TT_CHECK(x && weight_packed && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(m >= 0 && m <= 65535 * 64 && inter > 0 && k > 0, TT_ERR_INVALID_ARGUMENT, "bad GEMM shape");
+  TT_CHECK(tt::swiglu_gemm_supported(k, inter), TT_ERR_UNSUPPORTED,
+           "the fused gate|up + SwiGLU GEMM takes K == 2048 and I %% 24 == 0 (K %lld, I %lld)", (long long)k,
+           (long long)inter);
+  TT_CHECK(inter < ((int64_t)1 << 30), TT_ERR_UNSUPPORTED, "intermediate size too large");
+  TT_CHECK(ldx >= k && ldx % 8 == 0 && ldy >= inter && ldy % 4 == 0, TT_ERR_INVALID_ARGUMENT,
+           "ldx must be >= K and a multiple of 8, ldy >= I and a multiple of 4");
+  TT_CHECK(ldx < ((int64_t)1 << 24), TT_ERR_UNSUPPORTED, "x row stride too large");
+  TT_CHECK(aligned(x, 16) && aligned(weight_packed, 16) && aligned(y, 8), TT_ERR_INVALID_ARGUMENT,
+           "x and weight must be 16-byte aligned, y 8-byte aligned");
+  if (m == 0) return ok();
+  tt::SwigluGemmArgs a{};
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = ldx;
+  a.w = static_cast<const uint16_t *>(weight_packed);
+  a.out = static_cast<uint16_t *>(y);
+  a.ldo = ldy;
+  a.M = (int)m;
+  a.I = (int)inter;
+  a.K = (int)k;
+  (void)hipGetLastError();
+  return from_hip(tt::launch_swiglu_gemm(a, (hipStream_t)stream), "linear_swiglu launch");
+}
+
 int tt_add_rmsnorm_rows_bf16(float *x, const void *a, int64_t lda, const float *weight, float eps, void *y, int64_t m,
                              int64_t c, tt_stream_t stream) {
   TT_CHECK(x && weight && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");

@@ -231,6 +231,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
   }
 }
 
+// SwiGLU with the reference's autocast rounding points (mlp.py:44-45): the
+// projections return bf16, F.silu runs in bf16, the product rounds to bf16.
+__device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
+  const float gb = round_bf16(g);
+  const float act = round_bf16(gb / (1.0f + expf(-gb)));
+  return f32_to_bf16_bits(act * round_bf16(u));
+}
+
 // Partials of the fused gate|up projection: columns [0, I) gate, [I, 2I) up.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, int64_t MN2, int I, int M,
                                                        uint16_t *y) {
@@ -246,12 +254,114 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
   const f32x4 u = sum[1];
   uint16_t out[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float gb = round_bf16(g[e]);
-    const float act = round_bf16(gb / (1.0f + expf(-gb)));
-    out[e] = f32_to_bf16_bits(act * round_bf16(u[e]));
-  }
+  for (int e = 0; e < 4; ++e) out[e] = swiglu_bf16(g[e], u[e]);
   *reinterpret_cast<uint2 *>(y + i) = make_uint2(out[0] | ((uint32_t)out[1] << 16), out[2] | ((uint32_t)out[3] << 16));
+}
+
+// Gate|up projection with SwiGLU in the epilogue (mlp.py:24-26, 44-45):
+// a[m][c] = swiglu(x[m] . Wg[c], x[m] . Wu[c]) over the whole K inside one
+// workgroup, so no split-K partials and no second launch. The weight is the
+// fragment-ordered [gate|up] matrix with its rows interleaved by 8: 16-row
+// block j holds gate rows 8j .. 8j+7, then up rows 8j .. 8j+7, so the MFMA
+// output puts gate row r of a block in lane (n + 16g), g < 2, and up row r in
+// lane (n + 16g) ^ 32.
+//
+// A workgroup owns kSwiBlocks 16-row blocks (8 kSwiBlocks output columns)
+// and 2 kSwiBlocks waves: wave (block, half) streams its 16 rows x K/2 (one
+// burst, 128 registers at K = 2048). The x rows (64 per m tile) reach LDS by
+// DMA (buffer_load ... lds, one 1 KiB row chunk per instruction, rows past M
+// read as zero) in two rounds of K/4 columns per half, the first issued
+// before the weight burst, the second after the first round's MFMAs (its
+// loads retire after the weights, which they queue behind). The two halves
+// of a block meet in LDS (sum half 0 + half 1), then the gate lanes exchange
+// with the up lanes and write 4 bf16 outputs each.
+constexpr int kSwiBlocks = 3;
+constexpr int kSwiK = 2048;  // the K this kernel is built for (x row quarter = one 1 KiB DMA)
+
+__global__ __launch_bounds__(64 * 2 * kSwiBlocks, 2) void swiglu_gemm_kernel(SwigluGemmArgs a) {
+  constexpr int KS = kSwiK / 64;       // k steps per wave (its half of K)
+  constexpr int KQ = kSwiK / 4;        // columns per half per round
+  constexpr int ROW = KQ + 8;          // padded LDS row (elements)
+  constexpr int kWaves = 2 * kSwiBlocks;
+  constexpr int kRows = 2 * 64;        // LDS rows per round: 2 halves x 64 x rows
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kRows * ROW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = wave >> 1;           // row block of this workgroup
+  const int half = wave & 1;           // K half
+  const int nb = blockIdx.x * kSwiBlocks + blk;
+  const int m0 = blockIdx.z * 64;
+  const int mrows = min(64, a.M - m0);
+
+  // x rows m0 .. m0 + mrows - 1; offsets past the last valid row's data read zero
+  const auto rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t *>(a.x) + (int64_t)m0 * a.ldx, (short)0,
+      (int)(((int64_t)(mrows - 1) * a.ldx + kSwiK) * 2), 0x00020000);
+  auto stage = [&](int round) {
+    for (int i = wave; i < kRows; i += kWaves) {  // i = h * 64 + row
+      const int h = i >> 6, r = i & 63;
+      const int col = h * (kSwiK / 2) + round * KQ;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + i * ROW), 16,
+                                               16 * lane + (int)(((int64_t)r * a.ldx + col) * 2), 0, 0, 0);
+    }
+  };
+
+  stage(0);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t *wrow = a.w + (((int64_t)nb * (kSwiK / 32) + half * KS) * 64 + lane) * 8;
+  u32x4 wf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) wf[s] = *reinterpret_cast<const u32x4 *>(wrow + 512 * s);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt((KS & 15) | (7 << 4) | (15 << 8) | (((KS >> 4) & 3) << 14));  // this wave's x DMA
+  __syncthreads();
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t *xrow = xs + (half * 64 + (lane & 15)) * ROW + 8 * (lane >> 4);
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    if (round == 1) {
+      __syncthreads();  // every wave is done with the first round's x
+      stage(1);
+      __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+      __syncthreads();
+    }
+#pragma unroll
+    for (int s = 0; s < KS / 2; ++s) {
+      const bf16x8 af = __builtin_bit_cast(bf16x8, wf[round * (KS / 2) + s]);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(xrow + mb * 16 * ROW + 32 * s);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, acc[mb], 0, 0, 0);
+      }
+    }
+  }
+
+  // the halves meet: half 0 finishes m blocks 0-1, half 1 blocks 2-3
+  __syncthreads();
+  f32x4 *red = reinterpret_cast<f32x4 *>(xs);  // [block][half][2][64]
+#pragma unroll
+  for (int j = 0; j < 2; ++j) red[((blk * 2 + half) * 2 + j) * 64 + lane] = acc[half == 0 ? 2 + j : j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int mb = half == 0 ? j : 2 + j;
+    const f32x4 other = red[((blk * 2 + (1 - half)) * 2 + j) * 64 + lane];
+    const f32x4 sum = half == 0 ? acc[mb] + other : other + acc[mb];
+    f32x4 up;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(sum[r], 32, 64);
+    const int row = 16 * mb + (lane & 15);
+    if (lane < 32 && row < mrows) {
+      uint16_t o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = swiglu_bf16(sum[r], up[r]);
+      *reinterpret_cast<uint2 *>(a.out + (int64_t)(m0 + row) * a.ldo + 8 * nb + 4 * (lane >> 4)) =
+          make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+    }
+  }
 }
 
 // Prefill rows (many tokens, bf16 projection outputs from a library GEMM):
@@ -398,6 +508,14 @@ hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, con
   }
 #undef TT_ADD_RMSNORM_CASE
 #undef TT_ADD_RMSNORM_LAUNCH
+  return hipGetLastError();
+}
+
+bool swiglu_gemm_supported(int64_t K, int64_t I) { return K == kSwiK && I > 0 && I % (8 * kSwiBlocks) == 0; }
+
+hipError_t launch_swiglu_gemm(const SwigluGemmArgs &a, hipStream_t stream) {
+  const dim3 grid((unsigned)(a.I / (8 * kSwiBlocks)), 1, (unsigned)((a.M + 63) / 64));
+  hipLaunchKernelGGL(swiglu_gemm_kernel, grid, dim3(128 * kSwiBlocks), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -126,6 +126,19 @@ struct SkinnyGemmArgs {
 };
 
 hipError_t launch_skinny_gemm(const SkinnyGemmArgs &a, int kc, hipStream_t stream);
+
+// Gate|up projection + SwiGLU in one launch (weights: fragment-ordered, rows
+// interleaved by 8 gate / 8 up); out [M, I] bf16, row stride ldo.
+struct SwigluGemmArgs {
+  const uint16_t *x;  // bf16 [M, K], row stride ldx
+  int64_t ldx;
+  const uint16_t *w;  // packed interleaved [2I/16][K/32][64][8]
+  uint16_t *out;
+  int64_t ldo;
+  int M, I, K;
+};
+bool swiglu_gemm_supported(int64_t K, int64_t I);
+hipError_t launch_swiglu_gemm(const SwigluGemmArgs &a, hipStream_t stream);
 hipError_t launch_reduce_bf16(const float *P, int S, int64_t MN, uint16_t *y, hipStream_t stream);
 hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, const float *w, float eps, uint16_t *y,
                               hipStream_t stream);

@@ -302,10 +302,18 @@ class GPT(nn.Module):
         ent = self._stacked.get(i)
         if ent is None or ent[0] != key:
             with torch.no_grad():
+                gu = (ops.interleave_gate_up(srcs[4], srcs[5]) if self._swiglu_fused()
+                      else torch.cat(srcs[4:6]))
                 ent = (key, ops.PackedWeight(torch.cat(srcs[:3])), ops.PackedWeight(srcs[3]),
-                       ops.PackedWeight(torch.cat(srcs[4:6])), ops.PackedWeight(srcs[6]))
+                       ops.PackedWeight(gu), ops.PackedWeight(srcs[6]))
             self._stacked[i] = ent
         return ent[1:]
+
+    def _swiglu_fused(self) -> bool:
+        """gate|up + SwiGLU as one whole-K launch (ops.linear_swiglu) where the
+        kernel takes the shape; else split-K partials + ops.silu_mul."""
+        c = self.config
+        return ops.swiglu_supported(c.hidden_size, c.intermediate_size)
 
     def _stacked_plain(self, i: int):
         """Layer i's q|k|v and gate|up weights stacked row-wise (plain bf16) for
@@ -348,6 +356,7 @@ class GPT(nn.Module):
         eps = self.lnf.variance_epsilon
         kc_c, kc_i, kc_o = self._k_chunk(C), self._k_chunk(c.intermediate_size), self._k_chunk_small(C)
         kc_gu = self._k_chunk_wide(C)
+        swiglu_fused = self._swiglu_fused()
         first = cache.get_layer_cache(0)
         lens = first.seq_lens_host
         if len(set(lens)) == 1 and lens[0] != position_offset:
@@ -367,8 +376,10 @@ class GPT(nn.Module):
                 y = layer.attend(q_rot.view(B, Hq, D))
             P = ops.linear_partials(y.view(B, C), wo, partials=pbuf, k_chunk=kc_o)
             h = ops.add_rmsnorm(x, blk.ln_2.weight, eps, partials=P)
-            P = ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_gu)
-            a = ops.silu_mul(P)                                      # [B, I]
+            if swiglu_fused:
+                a = ops.linear_swiglu(h, wgu)                        # [B, I], one launch, no partials
+            else:
+                a = ops.silu_mul(ops.linear_partials(h, wgu, partials=pbuf, k_chunk=kc_gu))
             P = ops.linear_partials(a, wd, partials=pbuf, k_chunk=kc_i)
             nxt = self.blocks[i + 1].ln_1.weight if i + 1 < len(self.blocks) else self.lnf.weight
             h = ops.add_rmsnorm(x, nxt, eps, partials=P)             # residual add + next norm (or lnf)

@@ -546,6 +546,45 @@ def silu_mul(partials: torch.Tensor, out: torch.Tensor | None = None) -> torch.T
     return out
 
 
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """[2I, K]: the gate and up weights [I, K] with rows interleaved by 8 (rows
+    16j .. 16j+7 = gate rows 8j .. 8j+7, rows 16j+8 .. 16j+15 = up rows 8j ..
+    8j+7), the row order linear_swiglu's packed weight takes."""
+    inter, K = gate.shape
+    if up.shape != gate.shape or inter % 8:
+        raise ValueError("gate and up must both be [I, K] with I % 8 == 0")
+    return torch.stack([gate.reshape(inter // 8, 8, K), up.reshape(inter // 8, 8, K)], dim=1).reshape(2 * inter, K)
+
+
+def swiglu_supported(K: int, inter: int) -> bool:
+    """Whether linear_swiglu takes this K and intermediate size."""
+    return bool(_lib.load().tt_swiglu_gemm_supported(int(K), int(inter)))
+
+
+def linear_swiglu(x: torch.Tensor, weight: "PackedWeight", out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(bf16(silu(bf16 g)) * bf16 u) [M, I] with g = x @ Wg^T, u = x @ Wu^T in
+    fp32 over the whole K, in one launch (mlp.py:24-26, 44-45 under autocast).
+    ``weight`` is PackedWeight(interleave_gate_up(Wg, Wu))."""
+    if not isinstance(weight, PackedWeight):
+        raise ValueError("linear_swiglu takes a PackedWeight of interleave_gate_up(gate, up)")
+    _require_cuda(x, weight.data)
+    if x.dtype != torch.bfloat16 or weight.data.dtype != torch.bfloat16:
+        raise ValueError("linear_swiglu takes bf16 x and weight")
+    M, ldx = _rows(x, "x")
+    N, K = weight.shape
+    if x.shape[1] != K or N % 2:
+        raise ValueError(f"x {tuple(x.shape)} does not match the weight {weight.shape}")
+    inter = N // 2
+    if out is None:
+        out = torch.empty(M, inter, dtype=torch.bfloat16, device=x.device)
+    if out.dtype != torch.bfloat16 or out.shape != (M, inter) or out.stride(1) != 1:
+        raise ValueError(f"out must be bf16 [{M}, {inter}] with a contiguous last dimension")
+    st = _lib.load().tt_linear_swiglu_packed_bf16(_ptr(x), ldx, _ptr(weight.data), _ptr(out), out.stride(0), M,
+                                                  inter, K, _stream(x.device))
+    _lib.check(st, "linear_swiglu")
+    return out
+
+
 def prefill_attention(q: torch.Tensor, layout: KVLayout, positions: torch.Tensor, max_seq_len: int,
                       new_lens: torch.Tensor | None = None, out: torch.Tensor | None = None,
                       sm_scale: float | None = None) -> torch.Tensor:
