@@ -311,8 +311,10 @@ __global__ __launch_bounds__(64 * 2 * kSwiBlocks, 2) void swiglu_gemm_kernel(Swi
   const uint16_t *wrow = a.w + (((int64_t)nb * (kSwiK / 32) + half * KS) * 64 + lane) * 8;
   u32x4 wf[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) wf[s] = *reinterpret_cast<const u32x4 *>(wrow + 512 * s);
-  __builtin_amdgcn_sched_barrier(0);
+  for (int s = 0; s < KS; ++s) {  // in consumption order: each k step waits only for its own loads
+    wf[s] = *reinterpret_cast<const u32x4 *>(wrow + 512 * s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   __builtin_amdgcn_s_waitcnt((KS & 15) | (7 << 4) | (15 << 8) | (((KS >> 4) & 3) << 14));  // this wave's x DMA
   __syncthreads();
 
