@@ -160,8 +160,8 @@ def e2e_c5(args, torch):
         "decode_tokens_per_sec": round(tps, 1),
         "decode_tokens_per_sec_graphs": graph_tps,
         "decode_path": "fused bf16 decode step (8 launches per layer: RoPE + append inside the attention launch "
-                       "pair, gate|up and SwiGLU in one launch; "
-                       "pair) launched eagerly + one-launch sampler; decode_tokens_per_sec_graphs replays the step "
+                       "pair, gate|up and SwiGLU in one launch) launched eagerly + one-launch sampler; "
+                       "decode_tokens_per_sec_graphs replays the step "
                        "from HIP graphs (the two captures inside the timed window; same tokens, checked)",
         "decode_steps": int(stats["decode_tokens"] // B),
         "decode_tokens_per_sec_fp8_kv": round(fp8_stats["decode_tokens_per_sec"], 1),
