@@ -31,6 +31,14 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-source additions. prefill_attn: MFMA accumulators in the VGPR form, with
+# AGPRs left to the register allocator as spill room. The head_dim-128 bf16
+# prefill kernel (4 column blocks at up to 512 registers a wave) otherwise keeps
+# its loop-carried O accumulators in VGPRs and copies them to AGPRs and back
+# around every PV: about 290 v_accvgpr moves per 32-key tile, a third of the
+# tile's VALU instructions. The other kernels of the file compile the same.
+SOURCE_FLAGS = {"prefill_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -54,7 +62,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     OBJ_DIR.mkdir(exist_ok=True)
     inc = ["-I", str(PKG_DIR.parent / "include")]
     objs = [OBJ_DIR / (Path(s).stem + ".o") for s in SOURCES]
-    cmds = [[hipcc(), *HIPCC_FLAGS, *inc, "-c", str(CSRC / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    cmds = [[hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(s, []), *inc, "-c", str(CSRC / s), "-o", str(o)]
+            for s, o in zip(SOURCES, objs)]
     jobs = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 16)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         for f in [pool.submit(_run, c, verbose) for c in cmds]:
