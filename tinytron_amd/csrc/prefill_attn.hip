@@ -83,38 +83,20 @@ __device__ __forceinline__ bool qk_softmax_pf(float scale_log2, const f32x4 (&kc
   // st.m = -inf). A column moves iff one of its four lanes' own maxima is past
   // it (scaling by scale > 0 and rounding keep the order, -inf stays -inf), so
   // the maxima across the lane groups need only be formed when some column
-  // moves (same results). At head_dim 128 with a bf16 cache (4 column blocks
-  // at 512 registers a wave) that branch measured slower, and the maxima are
-  // formed on every tile there.
-  bool rescale;
-  float m_new;
-  if constexpr (D == 128 && !kFP8) {
+  // moves (same results).
+  const bool lane_past = (kFP8 ? mx : mx * scale_log2) > st.m + kLazyMax;
+  const bool rescale = __builtin_amdgcn_ballot_w64(lane_past) != 0;  // wave-uniform
+  alpha = 1.0f;
+  float m_new = st.m;
+  if (rescale) {  // across the four lane groups (lanes n, n+16, n+32, n+48 hold column n)
     const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     mx = mx2(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
     const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     mx = mx2(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
-    mx *= scale_log2;  // scale > 0: the maximum commutes with it (-inf stays -inf)
-    const bool bump = mx > st.m + kLazyMax;
-    rescale = __builtin_amdgcn_ballot_w64(bump) != 0;  // wave-uniform
-    m_new = bump ? mx : st.m;  // finite from the first tile on
-    alpha = 1.0f;
-    if (rescale) alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    if constexpr (!kFP8) mx *= scale_log2;
+    m_new = mx > st.m + kLazyMax ? mx : st.m;
+    alpha = __builtin_amdgcn_exp2f(st.m - m_new);
     st.m = m_new;
-  } else {
-    const bool lane_past = (kFP8 ? mx : mx * scale_log2) > st.m + kLazyMax;
-    rescale = __builtin_amdgcn_ballot_w64(lane_past) != 0;  // wave-uniform
-    alpha = 1.0f;
-    m_new = st.m;
-    if (rescale) {  // across the four lane groups (lanes n, n+16, n+32, n+48 hold column n)
-      const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = mx2(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
-      const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = mx2(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
-      if constexpr (!kFP8) mx *= scale_log2;
-      m_new = mx > st.m + kLazyMax ? mx : st.m;
-      alpha = __builtin_amdgcn_exp2f(st.m - m_new);
-      st.m = m_new;
-    }
   }
   float p[8];
 #pragma unroll
