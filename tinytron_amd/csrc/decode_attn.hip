@@ -358,7 +358,8 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
     auto load_rows = [&](int k0) {
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const int k = k0 + u < nk ? k0 + u : nk - 1;  // repeats are added with weight 0 below
+        if (k0 + u >= nk) break;  // uniform: rows past the batch's pieces are neither loaded nor added
+        const int k = k0 + u;
         const int64_t sk = seg + w0 + __builtin_amdgcn_readlane(slot_rel, k);
 #pragma unroll
         for (int h = 0; h < kMaxG; ++h)
