@@ -85,6 +85,11 @@ C5 = dict(num_layer=24, hidden_size=2048, num_attention_heads=32, num_key_value_
           intermediate_size=6144, init_std=0.02, batch=64, lo=64, hi=2048, page=16)
 
 
+def log(msg: str) -> None:
+    """Progress line on stderr (the JSON result alone goes to stdout)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
 def host_threads(torch) -> int:
     """Threads for the CPU baselines: the CPUs this process may run on, capped by
     OMP_NUM_THREADS when set (the GPU box gives a 16-CPU share)."""
@@ -174,70 +179,100 @@ def e2e_c5(args, torch):
         "cpu_baseline": None,
         "sampler": sampler_timing(torch),
     }
+    cpu_job = None
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = e2e_cpu_baseline(model, cfg, prompt, torch)
+        sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+        ctx = int(round(sum(lens) / B + steps / 2))
+
+        def cpu_job():
+            out["sampler"]["cpu_baseline"] = sampler_cpu_baseline(torch)
+            return e2e_cpu_baseline(sd, cfg, ctx, torch)
     del eng, model
     torch.cuda.empty_cache()
-    return out
+    return out, cpu_job
 
 
 def sampler_timing(torch, iters=50):
     """Microseconds per call of the one-launch sampler on C5's logits
-    ([64, 32000] bf16) beside the reference's op sequence on the same device
-    (filter_logits + softmax + multinomial, sampler.py:6-48)."""
-    from oracle.ref_path import filter_logits
+    ([64, 32000] bf16), HIP events on the stream it runs on."""
     from tinytron_amd import ops
 
+    logits = _sampler_logits(torch).cuda()
+    st = {name: timed_steps(torch, fn, iters, 5) for name, fn in (
+        ("greedy_us", lambda: ops.sample_tokens(logits, top_k=1)),
+        ("top_k50_top_p0.9_T0.8_us", lambda: ops.sample_tokens(logits, 0.8, 50, 0.9, 1, 0)),
+        ("top_p0.9_logprob_us", lambda: ops.sample_tokens(logits, 1.0, None, 0.9, 1, 0, return_logprob=True)))}
+    out = {"logits": "[64, 32000] bf16", "statistic": "median of per-call HIP event gaps"}
+    out.update({name: round(s["median_ms"] * 1e3, 2) for name, s in st.items()})
+    return out
+
+
+def _sampler_logits(torch):
     g = torch.Generator().manual_seed(0)
-    logits = (torch.randn(C5["batch"], C5["vocab_size"], generator=g) * 3).to(torch.bfloat16).cuda()
+    return (torch.randn(C5["batch"], C5["vocab_size"], generator=g) * 3).to(torch.bfloat16)
 
-    def timed(fn):
-        for _ in range(5):
-            fn()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
+
+def sampler_cpu_baseline(torch, iters=20):
+    """The reference's sampling op sequence (filter_logits + softmax +
+    multinomial, sampler.py:6-48, restated in oracle.ref_path) on the host, per
+    call on the same logits as sampler_timing."""
+    from oracle.ref_path import filter_logits
+
+    threads = host_threads(torch)
+    logits = _sampler_logits(torch)
+
+    def per_call_us(t, k, p):
+        torch.multinomial(torch.softmax(filter_logits(logits, t, k, p), dim=-1), 1)
+        t0 = time.perf_counter()
         for _ in range(iters):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return round(e0.elapsed_time(e1) * 1e3 / iters, 2)
+            torch.multinomial(torch.softmax(filter_logits(logits, t, k, p), dim=-1), 1)
+        return round((time.perf_counter() - t0) / iters * 1e6, 1)
 
-    def ref(t, k, p):
-        return torch.multinomial(torch.softmax(filter_logits(logits, t, k, p), dim=-1), 1)
-
-    return {
-        "logits": "[64, 32000] bf16",
-        "greedy_us": timed(lambda: ops.sample_tokens(logits, top_k=1)),
-        "top_k50_top_p0.9_T0.8_us": timed(lambda: ops.sample_tokens(logits, 0.8, 50, 0.9, 1, 0)),
-        "top_p0.9_logprob_us": timed(lambda: ops.sample_tokens(logits, 1.0, None, 0.9, 1, 0, return_logprob=True)),
-        "reference_ops_greedy_us": timed(lambda: ref(1.0, 1, None)),
-        "reference_ops_top_k50_top_p0.9_T0.8_us": timed(lambda: ref(0.8, 50, 0.9)),
-    }
+    return {"greedy_us": per_call_us(1.0, 1, None), "top_k50_top_p0.9_T0.8_us": per_call_us(0.8, 50, 0.9),
+            "unit": "us per call", "cores": threads, "kind": "port",
+            "sample": f"{iters} calls per setting on the same [64, 32000] bf16 logits, torch on the host"}
 
 
-def e2e_cpu_baseline(model, cfg, prompt, torch, prompt_cap=32, n_steps=6):
+def e2e_cpu_baseline(sd, cfg, ctx, torch, budget_s=10.0, max_steps=32):
     """The reference's op sequence (oracle.ref_model, fp32 on the host, as the
-    reference runs without a GPU) at C5's batch of 64: every sequence's first
-    prompt_cap tokens (a uniform batch, as the reference's one batch-wide length
-    requires) prefilled untimed, then n_steps greedy decode steps timed."""
+    reference runs without a GPU) on C5's decode shape: batch 64, every layer's
+    reference-layout cache (H_q-expanded LayerPagedKVCache) filled, untimed, to
+    ctx tokens -- the mean context of C5's decode (mean prompt length + half the
+    steps) -- then n_steps greedy decode steps timed (after one untimed step).
+    Decode time does not depend on the cached values, and the reference's one
+    batch-wide length cannot express ragged prompts, so a uniform batch at the
+    mean length stands in for the ragged one. Steps run until budget_s of
+    them is spent (at most max_steps)."""
     from oracle.ref_model import RefGPT
 
     threads = host_threads(torch)
-    sample = prompt[:, :prompt_cap].contiguous()
-    B = sample.shape[0]
-    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    B = C5["batch"]
     ref = RefGPT(sd, cfg.num_layer, cfg.num_attention_heads, cfg.num_key_value_heads)
-    t0 = time.perf_counter()
-    _, tps, _ = ref.generate_greedy(sample, n_steps, prompt_cap + n_steps + 1, page_size=16)
-    wall = time.perf_counter() - t0
-    del ref, sd
-    return {"value": round(tps, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"batch {B} (the C5 batch), each prompt capped at its first {prompt_cap} tokens, {n_steps} "
-                      f"greedy decode steps timed, fp32 on the host through the reference op sequence (H_q-expanded "
-                      f"LayerPagedKVCache); the short context understates the CPU's attention work, so the rate "
-                      f"is an upper bound for the U[64, 2048] prompts",
-            "seconds_including_prefill": round(wall, 2)}
+    caches = ref.new_caches(B, ctx + max_steps + 2, page_size=C5["page"])
+    g = torch.Generator().manual_seed(0)
+    tile = torch.randn(1, ref.hq, 64, ref.D, generator=g)  # a random 64-token pattern, repeated
+    pattern = tile.repeat(1, 1, (ctx + 63) // 64, 1)[:, :, :ctx].expand(B, -1, -1, -1)
+    for c in caches:
+        c._k_flat[:, :, :ctx].copy_(pattern)
+        c._v_flat[:, :, :ctx].copy_(pattern)
+        c.current_length = ctx
+    tok = torch.randint(0, cfg.vocab_size, (B, 1), generator=g)
+    with torch.no_grad():
+        logits = ref.forward(tok, caches, ctx)  # untimed first step
+        t0 = time.perf_counter()
+        n_steps = 0
+        while n_steps < max_steps and (n_steps == 0 or time.perf_counter() - t0 < budget_s):
+            tok = torch.argmax(logits[:, -1].float(), dim=-1)[:, None]
+            logits = ref.forward(tok, caches, ctx + 1 + n_steps)
+            n_steps += 1
+        wall = time.perf_counter() - t0
+    del ref, caches
+    return {"value": round(B * n_steps / wall, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"batch {B} (the C5 batch) at a uniform context of {ctx} tokens (C5's mean decode context: "
+                      f"mean prompt + half of the decode steps), every layer's H_q-expanded LayerPagedKVCache "
+                      f"filled untimed; {n_steps} greedy decode steps timed after one untimed step, fp32 on the "
+                      f"host through the reference op sequence (the reference has no ragged batches)",
+            "seconds": round(wall, 2)}
 
 
 def c1_record(args, torch):
@@ -245,7 +280,6 @@ def c1_record(args, torch):
     32000, fp32, prompt 128, 64 greedy steps, contiguous cache): the engine on
     the GPU (fp32, the CPU path's arithmetic) and the reference's op sequence on
     the host with the paged cache and with the tuple-concat cache."""
-    from oracle.ref_model import RefGPT
     from tinytron_amd.engine import InferenceEngine
     from tinytron_amd.model import GPT, ModelConfig
 
@@ -267,7 +301,13 @@ def c1_record(args, torch):
            "decode_path": "module path in fp32 (d 512 takes no fused kernels): RoPE + append + attention in one "
                           "launch pair per layer, graph-replayed steps"}
     del eng, model
-    if not args.no_cpu_baseline:
+    tokens = tokens.cpu()
+
+    def cpu_job():
+        """The whole C1 workload on the host (runs after every GPU leg): fills
+        out['cpu_baseline'] and out['greedy_tokens_equal_cpu']."""
+        from oracle.ref_model import RefGPT
+
         threads = host_threads(torch)
         ref = RefGPT(sd, cfg.num_layer, cfg.num_attention_heads, cfg.num_key_value_heads)
         res = {}
@@ -277,14 +317,15 @@ def c1_record(args, torch):
             ref_tokens, tps, _ = ref.generate_greedy(prompt, C1["steps"], cfg.block_size, page_size=C1["page"],
                                                      tuple_cache=tuple_cache)
             res[name] = (tps, ref_tokens)
-        out["greedy_tokens_equal_cpu"] = bool(torch.equal(tokens.cpu(), res["paged"][1]))
+        out["greedy_tokens_equal_cpu"] = bool(torch.equal(tokens, res["paged"][1]))
         out["cpu_baseline"] = {
             "value": round(res["paged"][0], 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "value_tuple_concat_cache": round(res["tuple_concat"][0], 2),
             "sample": "the whole C1 workload: fp32 on the host through the reference op sequence with "
                       "LayerPagedKVCache (value) and with use_paged_kv_cache=False's concatenated K/V "
                       "(value_tuple_concat_cache)"}
-    return out
+
+    return out, (None if args.no_cpu_baseline else cpu_job)
 
 
 def build_workload(cfg, seed, torch, ops):
@@ -485,11 +526,50 @@ def measured_traffic(config: str):
     return None
 
 
-def run_config(name, args, torch, ops, with_cpu):
-    """Time one attention config: the decode step (fused launch pair for bf16
-    caches, RoPE + append then attention for fp8), the two-launch step, and the
-    attention operator alone, each over args.steps steps after args.warmup,
-    bracketed by HIP events on the stream the kernels run on."""
+def timed_steps(torch, fn, steps, warmup, min_warm_s=0.1):
+    """Per-step GPU times of `steps` calls of fn on torch's current stream (the
+    stream the library's kernels are launched on): `warmup` untimed calls, more
+    until at least min_warm_s of them have run (clocks and caches settled), a
+    synchronize, then one event before the first step and one after every
+    step, so that step i's time is the gap between events i and i + 1 and the
+    steps together span the whole timed region. Returns the median (the
+    per-step figure reported), mean, min and max in ms."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < min_warm_s:
+        fn()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    steps = max(int(steps), 1)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    mid = steps // 2
+    median = per[mid] if steps % 2 else 0.5 * (per[mid - 1] + per[mid])
+    return {"median_ms": median, "mean_ms": ev[0].elapsed_time(ev[steps]) / steps, "min_ms": per[0],
+            "max_ms": per[-1], "warmup_calls": n}
+
+
+def spread(st):
+    """Per-step spread record (µs) of a timed_steps result."""
+    return {"median_us": round(st["median_ms"] * 1e3, 2), "mean_us": round(st["mean_ms"] * 1e3, 2),
+            "min_us": round(st["min_ms"] * 1e3, 2), "max_us": round(st["max_ms"] * 1e3, 2),
+            "warmup_calls": st["warmup_calls"]}
+
+
+def run_config(name, args, torch, ops):
+    """Time one attention config on the GPU: the decode step (fused launch pair
+    for bf16 caches, RoPE + append then attention for fp8), the two-launch step,
+    and the attention operator alone, each over args.steps steps (per-step HIP
+    events on the stream the kernels run on, median reported) after a warm-up
+    of at least args.warmup steps and 100 ms. Returns the record and the
+    workload (kept for the CPU baseline, which runs after every GPU leg)."""
     cfg = CONFIGS[name]
     wl = build_workload(cfg, args.seed, torch, ops)
     B, hq, D = cfg["batch"], cfg["hq"], cfg["head_dim"]
@@ -519,23 +599,12 @@ def run_config(name, args, torch, ops, with_cpu):
         ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
                              split_tokens=split, workspace=ws)
 
-    def timed(fn, warmup):
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / max(args.steps, 1)
-
     # each timed region gets its own warm-up: a kernel's first launch loads its code
     # object (~0.6 ms), which untimed warm-up keeps out of the per-step figures
-    ms = timed(step, args.warmup)
-    two_ms = timed(two_launch_step, args.warmup)  # the same step as two launches (RoPE + append, then attention)
-    attn_ms = timed(attn_only, args.warmup)       # the dominant operator alone (q rotated by the step above)
+    st_step = timed_steps(torch, step, args.steps, args.warmup)
+    st_two = timed_steps(torch, two_launch_step, args.steps, args.warmup)  # RoPE + append, then attention
+    st_attn = timed_steps(torch, attn_only, args.steps, args.warmup)  # the dominant operator alone (q rotated above)
+    ms, two_ms, attn_ms = st_step["median_ms"], st_two["median_ms"], st_attn["median_ms"]
     step_bytes, attn_bytes, tokens = algorithmic_bytes(cfg, wl["total"])
     value = step_bytes / (ms * 1e-3) / 1e9
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
@@ -544,6 +613,8 @@ def run_config(name, args, torch, ops, with_cpu):
         "unit": "GB/s",
         "ms_per_step": round(ms, 5),
         "ms_per_step_two_launches": round(two_ms, 5),
+        "per_step": {"step": spread(st_step), "two_launch_step": spread(st_two), "attention": spread(st_attn),
+                     "statistic": "median of per-step HIP event gaps (ms_per_step, value, roofline.avg_us)"},
         "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
         "dtype": "fp8-e4m3 cache, bf16 q/out" if cfg["fp8"] else "bf16",
         "config": {
@@ -572,12 +643,8 @@ def run_config(name, args, torch, ops, with_cpu):
         },
         "cpu_baseline": None,
     }
-    if with_cpu:
-        rec["cpu_baseline"] = cpu_baseline(cfg, wl, torch, args.cpu_seconds, sample=CPU_SAMPLE.get(name),
-                                           seed=args.seed)
-    del wl, layout, q_rot, out, ws
-    torch.cuda.empty_cache()
-    return rec
+    del layout, q_rot, out, ws
+    return rec, wl
 
 
 def main():
@@ -595,7 +662,10 @@ def main():
         return 1
     torch.cuda.set_device(0)
     if args.e2e_only:
-        print(json.dumps({"e2e": e2e_c5(args, torch)}), flush=True)
+        rec, job = e2e_c5(args, torch)
+        if job is not None:
+            rec["cpu_baseline"] = job()
+        print(json.dumps({"e2e": rec}), flush=True)
         return 0
 
     # a plain copy of known size, for scaling rocprof FETCH/WRITE counters
@@ -604,7 +674,15 @@ def main():
     calib_dst.copy_(calib)
     del calib, calib_dst
 
-    head = run_config(args.config, args, torch, ops, not args.no_cpu_baseline)
+    # every GPU leg first, then the host-only CPU baselines, so that no timed GPU
+    # region follows seconds of host-only work
+    names = [args.config] + [n for n in args.nested.split(",") if n and n != args.config]
+    recs, workloads = {}, {}
+    for name in names:
+        recs[name], workloads[name] = run_config(name, args, torch, ops)
+        log(f"{name}: step {recs[name]['ms_per_step'] * 1e3:.1f} us, attention {recs[name]['roofline']['avg_us']} us "
+            f"({recs[name]['roofline']['frac']:.4f} of peak)")
+    head = recs[args.config]
     result = {
         "metric": METRIC,
         "value": head["value"],
@@ -622,15 +700,34 @@ def main():
         "pct_of_peak_hbm": head["pct_of_peak_hbm"],
         "config": head["config"],
         "roofline": head["roofline"],
-        "cpu_baseline": head["cpu_baseline"],
+        "per_step": head["per_step"],
+        "cpu_baseline": None,
         "host": host_info(torch),
     }
-    for name in [n for n in args.nested.split(",") if n and n != args.config]:
-        result[name] = run_config(name, args, torch, ops, not args.no_cpu_baseline)
+    for name in names[1:]:
+        result[name] = recs[name]
+    cpu_jobs = []
     if not args.no_c1:
-        result["c1"] = c1_record(args, torch)
+        result["c1"], job = c1_record(args, torch)
+        cpu_jobs.append(job)
+        log(f"c1: {result['c1']['decode_tokens_per_sec']} tokens/s")
     if not args.no_e2e:
-        result["e2e"] = e2e_c5(args, torch)
+        result["e2e"], job = e2e_c5(args, torch)
+        log(f"e2e: {result['e2e']['decode_tokens_per_sec']} tokens/s")
+        if job is not None:
+            cpu_jobs.append(lambda j=job: result["e2e"].__setitem__("cpu_baseline", j()))
+    if not args.no_cpu_baseline:
+        for name in names:
+            target = result if name == args.config else result[name]
+            target["cpu_baseline"] = cpu_baseline(CONFIGS[name], workloads[name], torch, args.cpu_seconds,
+                                                  sample=CPU_SAMPLE.get(name), seed=args.seed)
+            log(f"{name} cpu baseline: {target['cpu_baseline']['value']} GB/s")
+            del workloads[name]
+            torch.cuda.empty_cache()
+        for job in cpu_jobs:
+            if job is not None:
+                job()
+                log("cpu baseline done")
     print(json.dumps(result), flush=True)
     return 0
 

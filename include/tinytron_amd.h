@@ -507,8 +507,11 @@ int tt_silu_mul_rows_bf16(const void *g, int64_t ldg, const void *u, int64_t ldu
  * tt_sample_workspace_bytes(m, vocab, top_k)): with 2 <= top_k <= 64, V >
  * 8192 and no logprobs rows, every 8192-logit chunk of a row first reduces to
  * its top-k candidates on a workgroup of its own, and the row is decided from
- * those (same tokens and log-probabilities as the one-workgroup-per-row path,
- * which runs when workspace is NULL or a row's candidates cannot decide it).
+ * those (the same tokens as the one-workgroup-per-row path, which runs when
+ * workspace is NULL or a row's candidates cannot decide it; token
+ * log-probabilities agree with that path's to within the rounding of the
+ * exp-sum order: this path adds them in rank order, that one by a block
+ * reduction). More than 65535 rows always take the one-workgroup-per-row path.
  * Calls that share a workspace must not overlap.
  */
 int tt_sample_bf16(const void *logits, int64_t ld, int64_t m, int64_t vocab, float temperature, int64_t top_k,

@@ -112,18 +112,23 @@ def quantize_e4m3_rows(x_f32: np.ndarray):
     """Per-row symmetric fp8 quantization: this build's fp8-e4m3 cache format
     (the reference has no fp8 cache; one scale per (token, head) row).
 
-    For each row (last axis = head_dim): absmax = max|x| in fp32,
-    scale = absmax / 448 (fp32 division, round to nearest), q = e4m3(x / scale)
-    with fp32 division; an all-zero row stores zeros with scale 0.
+    For each row (last axis = head_dim): absmax = max|x| in fp32 (NaN if the
+    row holds a NaN), scale = absmax / 448 (fp32 division, round to nearest),
+    q = e4m3(x / scale) with fp32 division; an all-zero row stores zeros with
+    scale 0, and a row whose scale is not finite (it holds a NaN or an
+    infinity, which the format cannot represent) stores NaN codes (0x7F).
     Returns (codes uint8 [..., D], scales fp32 [...]).
     """
     x = np.asarray(x_f32, dtype=np.float32)
-    absmax = np.max(np.abs(x), axis=-1).astype(np.float32)
-    scale = (absmax / np.float32(E4M3_MAX)).astype(np.float32)
-    safe = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
-    ratio = (x / safe[..., None]).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        absmax = np.max(np.abs(x), axis=-1).astype(np.float32)
+        scale = (absmax / np.float32(E4M3_MAX)).astype(np.float32)
+        bad = ~np.isfinite(scale)
+        safe = np.where((scale == 0) | bad, np.float32(1.0), scale).astype(np.float32)
+        ratio = np.where(bad[..., None], np.float32(0.0), x / safe[..., None]).astype(np.float32)
     codes = e4m3fn_encode(ratio)
     codes = np.where((scale == 0)[..., None], np.uint8(0), codes).astype(np.uint8)
+    codes = np.where(bad[..., None], np.uint8(_E4M3_NAN), codes).astype(np.uint8)
     return codes, scale
 
 

@@ -149,13 +149,18 @@ def test_c5_fp8_kv_cache_stays_close_to_bf16(c5):
         del cache
     a, b = runs
     rel = (a - b).norm(dim=-1) / a.norm(dim=-1)      # [steps + 1, B]
-    agree = float((a.argmax(-1) == b.argmax(-1)).float().mean())
+    top1 = a.argmax(-1) == b.argmax(-1)
+    agree = float(top1.float().mean())
+    first = float(top1[0].float().mean())  # the prefill's logits: the first generated token
     print(f"fp8 vs bf16 KV: row-relative L2 mean {float(rel.mean()):.3e} max {float(rel.max()):.3e}, "
-          f"top-1 agreement {agree:.3f}", flush=True)
+          f"top-1 agreement {agree:.3f} (first token {first:.3f})", flush=True)
     # e4m3 keeps 3 mantissa bits (|error| <= 1/16 of the value, ~2 % rms) per K/V
-    # element; through 24 layers the logits move by a few percent of their norm
-    assert float(rel.mean()) <= 0.1 and float(rel.max()) <= 0.25
-    assert agree >= 0.85
+    # element; through 24 layers the logits move by a few percent of their norm.
+    # Bounds set from the measured distribution of this seeded batch (mean 3.4e-2,
+    # max 0.17, top-1 93 %, first token 96.9 %), so that an fp8 accuracy
+    # regression of even 1.5x fails.
+    assert float(rel.mean()) <= 0.05 and float(rel.max()) <= 0.22
+    assert agree >= 0.9 and first >= 0.95
 
 
 @torch.no_grad()

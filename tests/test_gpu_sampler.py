@@ -224,3 +224,33 @@ def test_greedy_kernel_matches_full_sampler_on_ties(top_p):
     want[3] = 0.0
     assert torch.allclose(l1.cpu(), want, atol=1e-6)
     assert int(t1[0]) == 100 and int(t1[3]) == 2000
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p", CASES)
+def test_filter_logits_matches_oracle(temperature, top_k, top_p):
+    """tinytron_amd.sampler.filter_logits (the reference's exported function,
+    sampler.py:6-36): -inf exactly where the oracle filters, logits / T elsewhere."""
+    from tinytron_amd.sampler import filter_logits
+
+    M, V = 16, 32000
+    x = _logits(M, V, torch.bfloat16, seed=11 * V + (top_k or 0))
+    xn = _np(x)
+    got = filter_logits(x.to(DEV), temperature, top_k, top_p).cpu().numpy()
+    want = osm.filter_logits(xn, temperature, top_k, top_p)
+    rows = np.arange(M)
+    if top_p is not None:
+        rows = np.flatnonzero(osm.top_p_margin(xn, temperature, top_k, top_p) > 1e-6)
+        assert len(rows) >= M - 2
+    for r in rows:
+        fin = np.isfinite(want[r])
+        assert np.array_equal(np.isfinite(got[r]), fin), f"row {r}: kept set differs"
+        # the kept values are the reference's own op, logits / temperature, run by
+        # torch on the device (which multiplies by the reciprocal): within one fp32
+        # ulp of the host's correctly rounded division, equal at temperature 1
+        expect = (x[r].float() / temperature if temperature != 1.0 else x[r].float()).numpy()
+        if temperature == 1.0:
+            assert np.array_equal(got[r][fin], expect[fin]), f"row {r}: kept values differ"
+        else:
+            assert np.allclose(got[r][fin], expect[fin], rtol=2.4e-7, atol=0), f"row {r}: kept values differ"
+    with pytest.raises(ValueError):
+        filter_logits(x.to(DEV), temperature=0.0)

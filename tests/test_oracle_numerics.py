@@ -113,3 +113,30 @@ def test_quantize_matches_torch_cast_of_ratio():
     ratio = torch.from_numpy(x) / torch.from_numpy(scales)[:, None]
     ref = ratio.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(codes, ref)
+
+
+def test_quantize_rows_with_nan_or_inf_store_nan_codes():
+    """A row holding a NaN or an infinity has a non-finite scale (torch's amax
+    propagates NaN, as here) and stores NaN codes throughout; finite rows are
+    unaffected by their neighbours; an all-zero row stays zeros."""
+    x = np.zeros((5, 16), np.float32)
+    x[0, :] = np.linspace(-3, 3, 16)
+    x[1, :] = np.linspace(-3, 3, 16)
+    x[1, 4] = np.nan
+    x[2, :] = 1.0
+    x[2, 9] = np.inf
+    x[3, :] = -2.0
+    x[3, 0] = -np.inf
+    codes, scales = nm.quantize_e4m3_rows(x)
+    assert np.isnan(scales[1]) and np.isinf(scales[2]) and np.isinf(scales[3])
+    assert np.all(codes[1:4] == 0x7F)
+    assert scales[4] == 0 and np.all(codes[4] == 0)
+    want0, s0 = nm.quantize_e4m3_rows(x[:1])
+    assert np.array_equal(codes[0], want0[0]) and scales[0] == s0[0]
+    # torch's row recipe agrees on NaN-ness for the non-finite rows
+    t = torch.from_numpy(x)
+    ts = t.abs().amax(-1) / 448.0
+    assert torch.equal(torch.isfinite(ts), torch.from_numpy(np.isfinite(scales)))
+    # a planted mistake -- an absmax that skips NaN (fmax) -- gives finite codes
+    planted = np.nanmax(np.abs(x[1])) / np.float32(448.0)
+    assert np.isfinite(planted) and not np.isfinite(scales[1])

@@ -284,7 +284,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   const int64_t ws_waves =
       exact_slots ? tt::balanced_stream_waves((int)head_dim, batch, num_kv_heads, max_seq_len) : tt::kMaxStreamWaves;
   if (balanced) {
-    TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens) < ((int64_t)1 << 31),
+    // the per-sequence line prefix (int32) counts each sequence's tiles plus its segment start-up charge
+    TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens + tt::kStreamSegCost) < ((int64_t)1 << 31),
              TT_ERR_UNSUPPORTED, "batch * max_seq_len is too large for the balanced partition");
     need = balanced_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, ws_waves);
   } else {
@@ -535,7 +536,7 @@ int sample_common(bool f32, const void *logits, int64_t ld, int64_t m, int64_t v
   a.logprobs = logprobs;
   a.ld_lp = ld_logprobs;
   a.vec_out = logprobs != nullptr && aligned(logprobs, 16) && ld_logprobs % 4 == 0;
-  a.cand_chunks = tt::sample_cand_chunks(vocab, a.top_k, logprobs != nullptr);
+  a.cand_chunks = tt::sample_cand_chunks(m, vocab, a.top_k, logprobs != nullptr);
   a.cand = nullptr;
   if (workspace != nullptr && a.cand_chunks > 0) {
     const size_t need = (size_t)m * a.cand_chunks * sizeof(tt::CandRecord);
@@ -889,7 +890,7 @@ int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_stri
 
 size_t tt_sample_workspace_bytes(int64_t m, int64_t vocab, int64_t top_k) {
   if (m <= 0 || vocab <= 0) return 0;
-  const int chunks = tt::sample_cand_chunks(vocab, top_k > 0 && top_k < vocab ? top_k : 0, false);
+  const int chunks = tt::sample_cand_chunks(m, vocab, top_k > 0 && top_k < vocab ? top_k : 0, false);
   return (size_t)m * chunks * sizeof(tt::CandRecord);
 }
 

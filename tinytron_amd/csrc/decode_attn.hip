@@ -558,15 +558,15 @@ __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const Decode
         }
       } else {
         // per-(token, head) symmetric scale: absmax / 448, codes e4m3fn(x / scale)
-        const float kscale = wave_max(fmaxf(fabsf(k1), fabsf(k2))) / 448.0f;
-        const float vscale = wave_max(fmaxf(fabsf(v1), fabsf(v2))) / 448.0f;
+        const float kscale = wave_max_nan(absmax2(0.f, k1, k2)) / 448.0f;
+        const float vscale = wave_max_nan(absmax2(0.f, v1, v2)) / 448.0f;
         uint8_t *kcache = static_cast<uint8_t *>(const_cast<void *>(a.k_cache));
         uint8_t *vcache = static_cast<uint8_t *>(const_cast<void *>(a.v_cache));
         if (active) {
-          kcache[off + lane] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k1 / kscale);
-          kcache[off + H + lane] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k2 / kscale);
-          vcache[off + lane] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v1 / vscale);
-          vcache[off + H + lane] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v2 / vscale);
+          kcache[off + lane] = e4m3_row_code(k1, kscale);
+          kcache[off + H + lane] = e4m3_row_code(k2, kscale);
+          vcache[off + lane] = e4m3_row_code(v1, vscale);
+          vcache[off + H + lane] = e4m3_row_code(v2, vscale);
         }
         if (lane == 0) {
           const_cast<float *>(a.k_scale)[off / D] = kscale;
@@ -732,7 +732,7 @@ constexpr int stream_blocks_per_cu(int head_dim) { return head_dim == 64 ? 2 : 1
 // segments gets fewer tiles. Measured (fused step, 0 -> 2): C3 406 -> 387 us,
 // C4 802 -> 766 us, C2 113 -> 110 us, C5 layer 39.3 -> 37.8 us; 1, 3 and 4
 // were as good or worse on every config.
-constexpr int stream_seg_cost(int /*head_dim*/) { return 2; }
+constexpr int stream_seg_cost(int /*head_dim*/) { return kStreamSegCost; }
 
 // LDS of the split kernel: V slots [4 waves] | wave sums [4] | prefix [B + 1]
 // (| q staging [4 waves][16][D] bf16 for the fused variant).

@@ -92,17 +92,17 @@ __device__ __forceinline__ void finish_token(const RopeAppendArgs &a, int b, int
     }
   } else {
     // Per-(token, head) symmetric scale: absmax / 448, codes e4m3fn(x / scale).
-    const float kmax = wave_max(fmaxf(fabsf(k1), fabsf(k2)));
-    const float vmax = wave_max(fmaxf(fabsf(v1), fabsf(v2)));
+    const float kmax = wave_max_nan(absmax2(0.f, k1, k2));
+    const float vmax = wave_max_nan(absmax2(0.f, v1, v2));
     const float kscale = kmax / 448.0f;
     const float vscale = vmax / 448.0f;
     if (active) {
       uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
       uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
-      kc[off + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k1 / kscale);
-      kc[off + half + i] = kscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(k2 / kscale);
-      vc[off + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v1 / vscale);
-      vc[off + half + i] = vscale == 0.f ? (uint8_t)0 : f32_to_e4m3fn(v2 / vscale);
+      kc[off + i] = e4m3_row_code(k1, kscale);
+      kc[off + half + i] = e4m3_row_code(k2, kscale);
+      vc[off + i] = e4m3_row_code(v1, vscale);
+      vc[off + half + i] = e4m3_row_code(v2, vscale);
     }
     if (i == 0) {
       a.k_scale[off / a.head_dim] = kscale;
@@ -403,21 +403,21 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
       float km = 0.f, vm = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        km = fmaxf(km, fmaxf(fabsf(oa[e]), fabsf(ob[e])));
-        vm = fmaxf(vm, fmaxf(fabsf(va[e]), fabsf(vb[e])));
+        km = absmax2(km, oa[e], ob[e]);
+        vm = absmax2(vm, va[e], vb[e]);
       }
 #pragma unroll
       for (int m = lpt >> 1; m > 0; m >>= 1) {
-        km = fmaxf(km, __shfl_xor(km, m, 64));
-        vm = fmaxf(vm, __shfl_xor(vm, m, 64));
+        km = __builtin_elementwise_maximum(km, __shfl_xor(km, m, 64));
+        vm = __builtin_elementwise_maximum(vm, __shfl_xor(vm, m, 64));
       }
       const float ks = km / 448.0f;
       const float vs = vm / 448.0f;
       if (off >= 0) {
-        const uint32_t ka = ks == 0.f ? 0u : pack_e4m3fn_x4(oa[0] / ks, oa[1] / ks, oa[2] / ks, oa[3] / ks);
-        const uint32_t kb = ks == 0.f ? 0u : pack_e4m3fn_x4(ob[0] / ks, ob[1] / ks, ob[2] / ks, ob[3] / ks);
-        const uint32_t wa = vs == 0.f ? 0u : pack_e4m3fn_x4(va[0] / vs, va[1] / vs, va[2] / vs, va[3] / vs);
-        const uint32_t wb = vs == 0.f ? 0u : pack_e4m3fn_x4(vb[0] / vs, vb[1] / vs, vb[2] / vs, vb[3] / vs);
+        const uint32_t ka = e4m3_row_codes4(oa, ks);
+        const uint32_t kb = e4m3_row_codes4(ob, ks);
+        const uint32_t wa = e4m3_row_codes4(va, vs);
+        const uint32_t wb = e4m3_row_codes4(vb, vs);
         uint8_t *kc = static_cast<uint8_t *>(a.k_cache);
         uint8_t *vc = static_cast<uint8_t *>(a.v_cache);
         *reinterpret_cast<uint32_t *>(kc + off + e0) = ka;

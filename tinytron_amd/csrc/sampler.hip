@@ -938,9 +938,13 @@ hipError_t launch_ept(SampleArgs a, hipStream_t s) {
     hipLaunchKernelGGL((greedy_kernel<EPT, kF32>), dim3(a.M), dim3(kThreads), 0, s, a);
     return hipGetLastError();
   }
-  if (a.cand != nullptr && a.cand_chunks == sample_cand_chunks(a.V, a.top_k, a.logprobs != nullptr) &&
+  if (a.cand != nullptr && a.cand_chunks == sample_cand_chunks(a.M, a.V, a.top_k, a.logprobs != nullptr) &&
       a.cand_chunks > 0) {
+    // rows in grid y: sample_cand_chunks is 0 past kMaxCandRows rows
     hipLaunchKernelGGL((topk_candidates_kernel<kF32>), dim3(a.cand_chunks, a.M), dim3(kCandThreads), 0, s, a);
+    // sample_kernel must not read candidate records this call did not write
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
   } else {
     a.cand = nullptr;
   }
@@ -950,8 +954,8 @@ hipError_t launch_ept(SampleArgs a, hipStream_t s) {
 
 }  // namespace
 
-int sample_cand_chunks(int64_t vocab, int64_t top_k, bool logprobs_rows) {
-  if (logprobs_rows || top_k < 2 || top_k > kCandSlots || vocab <= kCandChunk) return 0;
+int sample_cand_chunks(int64_t rows, int64_t vocab, int64_t top_k, bool logprobs_rows) {
+  if (logprobs_rows || top_k < 2 || top_k > kCandSlots || vocab <= kCandChunk || rows > kMaxCandRows) return 0;
   return (int)((vocab + kCandChunk - 1) / kCandChunk);
 }
 

@@ -211,8 +211,11 @@ struct CandRecord {
 };
 
 hipError_t launch_sample(const SampleArgs &a, bool f32, hipStream_t stream);
-// chunks of the candidate path for this call (0: the whole-row path runs alone)
-int sample_cand_chunks(int64_t vocab, int64_t top_k, bool logprobs_rows);
+// chunks of the candidate path for this call (0: the whole-row path runs alone);
+// the candidate kernel puts rows in grid y, so more than kMaxCandRows rows take
+// the whole-row path
+constexpr int64_t kMaxCandRows = 65535;
+int sample_cand_chunks(int64_t rows, int64_t vocab, int64_t top_k, bool logprobs_rows);
 
 // Partition helpers shared by the ABI layer and the launchers.
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);
@@ -227,5 +230,8 @@ constexpr int kWavesPerBlock = 4;
 constexpr int kTileTokens = 32;  // tokens per wave iteration (two 16-row MFMA blocks)
 constexpr int kMaxStreamBlocks = 1024;  // balanced partition: grid cap (>= 3 workgroups on each of 256 CUs)
 constexpr int kMaxStreamWaves = kMaxStreamBlocks * kWavesPerBlock;
+// balanced partition: tiles' worth of line positions charged to every (sequence,
+// KV head) segment before its tiles (the start-up cost of a segment piece)
+constexpr int kStreamSegCost = 2;
 
 }  // namespace tt

@@ -62,4 +62,25 @@ __device__ __forceinline__ uint32_t pack_e4m3fn_x4(float a, float b, float c, fl
                e4m3fn_pos_nan_bit(d, 3));
 }
 
+// fp8 cache rows (one scale per (token, KV head) row): scale = absmax / 448
+// with a NaN-propagating absmax (IEEE-754-2019 maximum), codes e4m3fn(x /
+// scale); an all-zero row stores zeros (scale 0), and a row holding a NaN or
+// an infinity (scale not finite), which the format cannot represent, stores
+// NaN codes (0x7F) throughout.
+__device__ __forceinline__ float absmax2(float m, float x, float y) {
+  return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(fabsf(x), fabsf(y)));
+}
+
+__device__ __forceinline__ uint8_t e4m3_row_code(float x, float scale) {
+  if (scale == 0.f) return 0;
+  if (!(scale <= 3.402823466e38f)) return 0x7F;
+  return f32_to_e4m3fn(x / scale);
+}
+
+__device__ __forceinline__ uint32_t e4m3_row_codes4(const float (&x)[4], float scale) {
+  if (scale == 0.f) return 0u;
+  if (!(scale <= 3.402823466e38f)) return 0x7F7F7F7Fu;
+  return pack_e4m3fn_x4(x[0] / scale, x[1] / scale, x[2] / scale, x[3] / scale);
+}
+
 }  // namespace tt

@@ -35,6 +35,11 @@ __device__ __forceinline__ float wave_max(float x) {
   return wave_reduce(x, [](float u, float v) { return fmaxf(u, v); });
 }
 
+// maximum that propagates NaN (IEEE-754-2019 maximum)
+__device__ __forceinline__ float wave_max_nan(float x) {
+  return wave_reduce(x, [](float u, float v) { return __builtin_elementwise_maximum(u, v); });
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
   return wave_reduce(x, [](float u, float v) { return u + v; });
 }

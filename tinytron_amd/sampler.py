@@ -1,6 +1,6 @@
 """Token sampling on the device (tinytron/inference/sampler.py:6-62).
 
-``sample_next_token`` and ``sample_next_token_with_log_prob`` keep the
+``filter_logits``, ``sample_next_token`` and ``sample_next_token_with_log_prob`` keep the
 reference's signatures and run as one kernel launch per call
 (``ops.sample_tokens``): fp32 cast, temperature, top-k (values >= the k-th
 largest, ties kept), top-p (the shortest descending prefix whose cumulative
@@ -55,6 +55,22 @@ def _rows(logits: torch.Tensor) -> torch.Tensor:
     if logits.stride(1) != 1:
         logits = logits.contiguous()
     return logits
+
+
+def filter_logits(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
+                  top_p: float | None = None) -> torch.Tensor:
+    """sampler.py:6-36: the temperature / top-k / top-p filtered logits [B, V]
+    (fp32, -inf where filtered). The kept set comes from the device sampler,
+    whose log-probability rows are -inf exactly where these rules filter; the
+    kept values are logits.float() / temperature, the reference's own division."""
+    if temperature <= 0:
+        raise ValueError("temperature must be > 0")
+    rows = _rows(logits)
+    _, lp = ops.sample_tokens(rows, temperature, top_k, top_p, 0, 0, return_logprobs=True)
+    x = rows.float()
+    if temperature != 1.0:
+        x = x / temperature
+    return torch.where(lp == float("-inf"), torch.full_like(x, float("-inf")), x)
 
 
 def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_k: int | None = None,
