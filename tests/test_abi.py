@@ -81,7 +81,8 @@ def _attn(lib, **kw):
 @pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
 @pytest.mark.parametrize("kw,code,msg", [
     (dict(q=None), _lib.TT_ERR_INVALID_ARGUMENT, "NULL"),
-    (dict(head_dim=96, q_strides=(4096, 96)), _lib.TT_ERR_UNSUPPORTED, "head_dim"),
+    (dict(head_dim=136, q_strides=(4352, 136)), _lib.TT_ERR_UNSUPPORTED, "head_dim"),
+    (dict(head_dim=7, q_strides=(224, 7)), _lib.TT_ERR_UNSUPPORTED, "head_dim"),
     (dict(hq=48, hkv=2), _lib.TT_ERR_UNSUPPORTED, "group size"),
     (dict(hq=30, hkv=8), _lib.TT_ERR_INVALID_ARGUMENT, "divisible"),
     (dict(split=300), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),

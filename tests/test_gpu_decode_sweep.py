@@ -1,8 +1,9 @@
 """GPU parity: a seeded sweep of decode-attention shapes against the fp64
 oracle, beyond the hand-picked cases of test_gpu_decode_attention.py.
 
-Each case draws a batch size (1-12), group size and KV-head count (H_q <= 32),
-head_dim 64 / 128, layout (paged with a power-of-two page, or the reference's
+Each case draws a batch size (1-12), group size (powers of two and 3, 5, 6)
+and KV-head count (H_q <= 32), head_dim (24, 32, 48, 64, 96, 128: fp8 caches
+at 24 run the VALU kernel), layout (paged with a power-of-two page, or the reference's
 contiguous store with any page size), cache dtype (bf16 / fp8) and per-sequence
 lengths from a mix of edge values (1, page and tile boundaries) and uniform
 draws. Tolerance as in test_gpu_decode_attention.py.
@@ -22,9 +23,9 @@ EDGES = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 511, 512, 513]
 def _case(i):
     rng = np.random.default_rng(9000 + i)
     B = int(rng.integers(1, 13))
-    G = int(rng.choice([1, 2, 4, 8, 16]))
+    G = int(rng.choice([1, 2, 3, 4, 5, 6, 8, 16]))
     hkv = int(rng.choice([h for h in (1, 2, 4, 8) if G * h <= 32]))
-    D = int(rng.choice([64, 128]))
+    D = int(rng.choice([24, 32, 48, 64, 64, 96, 128, 128]))
     paged = bool(rng.integers(0, 2))
     P = int(rng.choice([16, 32, 64])) if paged else int(rng.choice([16, 48, 100]))
     fp8 = bool(rng.integers(0, 2))

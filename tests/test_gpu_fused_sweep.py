@@ -1,7 +1,7 @@
 """GPU: a seeded sweep of fused decode-step shapes (RoPE + append inside the
 attention launch, tt_decode_attn_append_*) against the two-launch path, bit
 for bit (test_gpu_decode_fused._run_both: output, every cache byte, fp8
-scales, lengths): batch sizes, group sizes, head_dim, bf16 / fp8 caches,
+scales, lengths): batch sizes, group sizes (3, 5, 6 too), head_dim 24-128, bf16 / fp8 caches,
 paged / contiguous layouts and page sizes, bf16 inputs or 1-4 split-K
 partials, edge and random lengths.
 """
@@ -21,10 +21,10 @@ EDGES = [1, 15, 16, 31, 32, 33, 64, 511, 512]
 def test_fused_step_sweep(i):
     rng = np.random.default_rng(5000 + i)
     B = int(rng.integers(1, 10))
-    G = int(rng.choice([1, 2, 4, 8, 16]))
+    G = int(rng.choice([1, 2, 3, 4, 5, 6, 8, 16]))
     hkv = int(rng.choice([h for h in (1, 2, 4) if G * h <= 32]))
-    D = int(rng.choice([64, 128]))
-    kv = str(rng.choice(["bf16", "fp8"]))
+    D = int(rng.choice([24, 32, 48, 64, 64, 96, 128, 128]))
+    kv = str(rng.choice(["bf16", "fp8"])) if D % 16 == 0 else "bf16"
     paged = bool(rng.integers(0, 2))
     page = int(rng.choice([16, 32, 64]))
     S = int(rng.integers(0, 5))

@@ -200,11 +200,12 @@ int64_t resolve_split(int64_t split_tokens, int64_t batch, int64_t hkv, int64_t 
   return split_tokens > 0 ? split_tokens : tt::auto_split_tokens(batch, hkv, max_len);
 }
 
+// Partial rows are tt::workspace_head_dim(head_dim) floats wide (every kernel's tile width fits).
 size_t workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t max_len, int64_t split) {
   const int64_t g = hq / (hkv > 0 ? hkv : 1);
   const int64_t splits = tt::num_splits(max_len, split);
   const int64_t items = batch * hkv * splits * g;
-  return (size_t)(items * head_dim + items * 2) * sizeof(float);
+  return (size_t)(items * tt::workspace_head_dim(head_dim) + items * 2) * sizeof(float);
 }
 
 // Balanced partition: the per-sequence tile prefix (padded to 16 bytes), then
@@ -219,7 +220,8 @@ size_t balanced_workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t 
                                 int64_t waves = tt::kMaxStreamWaves) {
   const int64_t g = hq / (hkv > 0 ? hkv : 1);
   const int64_t rows = balanced_slots(batch, hkv, waves) * g;
-  return (size_t)balanced_prefix_ints(batch) * sizeof(int32_t) + (size_t)(rows * head_dim + rows * 2) * sizeof(float);
+  return (size_t)balanced_prefix_ints(batch) * sizeof(int32_t) +
+         (size_t)(rows * tt::workspace_head_dim(head_dim) + rows * 2) * sizeof(float);
 }
 
 int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2], const void *k_cache,
@@ -239,12 +241,19 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   TT_CHECK(num_q_heads / num_kv_heads <= 16, TT_ERR_UNSUPPORTED, "GQA group size %lld > 16 is not supported",
            (long long)(num_q_heads / num_kv_heads));
   TT_CHECK(num_kv_heads <= 65535 && num_q_heads <= 65535, TT_ERR_UNSUPPORTED, "too many heads");
-  TT_CHECK(head_dim == 64 || head_dim == 128, TT_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld",
+  TT_CHECK(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 128, TT_ERR_UNSUPPORTED,
+           "head_dim must be even and <= 128, got %lld", (long long)head_dim);
+  // MFMA kernels on 32 / 64 / 128-wide tiles, or (0) the VALU kernel
+  const int tile = tt::tile_head_dim(head_dim, kind);
+  TT_CHECK(ap == nullptr || tile > 0, TT_ERR_UNSUPPORTED,
+           "the fused decode step needs head_dim a multiple of 8 (bf16 cache) or 16 (fp8 cache), got %lld",
            (long long)head_dim);
   TT_CHECK(max_seq_len >= 0 && max_seq_len < (int64_t)1 << 30, TT_ERR_INVALID_ARGUMENT,
            "max_seq_len out of range");
   if (kind == tt::CacheKind::kFP8) {
     TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+    TT_CHECK(cache_strides[0] % head_dim == 0 && cache_strides[1] % head_dim == 0 && cache_strides[2] % head_dim == 0,
+             TT_ERR_INVALID_ARGUMENT, "fp8 cache strides must be multiples of head_dim (one scale per row)");
   }
   int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
   if (rc != TT_OK) return rc;
@@ -263,7 +272,7 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     rc = check_contiguous_room(max_seq_len, head_dim, cache_strides, batch, num_kv_heads);
     if (rc != TT_OK) return rc;
   }
-  if (kind != tt::CacheKind::kF32) {
+  if (tile > 0) {
     TT_CHECK(batch <= 4096, TT_ERR_UNSUPPORTED, "batch %lld > 4096 is not supported (per-sequence split table in LDS)",
              (long long)batch);
     TT_CHECK((ap || aligned(q, 16)) && aligned(k_cache, 16) && aligned(v_cache, 16), TT_ERR_INVALID_ARGUMENT,
@@ -273,16 +282,18 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     TT_CHECK(cache_strides[0] % 8 == 0 && cache_strides[1] % 8 == 0 && cache_strides[2] % 8 == 0,
              TT_ERR_INVALID_ARGUMENT, "cache strides must be multiples of 8 elements");
   } else {
-    TT_CHECK(aligned(q, 4) && aligned(k_cache, 4) && aligned(v_cache, 4) && aligned(out, 4),
-             TT_ERR_INVALID_ARGUMENT, "fp32 pointers must be 4-byte aligned");
+    const size_t qa = kind == tt::CacheKind::kF32 ? 4 : 2;
+    const size_t ca = kind == tt::CacheKind::kF32 ? 4 : (kind == tt::CacheKind::kBF16 ? 2 : 1);
+    TT_CHECK(aligned(q, qa) && aligned(k_cache, ca) && aligned(v_cache, ca) && aligned(out, qa),
+             TT_ERR_INVALID_ARGUMENT, "q, cache and out pointers must be aligned to their element size");
   }
-  // split_tokens == 0 on the bf16/fp8 path: balanced partition (equal tiles per wave); otherwise fixed splits
-  const bool balanced = split_tokens == 0 && kind != tt::CacheKind::kF32;
+  // split_tokens == 0 on the MFMA path: balanced partition (equal tiles per wave); otherwise fixed splits
+  const bool balanced = split_tokens == 0 && tile > 0;
   int64_t split = 0, splits = 0;
   size_t need = 0;
   // partial slots beyond the segments: one per wave of the largest grid, or of the launched one
   const int64_t ws_waves =
-      exact_slots ? tt::balanced_stream_waves((int)head_dim, batch, num_kv_heads, max_seq_len) : tt::kMaxStreamWaves;
+      exact_slots ? tt::balanced_stream_waves(tile, batch, num_kv_heads, max_seq_len) : tt::kMaxStreamWaves;
   if (balanced) {
     // the per-sequence line prefix (int32) counts each sequence's tiles plus its segment start-up charge
     TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens + tt::kStreamSegCost) < ((int64_t)1 << 31),
@@ -326,7 +337,9 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.ws_prefix = balanced ? static_cast<int32_t *>(workspace) : nullptr;
   a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                      (balanced ? balanced_prefix_ints(batch) * sizeof(int32_t) : 0));
-  a.ws_ml = a.ws_o + rows * head_dim;
+  a.ws_ml = a.ws_o + rows * tt::workspace_head_dim(head_dim);
+  a.head_dim = (int)head_dim;
+  a.inv_head_dim = 1.0 / (double)head_dim;
   a.batch = (int)batch;
   a.hq = (int)num_q_heads;
   a.hkv = (int)num_kv_heads;
@@ -432,13 +445,16 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
            "num_attention_heads must be divisible by num_key_value_heads");
   const int64_t g = num_q_heads / num_kv_heads;
   TT_CHECK(g <= 16, TT_ERR_UNSUPPORTED, "GQA group size %lld > 16 is not supported", (long long)g);
-  TT_CHECK(head_dim == 64 || head_dim == 128, TT_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld",
+  TT_CHECK(tt::tile_head_dim(head_dim, kind) > 0, TT_ERR_UNSUPPORTED,
+           "prefill attention needs head_dim <= 128 and a multiple of 8 (bf16 cache) or 16 (fp8 cache), got %lld",
            (long long)head_dim);
   TT_CHECK(max_seq_len >= 0 && max_seq_len < ((int64_t)1 << 30), TT_ERR_INVALID_ARGUMENT, "max_seq_len out of range");
   TT_CHECK(batch * num_kv_heads < ((int64_t)1 << 26) && num_new < ((int64_t)1 << 24), TT_ERR_UNSUPPORTED,
            "grid too large");
   if (kind == tt::CacheKind::kFP8) {
     TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+    TT_CHECK(cache_strides[0] % head_dim == 0 && cache_strides[1] % head_dim == 0 && cache_strides[2] % head_dim == 0,
+             TT_ERR_INVALID_ARGUMENT, "fp8 cache strides must be multiples of head_dim (one scale per row)");
   }
   int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
   if (rc != TT_OK) return rc;
@@ -492,6 +508,8 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
   a.group = (int)g;
   a.page_shift = page_shift;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.head_dim = (int)head_dim;
+  a.inv_head_dim = 1.0 / (double)head_dim;
   a.positions = positions;
   a.new_lens = new_lens;
   a.num_new = (int)num_new;

@@ -83,6 +83,33 @@ struct KVTraits<true> {
   static __device__ __forceinline__ int q_offset(int s, int g) { return 64 * (s >> 1) + 16 * g + 8 * (s & 1); }
 };
 
+// Row length of the cache (its head_dim) for a kernel built on D-wide tiles:
+// D itself, or (kPad) the runtime head_dim a.head_dim < D (a multiple of 16
+// bytes: of 8 bf16 or 16 fp8 values). Padded kernels read each cached row with
+// the D-wide tile's 16-byte fragments, so a fragment that starts past the
+// row's end holds the first values of the next cached token of the same 16-token
+// block (the same sequence and KV head), or zero fill past the block's valid
+// rows. The query's entries past head_dim are zero, so Q K^T sums the real
+// head_dim only (those neighbouring values are finite unless a token this
+// query attends is itself non-finite, which makes the output NaN anyway), and
+// V columns past head_dim feed only output columns that are never written.
+template <int D, bool kPad>
+__device__ __forceinline__ int row_len(const DecodeArgs &a) {
+  if constexpr (kPad) return a.head_dim;
+  return D;
+}
+
+// Scale-array index of the row at element offset elem (a multiple of the row
+// length): elem / head_dim, exactly (a shift for the unpadded widths; for
+// padded ones a double-precision product with 1 / head_dim, rounded: the
+// error is below 2^-12 for offsets under 2^40, so the nearest integer is the
+// quotient).
+template <int D, bool kPad>
+__device__ __forceinline__ int64_t scale_row(const DecodeArgs &a, int64_t elem) {
+  if constexpr (kPad) return (int64_t)__builtin_rint((double)elem * a.inv_head_dim);
+  return elem / D;
+}
+
 template <int D, bool kFP8>
 struct Tile {
   static constexpr int NU = D * KVTraits<kFP8>::kElemBytes / 64;  // 16-byte fragments per lane per row
@@ -116,22 +143,24 @@ __device__ __forceinline__ int64_t token_elem(const DecodeArgs &a, int b, int hk
 // (num_records) and read as zero (or, for LDS loads, leave the LDS slot as
 // it was): no branch, no out-of-bounds access, and no garbage (possibly
 // NaN) from unused cache slots reaches the MFMAs.
-template <int D, bool kFP8>
+template <int D, bool kFP8, bool kPad = false>
 __device__ __forceinline__ void load_k_block(const DecodeArgs &a, int64_t elem, int rows, int lane,
                                              u32x4 (&k)[Tile<D, kFP8>::NU], f32x4 &ks, f32x4 &vs) {
   constexpr int E = KVTraits<kFP8>::kElemBytes;
   constexpr int NU = Tile<D, kFP8>::NU;
+  const int hd = row_len<D, kPad>(a);
   const auto rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char *>(static_cast<const char *>(a.k_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
-  const int off = (lane & 15) * D * E + 16 * (lane >> 4);
+      const_cast<char *>(static_cast<const char *>(a.k_cache)) + elem * E, (short)0, rows * hd * E, kBufferFlags);
+  const int off = (lane & 15) * hd * E + 16 * (lane >> 4);
 #pragma unroll
   for (int u = 0; u < NU; ++u)
     k[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * u, 0, 0));
   if constexpr (kFP8) {
     // this lane's score rows are tokens tb + 4g + r, r = 0..3
-    const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + elem / D, (short)0,
+    const int64_t srow = scale_row<D, kPad>(a, elem);
+    const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + srow, (short)0,
                                                        rows * 4, kBufferFlags);
-    const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + elem / D, (short)0,
+    const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + srow, (short)0,
                                                        rows * 4, kBufferFlags);
     ks = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rks, 16 * (lane >> 4), 0, 0));
     vs = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvs, 16 * (lane >> 4), 0, 0));
@@ -141,17 +170,18 @@ __device__ __forceinline__ void load_k_block(const DecodeArgs &a, int64_t elem, 
 // V rows of one 16-token block straight into this wave's LDS slots
 // (buffer_load ... lds: lane i's 16 bytes land at base + 16 i, the layout a
 // register load would have), so the next tile's V costs no VGPRs.
-template <int D, bool kFP8>
+template <int D, bool kFP8, bool kPad = false>
 __device__ __forceinline__ void load_v_block_lds(const DecodeArgs &a, int64_t elem, int rows, int lane, char *lds) {
   constexpr int E = KVTraits<kFP8>::kElemBytes;
   constexpr int NU = Tile<D, kFP8>::NU;
+  const int hd = row_len<D, kPad>(a);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * D * E, kBufferFlags);
+      const_cast<char *>(static_cast<const char *>(a.v_cache)) + elem * E, (short)0, rows * hd * E, kBufferFlags);
   // bf16 slots are swizzled for read_v's transposing reads: slot m + 16 g
   // holds token m ^ (8 (g & 1)) (chunk g), so that the two 8-column chunks
   // that one read takes from each of 8 tokens fill all 64 banks once
   const int tok = kFP8 ? (lane & 15) : ((lane & 15) ^ (8 * ((lane >> 4) & 1)));
-  const int off = tok * D * E + 16 * (lane >> 4);
+  const int off = tok * hd * E + 16 * (lane >> 4);
 #pragma unroll
   for (int u = 0; u < NU; ++u)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(lds + 1024 * u), 16,
@@ -377,9 +407,10 @@ constexpr int kChunkTiles = 16;  // tiles per page-table fetch and software-pipe
 // Element offset and valid rows of 16-token block `blk` of (b, hk). Paged:
 // `entry` holds, one per lane, the page-table entries of pages pbase.. (the
 // block's page index relative to pbase is < 64 for every block of the chunk).
-template <int D>
+template <int D, bool kPad = false>
 __device__ __forceinline__ void stream_block_addr(const DecodeArgs &a, int b, int hk, int L, int entry, int pbase,
                                                   int blk, int64_t &elem, int &rows) {
+  const int hd = row_len<D, kPad>(a);
   const int tb = 16 * blk;
   const int tc = min(tb, (L - 1) & ~15);  // blocks past the end keep an in-sequence address and zero rows
   rows = __builtin_amdgcn_readfirstlane(min(max(L - tb, 0), 16));
@@ -387,9 +418,9 @@ __device__ __forceinline__ void stream_block_addr(const DecodeArgs &a, int b, in
   if (a.page_table != nullptr) {
     int64_t phys = __builtin_amdgcn_readlane(entry, (tc >> a.page_shift) - pbase);
     phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
-    e = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & ((1 << a.page_shift) - 1)) * D;
+    e = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & ((1 << a.page_shift) - 1)) * hd;
   } else {
-    e = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)tc * D;
+    e = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)tc * hd;
   }
   elem = uniform64(e);
 }

@@ -52,11 +52,12 @@ __host__ __device__ constexpr int merge_floats(int G, int D) { return kWavesPerB
 // One split of one (sequence, KV head): the 4 waves of the workgroup each
 // stream kTiles 32-token tiles, merge their states in LDS and write one
 // partial (unnormalised output, max, sum) to the workspace.
-template <int D, bool kFP8, int kTiles>
+template <int D, bool kFP8, int kTiles, bool kPad>
 __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, int split, int L, int lane, int wave,
                                            char *smem_v, float *smem) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
+  const int hd = row_len<D, kPad>(a);
   constexpr int kWaveTokens = kTiles * kTileTokens;
   constexpr int kBlocks = 2 * kTiles;  // 16-token blocks per wave
   const int G = a.group;
@@ -87,14 +88,14 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
       int64_t phys = __builtin_amdgcn_readlane(entry, (tc >> a.page_shift) - j_first);
       phys = phys < 0 ? 0 : (phys >= a.num_pages ? a.num_pages - 1 : phys);
       brows[i] = min(max(L - tb, 0), 16);
-      belem[i] = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & pmask) * D;
+      belem[i] = phys * a.c_page + (int64_t)hk * a.c_head + (int64_t)(tc & pmask) * hd;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < kBlocks; ++i) {
       const int tb = w_begin + 16 * i;
       brows[i] = min(max(L - tb, 0), 16);
-      belem[i] = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)min(tb, (L - 1) & ~15) * D;
+      belem[i] = (int64_t)b * a.c_seq + (int64_t)hk * a.c_head + (int64_t)min(tb, (L - 1) & ~15) * hd;
     }
   }
 
@@ -105,7 +106,7 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
   }
 
   // q^T as the B operand: column n = query head hk*G + n (zero for n >= G),
-  // k step s holding the head_dim values the K fragments hold.
+  // k step s holding the head_dim values the K fragments hold (zero past hd).
   bf16x8 qf[NDB];
   {
     const uint16_t *q = static_cast<const uint16_t *>(a.q);
@@ -113,7 +114,7 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
 #pragma unroll
     for (int s = 0; s < NDB; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (n < G) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
+      if (n < G && (!kPad || TR::q_offset(s, g) < hd)) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
       qf[s] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -133,11 +134,11 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
   constexpr int NU = Tile<D, kFP8>::NU;
   char *vlds = smem_v + wave * Tile<D, kFP8>::kVBytes;
   Tile<D, kFP8> buf[2];
-  load_k_block<D, kFP8>(a, belem[0], brows[0], lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
-  load_k_block<D, kFP8>(a, belem[1], brows[1], lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
+  load_k_block<D, kFP8, kPad>(a, belem[0], brows[0], lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
+  load_k_block<D, kFP8, kPad>(a, belem[1], brows[1], lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
   __builtin_amdgcn_sched_barrier(0);
-  load_v_block_lds<D, kFP8>(a, belem[0], brows[0], lane, vlds);
-  load_v_block_lds<D, kFP8>(a, belem[1], brows[1], lane, vlds + NU * 1024);
+  load_v_block_lds<D, kFP8, kPad>(a, belem[0], brows[0], lane, vlds);
+  load_v_block_lds<D, kFP8, kPad>(a, belem[1], brows[1], lane, vlds + NU * 1024);
   // Vector-memory issue order, pinned with scheduling barriers so that the
   // explicit vmcnt waits below count exactly:
   //   prologue: K(0), V(0);  iteration i: K(i+1) | QK, softmax | wait V(i),
@@ -152,8 +153,8 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
     if (t0 >= L) break;  // uniform; later tiles are past the end too
     if (it + 1 < kTiles) {
       Tile<D, kFP8> &nx = buf[(it + 1) & 1];
-      load_k_block<D, kFP8>(a, belem[2 * it + 2], brows[2 * it + 2], lane, nx.k[0], nx.ks[0], nx.vs[0]);
-      load_k_block<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, nx.k[1], nx.ks[1], nx.vs[1]);
+      load_k_block<D, kFP8, kPad>(a, belem[2 * it + 2], brows[2 * it + 2], lane, nx.k[0], nx.ks[0], nx.vs[0]);
+      load_k_block<D, kFP8, kPad>(a, belem[2 * it + 3], brows[2 * it + 3], lane, nx.k[1], nx.ks[1], nx.vs[1]);
     }
     __builtin_amdgcn_sched_barrier(0);
     bf16x8 pa_hi, pa_lo;
@@ -169,8 +170,8 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
     __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < kTiles && t0 + kTileTokens < L) {
-      load_v_block_lds<D, kFP8>(a, belem[2 * it + 2], brows[2 * it + 2], lane, vlds);
-      load_v_block_lds<D, kFP8>(a, belem[2 * it + 3], brows[2 * it + 3], lane, vlds + NU * 1024);
+      load_v_block_lds<D, kFP8, kPad>(a, belem[2 * it + 2], brows[2 * it + 2], lane, vlds);
+      load_v_block_lds<D, kFP8, kPad>(a, belem[2 * it + 3], brows[2 * it + 3], lane, vlds + NU * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
     pv_tile<D, kFP8>(vr, ident8, pa_hi, pa_lo, st);
@@ -268,7 +269,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
 // of (sequence, split, KV head) items -- KV heads fastest, so workgroups that
 // run together read the head blocks of the same physical pages -- with no
 // workgroups for splits past a sequence's end.
-template <int D, bool kFP8, int kTiles>
+template <int D, bool kFP8, int kTiles, bool kPad>
 __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
   constexpr int kSplit = kWavesPerBlock * kTiles * kTileTokens;
   constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
     const int b = __builtin_amdgcn_readfirstlane(lo);
     const int split = sidx - __builtin_amdgcn_readfirstlane(prefix[b]);
     const int L = __builtin_amdgcn_readfirstlane(lens[b]);
-    split_item<D, kFP8, kTiles>(a, b, hk, split, L, lane, wave, smem_v, merge);
+    split_item<D, kFP8, kTiles, kPad>(a, b, hk, split, L, lane, wave, smem_v, merge);
     __syncthreads();  // the merge area is reused by the next item
   }
 }
@@ -335,7 +336,8 @@ __host__ __device__ __forceinline__ int64_t wave_of_tile(int64_t t, int64_t W, i
 template <int D, int kMaxG>
 __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk, int64_t seg, int64_t w0, int64_t w1,
                                               int64_t W, int64_t NW, int lane) {
-  constexpr int DPL = D / 64;
+  constexpr int DPL = D >= 64 ? D / 64 : 1;  // columns lane + 64 j of the D-wide partial rows
+  const bool lane_in = D >= 64 || lane < D;
   constexpr int kBatch = 64 / (kMaxG * DPL) < 2 ? 2 : (64 / (kMaxG * DPL) > 16 ? 16 : 64 / (kMaxG * DPL));
   const int G = a.group;  // <= kMaxG
   float M[kMaxG], Ls[kMaxG], acc[kMaxG][DPL];
@@ -365,7 +367,7 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
         for (int h = 0; h < kMaxG; ++h)
           if (h < G)
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) ov[u][h][j] = a.ws_o[(sk * G + h) * D + lane + 64 * j];
+            for (int j = 0; j < DPL; ++j) ov[u][h][j] = lane_in ? a.ws_o[(sk * G + h) * D + lane + 64 * j] : 0.f;
       }
     };
     load_rows(0);
@@ -409,7 +411,8 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
     if (h < G) {
       const float inv = Ls[h] > 0.f ? 1.0f / Ls[h] : 0.f;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) out[(int64_t)h * a.o_sh + lane + 64 * j] = f32_to_bf16_bits(acc[h][j] * inv);
+      for (int j = 0; j < DPL; ++j)
+        if (lane + 64 * j < a.head_dim) out[(int64_t)h * a.o_sh + lane + 64 * j] = f32_to_bf16_bits(acc[h][j] * inv);
     }
   }
 }
@@ -463,18 +466,19 @@ __device__ __forceinline__ float ap_value(const DecodeAppend &ap, const ApRaw<kP
 //    when the slot is outside the cache or the table, as that kernel skips it;
 //  - RoPE of the G query rows of (b, hk) into the wave's LDS staging area qs
 //    [G][D] (bf16), then the MFMA B fragments from it.
-template <int D, bool kFP8, bool kPartIn>
+template <int D, bool kFP8, bool kPartIn, bool kPad>
 __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const DecodeAppend &ap, int b, int hk, int pos,
                                                bool append, int lane, uint16_t *qs, bf16x8 (&qf)[D / 32]) {
-  constexpr int H = D / 2;
+  const int hd = row_len<D, kPad>(a);
+  const int H = hd / 2;   // rotation pairs (i, i + H) of a row
   constexpr int kIt = 4;  // query pairs per lane per round (one round for G * D <= 512)
   const int G = a.group;
   const int pairs = G * H;
   const bool in_table = pos >= 0 && pos < ap.table_len;
   const int tp = pos < 0 ? 0 : (pos >= ap.table_len ? (int)ap.table_len - 1 : pos);  // in bounds
-  const uint16_t *tab = static_cast<const uint16_t *>(ap.table) + (int64_t)tp * D;
+  const uint16_t *tab = static_cast<const uint16_t *>(ap.table) + (int64_t)tp * hd;
   const bool active = lane < H;
-  const int li = lane & (H - 1);
+  const int li = active ? lane : 0;  // lanes past H load pair 0 and drop it
 
   // loads: append inputs and slot (always, in bounds), then the query inputs;
   // all issued before the scheduling barrier, consumed after it
@@ -538,10 +542,10 @@ __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const Decode
     if (a.page_table != nullptr) {
       phys = __builtin_amdgcn_readfirstlane((int)phys);
       if (jp < a.max_pages && phys >= 0 && phys < a.num_pages)
-        base = phys * a.c_page + (int64_t)(pos - ((pos >> a.page_shift) << a.page_shift)) * D;
+        base = phys * a.c_page + (int64_t)(pos - ((pos >> a.page_shift) << a.page_shift)) * hd;
     } else {
       const int64_t j = pos / ap.page_size;
-      base = (int64_t)b * a.c_seq + j * a.c_page + (pos - j * ap.page_size) * D;
+      base = (int64_t)b * a.c_seq + j * a.c_page + (pos - j * ap.page_size) * hd;
     }
     if (base >= 0) {
       const int64_t off = base + (int64_t)hk * a.c_head;
@@ -569,8 +573,9 @@ __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const Decode
           vcache[off + H + lane] = e4m3_row_code(v2, vscale);
         }
         if (lane == 0) {
-          const_cast<float *>(a.k_scale)[off / D] = kscale;
-          const_cast<float *>(a.v_scale)[off / D] = vscale;
+          const int64_t srow = scale_row<D, kPad>(a, off);
+          const_cast<float *>(a.k_scale)[srow] = kscale;
+          const_cast<float *>(a.v_scale)[srow] = vscale;
         }
       }
     }
@@ -591,14 +596,15 @@ __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const Decode
 #pragma unroll
   for (int s = 0; s < D / 32; ++s) {
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (n < G) v = *reinterpret_cast<const u32x4 *>(qs + n * D + TR::q_offset(s, g));
+    // staging entries past hd were never written: zero (query values past head_dim)
+    if (n < G && (!kPad || TR::q_offset(s, g) < hd)) v = *reinterpret_cast<const u32x4 *>(qs + n * D + TR::q_offset(s, g));
     qf[s] = __builtin_bit_cast(bf16x8, v);
   }
   __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int D, bool kFP8, bool kAppend, bool kPartIn>
+template <int D, bool kFP8, bool kAppend, bool kPartIn, bool kPad>
 __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAppend *ap, int b, int hk, int L,
                                              int j0, int j1, bool append, int64_t w, int lane, char *vlds,
                                              uint16_t *qs, const bf16x8 (&ident16)[2],
@@ -617,7 +623,8 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
       const int pb0 = (kTileTokens * j0) >> a.page_shift;
       entry0 = a.page_table[(int64_t)b * a.max_pages + min(pb0 + lane, (L - 1) >> a.page_shift)];
     }
-    piece_prologue<D, kFP8, kPartIn>(a, *ap, b, hk, __builtin_amdgcn_readfirstlane(a.seq_lens[b]), append, lane, qs, qf);
+    piece_prologue<D, kFP8, kPartIn, kPad>(a, *ap, b, hk, __builtin_amdgcn_readfirstlane(a.seq_lens[b]), append, lane,
+                                           qs, qf);
     // The appended token is in this piece's last tile. Its loads are issued
     // after the tile loop's first explicit vmcnt wait (which retires the
     // stores above) unless it is one of the first chunk's first two tiles.
@@ -625,10 +632,11 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
   } else {
     const uint16_t *q = static_cast<const uint16_t *>(a.q);
     const int64_t qrow = (int64_t)b * a.q_sb + (int64_t)(hk * G + n) * a.q_sh;
+    const int hd = row_len<D, kPad>(a);
 #pragma unroll
     for (int s = 0; s < NDB; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (n < G) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
+      if (n < G && (!kPad || TR::q_offset(s, g) < hd)) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
       qf[s] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -659,24 +667,24 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
     Tile<D, kFP8> buf[2];
     int64_t e0, e1;
     int r0, r1;
-    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0, e0, r0);
-    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0 + 1, e1, r1);
-    load_k_block<D, kFP8>(a, e0, r0, lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
-    load_k_block<D, kFP8>(a, e1, r1, lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
+    stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * c0, e0, r0);
+    stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * c0 + 1, e1, r1);
+    load_k_block<D, kFP8, kPad>(a, e0, r0, lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
+    load_k_block<D, kFP8, kPad>(a, e1, r1, lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
     __builtin_amdgcn_sched_barrier(0);
-    load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
-    load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+    load_v_block_lds<D, kFP8, kPad>(a, e0, r0, lane, vlds);
+    load_v_block_lds<D, kFP8, kPad>(a, e1, r1, lane, vlds + NU * 1024);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < kChunkTiles; ++k) {
       const int it = c0 + k;
       if (it >= c1) break;  // uniform
       if (k + 1 < kChunkTiles) {
-        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 2, e0, r0);
-        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 3, e1, r1);
+        stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * it + 2, e0, r0);
+        stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * it + 3, e1, r1);
         Tile<D, kFP8> &nx = buf[(k + 1) & 1];
-        load_k_block<D, kFP8>(a, e0, r0, lane, nx.k[0], nx.ks[0], nx.vs[0]);
-        load_k_block<D, kFP8>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
+        load_k_block<D, kFP8, kPad>(a, e0, r0, lane, nx.k[0], nx.ks[0], nx.vs[0]);
+        load_k_block<D, kFP8, kPad>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
       }
       __builtin_amdgcn_sched_barrier(0);
       bf16x8 pa_hi, pa_lo;
@@ -692,8 +700,8 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
       __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
       __builtin_amdgcn_sched_barrier(0);
       if (k + 1 < kChunkTiles && it + 1 < c1) {
-        load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
-        load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+        load_v_block_lds<D, kFP8, kPad>(a, e0, r0, lane, vlds);
+        load_v_block_lds<D, kFP8, kPad>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
       pv_tile<D, kFP8>(vr, ident8, pa_hi, pa_lo, st);
@@ -724,7 +732,7 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
 // half the bytes, four waves keep too little in flight, and eight measured
 // better (C5 step -5 %, end to end +2 %).
 constexpr int kStreamOcc = 2;
-constexpr int stream_blocks_per_cu(int head_dim) { return head_dim == 64 ? 2 : 1; }
+constexpr int stream_blocks_per_cu(int tile_d) { return tile_d <= 64 ? 2 : 1; }
 
 // Tiles' worth of time a wave spends starting a segment piece (length and
 // page-table lookups, q fragments, the fused step's RoPE + append): charged to
@@ -736,7 +744,7 @@ constexpr int stream_seg_cost(int /*head_dim*/) { return kStreamSegCost; }
 
 // LDS of the split kernel: V slots [4 waves] | wave sums [4] | prefix [B + 1]
 // (| q staging [4 waves][16][D] bf16 for the fused variant).
-template <int D, bool kFP8, bool kAppend, bool kPartIn>
+template <int D, bool kFP8, bool kAppend, bool kPartIn, bool kPad>
 __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeAppend *ap) {
   constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
   extern __shared__ float smem[];
@@ -788,31 +796,31 @@ __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeApp
       const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b] + a.len_add, a.max_len));
       // The segment's last tile holds this step's token: only this wave reads
       // it, so the fused variant appends it at the start of this piece.
-      stream_piece<D, kFP8, kAppend, kPartIn>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nbe - a.seg_cost, w, lane,
-                                              vlds, qs, ident16, ident8);
+      stream_piece<D, kFP8, kAppend, kPartIn, kPad>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nbe - a.seg_cost, w,
+                                                    lane, vlds, qs, ident16, ident8);
     }
     t = stop;
   }
 }
 
-template <int D, bool kFP8>
+template <int D, bool kFP8, bool kPad>
 __global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeArgs a) {
-  stream_body<D, kFP8, false, false>(a, nullptr);
+  stream_body<D, kFP8, false, false, kPad>(a, nullptr);
 }
 
 // The same split kernel with this step's RoPE + append folded in (q rotated
 // per piece from the projection outputs; k / v written by the wave that
 // reads the segment's last tile).
-template <int D, bool kFP8, bool kPartIn>
+template <int D, bool kFP8, bool kPartIn, bool kPad>
 __global__ __launch_bounds__(256, kStreamOcc) void decode_stream_append_kernel(DecodeAppendArgs a) {
-  stream_body<D, kFP8, true, kPartIn>(a, &a.ap);
+  stream_body<D, kFP8, true, kPartIn, kPad>(a, &a.ap);
 }
 
 // One wave per segment (b, KV head): merge its pieces into the G output rows
 // (zeros for a sequence with nothing cached). kMaxG bounds the group size.
 template <int D, int kMaxG>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
-  constexpr int DPL = D / 64;
+  constexpr int DPL = D >= 64 ? D / 64 : 1;
   const int64_t seg = blockIdx.x;
   const int b = (int)(seg / a.hkv);
   const int hk = (int)(seg - (int64_t)b * a.hkv);
@@ -822,7 +830,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
   if (nb <= 0) {
     uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * a.group * a.o_sh;
     for (int h = 0; h < a.group; ++h)
-      for (int j = 0; j < DPL; ++j) out[(int64_t)h * a.o_sh + lane + 64 * j] = 0;
+      for (int j = 0; j < DPL; ++j)
+        if (lane + 64 * j < a.head_dim) out[(int64_t)h * a.o_sh + lane + 64 * j] = 0;
     return;
   }
   const int64_t W = (int64_t)a.ws_prefix[a.batch] * a.hkv;
@@ -834,13 +843,27 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
   merge_segment<D, kMaxG>(a, b, hk, seg, wave_of_tile(start, W, NW), wave_of_tile(last, W, NW), W, NW, lane);
 }
 
-// fp32 cache and activations: VALU path (small models run in fp32, e.g. the
-// reference without autocast). Same split / workspace contract as the MFMA
-// kernel. Each wave walks its tokens 64 at a time with one token per lane
-// for the scores, then one head_dim element per lane for P.V.
-template <int D>
-__global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
-  constexpr int DPL = D / 64;  // head_dim elements per lane
+// VALU path: fp32 caches (small models run in fp32, e.g. the reference
+// without autocast) and head dims the MFMA tiles do not take (not a multiple
+// of 16 bytes: of 8 bf16 or 16 fp8 values), any even head_dim <= 128. Fixed
+// splits, the same workspace contract as the MFMA split kernel (partial rows
+// D_ws = ws_d floats wide). Each wave walks its tokens 64 at a time with one
+// token per lane for the scores, then one head_dim entry per lane (two past
+// 64) for P.V. K/V values: fp32, bf16, or fp8-e4m3 codes times the row scale.
+template <CacheKind K>
+__device__ __forceinline__ float kv_value(const void *base, int64_t i) {
+  if constexpr (K == CacheKind::kF32) {
+    return static_cast<const float *>(base)[i];
+  } else if constexpr (K == CacheKind::kBF16) {
+    return bf16_bits_to_f32(static_cast<const uint16_t *>(base)[i]);
+  } else {
+    const uint32_t code = static_cast<const uint8_t *>(base)[i];
+    return (float)__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(code, 1.0f, false)[0];  // exact
+  }
+}
+
+template <CacheKind K>
+__global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, int ws_d) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -848,6 +871,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
   const int G = a.group;
+  const int hd = a.head_dim;
   const int L = min(a.seq_lens[b], a.max_len);
   const int s_begin = split * a.split_tokens;
   if (s_begin >= L) return;
@@ -856,40 +880,41 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
   const int w_begin = s_begin + wave * per_wave;
   const int w_end = min(s_end, w_begin + per_wave);
 
-  float *so = smem;                                  // [4][G][D]
-  float *sm = so + kWavesPerBlock * G * D;           // [4][16]
+  float *so = smem;                                  // [4][G][ws_d]
+  float *sm = so + kWavesPerBlock * G * ws_d;        // [4][16]
   float *sl = sm + kWavesPerBlock * 16;              // [4][16]
-  float *sq = sl + kWavesPerBlock * 16;              // [G][D] query rows
-  float *sp = sq + G * D + wave * 64;                // per-wave [64] probabilities
-  const float *q = static_cast<const float *>(a.q);
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int h = idx / D;
-    sq[idx] = q[(int64_t)b * a.q_sb + (int64_t)(hk * G + h) * a.q_sh + (idx - h * D)];
+  float *sq = sl + kWavesPerBlock * 16;              // [G][hd] query rows
+  float *sp = sq + G * hd + wave * 64;               // per-wave [64] probabilities
+  for (int idx = threadIdx.x; idx < G * hd; idx += blockDim.x) {
+    const int h = idx / hd;
+    const int64_t qi = (int64_t)b * a.q_sb + (int64_t)(hk * G + h) * a.q_sh + (idx - h * hd);
+    sq[idx] = K == CacheKind::kF32 ? static_cast<const float *>(a.q)[qi]
+                                   : bf16_bits_to_f32(static_cast<const uint16_t *>(a.q)[qi]);
   }
   __syncthreads();
 
-  const float *kc = static_cast<const float *>(a.k_cache);
-  const float *vc = static_cast<const float *>(a.v_cache);
-  float o[16][DPL];
+  float o[16][2];
   float mrun[16], lrun[16];
   for (int h = 0; h < 16; ++h) {
     mrun[h] = kNegInf;
     lrun[h] = 0.f;
-    for (int j = 0; j < DPL; ++j) o[h][j] = 0.f;
+    o[h][0] = o[h][1] = 0.f;
   }
   for (int t0 = w_begin; t0 < w_end; t0 += 64) {
     const int tok = t0 + lane;
     const bool valid = tok < w_end;
     int64_t koff = 0;
+    float ksc = 1.f;
     if (valid) {
-      koff = token_elem(a, b, hk, tok, D);
+      koff = token_elem(a, b, hk, tok, hd);
+      if constexpr (K == CacheKind::kFP8) ksc = a.k_scale[koff / hd];
     }
     for (int h = 0; h < G && h < 16; ++h) {
       float sc = kNegInf;
       if (valid) {
         float acc = 0.f;
-        for (int d = 0; d < D; ++d) acc += sq[h * D + d] * kc[koff + d];
-        sc = acc * a.scale_log2;
+        for (int d = 0; d < hd; ++d) acc += sq[h * hd + d] * kv_value<K>(a.k_cache, koff + d);
+        sc = acc * ksc * a.scale_log2;
       }
       float mx = sc;
       for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -903,12 +928,14 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
       sp[lane] = pr;
       __builtin_amdgcn_wave_barrier();
       const int nt = min(64, w_end - t0);
-      for (int j = 0; j < DPL; ++j) o[h][j] *= alpha;
+      o[h][0] *= alpha;
+      o[h][1] *= alpha;
       for (int t = 0; t < nt; ++t) {
-        const int tk = t0 + t;
-        const int64_t voff = token_elem(a, b, hk, tk, D);
-        const float pt = sp[t];
-        for (int j = 0; j < DPL; ++j) o[h][j] += pt * vc[voff + lane + 64 * j];
+        const int64_t voff = token_elem(a, b, hk, t0 + t, hd);
+        float pt = sp[t];
+        if constexpr (K == CacheKind::kFP8) pt *= a.v_scale[voff / hd];
+        for (int j = 0; j < 2; ++j)
+          if (lane + 64 * j < hd) o[h][j] += pt * kv_value<K>(a.v_cache, voff + lane + 64 * j);
       }
       __builtin_amdgcn_wave_barrier();
     }
@@ -923,22 +950,23 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
       sm[wave * 16 + h] = mrun[h];
       sl[wave * 16 + h] = lrun[h];
     }
-    for (int j = 0; j < DPL; ++j) so[(wave * G + h) * D + lane + 64 * j] = o[h][j];
+    for (int j = 0; j < 2; ++j)
+      if (lane + 64 * j < hd) so[(wave * G + h) * ws_d + lane + 64 * j] = o[h][j];
   }
   __syncthreads();
   const int64_t item = ((int64_t)b * a.hkv + hk) * a.max_splits + split;
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int head = idx / D;
-    const int d = idx - head * D;
+  for (int idx = threadIdx.x; idx < G * hd; idx += blockDim.x) {
+    const int head = idx / hd;
+    const int d = idx - head * hd;
     float M = kNegInf;
     for (int w = 0; w < kWavesPerBlock; ++w) M = fmaxf(M, sm[w * 16 + head]);
     float acc = 0.f, lsum = 0.f;
     for (int w = 0; w < kWavesPerBlock; ++w) {
       const float e = __builtin_amdgcn_exp2f(sm[w * 16 + head] - M);
-      acc += e * so[(w * G + head) * D + d];
+      acc += e * so[(w * G + head) * ws_d + d];
       lsum += e * sl[w * 16 + head];
     }
-    a.ws_o[(item * G + head) * D + d] = acc;
+    a.ws_o[(item * G + head) * ws_d + d] = acc;
     if (d == 0) {
       a.ws_ml[(item * G + head) * 2 + 0] = M;
       a.ws_ml[(item * G + head) * 2 + 1] = lsum;
@@ -947,9 +975,9 @@ __global__ __launch_bounds__(256) void decode_split_kernel_f32(DecodeArgs a) {
 }
 
 // Merge the splits of one (b, q head): out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
-template <int D, bool kBF16Out>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
-  constexpr int DPL = D / 64;
+// Partial rows are ws_d floats wide; head_dim entries lane + 64 j are written.
+template <bool kBF16Out>
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a, int ws_d) {
   const int hq = blockIdx.x;
   const int b = blockIdx.y;
   const int lane = threadIdx.x;
@@ -961,18 +989,19 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
   const int64_t item0 = ((int64_t)b * a.hkv + hk) * a.max_splits;
   float M = kNegInf;
   for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_ml[((item0 + s) * G + head) * 2]);
-  float acc[DPL];
-  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+  float acc[2] = {0.f, 0.f};
   float lsum = 0.f;
   for (int s = 0; s < nsplit; ++s) {
     const int64_t it = (item0 + s) * G + head;
     const float e = __builtin_amdgcn_exp2f(a.ws_ml[it * 2] - M);
     lsum += e * a.ws_ml[it * 2 + 1];
-    for (int j = 0; j < DPL; ++j) acc[j] += e * a.ws_o[it * D + lane + 64 * j];
+    for (int j = 0; j < 2; ++j)
+      if (lane + 64 * j < a.head_dim) acc[j] += e * a.ws_o[it * ws_d + lane + 64 * j];
   }
   const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
   const int64_t dst = (int64_t)b * a.o_sb + (int64_t)hq * a.o_sh;
-  for (int j = 0; j < DPL; ++j) {
+  for (int j = 0; j < 2; ++j) {
+    if (lane + 64 * j >= a.head_dim) continue;
     const float v = acc[j] * inv;
     if constexpr (kBF16Out) {
       static_cast<uint16_t *>(a.out)[dst + lane + 64 * j] = f32_to_bf16_bits(v);
@@ -982,7 +1011,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
   }
 }
 
-template <int D, bool kFP8>
+template <int D, bool kFP8, bool kPad>
 hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStream_t stream) {
   const int cus = device_cu_count();
   const int64_t items = (int64_t)a.batch * a.hkv * a.max_splits;  // upper bound of the dense item count
@@ -991,22 +1020,22 @@ hipError_t launch_mfma(const DecodeArgs &a, dim3 block, size_t lds_merge, hipStr
                      sizeof(int) * (kWavesPerBlock + 2 * (size_t)a.batch + 1);
   switch (a.split_tokens / (kWavesPerBlock * kTileTokens)) {
     case 2:
-      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 2>), grid, block, lds, stream, a);
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 2, kPad>), grid, block, lds, stream, a);
       break;
     case 4:
-      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 4>), grid, block, lds, stream, a);
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 4, kPad>), grid, block, lds, stream, a);
       break;
     case 8:
-      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 8>), grid, block, lds, stream, a);
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 8, kPad>), grid, block, lds, stream, a);
       break;
     default:
-      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 1>), grid, block, lds, stream, a);
+      hipLaunchKernelGGL((decode_split_kernel<D, kFP8, 1, kPad>), grid, block, lds, stream, a);
       break;
   }
   return hipGetLastError();
 }
 
-template <int D, bool kFP8>
+template <int D, bool kFP8, bool kPad>
 hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream_t stream) {
   DecodeArgs a = a0;
   const int64_t blocks = balanced_stream_waves(D, a.batch, a.hkv, a.max_len) / kWavesPerBlock;
@@ -1020,14 +1049,14 @@ hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream
     static_cast<DecodeArgs &>(f) = a;
     f.ap = *ap;
     if (ap->part_splits > 0)
-      hipLaunchKernelGGL((decode_stream_append_kernel<D, kFP8, true>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((decode_stream_append_kernel<D, kFP8, true, kPad>), dim3((unsigned)blocks),
                          dim3(64 * kWavesPerBlock), lds, stream, f);
     else
-      hipLaunchKernelGGL((decode_stream_append_kernel<D, kFP8, false>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((decode_stream_append_kernel<D, kFP8, false, kPad>), dim3((unsigned)blocks),
                          dim3(64 * kWavesPerBlock), lds, stream, f);
   } else {
-    hipLaunchKernelGGL((decode_stream_kernel<D, kFP8>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock), lds, stream,
-                       a);
+    hipLaunchKernelGGL((decode_stream_kernel<D, kFP8, kPad>), dim3((unsigned)blocks), dim3(64 * kWavesPerBlock), lds,
+                       stream, a);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -1041,35 +1070,51 @@ hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream
   return hipGetLastError();
 }
 
-template <int D>
+// MFMA kernels on D-wide tiles (kPad: rows of a.head_dim < D).
+template <int D, bool kPad>
 hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
-  if (kind != CacheKind::kF32 && a.split_tokens == 0)
-    return kind == CacheKind::kFP8 ? launch_stream<D, true>(a, nullptr, stream) : launch_stream<D, false>(a, nullptr, stream);
-  const dim3 grid(a.max_splits, a.hkv, a.batch);
   const dim3 block(64 * kWavesPerBlock);
   const size_t lds = sizeof(float) * (kWavesPerBlock * a.group * D + 2 * kWavesPerBlock * 16);
   hipError_t err = hipSuccess;
-  switch (kind) {
-    case CacheKind::kBF16:
-      err = launch_mfma<D, false>(a, block, lds, stream);
-      break;
-    case CacheKind::kFP8:
-      err = launch_mfma<D, true>(a, block, lds, stream);
-      break;
-    case CacheKind::kF32: {
-      const size_t lds32 = lds + sizeof(float) * (a.group * D + kWavesPerBlock * 64);
-      hipLaunchKernelGGL((decode_split_kernel_f32<D>), grid, block, lds32, stream, a);
-      err = hipGetLastError();
-      break;
+  if (kind == CacheKind::kFP8) {
+    if constexpr (D >= 64) {  // fp8 tiles are at least 64 wide (one 16-byte fragment per lane and row)
+      if (a.split_tokens == 0) return launch_stream<D, true, kPad>(a, nullptr, stream);
+      err = launch_mfma<D, true, kPad>(a, block, lds, stream);
+    } else {
+      return hipErrorInvalidValue;
     }
+  } else {
+    if (a.split_tokens == 0) return launch_stream<D, false, kPad>(a, nullptr, stream);
+    err = launch_mfma<D, false, kPad>(a, block, lds, stream);
   }
   if (err != hipSuccess) return err;
-  const dim3 cgrid(a.hq, a.batch);
-  if (kind == CacheKind::kF32) {
-    hipLaunchKernelGGL((decode_combine_kernel<D, false>), cgrid, dim3(64), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((decode_combine_kernel<D, true>), cgrid, dim3(64), 0, stream, a);
+  hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(a.hq, a.batch), dim3(64), 0, stream, a, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_valu(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
+  const int ws_d = workspace_head_dim(a.head_dim, kind);
+  const dim3 grid(a.max_splits, a.hkv, a.batch);
+  const dim3 block(64 * kWavesPerBlock);
+  const size_t lds = sizeof(float) * (kWavesPerBlock * a.group * ws_d + 2 * kWavesPerBlock * 16 +
+                                      a.group * a.head_dim + kWavesPerBlock * 64);
+  switch (kind) {
+    case CacheKind::kF32:
+      hipLaunchKernelGGL((decode_split_kernel_valu<CacheKind::kF32>), grid, block, lds, stream, a, ws_d);
+      break;
+    case CacheKind::kBF16:
+      hipLaunchKernelGGL((decode_split_kernel_valu<CacheKind::kBF16>), grid, block, lds, stream, a, ws_d);
+      break;
+    case CacheKind::kFP8:
+      hipLaunchKernelGGL((decode_split_kernel_valu<CacheKind::kFP8>), grid, block, lds, stream, a, ws_d);
+      break;
   }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  if (kind == CacheKind::kF32)
+    hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(a.hq, a.batch), dim3(64), 0, stream, a, ws_d);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(a.hq, a.batch), dim3(64), 0, stream, a, ws_d);
   return hipGetLastError();
 }
 
@@ -1094,15 +1139,26 @@ int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
 }
 
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
-  if (head_dim == 64) return launch_d<64>(a, kind, stream);
-  return launch_d<128>(a, kind, stream);
+  const int D = tile_head_dim(head_dim, kind);
+  const bool pad = D != head_dim;
+  if (D == 0) return launch_valu(a, kind, stream);
+  if (D == 32) return pad ? launch_d<32, true>(a, kind, stream) : launch_d<32, false>(a, kind, stream);
+  if (D == 64) return pad ? launch_d<64, true>(a, kind, stream) : launch_d<64, false>(a, kind, stream);
+  return pad ? launch_d<128, true>(a, kind, stream) : launch_d<128, false>(a, kind, stream);
 }
 
 hipError_t launch_decode_attn_append(const DecodeAppendArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
-  const bool fp8 = kind == CacheKind::kFP8;
-  if (head_dim == 64)
-    return fp8 ? launch_stream<64, true>(a, &a.ap, stream) : launch_stream<64, false>(a, &a.ap, stream);
-  return fp8 ? launch_stream<128, true>(a, &a.ap, stream) : launch_stream<128, false>(a, &a.ap, stream);
+  const int D = tile_head_dim(head_dim, kind);
+  const bool pad = D != head_dim;
+  if (kind == CacheKind::kFP8) {
+    if (D == 64) return pad ? launch_stream<64, true, true>(a, &a.ap, stream) : launch_stream<64, true, false>(a, &a.ap, stream);
+    if (D == 128) return pad ? launch_stream<128, true, true>(a, &a.ap, stream) : launch_stream<128, true, false>(a, &a.ap, stream);
+    return hipErrorInvalidValue;
+  }
+  if (D == 32) return pad ? launch_stream<32, false, true>(a, &a.ap, stream) : launch_stream<32, false, false>(a, &a.ap, stream);
+  if (D == 64) return pad ? launch_stream<64, false, true>(a, &a.ap, stream) : launch_stream<64, false, false>(a, &a.ap, stream);
+  if (D == 128) return pad ? launch_stream<128, false, true>(a, &a.ap, stream) : launch_stream<128, false, false>(a, &a.ap, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace tt

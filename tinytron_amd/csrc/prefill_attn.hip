@@ -164,7 +164,7 @@ __device__ __forceinline__ void pv_block(const bf16x8 (&vb)[D / 16], bf16x8 pa_h
 // VALU work that needs the second workgroup to hide.
 template <int D, bool kFP8>
 constexpr int prefill_blocks() {
-  return D == 64 ? 4 : (kFP8 ? 2 : 4);
+  return D <= 64 ? 4 : (kFP8 ? 2 : 4);
 }
 
 template <int D, bool kFP8>
@@ -172,9 +172,10 @@ constexpr int prefill_wgs_per_cu() {
   return (D == 128 && !kFP8) ? 1 : 2;
 }
 
-template <int D, bool kFP8, int NB>
+template <int D, bool kFP8, int NB, bool kPad>
 __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_attn_kernel(PrefillArgs a) {
   using TR = KVTraits<kFP8>;
+  const int hd = row_len<D, kPad>(a);
   constexpr int NDB = D / 32;
   constexpr int NU = Tile<D, kFP8>::NU;
   constexpr int kKLoads = 2 * NU + (kFP8 ? 4 : 0);
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_
 #pragma unroll
     for (int s = 0; s < NDB; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (col_valid) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
+      if (col_valid && (!kPad || TR::q_offset(s, g) < hd)) v = *reinterpret_cast<const u32x4 *>(q + qrow + TR::q_offset(s, g));
       qf[j][s] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -260,24 +261,24 @@ __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_
     Tile<D, kFP8> buf[2];
     int64_t e0, e1;
     int r0, r1;
-    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0, e0, r0);
-    stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * c0 + 1, e1, r1);
-    load_k_block<D, kFP8>(a, e0, r0, lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
-    load_k_block<D, kFP8>(a, e1, r1, lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
+    stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * c0, e0, r0);
+    stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * c0 + 1, e1, r1);
+    load_k_block<D, kFP8, kPad>(a, e0, r0, lane, buf[0].k[0], buf[0].ks[0], buf[0].vs[0]);
+    load_k_block<D, kFP8, kPad>(a, e1, r1, lane, buf[0].k[1], buf[0].ks[1], buf[0].vs[1]);
     __builtin_amdgcn_sched_barrier(0);
-    load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
-    load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+    load_v_block_lds<D, kFP8, kPad>(a, e0, r0, lane, vlds);
+    load_v_block_lds<D, kFP8, kPad>(a, e1, r1, lane, vlds + NU * 1024);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < kPrefillChunkTiles; ++k) {
       const int it = c0 + k;
       if (it >= c1) break;  // uniform
       if (k + 1 < kPrefillChunkTiles) {
-        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 2, e0, r0);
-        stream_block_addr<D>(a, b, hk, L, entry, pbase, 2 * it + 3, e1, r1);
+        stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * it + 2, e0, r0);
+        stream_block_addr<D, kPad>(a, b, hk, L, entry, pbase, 2 * it + 3, e1, r1);
         Tile<D, kFP8> &nx = buf[(k + 1) & 1];
-        load_k_block<D, kFP8>(a, e0, r0, lane, nx.k[0], nx.ks[0], nx.vs[0]);
-        load_k_block<D, kFP8>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
+        load_k_block<D, kFP8, kPad>(a, e0, r0, lane, nx.k[0], nx.ks[0], nx.vs[0]);
+        load_k_block<D, kFP8, kPad>(a, e1, r1, lane, nx.k[1], nx.ks[1], nx.vs[1]);
       }
       __builtin_amdgcn_sched_barrier(0);
       const int t0 = kTileTokens * it;
@@ -309,8 +310,8 @@ __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_
       __builtin_amdgcn_s_waitcnt(kLgkmcntZero);
       __builtin_amdgcn_sched_barrier(0);
       if (k + 1 < kPrefillChunkTiles && it + 1 < c1) {
-        load_v_block_lds<D, kFP8>(a, e0, r0, lane, vlds);
-        load_v_block_lds<D, kFP8>(a, e1, r1, lane, vlds + NU * 1024);
+        load_v_block_lds<D, kFP8, kPad>(a, e0, r0, lane, vlds);
+        load_v_block_lds<D, kFP8, kPad>(a, e1, r1, lane, vlds + NU * 1024);
       }
       __builtin_amdgcn_sched_barrier(0);
       bf16x8 vb[D / 16];
@@ -348,6 +349,7 @@ __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_
 #pragma unroll
       for (int c = 0; c < 2 * NDB; ++c) {
         const int d0 = o_col_d<kFP8>(c, 4 * g);
+        if (kPad && d0 >= hd) continue;  // columns past head_dim (hd is a multiple of 8)
         const uint2 w = make_uint2(pack_bf16x2(st[j].o[c][0] * inv, st[j].o[c][1] * inv),
                                    pack_bf16x2(st[j].o[c][2] * inv, st[j].o[c][3] * inv));
         if (a.vec_out) {
@@ -363,7 +365,7 @@ __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_
   }
 }
 
-template <int D, bool kFP8>
+template <int D, bool kFP8, bool kPad>
 hipError_t launch_d(const PrefillArgs &a0, hipStream_t stream) {
   constexpr int NB = prefill_blocks<D, kFP8>();
   PrefillArgs a = a0;
@@ -373,16 +375,25 @@ hipError_t launch_d(const PrefillArgs &a0, hipStream_t stream) {
   const int64_t slots = (pairs + kXcds - 1) / kXcds * a.wg_per_pair;
   const int64_t grid = slots * kXcds;
   const size_t lds = (size_t)kWavesPerBlock * Tile<D, kFP8>::kVBytes;
-  hipLaunchKernelGGL((prefill_attn_kernel<D, kFP8, NB>), dim3((unsigned)grid), dim3(64 * kWavesPerBlock), lds, stream,
-                     a);
+  hipLaunchKernelGGL((prefill_attn_kernel<D, kFP8, NB, kPad>), dim3((unsigned)grid), dim3(64 * kWavesPerBlock), lds,
+                     stream, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_prefill_attn(const PrefillArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
-  if (head_dim == 64) return kind == CacheKind::kFP8 ? launch_d<64, true>(a, stream) : launch_d<64, false>(a, stream);
-  return kind == CacheKind::kFP8 ? launch_d<128, true>(a, stream) : launch_d<128, false>(a, stream);
+  const int D = tile_head_dim(head_dim, kind);
+  const bool pad = D != head_dim;
+  if (kind == CacheKind::kFP8) {
+    if (D == 64) return pad ? launch_d<64, true, true>(a, stream) : launch_d<64, true, false>(a, stream);
+    if (D == 128) return pad ? launch_d<128, true, true>(a, stream) : launch_d<128, true, false>(a, stream);
+    return hipErrorInvalidValue;
+  }
+  if (D == 32) return pad ? launch_d<32, false, true>(a, stream) : launch_d<32, false, false>(a, stream);
+  if (D == 64) return pad ? launch_d<64, false, true>(a, stream) : launch_d<64, false, false>(a, stream);
+  if (D == 128) return pad ? launch_d<128, false, true>(a, stream) : launch_d<128, false, false>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace tt

@@ -90,6 +90,10 @@ struct DecodeArgs {
   // before its tiles, so that a wave's share counts the fixed start-up cost of
   // every segment piece it holds, not only its tiles (set by the launcher)
   int seg_cost;
+  // the cache's head_dim (row length) and 1 / head_dim; kernels built for a
+  // wider tile (tile_head_dim) read rows of this length
+  int head_dim;
+  double inv_head_dim;
 };
 
 // Fused decode step: the split kernel also applies RoPE to this step's token
@@ -225,6 +229,22 @@ int64_t balanced_stream_waves(int head_dim, int64_t batch, int64_t hkv, int64_t 
 inline int64_t num_splits(int64_t max_len, int64_t split_tokens) {
   return max_len <= 0 ? 1 : (max_len + split_tokens - 1) / split_tokens;
 }
+
+// Tile width of the MFMA attention kernels for a bf16 / fp8 cache of this
+// head_dim: the smallest of 32 (bf16 only), 64 and 128 that holds it, when a
+// row is a whole number of 16-byte fragments (head_dim a multiple of 8 bf16 /
+// 16 fp8 values) and head_dim <= 128; 0 otherwise (fp32 caches and other head
+// dims take the VALU kernel).
+inline int tile_head_dim(int64_t head_dim, CacheKind kind) {
+  if (kind == CacheKind::kF32 || head_dim <= 0 || head_dim > 128) return 0;
+  if (head_dim % (kind == CacheKind::kFP8 ? 16 : 8) != 0) return 0;
+  if (kind == CacheKind::kBF16 && head_dim <= 32) return 32;
+  return head_dim <= 64 ? 64 : 128;
+}
+
+// Width (floats) of the attention workspace's partial rows for any kernel and
+// cache type: at least the tile width and head_dim.
+inline int workspace_head_dim(int64_t head_dim, CacheKind = CacheKind::kBF16) { return head_dim <= 64 ? 64 : 128; }
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kTileTokens = 32;  // tokens per wave iteration (two 16-row MFMA blocks)

@@ -127,7 +127,8 @@ class Attention(nn.Module):
         if len(set(lens)) == 1 and lens[0] != position_offset:
             raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
         table = rope_table_for(past_kv.max_seq_len + T, self.head_dim, self.config.rope_theta, act, x.device)
-        if T == 1 and act == torch.bfloat16 and past_kv.layout.kind == "bf16":
+        if T == 1 and act == torch.bfloat16 and past_kv.layout.kind == "bf16" \
+                and ops.attention_tile_dim(self.head_dim, "bf16"):
             y = past_kv.decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], table)  # RoPE + append + attention
             y = y.view(B, 1, C)
         elif T == 1:
@@ -148,7 +149,8 @@ class Attention(nn.Module):
         q_rot = cache.rope_append(q, k, v, table, new_lens=new)
         y = torch.zeros(B, T, self.n_embd, dtype=q.dtype, device=q.device)
         if self.prefill_kernel and q.dtype == torch.bfloat16 and cache.layout.kind in ("bf16", "fp8") \
-                and D in (64, 128) and self.num_attention_heads // self.num_key_value_heads <= 16:
+                and ops.attention_tile_dim(D, cache.layout.kind) \
+                and self.num_attention_heads // self.num_key_value_heads <= 16:
             cache.prefill_attend(q_rot, new, out=y.view(B, T, self.num_attention_heads, D))
             return y
         rep = self.num_attention_heads // self.num_key_value_heads
@@ -369,7 +371,8 @@ class GPT(nn.Module):
             layer = cache.get_layer_cache(i)
             wqkv, wo, wgu, wd = self._stacked_weights(i)
             P = ops.linear_partials(h, wqkv, partials=pbuf, k_chunk=kc_c)
-            if P.shape[0] <= ops.FUSED_STEP_MAX_SPLITS and layer.layout.kind == "bf16":
+            if P.shape[0] <= ops.FUSED_STEP_MAX_SPLITS and layer.layout.kind == "bf16" \
+                    and ops.attention_tile_dim(D, "bf16"):
                 y = layer.decode_step_partials(P, Hq, table)        # RoPE + append + attention, [B, Hq, D]
             else:
                 q_rot = layer.rope_append_partials(P, Hq, table)     # sums the q|k|v partials itself
@@ -392,11 +395,12 @@ class GPT(nn.Module):
         if not self.fused_prefill or self.compute_dtype != torch.bfloat16 or not self.wte.weight.is_cuda:
             return False
         D = c.hidden_size // c.num_attention_heads
-        if not (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192 and D in (64, 128)
+        if not (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192
                 and c.num_attention_heads // c.num_key_value_heads <= 16 and c.intermediate_size % 4 == 0
                 and all(blk.attn.prefill_kernel for blk in self.blocks)
                 and all(_is_fused_cache(cache.get_layer_cache(i))
-                        and cache.get_layer_cache(i).layout.kind in ("bf16", "fp8") for i in range(len(self.blocks)))):
+                        and ops.attention_tile_dim(D, cache.get_layer_cache(i).layout.kind)
+                        for i in range(len(self.blocks)))):
             return False
         # every requested logit row must be one of the sequence's new tokens
         B, T = idx.shape

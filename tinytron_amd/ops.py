@@ -254,6 +254,22 @@ class Workspace:
         return self.buf
 
 
+def attention_tile_dim(head_dim: int, kind: str) -> int:
+    """Tile width of the MFMA attention kernels for a ``kind`` ("bf16" / "fp8")
+    cache of this head_dim (the library's tile rule): 32 (bf16 only), 64 or 128
+    when a row is a whole number of 16-byte fragments (head_dim a multiple of 8
+    bf16 / 16 fp8 values) and head_dim <= 128; 0 otherwise, where decode
+    attention runs the VALU kernel and the fused decode step and the prefill
+    kernel do not apply."""
+    if kind not in ("bf16", "fp8") or head_dim <= 0 or head_dim > 128:
+        return 0
+    if head_dim % (16 if kind == "fp8" else 8):
+        return 0
+    if kind == "bf16" and head_dim <= 32:
+        return 32
+    return 64 if head_dim <= 64 else 128
+
+
 def split_tokens_for(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
     return int(_lib.load().tt_decode_split_tokens(batch, num_kv_heads, max_seq_len))
 
