@@ -527,13 +527,19 @@ def measured_traffic(config: str):
 
 
 def timed_steps(torch, fn, steps, warmup, min_warm_s=0.1):
-    """Per-step GPU times of `steps` calls of fn on torch's current stream (the
-    stream the library's kernels are launched on): `warmup` untimed calls, more
-    until at least min_warm_s of them have run (clocks and caches settled), a
-    synchronize, then one event before the first step and one after every
-    step, so that step i's time is the gap between events i and i + 1 and the
-    steps together span the whole timed region. Returns the median (the
-    per-step figure reported), mean, min and max in ms."""
+    """GPU time of `steps` calls of fn on torch's current stream (the stream
+    the library's kernels are launched on), after `warmup` untimed calls and
+    more until at least min_warm_s of them have run (clocks and caches
+    settled). Two timed passes of `steps` calls each:
+      - window: one event before the first call and one after the last, so
+        that nothing but the steps themselves is enqueued between them; the
+        window mean is the per-step figure reported (mean_ms);
+      - per step: one event after every call, so that step i's time is the gap
+        between events i and i + 1 (median, min, max). Each event is a marker
+        packet between two steps, which costs the stream a few microseconds
+        per step: these figures bound the window mean from above and show the
+        spread (a stall inside the window shows as a max far above the median).
+    """
     t0 = time.perf_counter()
     n = 0
     while n < warmup or time.perf_counter() - t0 < min_warm_s:
@@ -543,6 +549,13 @@ def timed_steps(torch, fn, steps, warmup, min_warm_s=0.1):
             torch.cuda.synchronize()
     torch.cuda.synchronize()
     steps = max(int(steps), 1)
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0.record()
+    for _ in range(steps):
+        fn()
+    w1.record()
+    torch.cuda.synchronize()
+    mean = w0.elapsed_time(w1) / steps
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record()
     for i in range(steps):
@@ -552,23 +565,23 @@ def timed_steps(torch, fn, steps, warmup, min_warm_s=0.1):
     per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
     mid = steps // 2
     median = per[mid] if steps % 2 else 0.5 * (per[mid - 1] + per[mid])
-    return {"median_ms": median, "mean_ms": ev[0].elapsed_time(ev[steps]) / steps, "min_ms": per[0],
-            "max_ms": per[-1], "warmup_calls": n}
+    return {"mean_ms": mean, "median_ms": median, "min_ms": per[0], "max_ms": per[-1], "warmup_calls": n}
 
 
 def spread(st):
-    """Per-step spread record (µs) of a timed_steps result."""
-    return {"median_us": round(st["median_ms"] * 1e3, 2), "mean_us": round(st["mean_ms"] * 1e3, 2),
-            "min_us": round(st["min_ms"] * 1e3, 2), "max_us": round(st["max_ms"] * 1e3, 2),
+    """Timing record (µs) of a timed_steps result."""
+    return {"window_mean_us": round(st["mean_ms"] * 1e3, 2), "per_step_median_us": round(st["median_ms"] * 1e3, 2),
+            "per_step_min_us": round(st["min_ms"] * 1e3, 2), "per_step_max_us": round(st["max_ms"] * 1e3, 2),
             "warmup_calls": st["warmup_calls"]}
 
 
 def run_config(name, args, torch, ops):
     """Time one attention config on the GPU: the decode step (fused launch pair
     for bf16 caches, RoPE + append then attention for fp8), the two-launch step,
-    and the attention operator alone, each over args.steps steps (per-step HIP
-    events on the stream the kernels run on, median reported) after a warm-up
-    of at least args.warmup steps and 100 ms. Returns the record and the
+    and the attention operator alone, each over args.steps steps (a window of
+    back-to-back steps between two HIP events on the stream the kernels run on,
+    then a pass with per-step events for the spread) after a warm-up of at
+    least args.warmup steps and 100 ms. Returns the record and the
     workload (kept for the CPU baseline, which runs after every GPU leg)."""
     cfg = CONFIGS[name]
     wl = build_workload(cfg, args.seed, torch, ops)
@@ -604,7 +617,7 @@ def run_config(name, args, torch, ops):
     st_step = timed_steps(torch, step, args.steps, args.warmup)
     st_two = timed_steps(torch, two_launch_step, args.steps, args.warmup)  # RoPE + append, then attention
     st_attn = timed_steps(torch, attn_only, args.steps, args.warmup)  # the dominant operator alone (q rotated above)
-    ms, two_ms, attn_ms = st_step["median_ms"], st_two["median_ms"], st_attn["median_ms"]
+    ms, two_ms, attn_ms = st_step["mean_ms"], st_two["mean_ms"], st_attn["mean_ms"]
     step_bytes, attn_bytes, tokens = algorithmic_bytes(cfg, wl["total"])
     value = step_bytes / (ms * 1e-3) / 1e9
     achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
@@ -614,7 +627,8 @@ def run_config(name, args, torch, ops):
         "ms_per_step": round(ms, 5),
         "ms_per_step_two_launches": round(two_ms, 5),
         "per_step": {"step": spread(st_step), "two_launch_step": spread(st_two), "attention": spread(st_attn),
-                     "statistic": "median of per-step HIP event gaps (ms_per_step, value, roofline.avg_us)"},
+                     "statistic": "ms_per_step, value and roofline.avg_us: mean over one event-bracketed window of "
+                                  "back-to-back steps; per_step_*: a second pass with an event after every step"},
         "pct_of_peak_hbm": round(100.0 * value / PEAK_HBM_GBS, 2),
         "dtype": "fp8-e4m3 cache, bf16 q/out" if cfg["fp8"] else "bf16",
         "config": {
