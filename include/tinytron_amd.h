@@ -384,6 +384,42 @@ int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_stri
                                        int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale,
                                        tt_stream_t stream);
 
+/*
+ * Row attention: `rows` query rows, row r attending to the first
+ * row_lens[r] cached tokens of sequence seq_of_row[r] (< num_seqs; the
+ * cache holds num_seqs sequences, addressed as in tt_gqa_decode_attn_*).
+ * With rows = the new tokens of a prefill chunk (row r = token t of
+ * sequence b, row_lens[r] = tokens cached before the chunk + t + 1) this is
+ * the prefill branch of the reference attention with its cache-causal mask
+ * (attn.py:321-341: build_cache_causal_mask + F.scaled_dot_product_attention
+ * after cache.append / get_kv, cache.py:34-51) for the cases the prefill
+ * kernel does not take: fp32 caches and activations (the reference's fp32
+ * path), and head dims whose rows are not whole 16-byte fragments. Runs the
+ * VALU split kernel and its combine; q / out as in tt_gqa_decode_attn_*
+ * (strides {row, head}); row_lens[r] <= 0 gives zeros; rows <= 65535;
+ * workspace as tt_decode_workspace_bytes(rows, ..., max_row_len,
+ * 0).
+ */
+int tt_rows_attn_bf16(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                      const int64_t cache_strides[3], const int32_t *seq_of_row, const int32_t *row_lens,
+                      int64_t max_row_len, const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                      int64_t num_seqs, void *out, const int64_t out_strides[2], int64_t rows, int64_t num_q_heads,
+                      int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
+                      size_t workspace_bytes, tt_stream_t stream);
+int tt_rows_attn_fp8(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                     const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                     const int32_t *seq_of_row, const int32_t *row_lens, int64_t max_row_len,
+                     const int32_t *page_table, int64_t max_pages, int64_t num_pages, int64_t num_seqs, void *out,
+                     const int64_t out_strides[2], int64_t rows, int64_t num_q_heads, int64_t num_kv_heads,
+                     int64_t head_dim, int64_t page_size, float sm_scale, void *workspace, size_t workspace_bytes,
+                     tt_stream_t stream);
+int tt_rows_attn_f32(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                     const int64_t cache_strides[3], const int32_t *seq_of_row, const int32_t *row_lens,
+                     int64_t max_row_len, const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                     int64_t num_seqs, void *out, const int64_t out_strides[2], int64_t rows, int64_t num_q_heads,
+                     int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
+                     size_t workspace_bytes, tt_stream_t stream);
+
 /* Fixed split size the fp32 entry point uses when split_tokens == 0. */
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 

@@ -208,9 +208,10 @@ def test_fused_decode_step_matches_module_path():
 
 
 @pytest.mark.parametrize("kv_dtype", [None, "fp8"])
-def test_prefill_kernel_matches_sdpa_path(kv_dtype):
-    """Attention._prefill through the prefill kernel equals the per-sequence
-    SDPA path on the same (ragged, partly cached) inputs, to bf16 rounding."""
+def test_prefill_kernel_matches_row_attention_path(kv_dtype):
+    """Attention._prefill through the prefill kernel equals the row-attention
+    path (one query row per new token, the VALU kernel) on the same (ragged,
+    partly cached) inputs, to bf16 rounding."""
     from tinytron_amd.cache import PagedKVCache
     from tinytron_amd.model import Attention
 

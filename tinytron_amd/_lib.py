@@ -67,6 +67,15 @@ _ATTN_TAIL = [
     _vp,                                             # stream
 ]
 
+_ROWS_TAIL = [
+    _i64p,                                           # cache_strides
+    _i32p, _i32p, _i64,                              # seq_of_row, row_lens, max_row_len
+    _i32p, _i64, _i64, _i64,                         # page_table, max_pages, num_pages, num_seqs
+    _vp, _i64p,                                      # out, out_strides
+    _i64, _i64, _i64, _i64, _i64,                    # rows, hq, hkv, head_dim, page_size
+    _f32, _vp, _size, _vp,                           # sm_scale, workspace, workspace_bytes, stream
+]
+
 _DECODE_APPEND_HEAD = [
     _vp, _i64p, _vp, _i64p, _vp, _i64p,             # q_in, k_in, v_in (+ {batch, head} strides)
     _i64, _i64,                                      # splits, split_stride
@@ -114,6 +123,9 @@ SIGNATURES = {
     "tt_gqa_decode_attn_bf16": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
     "tt_gqa_decode_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ATTN_TAIL, ctypes.c_int),
     "tt_gqa_decode_attn_f32": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
+    "tt_rows_attn_bf16": (_ATTN_HEAD + _ROWS_TAIL, ctypes.c_int),
+    "tt_rows_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ROWS_TAIL, ctypes.c_int),
+    "tt_rows_attn_f32": (_ATTN_HEAD + _ROWS_TAIL, ctypes.c_int),
     "tt_decode_split_tokens": ([_i64, _i64, _i64], ctypes.c_int64),
     "tt_decode_workspace_bytes": ([_i64, _i64, _i64, _i64, _i64, _i64], ctypes.c_size_t),
     "tt_prefill_attn_bf16": ([_vp, _i64p, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),

@@ -206,13 +206,28 @@ class _LayerCacheBase:
         self._advance_all(1)
         return out
 
-    def prefill_attend(self, q_rot: torch.Tensor, new_lens, out: torch.Tensor | None = None) -> torch.Tensor:
+    def prefill_attend(self, q_rot: torch.Tensor, new_lens, out: torch.Tensor | None = None,
+                       kernel: bool = True) -> torch.Tensor:
         """Causal attention of the chunk just appended by rope_append (q_rot
         [B, H_q, T, D], new_lens[b] tokens of sequence b) over each sequence's
-        cache; returns [B, T, H_q, D], rows past new_lens[b] untouched."""
-        prev = self._lens_dev[1 - self._cur]  # the lengths before the append (the other buffer)
-        nl = torch.tensor([int(n) for n in new_lens], dtype=torch.int32).to(prev.device, non_blocking=True)
-        return ops.prefill_attention(q_rot, self.layout, prev, self.current_length, new_lens=nl, out=out)
+        cache; returns [B, T, H_q, D]. bf16 activations over a bf16 / fp8 cache
+        whose rows are whole 16-byte fragments take the prefill kernel (rows
+        past new_lens[b] untouched); fp32 and the other head dims take row
+        attention, one query row per new token (rows past new_lens[b] zero;
+        ``kernel=False`` takes it for every case)."""
+        lay = self.layout
+        T = q_rot.shape[2]
+        if kernel and q_rot.dtype == torch.bfloat16 and lay.kind in ("bf16", "fp8") \
+                and ops.attention_tile_dim(lay.head_dim, lay.kind) \
+                and q_rot.shape[1] // lay.num_heads <= 16:
+            prev = self._lens_dev[1 - self._cur]  # the lengths before the append (the other buffer)
+            nl = torch.tensor([int(n) for n in new_lens], dtype=torch.int32).to(prev.device, non_blocking=True)
+            return ops.prefill_attention(q_rot, lay, prev, self.current_length, new_lens=nl, out=out)
+        adds = [min(int(n), T) for n in new_lens]
+        cached = [x - a for x, a in zip(self._host_lens, adds)]
+        if self.workspace is None:
+            self.workspace = ops.Workspace(q_rot.device)
+        return ops.prefill_attention_rows(q_rot, lay, cached, adds, out=out, workspace=self.workspace)
 
     def attend(self, q: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """GQA decode attention of q [B, H_q, D] over every cached token of each sequence."""
@@ -487,3 +502,70 @@ class PagedKVCache:
         """Raise the reference's overflow error unless every sequence can take ``add`` more tokens."""
         for c in self._layer_caches:
             c._check_room([add] * c.batch_size)
+
+
+class ConcatKVStore:
+    """Device store behind the reference's non-paged cache: the per-layer tuple
+    (k, v) of GQA-expanded heads [B, H_q, T, D] that attn.py:174-186 grows by
+    torch.cat at every call (engine.py:168-178 with use_paged_kv_cache=False).
+
+    The tuples handed out are views ``[:, :, :length]`` of a contiguous
+    [B, H_q, capacity, D] store that the kernels address as a contiguous
+    [B, H, pages, 16, D] cache with H = H_q (one KV head per query head, as
+    the expanded tensors are). A call that continues the newest tuple appends
+    in place; one that continues an older or a foreign tuple gets a new store
+    with that tuple copied in, so earlier tuples keep the values they had (the
+    reference's torch.cat never changes its inputs). Capacity grows by
+    doubling (16-token pages)."""
+
+    PAGE = 16
+
+    def __init__(self) -> None:
+        self.k = self.v = None
+        self.length = 0
+        self.capacity = 0
+        self.layout = None
+
+    def _owns(self, past) -> bool:
+        k, v = past
+        return (self.k is not None and k.data_ptr() == self.k.data_ptr() and v.data_ptr() == self.v.data_ptr()
+                and k.shape[2] == self.length and k.stride() == self.k.stride() and v.stride() == self.v.stride())
+
+    def _allocate(self, B: int, H: int, D: int, capacity: int, dtype, device) -> None:
+        cap = -(-capacity // self.PAGE) * self.PAGE
+        self.k = torch.empty(B, H, cap, D, dtype=dtype, device=device)
+        self.v = torch.empty(B, H, cap, D, dtype=dtype, device=device)
+        self.capacity = cap
+        self.layout = ops.KVLayout(k=self.k.view(-1), v=self.v.view(-1), strides=(H * cap * D, self.PAGE * D, cap * D),
+                                   num_heads=H, head_dim=D, page_size=self.PAGE, capacity=cap,
+                                   kind=cache_kind(dtype))
+
+    def prepare(self, past, B: int, H: int, D: int, add: int, dtype, device) -> int:
+        """Make room for `add` tokens after `past` (None or a (k, v) tuple
+        [B, H, T_past, D]); returns T_past."""
+        if past is None:
+            t_past = 0
+        else:
+            k, v = past
+            if k.dim() != 4 or k.shape[:2] != (B, H) or k.shape[3] != D or v.shape != k.shape:
+                raise ValueError(f"past key/value shapes {tuple(k.shape)} / {tuple(v.shape)} do not match "
+                                 f"[{B}, {H}, T, {D}]")
+            t_past = int(k.shape[2])
+        need = t_past + add
+        fits = self.k is not None and self.k.shape[:2] == (B, H) and self.k.dtype == dtype and \
+            self.k.device == torch.device(device) and need <= self.capacity
+        if past is not None and self._owns(past) and fits:
+            return t_past  # continue the newest tuple in place
+        old_k = old_v = None
+        if past is not None:
+            old_k, old_v = past
+        self._allocate(B, H, D, max(need, 2 * self.capacity if self.k is not None else need), dtype, device)
+        if t_past:
+            self.k[:, :, :t_past].copy_(old_k)
+            self.v[:, :, :t_past].copy_(old_v)
+        return t_past
+
+    def views(self, length: int):
+        """The (k, v) tuple of the first `length` tokens; they become the newest."""
+        self.length = length
+        return self.k[:, :, :length], self.v[:, :, :length]

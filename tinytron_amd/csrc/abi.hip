@@ -230,9 +230,11 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
                   int64_t num_pages, void *out, const int64_t out_strides[2], int64_t batch, int64_t num_q_heads,
                   int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
                   void *workspace, size_t ws_bytes, tt_stream_t stream, const tt::DecodeAppend *ap = nullptr,
-                  bool exact_slots = false) {
+                  bool exact_slots = false, const int32_t *seq_of_row = nullptr, int64_t num_seqs = 0) {
   // ap != null: the fused step (q / k / v from ap, seq_lens = lengths before the step)
   // exact_slots: the balanced workspace holds slots for the launched grid only (allocation-free entry point)
+  // seq_of_row != null: `batch` query rows, row b reading the cache of sequence seq_of_row[b] < num_seqs
+  //   (the VALU kernel)
   TT_CHECK((ap || q) && k_cache && v_cache && seq_lens && out, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK((ap || q_strides) && out_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
   TT_CHECK(batch >= 0 && batch <= 65535, TT_ERR_INVALID_ARGUMENT, "batch must be in [0, 65535]");
@@ -243,8 +245,10 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   TT_CHECK(num_kv_heads <= 65535 && num_q_heads <= 65535, TT_ERR_UNSUPPORTED, "too many heads");
   TT_CHECK(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 128, TT_ERR_UNSUPPORTED,
            "head_dim must be even and <= 128, got %lld", (long long)head_dim);
-  // MFMA kernels on 32 / 64 / 128-wide tiles, or (0) the VALU kernel
-  const int tile = tt::tile_head_dim(head_dim, kind);
+  TT_CHECK(seq_of_row == nullptr || (ap == nullptr && num_seqs >= 1 && num_seqs <= INT32_MAX), TT_ERR_INVALID_ARGUMENT,
+           "row attention needs 1 <= num_seqs <= INT32_MAX (got %lld)", (long long)num_seqs);
+  // MFMA kernels on 32 / 64 / 128-wide tiles, or (0) the VALU kernel (which row attention always takes)
+  const int tile = seq_of_row != nullptr ? 0 : tt::tile_head_dim(head_dim, kind);
   TT_CHECK(ap == nullptr || tile > 0, TT_ERR_UNSUPPORTED,
            "the fused decode step needs head_dim a multiple of 8 (bf16 cache) or 16 (fp8 cache), got %lld",
            (long long)head_dim);
@@ -269,7 +273,7 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     TT_CHECK(cache_strides[1] == page_size * head_dim, TT_ERR_UNSUPPORTED,
              "the contiguous store needs dense pages (page stride %lld != page_size * head_dim)",
              (long long)cache_strides[1]);
-    rc = check_contiguous_room(max_seq_len, head_dim, cache_strides, batch, num_kv_heads);
+    rc = check_contiguous_room(max_seq_len, head_dim, cache_strides, seq_of_row ? num_seqs : batch, num_kv_heads);
     if (rc != TT_OK) return rc;
   }
   if (tile > 0) {
@@ -340,6 +344,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.ws_ml = a.ws_o + rows * tt::workspace_head_dim(head_dim);
   a.head_dim = (int)head_dim;
   a.inv_head_dim = 1.0 / (double)head_dim;
+  a.seq_of_row = seq_of_row;
+  a.num_seqs = (int)num_seqs;
   a.batch = (int)batch;
   a.hq = (int)num_q_heads;
   a.hkv = (int)num_kv_heads;
@@ -726,6 +732,46 @@ int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2], const void
   return decode_common(tt::CacheKind::kF32, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides, seq_lens,
                        max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
                        num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+}
+
+int tt_rows_attn_bf16(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                      const int64_t cache_strides[3], const int32_t *seq_of_row, const int32_t *row_lens,
+                      int64_t max_row_len, const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                      int64_t num_seqs, void *out, const int64_t out_strides[2], int64_t rows, int64_t num_q_heads,
+                      int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
+                      size_t workspace_bytes, tt_stream_t stream) {
+  TT_CHECK(seq_of_row != nullptr, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  return decode_common(tt::CacheKind::kBF16, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides, row_lens,
+                       max_row_len, page_table, max_pages, num_pages, out, out_strides, rows, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, workspace_bytes, stream, nullptr,
+                       false, seq_of_row, num_seqs);
+}
+
+int tt_rows_attn_fp8(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                     const float *k_scale, const float *v_scale, const int64_t cache_strides[3],
+                     const int32_t *seq_of_row, const int32_t *row_lens, int64_t max_row_len,
+                     const int32_t *page_table, int64_t max_pages, int64_t num_pages, int64_t num_seqs, void *out,
+                     const int64_t out_strides[2], int64_t rows, int64_t num_q_heads, int64_t num_kv_heads,
+                     int64_t head_dim, int64_t page_size, float sm_scale, void *workspace, size_t workspace_bytes,
+                     tt_stream_t stream) {
+  TT_CHECK(seq_of_row != nullptr, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  return decode_common(tt::CacheKind::kFP8, q, q_strides, k_cache, v_cache, k_scale, v_scale, cache_strides, row_lens,
+                       max_row_len, page_table, max_pages, num_pages, out, out_strides, rows, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, workspace_bytes, stream, nullptr,
+                       false, seq_of_row, num_seqs);
+}
+
+int tt_rows_attn_f32(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
+                     const int64_t cache_strides[3], const int32_t *seq_of_row, const int32_t *row_lens,
+                     int64_t max_row_len, const int32_t *page_table, int64_t max_pages, int64_t num_pages,
+                     int64_t num_seqs, void *out, const int64_t out_strides[2], int64_t rows, int64_t num_q_heads,
+                     int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
+                     size_t workspace_bytes, tt_stream_t stream) {
+  TT_CHECK(seq_of_row != nullptr, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  return decode_common(tt::CacheKind::kF32, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides, row_lens,
+                       max_row_len, page_table, max_pages, num_pages, out, out_strides, rows, num_q_heads,
+                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, workspace_bytes, stream, nullptr,
+                       false, seq_of_row, num_seqs);
 }
 
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len) {

@@ -875,6 +875,8 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
   const int L = min(a.seq_lens[b], a.max_len);
   const int s_begin = split * a.split_tokens;
   if (s_begin >= L) return;
+  // the sequence whose cache row b attends to
+  const int bs = a.seq_of_row == nullptr ? b : min(max(a.seq_of_row[b], 0), a.num_seqs - 1);
   const int s_end = min(L, s_begin + a.split_tokens);
   const int per_wave = a.split_tokens / kWavesPerBlock;
   const int w_begin = s_begin + wave * per_wave;
@@ -906,7 +908,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
     int64_t koff = 0;
     float ksc = 1.f;
     if (valid) {
-      koff = token_elem(a, b, hk, tok, hd);
+      koff = token_elem(a, bs, hk, tok, hd);
       if constexpr (K == CacheKind::kFP8) ksc = a.k_scale[koff / hd];
     }
     for (int h = 0; h < G && h < 16; ++h) {
@@ -931,7 +933,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
       o[h][0] *= alpha;
       o[h][1] *= alpha;
       for (int t = 0; t < nt; ++t) {
-        const int64_t voff = token_elem(a, b, hk, t0 + t, hd);
+        const int64_t voff = token_elem(a, bs, hk, t0 + t, hd);
         float pt = sp[t];
         if constexpr (K == CacheKind::kFP8) pt *= a.v_scale[voff / hd];
         for (int j = 0; j < 2; ++j)
@@ -1141,7 +1143,9 @@ int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
 hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
   const int D = tile_head_dim(head_dim, kind);
   const bool pad = D != head_dim;
-  if (D == 0) return launch_valu(a, kind, stream);
+  // row attention (a row -> sequence map) exists only in the VALU kernel; the
+  // MFMA kernels address the cache by row index and must never see it
+  if (D == 0 || a.seq_of_row != nullptr) return launch_valu(a, kind, stream);
   if (D == 32) return pad ? launch_d<32, true>(a, kind, stream) : launch_d<32, false>(a, kind, stream);
   if (D == 64) return pad ? launch_d<64, true>(a, kind, stream) : launch_d<64, false>(a, kind, stream);
   return pad ? launch_d<128, true>(a, kind, stream) : launch_d<128, false>(a, kind, stream);

@@ -81,6 +81,10 @@ struct DecodeArgs {
   float *ws_ml;  // [B][H_kv][max_splits][G][2] (running max in log2 units, sum)
                  // balanced partition (split_tokens == 0): [B * H_kv + kMaxStreamWaves][G][D] and [..][G][2]
   int32_t *ws_prefix;  // balanced partition: per-sequence tile prefix [B + 1], written by the split kernel
+  // VALU kernel only: query row b reads the K/V of sequence seq_of_row[b]
+  // (clamped into [0, num_seqs)) instead of sequence b (null: the identity)
+  const int32_t *seq_of_row;
+  int num_seqs;
   int stream_waves;    // balanced partition: waves of the split kernel's grid (set by the launcher)
   int batch, hq, hkv, group, split_tokens, max_splits;
   int page_shift;    // paged pools: log2(page_size); the contiguous store is addressed linearly

@@ -86,8 +86,9 @@ class InferenceEngine:
             self.device = torch.device("cuda:0")
         else:
             torch.cuda.set_device(self.device)
-        if not use_paged_kv_cache:
-            raise ValueError("the gfx950 decode path needs a KV cache (use_paged_kv_cache=True)")
+        if not use_paged_kv_cache and kv_cache_dtype is not None:
+            raise ValueError("a kv_cache_dtype needs the paged KV cache (use_paged_kv_cache=True)")
+        self.use_paged_kv_cache = use_paged_kv_cache
         self.model_config = model_config
         self.kv_cache_page_size = kv_cache_page_size
         self.kv_cache_dtype = kv_cache_dtype
@@ -122,11 +123,19 @@ class InferenceEngine:
                 f"Requested total sequence length {total_len} exceeds block_size {self.model_config.block_size}")
         tokens = torch.zeros(batch_size, total_len, dtype=prompt.dtype, device=self.device)
         tokens[:, :prompt_len] = prompt
-        cache = PagedKVCache.from_model_config(
-            self.model_config, batch_size=batch_size, page_size=self.kv_cache_page_size, device=self.device,
-            dtype=self.dtype, kv_cache_dtype=self.kv_cache_dtype,
-            seq_capacity=[n + max_new_tokens for n in lens], paged_pool=self.paged_pool, page_seed=self.page_seed)
-        cache.set_pending_new_lens(lens)
+        paged = self.use_paged_kv_cache
+        if paged:
+            cache = PagedKVCache.from_model_config(
+                self.model_config, batch_size=batch_size, page_size=self.kv_cache_page_size, device=self.device,
+                dtype=self.dtype, kv_cache_dtype=self.kv_cache_dtype,
+                seq_capacity=[n + max_new_tokens for n in lens], paged_pool=self.paged_pool,
+                page_seed=self.page_seed)
+            cache.set_pending_new_lens(lens)
+        else:
+            # engine.py:168-178: the per-layer (k, v) tuples grown by concatenation; one batch-wide length
+            if min(lens) != prompt_len:
+                raise ValueError("ragged prompts (prompt_lens) need the paged KV cache (use_paged_kv_cache=True)")
+            cache = None
         lens_t = torch.tensor(lens, device=self.device)
         rows = torch.arange(batch_size, device=self.device)
 
@@ -134,7 +143,8 @@ class InferenceEngine:
         prefill_t0 = time.perf_counter()
         logits, cache = self.model(prompt, use_cache=True, past_key_values=cache, position_offset=0,
                                    logits_index=lens_t - 1)
-        cache.set_pending_new_lens(None)
+        if paged:
+            cache.set_pending_new_lens(None)
         next_logits = logits[:, -1, :]
         torch.cuda.synchronize(self.device)
         prefill_t1 = time.perf_counter()
@@ -144,11 +154,12 @@ class InferenceEngine:
         cur = lens_t.clone()
         uniform = len(set(lens)) == 1
         graphs = None
-        use_graphs = self.use_graphs
-        if use_graphs is None:
+        use_graphs = self.use_graphs and paged  # the tuple cache's tensors change every step: eager only
+        if use_graphs is None and paged:
             fused = hasattr(self.model, "_fused_decode_ok") and self.model._fused_decode_ok(cache, batch_size)
             use_graphs = not (fused and cache.get_layer_cache(0).layout.kind == "bf16")
-        cache.set_static_max_len(max(lens) + max_new_tokens)
+        if paged:
+            cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
         for step in range(max_new_tokens):
             if return_logprobs:
@@ -172,7 +183,8 @@ class InferenceEngine:
             next_logits = logits[:, -1, :]
         torch.cuda.synchronize(self.device)
         decode_t1 = time.perf_counter()
-        cache.set_static_max_len(None)
+        if paged:
+            cache.set_static_max_len(None)
 
         out_len = max(lens) + decode_steps
         tokens = tokens[:, :out_len]

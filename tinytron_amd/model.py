@@ -43,7 +43,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .cache import LayerPagedKVCache, PagedLayerKVCache
+from .cache import ConcatKVStore, LayerPagedKVCache, PagedLayerKVCache
 
 
 @dataclass(frozen=True)
@@ -101,7 +101,8 @@ class Attention(nn.Module):
         self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.c_proj = nn.Linear(config.hidden_size, config.hidden_size, **kw)
-        self.prefill_kernel = True  # bf16 prefill through the prefill attention kernel (else SDPA per sequence)
+        self.prefill_kernel = True  # bf16 prefill through the prefill attention kernel (else row attention)
+        self._concat = None  # ConcatKVStore behind the non-paged (tuple) cache, made on first use
         self._init_weights(config.seed, layer_idx)
 
     def _init_weights(self, base_seed: int, layer_idx: int) -> None:
@@ -121,8 +122,7 @@ class Attention(nn.Module):
         k = self.k_proj(xa).view(B, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(xa).view(B, T, self.num_key_value_heads, self.head_dim).transpose(1, 2)
         if not _is_fused_cache(past_kv):
-            raise TypeError("tinytron_amd.Attention needs a tinytron_amd KV cache "
-                            "(LayerPagedKVCache / PagedLayerKVCache); there is no uncached fallback")
+            return self._forward_concat(q, k, v, past_kv, use_cache, position_offset)
         lens = past_kv.seq_lens_host
         if len(set(lens)) == 1 and lens[0] != position_offset:
             raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
@@ -140,36 +140,47 @@ class Attention(nn.Module):
         y = self.c_proj(y)
         return y, (past_kv if use_cache else None)
 
+    def _forward_concat(self, q, k, v, past_kv, use_cache: bool, position_offset: int):
+        """The reference's non-paged paths (attn.py:174-186, 314-341): past_kv
+        None or the (k, v) tuple of GQA-expanded heads [B, H_q, T_past, D];
+        returns the new tuple [B, H_q, T_past + T, D] with use_cache (else
+        None). RoPE + append of the new tokens (k / v expanded first, as the
+        reference appends after gqa_impl) into the layer's ConcatKVStore, then
+        decode attention (T = 1) or causal prefill attention over it with one
+        KV head per query head."""
+        B, Hq, T, D = q.shape
+        act = q.dtype
+        if self._concat is None:
+            self._concat = ConcatKVStore()
+        store = self._concat
+        t_past = store.prepare(past_kv, B, Hq, D, T, act, q.device)
+        if position_offset != t_past:
+            raise ValueError(f"position_offset {position_offset} does not match the cached length {t_past}")
+        G = Hq // self.num_key_value_heads
+        ke = k.repeat_interleave(G, dim=1) if G > 1 else k
+        ve = v.repeat_interleave(G, dim=1) if G > 1 else v
+        table = rope_table_for(t_past + T, D, self.config.rope_theta, act, q.device)
+        pos = torch.full((B,), t_past, dtype=torch.int32, device=q.device)
+        q_rot = ops.rope_append(q, ke, ve, table, pos, store.layout)
+        if T == 1:
+            y = ops.decode_attention(q_rot.view(B, Hq, D), store.layout, pos + 1, t_past + 1).view(B, 1, self.n_embd)
+        elif self.prefill_kernel and act == torch.bfloat16 and ops.attention_tile_dim(D, store.layout.kind):
+            y = ops.prefill_attention(q_rot, store.layout, pos, t_past + T).view(B, T, self.n_embd)
+        else:
+            y = ops.prefill_attention_rows(q_rot, store.layout, [t_past] * B, [T] * B).view(B, T, self.n_embd)
+        new_kv = store.views(t_past + T) if use_cache else None
+        return self.c_proj(y), new_kv
+
     def _prefill(self, q, k, v, cache, table, lens_before):
         """T > 1: append all (ragged) prompt tokens with the fused kernel, then
         causal attention over each sequence's cached prefix (attn.py:321-341):
-        the prefill kernel for bf16 activations, SDPA per sequence otherwise."""
+        the prefill kernel for bf16 activations, row attention (one query row
+        per new token) for fp32 and the head dims that kernel does not take."""
         B, _, T, D = q.shape
         new = cache._pending_new_lens or [T] * B
         q_rot = cache.rope_append(q, k, v, table, new_lens=new)
         y = torch.zeros(B, T, self.n_embd, dtype=q.dtype, device=q.device)
-        if self.prefill_kernel and q.dtype == torch.bfloat16 and cache.layout.kind in ("bf16", "fp8") \
-                and ops.attention_tile_dim(D, cache.layout.kind) \
-                and self.num_attention_heads // self.num_key_value_heads <= 16:
-            cache.prefill_attend(q_rot, new, out=y.view(B, T, self.num_attention_heads, D))
-            return y
-        rep = self.num_attention_heads // self.num_key_value_heads
-        for b in range(B):
-            n = int(new[b])
-            if n == 0:
-                continue
-            past = int(lens_before[b])
-            K, V = cache.gather(b, past + n, dtype=q.dtype)                 # [1, H_kv, past+n, D]
-            K = K.repeat_interleave(rep, dim=1).contiguous()
-            V = V.repeat_interleave(rep, dim=1).contiguous()
-            qb = q_rot[b:b + 1, :, :n].contiguous()
-            if past == 0:
-                yb = F.scaled_dot_product_attention(qb, K, V, is_causal=True)
-            else:
-                qpos = past + torch.arange(n, device=q.device).unsqueeze(-1)
-                mask = torch.arange(past + n, device=q.device).unsqueeze(0) <= qpos
-                yb = F.scaled_dot_product_attention(qb, K, V, attn_mask=mask)
-            y[b, :n] = yb[0].transpose(0, 1).reshape(n, self.n_embd)
+        cache.prefill_attend(q_rot, new, out=y.view(B, T, self.num_attention_heads, D), kernel=self.prefill_kernel)
         return y
 
 
@@ -457,6 +468,27 @@ class GPT(nn.Module):
             h = ops.add_rmsnorm_rows(x, nxt, eps, addend=F.linear(m, blk.mlp.down_proj.weight))
         return F.linear(h.index_select(0, rows), self.lm_head_weight()).unsqueeze(1)
 
+    def _forward_concat(self, idx, past_key_values, use_cache: bool, position_offset: int, logits_index):
+        """gpt.py:95-115 without a paged cache: past_key_values None (the
+        uncached forward, or the first call of the non-paged cache) or the list
+        of per-layer (k, v) tuples; returns logits, plus the new list with
+        use_cache."""
+        B, _ = idx.size()
+        if past_key_values is not None and len(past_key_values) != len(self.blocks):
+            raise ValueError(f"past_key_values holds {len(past_key_values)} layers, the model {len(self.blocks)}")
+        x = self.wte(idx)
+        new_past = [] if use_cache else None
+        for layer_idx, block in enumerate(self.blocks):
+            layer_past = past_key_values[layer_idx] if past_key_values is not None else None
+            x, _, new_kv = block(x, past_kv=layer_past, use_cache=use_cache, position_offset=position_offset)
+            if use_cache:
+                new_past.append(new_kv)
+        if logits_index is not None:
+            x = x[torch.arange(B, device=x.device), logits_index].unsqueeze(1)
+        x = self.lnf(x)
+        logits = F.linear(x.to(self.compute_dtype), self.lm_head_weight())
+        return (logits, new_past) if use_cache else logits
+
     def forward(self, idx: torch.Tensor, targets=None, past_key_values=None, use_cache: bool = False,
                 position_offset: int = 0, logits_index: torch.Tensor | None = None):
         """gpt.py:84-115. ``logits_index`` ([B], optional, prefill only)
@@ -464,9 +496,12 @@ class GPT(nn.Module):
         all T."""
         B, T = idx.size()
         assert T <= self.config.block_size, f"Cannot forward sequence of length {T}, block size is only {self.config.block_size}"
+        if targets is not None:
+            raise NotImplementedError("tinytron_amd.GPT is the inference path: the training loss (targets) is not "
+                                      "part of it")
         paged_cache = past_key_values if hasattr(past_key_values, "get_layer_cache") else None
         if paged_cache is None:
-            raise TypeError("tinytron_amd.GPT runs with a tinytron_amd PagedKVCache")
+            return self._forward_concat(idx, past_key_values, use_cache, position_offset, logits_index)
         if T == 1 and logits_index is None and targets is None and self._fused_decode_ok(paged_cache, B):
             logits = self._decode_step_fused(idx, paged_cache, position_offset)
             return (logits, paged_cache) if use_cache else logits

@@ -329,6 +329,87 @@ def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, 
     return out
 
 
+ROWS_ATTN_MAX_ROWS = 65535  # query rows per tt_rows_attn_* launch
+
+
+def rows_attention(q: torch.Tensor, layout: KVLayout, seq_of_row: torch.Tensor, row_lens: torch.Tensor,
+                   max_row_len: int, num_seqs: int, out: torch.Tensor | None = None, sm_scale: float | None = None,
+                   workspace: Workspace | None = None) -> torch.Tensor:
+    """GQA attention of query rows q [R, H_q, D], row r over the first
+    row_lens[r] cached tokens of sequence seq_of_row[r] (int32 [R] each; the
+    cache holds num_seqs sequences); returns out [R, H_q, D] (zeros where
+    row_lens[r] <= 0). Rows t of a prefill chunk with row_lens = cached + t + 1
+    give the reference's cache-causal prefill attention (attn.py:321-341) for
+    the caches and head dims the prefill kernel does not take (fp32, rows that
+    are not whole 16-byte fragments); launches of at most ROWS_ATTN_MAX_ROWS
+    rows."""
+    _require_cuda(q, layout.k, layout.v, seq_of_row, row_lens)
+    _check_lastdim("q", q, 3)
+    R, Hq, D = q.shape
+    kind = _act_kind(q.dtype)
+    if layout.kind == "fp8":
+        if kind != "bf16":
+            raise ValueError("an fp8 cache takes bf16 queries")
+    elif layout.kind != kind:
+        raise ValueError(f"cache dtype {layout.kind} does not match q {kind}")
+    if D != layout.head_dim:
+        raise ValueError(f"head_dim {D} does not match the cache's {layout.head_dim}")
+    for name, t in (("seq_of_row", seq_of_row), ("row_lens", row_lens)):
+        if t.dtype != torch.int32 or t.shape != (R,):
+            raise ValueError(f"{name} must be int32 [R]")
+    if max_row_len > layout.capacity:
+        raise ValueError(f"max_row_len {max_row_len} exceeds the cache capacity {layout.capacity}")
+    if out is None:
+        out = torch.empty(R, Hq, D, dtype=q.dtype, device=q.device)
+    _check_lastdim("out", out, 3)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    hkv = layout.num_heads
+    lib = _lib.load()
+    fn = {"fp8": lib.tt_rows_attn_fp8, "bf16": lib.tt_rows_attn_bf16, "f32": lib.tt_rows_attn_f32}[layout.kind]
+    scales = [_ptr(layout.k_scale), _ptr(layout.v_scale)] if layout.kind == "fp8" else []
+    workspace = workspace or Workspace(q.device)
+    for r0 in range(0, R, ROWS_ATTN_MAX_ROWS):
+        n = min(ROWS_ATTN_MAX_ROWS, R - r0)
+        ws = workspace.get(workspace_bytes(n, Hq, hkv, D, max_row_len, 0))
+        qc, oc = q[r0:r0 + n], out[r0:r0 + n]
+        st = fn(_ptr(qc), _lib.strides(*qc.stride()[:2]), _ptr(layout.k), _ptr(layout.v), *scales,
+                _lib.strides(*layout.strides), _ptr(seq_of_row[r0:r0 + n]), _ptr(row_lens[r0:r0 + n]),
+                int(max_row_len), _ptr(layout.page_table), layout.max_pages, layout.num_pages, int(num_seqs),
+                _ptr(oc), _lib.strides(*oc.stride()[:2]), n, Hq, hkv, D, layout.page_size, float(sm_scale),
+                _ptr(ws), ws.numel(), _stream(q.device))
+        _lib.check(st, "rows_attention")
+    return out
+
+
+def prefill_attention_rows(q: torch.Tensor, layout: KVLayout, cached, new_lens, out: torch.Tensor | None = None,
+                           sm_scale: float | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """prefill_attention through rows_attention: q [B, H_q, T, D] (rotated),
+    host lists cached[b] (tokens before the chunk) and new_lens[b]; returns out
+    [B, T, H_q, D] with row t < new_lens[b] of sequence b attending to its
+    cached[b] + t + 1 first tokens (rows past new_lens[b] are zero)."""
+    B, Hq, T, D = q.shape
+    cached = [int(x) for x in cached]
+    new_lens = [min(int(x), T) for x in new_lens]
+    lens = torch.zeros(B, T, dtype=torch.int32)
+    steps = torch.arange(1, T + 1, dtype=torch.int32)
+    for b in range(B):
+        n = new_lens[b]
+        lens[b, :n] = cached[b] + steps[:n]
+    seq = torch.arange(B, dtype=torch.int32).repeat_interleave(T)
+    q_rows = q.transpose(1, 2).contiguous().view(B * T, Hq, D)
+    if out is None:
+        out = torch.empty(B, T, Hq, D, dtype=q.dtype, device=q.device)
+    o_rows = out.view(B * T, Hq, D) if out.is_contiguous() else torch.empty(B * T, Hq, D, dtype=q.dtype,
+                                                                            device=q.device)
+    max_len = max((c + n for c, n in zip(cached, new_lens)), default=0)
+    rows_attention(q_rows, layout, seq.to(q.device, non_blocking=True), lens.view(-1).to(q.device, non_blocking=True),
+                   max(max_len, 1), B, out=o_rows, sm_scale=sm_scale, workspace=workspace)
+    if o_rows.data_ptr() != out.data_ptr():
+        out.copy_(o_rows.view(B, T, Hq, D))
+    return out
+
+
 FUSED_STEP_MAX_SPLITS = 4  # split-K partials decode_attention_append sums per input
 
 
