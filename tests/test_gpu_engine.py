@@ -139,6 +139,35 @@ def test_ragged_batch_equals_batch_one(kv_dtype):
     assert mismatched <= 1, f"{mismatched} of {len(lens)} sequences diverged"
 
 
+def test_default_preset_ragged_batch_equals_batch_one():
+    """The reference's default 0.25B model (scripts/debug/inference.sh:52-57:
+    12 layers, d 1024, 32 / 4 heads, head_dim 32, ffn 4096), bf16, through the
+    engine: the fused decode step at head_dim 32 takes every step (asserted),
+    and each sequence's greedy tokens in one ragged batch equal its batch-1
+    run (one near-tie flip allowed, as above)."""
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=12, hidden_size=1024, num_attention_heads=32, num_key_value_heads=4,
+                     intermediate_size=4096, block_size=256)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True, model=model)
+    calls = []
+    fused = model._decode_step_fused
+    model._decode_step_fused = lambda *a, **k: (calls.append(1), fused(*a, **k))[1]
+    g = torch.Generator().manual_seed(11)
+    lens = [7, 40, 96]
+    steps = 16
+    prompt = torch.randint(0, cfg.vocab_size, (len(lens), max(lens)), generator=g)
+    batch = eng.generate(prompt, steps, top_k=1, prompt_lens=lens)
+    assert len(calls) == steps, f"fused decode step ran {len(calls)} times for {steps} model steps"
+    mismatched = 0
+    for b, n in enumerate(lens):
+        single = eng.generate(prompt[b:b + 1, :n], steps, top_k=1)
+        mismatched += not torch.equal(batch[b, n:n + steps].cpu(), single[0, n:n + steps].cpu())
+    assert mismatched <= 1, f"{mismatched} of {len(lens)} sequences diverged"
+
+
 @pytest.mark.parametrize("kv_dtype,sync_each_step", [(None, True), ("fp8", False)])
 def test_graph_replay_equals_eager(kv_dtype, sync_each_step):
     """Decode steps replayed from the two captured graphs give the eager path's

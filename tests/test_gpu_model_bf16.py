@@ -224,18 +224,24 @@ def test_one_layer_fused_path_matches_reference_autocast():
         greedy_agrees(toks[b].tolist(), lb, noise, f"1-layer fused, sequence {b}")
 
 
-@pytest.mark.parametrize("name", ["c1_module", "d1024_fused", "d2048_fused"])
+@pytest.mark.parametrize("name", ["c1_module", "d1024_fused", "d2048_fused", "default_0.25b"])
 def test_several_layers_match_reference_autocast(name):
     """C1's model through the module path (contiguous cache, prompt 128, 64
     greedy steps), a 4-layer d 1024 model through the packed prefill and the
-    fused decode step (paged pool, ragged batch, 12 steps), and a 2-layer
+    fused decode step (paged pool, ragged batch, 12 steps), a 2-layer
     model of C5's width (d 2048, ffn 6144: gate|up + SwiGLU as one whole-K
-    launch) the same way."""
+    launch) the same way, and the reference's default 0.25B model
+    (scripts/debug/inference.sh:52-57: 12 layers, d 1024, 32 / 4 heads, so
+    head_dim 32, ffn 4096) through the same fused paths."""
     from tinytron_amd.model import GPT
 
     if name == "c1_module":
         cfg = _config()
         lens, steps, paged, seed = [128], 64, False, 1337
+    elif name == "default_0.25b":
+        cfg = _config(num_layer=12, hidden_size=1024, num_attention_heads=32, num_key_value_heads=4,
+                      intermediate_size=4096, vocab_size=32000, block_size=256)
+        lens, steps, paged, seed = [70, 9, 33], 8, True, 53
     elif name == "d2048_fused":
         cfg = _config(num_layer=2, hidden_size=2048, num_attention_heads=32, num_key_value_heads=8,
                       intermediate_size=6144, vocab_size=8192, block_size=256)
