@@ -151,7 +151,8 @@ def test_default_preset_ragged_batch_equals_batch_one():
     cfg = _c1_config(num_layer=12, hidden_size=1024, num_attention_heads=32, num_key_value_heads=4,
                      intermediate_size=4096, block_size=256)
     model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
-    eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True, model=model)
+    eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True, model=model,
+                          use_graphs=False)  # eager, so that every step's model call is seen
     calls = []
     fused = model._decode_step_fused
     model._decode_step_fused = lambda *a, **k: (calls.append(1), fused(*a, **k))[1]
@@ -168,16 +169,21 @@ def test_default_preset_ragged_batch_equals_batch_one():
     assert mismatched <= 1, f"{mismatched} of {len(lens)} sequences diverged"
 
 
-@pytest.mark.parametrize("kv_dtype,sync_each_step", [(None, True), ("fp8", False)])
-def test_graph_replay_equals_eager(kv_dtype, sync_each_step):
-    """Decode steps replayed from the two captured graphs give the eager path's
-    tokens and log-probabilities bit for bit, on every replay (ragged batch,
-    paged pool). ``eos_token_id=-1`` never fires but makes the loop synchronise
-    with the host after every step, between replays."""
+@pytest.mark.parametrize("kv_dtype,sync_each_step,hidden", [(None, True, 512), ("fp8", False, 512),
+                                                             (None, False, 1024), (None, True, 1024),
+                                                             ("fp8", False, 1024)])
+def test_graph_replay_equals_eager(kv_dtype, sync_each_step, hidden):
+    """Decode steps replayed from the two captured graphs (the engine's
+    default) give the eager path's tokens and log-probabilities bit for bit,
+    on every replay (ragged batch, paged pool): the module path (d 512) and
+    the fused decode step (d 1024; bf16 and fp8 caches). ``eos_token_id=-1``
+    never fires but makes the loop synchronise with the host after every step,
+    between replays."""
     from tinytron_amd.engine import InferenceEngine
     from tinytron_amd.model import GPT
 
-    cfg = _c1_config(num_layer=3, block_size=512, vocab_size=4096)
+    heads = dict(num_attention_heads=16, num_key_value_heads=4) if hidden == 1024 else {}
+    cfg = _c1_config(num_layer=3, block_size=512, vocab_size=4096, hidden_size=hidden, **heads)
     model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
     kvd = torch.float8_e4m3fn if kv_dtype == "fp8" else None
     g = torch.Generator().manual_seed(11)

@@ -12,16 +12,13 @@ past_key_values=cache, position_offset=...)``; positions come from the
 cache's per-sequence lengths, so there is no host synchronisation in the
 loop (the reference syncs once per layer at attn.py:395).
 
-With ``use_graphs`` the one-token model call is captured in HIP graphs
-after the first decode step and replayed for the rest, which removes the
-per-kernel launch cost. By default (``None``) the fused step with a bf16
-cache (9 launches per layer, one launch pair for RoPE + append + attention)
-runs eagerly: the host keeps the GPU busy on its own, and eager launches
-measured 2 % faster than replay plus the two captures (C5, 256 steps).
-Everything else replays graphs: the module-by-module step (about 30
-launches per layer), and the fused step with an fp8 cache, whose separate
-RoPE + append launch makes the host the bottleneck (C5: 22.8 k tokens/s
-eager, 27.6 k replayed).
+With ``use_graphs`` (the default for the paged caches; ``False`` launches
+eagerly) the one-token model call is captured in HIP graphs after the first
+decode step and replayed for the rest, which removes the per-kernel launch
+cost: the fused bf16 step issues 8 launches per layer, about as fast as the
+host can issue them (C5: 26.8 k tokens/s eager against 28.4 k replayed,
+captures included), the fused step with an fp8 cache one more, and the
+module-by-module step about 30.
 The caches keep their lengths in two device buffers that swap every step, so
 two graphs are captured, one per buffer parity. The attention launch bound is
 fixed at the largest sequence capacity for the whole decode loop, so the
@@ -154,10 +151,8 @@ class InferenceEngine:
         cur = lens_t.clone()
         uniform = len(set(lens)) == 1
         graphs = None
-        use_graphs = self.use_graphs and paged  # the tuple cache's tensors change every step: eager only
-        if use_graphs is None and paged:
-            fused = hasattr(self.model, "_fused_decode_ok") and self.model._fused_decode_ok(cache, batch_size)
-            use_graphs = not (fused and cache.get_layer_cache(0).layout.kind == "bf16")
+        # the tuple cache's tensors change every step: it launches eagerly
+        use_graphs = paged and (self.use_graphs is None or bool(self.use_graphs))
         if paged:
             cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
