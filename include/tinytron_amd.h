@@ -470,7 +470,7 @@ int tt_splitk_reduce_bf16(const float *partials, int64_t splits, int64_t m, int6
  * x[m] += bf16(sum_s partials[s][m]) first; then
  * y[m] = bf16(weight * (x[m] * rsqrt(mean(x[m]^2) + eps))), the normalised
  * row as the next projection's bf16 input. partials may be NULL (plain
- * RMSNorm). x, weight fp32; C % 1024 == 0, 1024 <= C <= 8192.
+ * RMSNorm). x, weight fp32; C a multiple of 4, 4 <= C <= 8192.
  */
 int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const float *weight, float eps, void *y,
                         int64_t m, int64_t c, tt_stream_t stream);
@@ -490,7 +490,7 @@ int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t i
  * (as tt_linear_splitk_packed_bf16) matrix of 2I rows interleaved by 8:
  * rows 16j .. 16j+7 are gate rows 8j .. 8j+7, rows 16j+8 .. 16j+15 up rows
  * 8j .. 8j+7. x bf16 [M, K] (row stride ldx), y bf16 [M, I] (row stride
- * ldy). Requirements: K == 2048, I % 24 == 0 (tt_swiglu_gemm_supported),
+ * ldy). Requirements: K 1024 or 2048, I a multiple of 16 or 24 (tt_swiglu_gemm_supported),
  * ldx % 8 == 0, ldy % 4 == 0, 16-byte aligned x and weight, 8-byte aligned y.
  * (Replaces the gate|up tt_linear_splitk_packed_bf16 + tt_silu_mul_bf16 pair;
  * the interleaved layout is this library's, no counterpart in the reference.)

@@ -131,7 +131,8 @@ def test_prefill_row_entries_reject_invalid_arguments():
         return lib.tt_last_error_string().decode()
 
     # residual add + RMSNorm over prompt rows
-    assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 2048, FAKE, 1e-6, FAKE, 10, 1000, None) == _lib.TT_ERR_UNSUPPORTED
+    assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 2048, FAKE, 1e-6, FAKE, 10, 1002, None) == _lib.TT_ERR_UNSUPPORTED
+    assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 9000, FAKE, 1e-6, FAKE, 10, 8196, None) == _lib.TT_ERR_UNSUPPORTED
     assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 1024, FAKE, 1e-6, FAKE, 10, 2048, None) == \
         _lib.TT_ERR_INVALID_ARGUMENT and "row stride" in err()
     assert lib.tt_add_rmsnorm_rows_bf16(FAKE, FAKE, 2048, FAKE, 1e-6, FAKE + 2, 10, 2048, None) == \

@@ -196,19 +196,31 @@ def _run_gpu(model, cfg, prompt, lens, steps, paged):
     return torch.stack(logits, 1), torch.stack(toks, 1)
 
 
-def test_one_layer_fused_path_matches_reference_autocast():
-    """One layer at d 1024 (16/4 heads, D 64): packed prefill and fused decode
-    steps (split-K GEMMs, RoPE + append inside attention, fused add + RMSNorm,
-    SwiGLU) against the oracle, per sequence of a ragged batch."""
+@pytest.mark.parametrize("shape", ["d1024", "preset_0.1b", "preset_0.25b", "preset_13b"])
+def test_one_layer_fused_path_matches_reference_autocast(shape):
+    """One layer through the packed prefill and the fused decode step
+    (split-K GEMMs, RoPE + append with the attention, fused add + RMSNorm,
+    SwiGLU) against the oracle, per sequence of a ragged batch, at d 1024
+    (16/4 heads, D 64) and at the reference presets' layer shapes
+    (scripts/debug/inference.sh:71-77, 52-57, 101-107): 0.1B d 768 (16/4
+    heads, D 48, ffn 3072), 0.25B d 1024 (32/4 heads, D 32, ffn 4096: gate|up
+    + SwiGLU in one K = 1024 launch), 13B d 5120 (40/8 heads: G 5, D 128,
+    ffn 13824). The fused decode step runs every step (asserted)."""
     from tinytron_amd.model import GPT
 
-    cfg = _config(num_layer=1, hidden_size=1024, num_attention_heads=16, num_key_value_heads=4,
-                  intermediate_size=2048, vocab_size=8192, block_size=256)
+    dims = {"d1024": (1024, 16, 4, 2048), "preset_0.1b": (768, 16, 4, 3072), "preset_0.25b": (1024, 32, 4, 4096),
+            "preset_13b": (5120, 40, 8, 13824)}[shape]
+    cfg = _config(num_layer=1, hidden_size=dims[0], num_attention_heads=dims[1], num_key_value_heads=dims[2],
+                  intermediate_size=dims[3], vocab_size=8192, block_size=256)
     model = GPT(cfg, device=DEV, dtype=BF16)
+    calls = []
+    fused = model._decode_step_fused
+    model._decode_step_fused = lambda *a, **k: (calls.append(1), fused(*a, **k))[1]
     ob, of = _oracles(model, cfg)
     lens, steps = [70, 9, 33], 8
     prompt = torch.randint(0, cfg.vocab_size, (len(lens), max(lens)), generator=torch.Generator().manual_seed(31))
     gpu, toks = _run_gpu(model, cfg, prompt, lens, steps, paged=True)
+    assert len(calls) == steps, f"fused decode step ran {len(calls)} of {steps} steps"
     for b, n in enumerate(lens):
         lb = _oracle_steps(ob, prompt[b, :n], toks[b].tolist(), 128)
         lf = _oracle_steps(of, prompt[b, :n], toks[b].tolist(), 128)

@@ -817,8 +817,8 @@ int tt_add_rmsnorm_bf16(float *x, const float *partials, int64_t splits, const f
                         int64_t m, int64_t c, tt_stream_t stream) {
   TT_CHECK(x && weight && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK(m >= 0 && m <= 0x7fffffff, TT_ERR_INVALID_ARGUMENT, "bad row count");
-  TT_CHECK(c % 1024 == 0 && c >= 1024 && c <= 8192, TT_ERR_UNSUPPORTED,
-           "hidden size must be a multiple of 1024 in [1024, 8192], got %lld", (long long)c);
+  TT_CHECK(c % 4 == 0 && c >= 4 && c <= 8192, TT_ERR_UNSUPPORTED,
+           "hidden size must be a multiple of 4 in [4, 8192], got %lld", (long long)c);
   TT_CHECK(partials == nullptr || (splits >= 1 && splits <= 4096), TT_ERR_INVALID_ARGUMENT, "bad split count");
   TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(y, 8) && (partials == nullptr || aligned(partials, 16)),
            TT_ERR_INVALID_ARGUMENT, "x / weight / partials must be 16-byte aligned, y 8-byte aligned");
@@ -848,7 +848,7 @@ int tt_linear_swiglu_packed_bf16(const void *x, int64_t ldx, const void *weight_
   TT_CHECK(x && weight_packed && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK(m >= 0 && m <= 65535 * 64 && inter > 0 && k > 0, TT_ERR_INVALID_ARGUMENT, "bad GEMM shape");
   TT_CHECK(tt::swiglu_gemm_supported(k, inter), TT_ERR_UNSUPPORTED,
-           "the fused gate|up + SwiGLU GEMM takes K == 2048 and I %% 24 == 0 (K %lld, I %lld)", (long long)k,
+           "the fused gate|up + SwiGLU GEMM takes K 1024 or 2048 and I a multiple of 16 or 24 (K %lld, I %lld)", (long long)k,
            (long long)inter);
   TT_CHECK(inter < ((int64_t)1 << 30), TT_ERR_UNSUPPORTED, "intermediate size too large");
   TT_CHECK(ldx >= k && ldx % 8 == 0 && ldy >= inter && ldy % 4 == 0, TT_ERR_INVALID_ARGUMENT,
@@ -874,8 +874,8 @@ int tt_add_rmsnorm_rows_bf16(float *x, const void *a, int64_t lda, const float *
                              int64_t c, tt_stream_t stream) {
   TT_CHECK(x && weight && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK(m >= 0 && m <= 0x7fffffff, TT_ERR_INVALID_ARGUMENT, "bad row count");
-  TT_CHECK(c % 1024 == 0 && c >= 1024 && c <= 8192, TT_ERR_UNSUPPORTED,
-           "hidden size must be a multiple of 1024 in [1024, 8192], got %lld", (long long)c);
+  TT_CHECK(c % 4 == 0 && c >= 4 && c <= 8192, TT_ERR_UNSUPPORTED,
+           "hidden size must be a multiple of 4 in [4, 8192], got %lld", (long long)c);
   TT_CHECK(a == nullptr || (lda >= c && lda % 4 == 0), TT_ERR_INVALID_ARGUMENT, "addend row stride must be >= C and a multiple of 4");
   TT_CHECK(aligned(x, 16) && aligned(weight, 16) && aligned(y, 8) && (a == nullptr || aligned(a, 8)),
            TT_ERR_INVALID_ARGUMENT, "x / weight must be 16-byte aligned, y / addend 8-byte aligned");

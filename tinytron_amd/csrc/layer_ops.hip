@@ -185,7 +185,10 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 // bf16-rounded sum of the partials (the projection's autocast output). Every
 // load of the row (x and up to SMAX splits) is issued before the first add,
 // so the row costs one memory round trip; the splits are added in order.
-template <int PER, int SMAX>  // PER float4 groups per thread (C = 1024 * PER); SMAX splits loaded at once
+// PER float4 groups per thread (C <= 1024 * PER, C a multiple of 4; groups
+// past C are neither loaded nor stored and add 0 to the sum of squares);
+// SMAX splits loaded at once
+template <int PER, int SMAX>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float *P, int S, int64_t MN,
                                                           const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
@@ -195,17 +198,20 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    v[j] = *reinterpret_cast<const f32x4 *>(x + row + c);
+    const bool in = c < C;
+    v[j] = in ? *reinterpret_cast<const f32x4 *>(x + row + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     if (P != nullptr) {
 #pragma unroll
       for (int s = 0; s < SMAX; ++s)  // splits past S reload split 0 and are not added
-        pv[j][s] = *reinterpret_cast<const f32x4 *>(P + (int64_t)(s < S ? s : 0) * MN + row + c);
+        pv[j][s] = in ? *reinterpret_cast<const f32x4 *>(P + (int64_t)(s < S ? s : 0) * MN + row + c)
+                      : f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
+    if (c >= C) continue;
     if (P != nullptr) {
       f32x4 d = pv[j][0];
 #pragma unroll
@@ -224,6 +230,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
+    if (c >= C) continue;
     const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
     uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
     uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
@@ -266,8 +273,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
 // output puts gate row r of a block in lane (n + 16g), g < 2, and up row r in
 // lane (n + 16g) ^ 32.
 //
-// A workgroup owns kSwiBlocks 16-row blocks (8 kSwiBlocks output columns)
-// and 2 kSwiBlocks waves: wave (block, half) streams its 16 rows x K/2 (one
+// A workgroup owns NB 16-row blocks (8 NB output columns) and 2 NB waves:
+// wave (block, half) streams its 16 rows x K/2 (one
 // burst, 128 registers at K = 2048). The x rows (64 per m tile) reach LDS by
 // DMA (buffer_load ... lds, one 1 KiB row chunk per instruction, rows past M
 // read as zero) in two rounds of K/4 columns per half, the first issued
@@ -275,32 +282,38 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
 // loads retire after the weights, which they queue behind). The two halves
 // of a block meet in LDS (sum half 0 + half 1), then the gate lanes exchange
 // with the up lanes and write 4 bf16 outputs each.
-constexpr int kSwiBlocks = 3;
-constexpr int kSwiK = 2048;  // the K this kernel is built for (x row quarter = one 1 KiB DMA)
-
-__global__ __launch_bounds__(64 * 2 * kSwiBlocks, 2) void swiglu_gemm_kernel(SwigluGemmArgs a) {
-  constexpr int KS = kSwiK / 64;       // k steps per wave (its half of K)
-  constexpr int KQ = kSwiK / 4;        // columns per half per round
+// K = 1024 R (R = 1, 2): R staging rounds, each one 512-column (1 KiB) row
+// chunk per half, so the LDS holds one round (133 KB, one workgroup per CU)
+// whatever K. NB = 2, 3 or 4 row blocks per workgroup (the launcher picks one
+// that divides I / 8: 3 where it can, the measured layout).
+// (Register budget: two workgroups' worth per CU, as measured for NB = 3;
+// NB = 4 with 128 weight registers per lane fits one.)
+template <int K, int NB>
+__global__ __launch_bounds__(64 * 2 * NB, NB == 4 ? 1 : 2) void swiglu_gemm_kernel(SwigluGemmArgs a) {
+  constexpr int R = K / 1024;          // staging rounds
+  constexpr int KS = K / 64;           // k steps per wave (its half of K)
+  constexpr int KQ = K / (2 * R);      // columns per half per round (512)
   constexpr int ROW = KQ + 8;          // padded LDS row (elements)
-  constexpr int kWaves = 2 * kSwiBlocks;
+  static_assert(K % 1024 == 0 && KQ == 512 && KS <= 32, "K = 1024 or 2048");
+  constexpr int kWaves = 2 * NB;
   constexpr int kRows = 2 * 64;        // LDS rows per round: 2 halves x 64 x rows
   __shared__ __attribute__((aligned(16))) uint16_t xs[kRows * ROW];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int blk = wave >> 1;           // row block of this workgroup
   const int half = wave & 1;           // K half
-  const int nb = blockIdx.x * kSwiBlocks + blk;
+  const int nb = blockIdx.x * NB + blk;
   const int m0 = blockIdx.z * 64;
   const int mrows = min(64, a.M - m0);
 
   // x rows m0 .. m0 + mrows - 1; offsets past the last valid row's data read zero
   const auto rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t *>(a.x) + (int64_t)m0 * a.ldx, (short)0,
-      (int)(((int64_t)(mrows - 1) * a.ldx + kSwiK) * 2), 0x00020000);
+      (int)(((int64_t)(mrows - 1) * a.ldx + K) * 2), 0x00020000);
   auto stage = [&](int round) {
     for (int i = wave; i < kRows; i += kWaves) {  // i = h * 64 + row
       const int h = i >> 6, r = i & 63;
-      const int col = h * (kSwiK / 2) + round * KQ;
+      const int col = h * (K / 2) + round * KQ;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void *)(xs + i * ROW), 16,
                                                16 * lane + (int)(((int64_t)r * a.ldx + col) * 2), 0, 0, 0);
     }
@@ -308,7 +321,7 @@ __global__ __launch_bounds__(64 * 2 * kSwiBlocks, 2) void swiglu_gemm_kernel(Swi
 
   stage(0);
   __builtin_amdgcn_sched_barrier(0);
-  const uint16_t *wrow = a.w + (((int64_t)nb * (kSwiK / 32) + half * KS) * 64 + lane) * 8;
+  const uint16_t *wrow = a.w + (((int64_t)nb * (K / 32) + half * KS) * 64 + lane) * 8;
   u32x4 wf[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {  // in consumption order: each k step waits only for its own loads
@@ -323,16 +336,16 @@ __global__ __launch_bounds__(64 * 2 * kSwiBlocks, 2) void swiglu_gemm_kernel(Swi
   for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint16_t *xrow = xs + (half * 64 + (lane & 15)) * ROW + 8 * (lane >> 4);
 #pragma unroll
-  for (int round = 0; round < 2; ++round) {
-    if (round == 1) {
-      __syncthreads();  // every wave is done with the first round's x
-      stage(1);
+  for (int round = 0; round < R; ++round) {
+    if (round > 0) {
+      __syncthreads();  // every wave is done with the previous round's x
+      stage(round);
       __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
       __syncthreads();
     }
 #pragma unroll
-    for (int s = 0; s < KS / 2; ++s) {
-      const bf16x8 af = __builtin_bit_cast(bf16x8, wf[round * (KS / 2) + s]);
+    for (int s = 0; s < KS / R; ++s) {
+      const bf16x8 af = __builtin_bit_cast(bf16x8, wf[round * (KS / R) + s]);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(xrow + mb * 16 * ROW + 32 * s);
@@ -370,7 +383,7 @@ __global__ __launch_bounds__(64 * 2 * kSwiBlocks, 2) void swiglu_gemm_kernel(Swi
 // x += float(a[m]) (a: bf16 [M, C] with row stride lda, the projection's
 // autocast output; a == nullptr skips the add), then
 // y = bf16(w * x * rsqrt(mean(x^2) + eps)) as in add_rmsnorm_kernel.
-template <int PER>
+template <int PER>  // as add_rmsnorm_kernel: C <= 1024 * PER, groups past C masked
 __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const uint16_t *a, int64_t lda,
                                                                const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
@@ -380,13 +393,15 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    v[j] = *reinterpret_cast<const f32x4 *>(x + row + c);
+    const bool in = c < C;
+    v[j] = in ? *reinterpret_cast<const f32x4 *>(x + row + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     av[j] = make_uint2(0u, 0u);
-    if (a != nullptr) av[j] = *reinterpret_cast<const uint2 *>(a + (int64_t)blockIdx.x * lda + c);
+    if (a != nullptr && in) av[j] = *reinterpret_cast<const uint2 *>(a + (int64_t)blockIdx.x * lda + c);
   }
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
+    if (4 * (threadIdx.x + 256 * j) >= C) continue;
     if (a != nullptr) {
       v[j][0] += __builtin_bit_cast(float, av[j].x << 16);
       v[j][1] += __builtin_bit_cast(float, av[j].x & 0xffff0000u);
@@ -402,6 +417,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
+    if (c >= C) continue;
     const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
     uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
     uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
@@ -496,7 +512,7 @@ hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, con
     else                                        \
       TT_ADD_RMSNORM_LAUNCH(n, (n <= 2 ? 16 : 4)); \
     break;
-  switch (C / 1024) {  // C in {1024, 2048, ..., 8192}, checked by the caller
+  switch ((C + 1023) / 1024) {  // C a multiple of 4 in [4, 8192], checked by the caller
     TT_ADD_RMSNORM_CASE(1)
     TT_ADD_RMSNORM_CASE(2)
     TT_ADD_RMSNORM_CASE(3)
@@ -513,12 +529,35 @@ hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, con
   return hipGetLastError();
 }
 
-bool swiglu_gemm_supported(int64_t K, int64_t I) { return K == kSwiK && I > 0 && I % (8 * kSwiBlocks) == 0; }
+bool swiglu_gemm_supported(int64_t K, int64_t I) {
+  return (K == 1024 || K == 2048) && I > 0 && (I % 24 == 0 || I % 16 == 0);
+}
+
+// Row blocks per workgroup for intermediate size I: 3 (the measured layout)
+// when 24 divides I, else 4 while that still gives every CU a workgroup, else 2.
+int swiglu_row_blocks(int64_t I) {
+  if (I % 24 == 0) return 3;
+  if (I % 32 == 0 && I / 32 >= device_cu_count()) return 4;
+  return 2;
+}
+
+template <int K>
+hipError_t launch_swiglu_k(const SwigluGemmArgs &a, hipStream_t stream) {
+  const int nb = swiglu_row_blocks(a.I);
+  const dim3 grid((unsigned)(a.I / (8 * nb)), 1, (unsigned)((a.M + 63) / 64));
+  if (nb == 3)
+    hipLaunchKernelGGL((swiglu_gemm_kernel<K, 3>), grid, dim3(128 * 3), 0, stream, a);
+  else if (nb == 4)
+    hipLaunchKernelGGL((swiglu_gemm_kernel<K, 4>), grid, dim3(128 * 4), 0, stream, a);
+  else
+    hipLaunchKernelGGL((swiglu_gemm_kernel<K, 2>), grid, dim3(128 * 2), 0, stream, a);
+  return hipGetLastError();
+}
 
 hipError_t launch_swiglu_gemm(const SwigluGemmArgs &a, hipStream_t stream) {
-  const dim3 grid((unsigned)(a.I / (8 * kSwiBlocks)), 1, (unsigned)((a.M + 63) / 64));
-  hipLaunchKernelGGL(swiglu_gemm_kernel, grid, dim3(128 * kSwiBlocks), 0, stream, a);
-  return hipGetLastError();
+  if (a.K == 1024) return launch_swiglu_k<1024>(a, stream);
+  if (a.K == 2048) return launch_swiglu_k<2048>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hipStream_t stream) {
@@ -530,7 +569,7 @@ hipError_t launch_silu_mul(const float *P, int S, int M, int I, uint16_t *y, hip
 
 hipError_t launch_add_rmsnorm_rows(float *x, const uint16_t *a, int64_t lda, int M, int C, const float *w, float eps,
                                    uint16_t *y, hipStream_t stream) {
-  switch (C / 1024) {  // C in {1024, 2048, ..., 8192}, checked by the caller
+  switch ((C + 1023) / 1024) {  // C a multiple of 4 in [4, 8192], checked by the caller
 #define TT_ROWS_CASE(n)                                                                                              \
   case n:                                                                                                            \
     hipLaunchKernelGGL((add_rmsnorm_rows_kernel<n>), dim3(M), dim3(256), 0, stream, x, a, lda, w, eps, y, C);     \

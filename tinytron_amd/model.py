@@ -299,7 +299,7 @@ class GPT(nn.Module):
             return False
         D = c.hidden_size // c.num_attention_heads
         n_qkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * D
-        return (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192 and n_qkv % 64 == 0
+        return (c.hidden_size <= 8192 and n_qkv % 64 == 0
                 and (2 * c.intermediate_size) % 64 == 0 and self._k_chunk(c.hidden_size) > 0
                 and self._k_chunk_small(c.hidden_size) > 0 and self._k_chunk(c.intermediate_size) > 0
                 and all(_is_fused_cache(cache.get_layer_cache(i)) for i in range(len(self.blocks))))
@@ -406,7 +406,7 @@ class GPT(nn.Module):
         if not self.fused_prefill or self.compute_dtype != torch.bfloat16 or not self.wte.weight.is_cuda:
             return False
         D = c.hidden_size // c.num_attention_heads
-        if not (c.hidden_size % 1024 == 0 and c.hidden_size <= 8192
+        if not (c.hidden_size % 4 == 0 and c.hidden_size <= 8192
                 and c.num_attention_heads // c.num_key_value_heads <= 16 and c.intermediate_size % 4 == 0
                 and all(blk.attn.prefill_kernel for blk in self.blocks)
                 and all(_is_fused_cache(cache.get_layer_cache(i))
