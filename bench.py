@@ -366,10 +366,9 @@ def build_workload(cfg, seed, torch, ops):
     if cfg["fp8"]:
         k_store = torch.empty(numel, dtype=torch.uint8, device=dev)
         v_store = torch.empty(numel, dtype=torch.uint8, device=dev)
-        k_scale = torch.empty(numel // D, dtype=torch.float32, device=dev)
-        v_scale = torch.empty(numel // D, dtype=torch.float32, device=dev)
         chunk = 1 << 24  # rows of D per chunk
         rows = numel // D
+        k_scale, v_scale = ops.fp8_scales(rows, dev)  # one array, K and V scales of each 16 rows in one line
         for dst, sc in ((k_store, k_scale), (v_store, v_scale)):
             for r0 in range(0, rows, chunk):
                 r1 = min(rows, r0 + chunk)
@@ -377,7 +376,7 @@ def build_workload(cfg, seed, torch, ops):
                 s = x.abs().amax(dim=-1) / 448.0
                 codes = torch.where(s[:, None] > 0, x / torch.where(s > 0, s, 1.0)[:, None], 0.0)
                 dst[r0 * D:r1 * D] = codes.to(ops.FP8_DTYPE).view(torch.uint8).reshape(-1)
-                sc[r0:r1] = s
+                sc[ops.fp8_scale_index(torch.arange(r0, r1, device=dev))] = s
                 del x, codes
     else:
         k_store = torch.randn(numel, generator=gd, device=dev, dtype=torch.bfloat16)
@@ -426,7 +425,9 @@ def _gather_sequence(cfg, wl, torch, b):
     heads = torch.arange(hkv, device="cuda") * layout.strides[2]
     idx = base[:, None, None] + heads[None, :, None] + torch.arange(D, device="cuda")[None, None, :]
     if cfg["fp8"]:
-        sidx = (base[:, None] + heads[None, :]) // D
+        from tinytron_amd import ops
+
+        sidx = ops.fp8_scale_index((base[:, None] + heads[None, :]) // D)
         k = (layout.k[idx].view(torch.float8_e4m3fn).float() * layout.k_scale[sidx][..., None]).to(torch.bfloat16)
         v = (layout.v[idx].view(torch.float8_e4m3fn).float() * layout.v_scale[sidx][..., None]).to(torch.bfloat16)
     else:

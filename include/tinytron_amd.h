@@ -32,9 +32,14 @@
  * store, cache.py:27-32, with H = num_kv_heads), and
  * base(b, j) = page_table[b * max_pages + j] * cache_strides[1] for a paged
  * pool [num_pages, H, P, D] (page_table int32 [B, max_pages]).
- * fp8 caches keep one fp32 scale per (token, KV head) at index
- * (element offset of d = 0) / head_dim in k_scale / v_scale, i.e. the scale
- * arrays follow the cache layout with head_dim collapsed.
+ * fp8 caches keep one fp32 scale per (token, KV head). With row r = (element
+ * offset of d = 0) / head_dim, the K scale is k_scale[r + 16 * (r / 16)] and
+ * the V scale v_scale[r + 16 * (r / 16)]: rows are grouped by 16, and one
+ * array of 2 x rows entries (rows rounded up to 16) holds both with
+ * v_scale = k_scale + 16, so that each group's 16 K scales and 16 V scales
+ * share one 128-byte line. fp8 caches need every 16-token block of a
+ * (sequence, head) to start a group: page and head strides (paged pool) or
+ * sequence and head strides (contiguous store) multiples of 16 * head_dim.
  */
 #ifndef TINYTRON_AMD_H
 #define TINYTRON_AMD_H
@@ -46,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 2
+#define TT_ABI_VERSION 3
 
 #define TT_OK 0
 #define TT_ERR_INVALID_ARGUMENT (-1)
@@ -129,7 +134,7 @@ int tt_rope_append_f32(const void *q_in, const int64_t q_in_strides[3],
  * Per (token, KV head): absmax = max|x| over D of the rotated bf16 K (of the
  * raw V), scale = absmax / 448 (fp32), code = e4m3fn_rne(x / scale); an
  * all-zero row stores code 0 and scale 0. Scales are written to k_scale /
- * v_scale (fp32, cache layout with head_dim collapsed).
+ * v_scale (fp32, grouped by 16 rows as described at the top).
  */
 int tt_rope_append_fp8(const void *q_in, const int64_t q_in_strides[3],
                        const void *k_in, const int64_t k_in_strides[3],

@@ -146,8 +146,23 @@ def append(cache: np.ndarray, layout: CacheLayout, x: np.ndarray, positions, new
                 cache[off:off + D] = x[b, h, t]
 
 
+def fp8_scale_index(row):
+    """Scale slot of a (token, head) row of an fp8 cache, row = element offset
+    of d = 0 / head_dim (no counterpart in the reference, whose cache has no
+    fp8): rows are grouped by 16, and group g's 16 K scales sit at 32g ..
+    32g + 15 of the K-scale array, its 16 V scales at the same slots of the
+    V-scale array (one array of 2 x rows floats with the V view 16 slots in)."""
+    return row + (row // 16) * 16
+
+
+def fp8_scale_numel(rows: int) -> int:
+    """Floats of the one array that holds K and V scales for `rows` rows."""
+    return 2 * (-(-int(rows) // 16) * 16)
+
+
 def append_fp8(codes: np.ndarray, scales: np.ndarray, layout: CacheLayout, x: np.ndarray, positions, new_lens=None) -> None:
-    """Quantize x [B, H, T, D] per (token, head) and write codes and scales."""
+    """Quantize x [B, H, T, D] per (token, head) and write codes and scales
+    (scales: the K or the V view, slots by fp8_scale_index)."""
     B, H, T, D = x.shape
     q, s = quantize_e4m3_rows(x)
     for b in range(B):
@@ -157,7 +172,7 @@ def append_fp8(codes: np.ndarray, scales: np.ndarray, layout: CacheLayout, x: np
             for h in range(H):
                 off = layout.token_offset(b, h, pos)
                 codes[off:off + D] = q[b, h, t]
-                scales[off // D] = s[b, h, t]
+                scales[fp8_scale_index(off // D)] = s[b, h, t]
 
 
 def gather(cache: np.ndarray, layout: CacheLayout, b: int, h: int, length: int) -> np.ndarray:
@@ -172,7 +187,8 @@ def gather(cache: np.ndarray, layout: CacheLayout, b: int, h: int, length: int) 
 
 def gather_scales(scales: np.ndarray, layout: CacheLayout, b: int, h: int, length: int) -> np.ndarray:
     D = layout.head_dim
-    return np.array([scales[layout.token_offset(b, h, t) // D] for t in range(length)], dtype=np.float32)
+    return np.array([scales[fp8_scale_index(layout.token_offset(b, h, t) // D)] for t in range(length)],
+                    dtype=np.float32)
 
 
 class LayerPagedKVCacheRef:

@@ -20,7 +20,18 @@ def bf16_randn(rng: np.random.Generator, shape, scale: float = 1.0):
     return bits, bf16_bits_to_f32(bits)
 
 
-def contiguous_geometry(batch, num_heads, head_dim, max_seq_len, page_size):
+def fp8_capacity(max_seq_len, page_size):
+    """Token slots of a contiguous fp8 store: whole pages, a multiple of 16 in
+    all (its scales group 16 rows; tinytron_amd.cache rounds the same way)."""
+    pages = -(-int(max_seq_len) // page_size)
+    while (pages * page_size) % 16:
+        pages += 1
+    return pages * page_size
+
+
+def contiguous_geometry(batch, num_heads, head_dim, max_seq_len, page_size, fp8=False):
+    if fp8:
+        max_seq_len = fp8_capacity(max_seq_len, page_size)
     layout = okv.contiguous_layout(batch, num_heads, head_dim, max_seq_len, page_size)
     numel = okv.contiguous_numel(batch, num_heads, head_dim, max_seq_len, page_size)
     return layout, numel
@@ -50,8 +61,8 @@ def fill_cache_values(layout, numel, batch, lengths, rng, fp8=False, key_gain=No
 
         kc = np.full(numel, 0x7F, dtype=np.uint8)
         vc = np.full(numel, 0x7F, dtype=np.uint8)
-        ks = np.full(numel // D, np.nan, dtype=np.float32)
-        vs = np.full(numel // D, np.nan, dtype=np.float32)
+        kvs = np.full(okv.fp8_scale_numel(numel // D), np.nan, dtype=np.float32)  # K and V scales, 16-row groups
+        ks, vs = kvs, kvs[16:]
     else:
         kc = np.full(numel, nan_bits, dtype=np.uint16)
         vc = np.full(numel, nan_bits, dtype=np.uint16)
@@ -72,8 +83,8 @@ def fill_cache_values(layout, numel, batch, lengths, rng, fp8=False, key_gain=No
         if fp8:
             kc[idx] = kq.reshape(-1)
             vc[idx] = vq.reshape(-1)
-            ks[(offs // D).reshape(-1)] = ksc.reshape(-1)
-            vs[(offs // D).reshape(-1)] = vsc.reshape(-1)
+            ks[okv.fp8_scale_index(offs // D).reshape(-1)] = ksc.reshape(-1)
+            vs[okv.fp8_scale_index(offs // D).reshape(-1)] = vsc.reshape(-1)
         else:
             kc[idx] = f32_to_bf16_bits(kb).reshape(-1)
             vc[idx] = f32_to_bf16_bits(vb).reshape(-1)

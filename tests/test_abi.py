@@ -47,7 +47,7 @@ def test_noalloc_scratch_size_matches_header():
 
 
 def test_abi_version():
-    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_workspace_and_split_sizing():

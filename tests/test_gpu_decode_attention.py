@@ -38,7 +38,7 @@ def run_case(lengths, Hq=32, Hkv=8, D=128, P=16, paged=False, fp8=False, seed=0,
         layout, numel, ptab, num_pages = paged_geometry(lengths, Hkv, D, P, rng)
     else:
         cap = ((max_len + P - 1) // P) * P
-        layout, numel = contiguous_geometry(B, Hkv, D, cap, P)
+        layout, numel = contiguous_geometry(B, Hkv, D, cap, P, fp8=fp8)
     if f32:
         keys = [rng.standard_normal((int(L), Hkv, D)).astype(np.float32) for L in lengths]
         values = [rng.standard_normal((int(L), Hkv, D)).astype(np.float32) for L in lengths]

@@ -27,6 +27,7 @@ torch = pytest.importorskip("torch")
 
 import bench
 from oracle.attention import decode_attention as ref_attention
+from oracle import kvcache as okv
 from oracle.kvcache import CacheLayout
 from oracle.numerics import dequantize_e4m3_rows, f32_to_bf16_bits, quantize_e4m3_rows
 from oracle.rope import rope_apply
@@ -91,7 +92,7 @@ def _check_append(cfg, wl, olay, before, after):
         vc, vs = quantize_e4m3_rows(v)
         want = [kc.reshape(-1), vc.reshape(-1)]
         want_s = [ks.reshape(-1), vs.reshape(-1)]
-        rows = torch.from_numpy((offs // D).reshape(-1)).to(DEV)
+        rows = torch.from_numpy(okv.fp8_scale_index(offs // D).reshape(-1)).to(DEV)
     else:
         want = [f32_to_bf16_bits(k_rot).reshape(-1).view(np.int16), f32_to_bf16_bits(v).reshape(-1).view(np.int16)]
     for i in range(2):
@@ -106,7 +107,9 @@ def _check_append(cfg, wl, olay, before, after):
         for i in range(2):
             a, z = after[2 + i], before[2 + i]
             changed = torch.nonzero(_bits(a) != _bits(z)).flatten()
-            assert torch.isin(changed, rows).all(), "scale written outside the appended slots"
+            # the K and V views share one array (V 16 slots in): the other view's writes show 16 slots away
+            slots = torch.cat([rows, rows + 16, rows - 16])
+            assert torch.isin(changed, slots).all(), "scale written outside the appended slots"
             assert np.array_equal(a[rows].cpu().numpy(), want_s[i]), "appended scales differ from the oracle"
 
 
@@ -151,7 +154,7 @@ def test_full_size_step(config):
         L = int(total[b])
         if cfg["fp8"]:
             kc, vc = _gather(lay.k.view(torch.uint8), olay, b, L), _gather(lay.v.view(torch.uint8), olay, b, L)
-            rows = torch.from_numpy(olay.token_offsets(b, L) // D).to(DEV)
+            rows = torch.from_numpy(okv.fp8_scale_index(olay.token_offsets(b, L) // D)).to(DEV)
             keys = dequantize_e4m3_rows(kc.cpu().numpy(), lay.k_scale[rows].cpu().numpy())
             values = dequantize_e4m3_rows(vc.cpu().numpy(), lay.v_scale[rows].cpu().numpy())
         else:

@@ -112,7 +112,7 @@ def _layout(B, fp8):
     if fp8:
         k = torch.full((numel,), 0x55, dtype=torch.uint8, device=DEV)
         v = k.clone()
-        ks = torch.full((numel // D,), -1.0, dtype=torch.float32, device=DEV)
+        ks = torch.full((okv.fp8_scale_numel(numel // D),), -1.0, dtype=torch.float32, device=DEV)
         vs = ks.clone()
     else:
         k = torch.zeros(numel, dtype=torch.bfloat16, device=DEV)
@@ -140,7 +140,7 @@ def _check_fp8_rows(kv, lay, rows_k, rows_v, positions):
             assert np.array_equal(got, want_c[b]), (
                 f"{name} row {b}: codes differ at {np.flatnonzero(got != want_c[b])[:8]} "
                 f"(got {got[got != want_c[b]][:8]}, want {want_c[b][got != want_c[b]][:8]})")
-            gs, ws = scales[off // D], want_s[b]
+            gs, ws = scales[okv.fp8_scale_index(off // D)], want_s[b]
             assert (np.isnan(gs) and np.isnan(ws)) or gs.view(np.uint32) == ws.view(np.uint32), (
                 f"{name} row {b}: scale {gs!r} != {ws!r}")
 

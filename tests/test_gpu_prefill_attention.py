@@ -39,7 +39,7 @@ def run_prefill(past, new, Hq=32, Hkv=8, D=128, P=16, paged=True, fp8=False, see
         layout, numel, ptab, num_pages = paged_geometry(total, Hkv, D, P, rng)
     else:
         cap = ((max_len + P - 1) // P) * P
-        layout, numel = contiguous_geometry(B, Hkv, D, cap, P)
+        layout, numel = contiguous_geometry(B, Hkv, D, cap, P, fp8=fp8)
     data = fill_cache_values(layout, numel, B, total, rng, fp8=fp8, key_gain=key_gain)
     if transposed_q:
         qb, qf = bf16_randn(rng, (B, T, Hq, D))

@@ -41,7 +41,7 @@ def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False, from_par
     if paged:
         layout, numel, ptab, num_pages = paged_geometry(cap_needed + 7, Hkv, D, P, rng)
     else:
-        layout, numel = contiguous_geometry(B, Hkv, D, max_seq, P)
+        layout, numel = contiguous_geometry(B, Hkv, D, max_seq, P, fp8=kind == "fp8")
     # inputs laid out [B, T, H, D] and viewed [B, H, T, D] as q_proj(x).view().transpose() gives
     qb, qf = bf16_randn(rng, (B, T, Hq, D))
     kb, kf = bf16_randn(rng, (B, T, Hkv, D))
@@ -74,8 +74,8 @@ def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False, from_par
     if kind == "fp8":
         k_store = torch.full((numel,), 0x7E, dtype=torch.uint8, device=DEV)
         v_store = torch.full((numel,), 0x7E, dtype=torch.uint8, device=DEV)
-        k_scale = torch.full((numel // D,), -1.0, dtype=torch.float32, device=DEV)
-        v_scale = torch.full((numel // D,), -1.0, dtype=torch.float32, device=DEV)
+        k_scale = torch.full((okv.fp8_scale_numel(numel // D),), -1.0, dtype=torch.float32, device=DEV)
+        v_scale = k_scale.clone()
     elif kind == "bf16":
         k_store = torch.full((numel,), int(sentinel16.view(np.int16)), dtype=torch.int16, device=DEV).view(torch.bfloat16)
         v_store = k_store.clone()
@@ -116,8 +116,8 @@ def _case(kind, paged, D, T, seed, Hq=8, Hkv=2, P=16, ragged_new=False, from_par
     if kind == "fp8":
         exp_k = np.full(numel, 0x7E, np.uint8)
         exp_v = np.full(numel, 0x7E, np.uint8)
-        exp_ks = np.full(numel // D, -1.0, np.float32)
-        exp_vs = np.full(numel // D, -1.0, np.float32)
+        exp_ks = np.full(okv.fp8_scale_numel(numel // D), -1.0, np.float32)
+        exp_vs = exp_ks.copy()
         okv.append_fp8(exp_k, exp_ks, layout, k_ref.transpose(0, 2, 1, 3), positions, new_lens)
         okv.append_fp8(exp_v, exp_vs, layout, v_ref.transpose(0, 2, 1, 3), positions, new_lens)
         got_k = k_store.cpu().numpy()

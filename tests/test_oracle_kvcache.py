@@ -136,12 +136,30 @@ def test_fp8_append_writes_codes_and_scales():
     layout = okv.contiguous_layout(B, H, D, 32, P)
     n = okv.contiguous_numel(B, H, D, 32, P)
     codes = np.zeros(n, np.uint8)
-    scales = np.full(n // D, -1.0, np.float32)
+    scales = np.full(okv.fp8_scale_numel(n // D), -1.0, np.float32)
     x = rng.standard_normal((B, H, 1, D)).astype(np.float32)
     okv.append_fp8(codes, scales, layout, x, [3, 9])
     for b, pos in enumerate([3, 9]):
         for h in range(H):
             off = layout.token_offset(b, h, pos)
-            assert scales[off // D] == np.float32(np.abs(x[b, h, 0]).max() / np.float32(448))
+            row = off // D
+            assert scales[32 * (row // 16) + row % 16] == np.float32(np.abs(x[b, h, 0]).max() / np.float32(448))
             assert np.max(codes[off:off + D] & 0x7F) == 0x7E
     assert np.sum(scales != -1.0) == B * H
+
+
+def test_fp8_scale_slots_group_k_and_v_by_16_rows():
+    """Brute force over 0 .. 99 rows: every row's K slot (k) and V slot
+    (16 + k in the one array) are distinct from every other slot, lie inside
+    fp8_scale_numel, and rows 16g .. 16g + 15 fill exactly the 128-byte line
+    [32g, 32g + 32) of the array: K scales first, then V."""
+    rows = np.arange(100)
+    k = okv.fp8_scale_index(rows)
+    v = k + 16
+    slots = np.concatenate([k, v])
+    assert len(set(slots.tolist())) == 200 and slots.max() < okv.fp8_scale_numel(100) == 224
+    for g in range(100 // 16):
+        grp = rows[16 * g:16 * g + 16]
+        assert set(okv.fp8_scale_index(grp).tolist()) == set(range(32 * g, 32 * g + 16))
+        assert set((okv.fp8_scale_index(grp) + 16).tolist()) == set(range(32 * g + 16, 32 * g + 32))
+        assert (32 * g * 4) // 128 == ((32 * g + 31) * 4) // 128  # one 128-byte line

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TT_OK = 0
 TT_ERR_INVALID_ARGUMENT = -1

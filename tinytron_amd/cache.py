@@ -264,7 +264,8 @@ class _LayerCacheBase:
         idx = base[None, :, None] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None, None] \
             + torch.arange(D, device=base.device)[None, None, :]              # [H, L, D]
         if lay.kind == "fp8":
-            sidx = (base[None, :] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None]) // D
+            sidx = ops.fp8_scale_index((base[None, :] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None])
+                                       // D)
             k = lay.k[idx].view(FP8).float() * lay.k_scale[sidx][..., None]
             v = lay.v[idx].view(FP8).float() * lay.v_scale[sidx][..., None]
             dt = dtype or torch.bfloat16
@@ -280,7 +281,8 @@ class _LayerCacheBase:
         idx = base[None, :, None] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None, None] \
             + torch.arange(D, device=base.device)[None, None, :]
         if lay.kind == "fp8":
-            sidx = (base[None, :] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None]) // D
+            sidx = ops.fp8_scale_index((base[None, :] + (torch.arange(H, device=base.device) * lay.strides[2])[:, None])
+                                       // D)
             kc, ks = _quantize_rows(k)
             vc, vs = _quantize_rows(v)
             lay.k[idx] = kc
@@ -330,6 +332,9 @@ class LayerPagedKVCache(_LayerCacheBase):
         self.page_size = page_size
         kind = cache_kind(dtype)
         num_pages = math.ceil(max_seq_len / page_size)
+        if kind == "fp8":  # its scales group 16 rows: a (sequence, head) holds a multiple of 16 token slots
+            while (num_pages * page_size) % 16:
+                num_pages += 1
         shape = (batch_size, num_heads, num_pages, page_size, head_dim)
         store = torch.uint8 if kind == "fp8" else dtype
         self._k_pages = torch.empty(shape, device=device, dtype=store)
@@ -338,8 +343,7 @@ class LayerPagedKVCache(_LayerCacheBase):
         self._v_flat = self._v_pages.view(batch_size, num_heads, num_pages * page_size, head_dim)
         k_scale = v_scale = None
         if kind == "fp8":
-            k_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
-            v_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
+            k_scale, v_scale = ops.fp8_scales(math.prod(shape[:-1]), device)
         pd = page_size * head_dim
         self.layout = ops.KVLayout(
             k=self._k_pages.view(-1), v=self._v_pages.view(-1),
@@ -393,8 +397,7 @@ class PagedLayerKVCache(_LayerCacheBase):
         self._v = torch.empty(shape, device=device, dtype=store)
         k_scale = v_scale = None
         if kind == "fp8":
-            k_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
-            v_scale = torch.empty(shape[:-1], device=device, dtype=torch.float32).view(-1)
+            k_scale, v_scale = ops.fp8_scales(math.prod(shape[:-1]), device)
         self.layout = ops.KVLayout(
             k=self._k.view(-1), v=self._v.view(-1), strides=(0, num_heads * page_size * head_dim, page_size * head_dim),
             num_heads=num_heads, head_dim=head_dim, page_size=page_size,

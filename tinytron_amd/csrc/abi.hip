@@ -103,6 +103,21 @@ int check_layout(const int32_t *page_table, int64_t max_pages, int64_t num_pages
 // dimension has more than one entry must be at least max_seq_len * head_dim
 // (the reference's [B, H, pages, P, D] store has c_head = pages * P * D and
 // c_seq = H * c_head).
+// fp8 caches: one scale per row (strides multiples of head_dim), and every
+// 16-token block of a (sequence, head) starting a 16-row scale group: page
+// and head strides (pool) or sequence and head strides (contiguous store)
+// multiples of 16 head_dim (tt::fp8_scale_index).
+int check_fp8_strides(const int32_t *page_table, const int64_t cache_strides[3], int64_t head_dim) {
+  TT_CHECK(cache_strides[0] % head_dim == 0 && cache_strides[1] % head_dim == 0 && cache_strides[2] % head_dim == 0,
+           TT_ERR_INVALID_ARGUMENT, "fp8 cache strides must be multiples of head_dim (one scale per row)");
+  const int64_t group = 16 * head_dim;
+  const int64_t outer = page_table != nullptr ? cache_strides[1] : cache_strides[0];
+  TT_CHECK(outer % group == 0 && cache_strides[2] % group == 0, TT_ERR_INVALID_ARGUMENT,
+           "fp8 caches group their scales by 16 rows: the %s and head strides must be multiples of 16 * head_dim "
+           "(a contiguous store's capacity a multiple of 16 tokens)", page_table != nullptr ? "page" : "sequence");
+  return TT_OK;
+}
+
 int check_contiguous_room(int64_t max_seq_len, int64_t head_dim, const int64_t cache_strides[3], int64_t batch,
                           int64_t num_kv_heads) {
   const int64_t need = max_seq_len * head_dim;
@@ -141,6 +156,9 @@ int rope_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_in_
            "grid too large");
   if (kind == tt::CacheKind::kFP8) {
     TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
+    TT_CHECK(cache_strides != nullptr, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
+    const int frc = check_fp8_strides(page_table, cache_strides, head_dim);
+    if (frc != TT_OK) return frc;
   }
   TT_CHECK(lens_out == nullptr || ((const void *)lens_out != (const void *)positions &&
                                    (const void *)lens_out != (const void *)new_lens),
@@ -256,8 +274,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
            "max_seq_len out of range");
   if (kind == tt::CacheKind::kFP8) {
     TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
-    TT_CHECK(cache_strides[0] % head_dim == 0 && cache_strides[1] % head_dim == 0 && cache_strides[2] % head_dim == 0,
-             TT_ERR_INVALID_ARGUMENT, "fp8 cache strides must be multiples of head_dim (one scale per row)");
+    const int frc = check_fp8_strides(page_table, cache_strides, head_dim);
+    if (frc != TT_OK) return frc;
   }
   int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
   if (rc != TT_OK) return rc;
@@ -459,8 +477,8 @@ int prefill_common(tt::CacheKind kind, const void *q, const int64_t q_strides[3]
            "grid too large");
   if (kind == tt::CacheKind::kFP8) {
     TT_CHECK(k_scale && v_scale, TT_ERR_INVALID_ARGUMENT, "fp8 cache needs k_scale and v_scale");
-    TT_CHECK(cache_strides[0] % head_dim == 0 && cache_strides[1] % head_dim == 0 && cache_strides[2] % head_dim == 0,
-             TT_ERR_INVALID_ARGUMENT, "fp8 cache strides must be multiples of head_dim (one scale per row)");
+    const int frc = check_fp8_strides(page_table, cache_strides, head_dim);
+    if (frc != TT_OK) return frc;
   }
   int rc = check_layout(page_table, max_pages, num_pages, cache_strides, page_size);
   if (rc != TT_OK) return rc;

@@ -157,10 +157,12 @@ __device__ __forceinline__ void load_k_block(const DecodeArgs &a, int64_t elem, 
     k[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * u, 0, 0));
   if constexpr (kFP8) {
     // this lane's score rows are tokens tb + 4g + r, r = 0..3
-    const int64_t srow = scale_row<D, kPad>(a, elem);
-    const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + srow, (short)0,
+    // the block starts a 16-row scale group (the host checks the strides), so
+    // its K and V scales are 16 consecutive entries of each array
+    const int64_t sidx = fp8_scale_index(scale_row<D, kPad>(a, elem));
+    const auto rks = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.k_scale) + sidx, (short)0,
                                                        rows * 4, kBufferFlags);
-    const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + srow, (short)0,
+    const auto rvs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.v_scale) + sidx, (short)0,
                                                        rows * 4, kBufferFlags);
     ks = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rks, 16 * (lane >> 4), 0, 0));
     vs = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rvs, 16 * (lane >> 4), 0, 0));

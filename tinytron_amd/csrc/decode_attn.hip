@@ -573,9 +573,9 @@ __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const Decode
           vcache[off + H + lane] = e4m3_row_code(v2, vscale);
         }
         if (lane == 0) {
-          const int64_t srow = scale_row<D, kPad>(a, off);
-          const_cast<float *>(a.k_scale)[srow] = kscale;
-          const_cast<float *>(a.v_scale)[srow] = vscale;
+          const int64_t sidx = fp8_scale_index(scale_row<D, kPad>(a, off));
+          const_cast<float *>(a.k_scale)[sidx] = kscale;
+          const_cast<float *>(a.v_scale)[sidx] = vscale;
         }
       }
     }
@@ -909,7 +909,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
     float ksc = 1.f;
     if (valid) {
       koff = token_elem(a, bs, hk, tok, hd);
-      if constexpr (K == CacheKind::kFP8) ksc = a.k_scale[koff / hd];
+      if constexpr (K == CacheKind::kFP8) ksc = a.k_scale[fp8_scale_index(koff / hd)];
     }
     for (int h = 0; h < G && h < 16; ++h) {
       float sc = kNegInf;
@@ -935,7 +935,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
       for (int t = 0; t < nt; ++t) {
         const int64_t voff = token_elem(a, bs, hk, t0 + t, hd);
         float pt = sp[t];
-        if constexpr (K == CacheKind::kFP8) pt *= a.v_scale[voff / hd];
+        if constexpr (K == CacheKind::kFP8) pt *= a.v_scale[fp8_scale_index(voff / hd)];
         for (int j = 0; j < 2; ++j)
           if (lane + 64 * j < hd) o[h][j] += pt * kv_value<K>(a.v_cache, voff + lane + 64 * j);
       }

@@ -105,8 +105,8 @@ __device__ __forceinline__ void finish_token(const RopeAppendArgs &a, int b, int
       vc[off + half + i] = e4m3_row_code(v2, vscale);
     }
     if (i == 0) {
-      a.k_scale[off / a.head_dim] = kscale;
-      a.v_scale[off / a.head_dim] = vscale;
+      a.k_scale[fp8_scale_index(off / a.head_dim)] = kscale;
+      a.v_scale[fp8_scale_index(off / a.head_dim)] = vscale;
     }
   }
 }
@@ -425,8 +425,8 @@ __global__ __launch_bounds__(64) void rope_append_vec_kernel(RopeAppendArgs a) {
         *reinterpret_cast<uint32_t *>(vc + off + e0) = wa;
         *reinterpret_cast<uint32_t *>(vc + off + half + e0) = wb;
         if (e0 == 0) {
-          a.k_scale[off >> dsh] = ks;
-          a.v_scale[off >> dsh] = vs;
+          a.k_scale[fp8_scale_index(off >> dsh)] = ks;
+          a.v_scale[fp8_scale_index(off >> dsh)] = vs;
         }
       }
     }

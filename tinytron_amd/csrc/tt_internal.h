@@ -28,6 +28,14 @@ inline int device_cu_count() {
 
 enum class CacheKind { kBF16, kF32, kFP8 };
 
+// fp8 caches keep their fp32 scales in groups of 16 rows (row = element
+// offset of d = 0 / head_dim): rows 16g .. 16g + 15 have their K scales at
+// 32g .. 32g + 15 of k_scale and their V scales at the same indices of
+// v_scale, laid out so that one array of 2 x rows entries serves both with
+// v_scale = k_scale + 16. A 16-token block's K and V scales then fill one
+// 128-byte line, which the attention kernels read whole.
+__host__ __device__ __forceinline__ int64_t fp8_scale_index(int64_t row) { return row + (row & ~(int64_t)15); }
+
 struct RopeAppendArgs {
   const void *q_in;
   int64_t qi_sb, qi_sh, qi_st;

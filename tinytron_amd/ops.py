@@ -44,7 +44,7 @@ class KVLayout:
     ``strides`` = (seq, page, head) element strides; ``page_table`` is None
     for the contiguous [B, H, pages, P, D] store or an int32 [B, max_pages]
     device tensor for the pool [num_pages, H, P, D]. fp8 scales are fp32 in
-    the cache layout with head_dim collapsed.
+    16-row groups (``fp8_scale_index``; ``fp8_scales`` allocates them).
     """
 
     k: torch.Tensor
@@ -63,6 +63,23 @@ class KVLayout:
     @property
     def max_pages(self) -> int:
         return 0 if self.page_table is None else int(self.page_table.shape[1])
+
+
+def fp8_scale_index(row):
+    """Index of row ``row``'s K scale in k_scale (and of its V scale in v_scale)
+    of an fp8 cache, row = element offset of d = 0 / head_dim: rows grouped by
+    16, each group's 16 K scales then its 16 V scales (ints, numpy or torch
+    integer arrays)."""
+    return row + (row // 16) * 16
+
+
+def fp8_scales(rows: int, device) -> tuple:
+    """(k_scale, v_scale) of an fp8 cache with ``rows`` (token, head) rows: one
+    fp32 array of 2 x rows entries (rows rounded up to 16) and its view 16
+    entries in, so that each 16-row group's K and V scales share a 128-byte
+    line (fp8_scale_index)."""
+    t = torch.empty(2 * (-(-int(rows) // 16) * 16), dtype=torch.float32, device=device)
+    return t, t[16:]
 
 
 def _stream(device: torch.device) -> int:
