@@ -359,3 +359,27 @@ def test_sampled_generation_is_seeded_and_graph_invariant():
     assert lp.shape == (len(lens), 24) and bool(torch.isfinite(lp).all()) and bool((lp <= 0).all())
     assert int(toks.max()) < cfg.vocab_size
     assert len({tuple(r.tolist()) for r in toks}) > 1
+
+
+def test_auto_launch_mode_gives_the_eager_tokens():
+    """The engine's default launch mode (eager or graph replay, chosen on the
+    second step from the host's issue time) changes no token or
+    log-probability: it equals a forced-eager run bit for bit, and says which
+    mode it took."""
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=2, block_size=256, vocab_size=4096, hidden_size=1024, num_attention_heads=16,
+                     num_key_value_heads=4)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    lens = [9, 50, 31]
+    prompt = torch.randint(0, cfg.vocab_size, (len(lens), max(lens)), generator=torch.Generator().manual_seed(19))
+    runs = []
+    for mode in (None, False):
+        eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True,
+                              model=model, use_graphs=mode)
+        toks, extra = eng.generate(prompt, 20, top_k=1, prompt_lens=lens, return_logprobs=True)
+        runs.append((toks.cpu(), extra["token_log_probs"].cpu(), eng.last_decode_launch))
+    (t0, lp0, mode0), (t1, lp1, mode1) = runs
+    assert mode0 in ("eager", "graphs") and mode1 == "eager"
+    assert torch.equal(t0, t1) and torch.equal(lp0, lp1)

@@ -12,13 +12,16 @@ past_key_values=cache, position_offset=...)``; positions come from the
 cache's per-sequence lengths, so there is no host synchronisation in the
 loop (the reference syncs once per layer at attn.py:395).
 
-With ``use_graphs`` (the default for the paged caches; ``False`` launches
-eagerly) the one-token model call is captured in HIP graphs after the first
-decode step and replayed for the rest, which removes the per-kernel launch
-cost: the fused bf16 step issues 8 launches per layer, about as fast as the
-host can issue them (C5: 26.8 k tokens/s eager against 28.4 k replayed,
-captures included), the fused step with an fp8 cache one more, and the
-module-by-module step about 30.
+With ``use_graphs=True`` the one-token model call is captured in HIP graphs
+after the first decode step and replayed for the rest, which removes the
+per-kernel launch cost; ``False`` launches every step eagerly. By default
+(``None``) the engine times the second step eagerly, alone (one
+synchronisation), and replays graphs only when the host needs at least 0.9x
+the step's GPU time to issue it: the fused bf16 step issues 8 launches per
+layer, about as fast as a fast host issues them (C5: eager 28.5-29.3 k
+tokens/s against 27.7-28.6 k replayed with the two captures inside the loop;
+a slower host read 26.8 k eager against 28.4 k replayed), the fused step
+with an fp8 cache one launch more, and the module-by-module step about 30.
 The caches keep their lengths in two device buffers that swap every step, so
 two graphs are captured, one per buffer parity. The attention launch bound is
 fixed at the largest sequence capacity for the whole decode loop, so the
@@ -151,8 +154,15 @@ class InferenceEngine:
         cur = lens_t.clone()
         uniform = len(set(lens)) == 1
         graphs = None
-        # the tuple cache's tensors change every step: it launches eagerly
-        use_graphs = paged and (self.use_graphs is None or bool(self.use_graphs))
+        # the tuple cache's tensors change every step: it launches eagerly. The
+        # paged caches replay graphs when asked (use_graphs=True), launch
+        # eagerly when told not to (False), and by default (None) decide on the
+        # second step: replay when the host takes at least 0.9x the GPU's time
+        # to issue one eager step (the GPU would wait on the host), else stay
+        # eager (replay would only add the two captures to the loop).
+        use_graphs = paged and bool(self.use_graphs)
+        auto = paged and self.use_graphs is None
+        self.last_decode_launch = "graphs" if use_graphs else "eager"
         if paged:
             cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
@@ -172,6 +182,19 @@ class InferenceEngine:
                 graphs = DecodeGraphs(self.model, cache, batch_size, position, uniform, self.device)
             if graphs is not None:
                 logits = graphs.step(next_token)
+            elif auto and step == 1:
+                # one eager step timed alone: host issue time against its GPU time
+                torch.cuda.synchronize(self.device)
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                ev[0].record()
+                h0 = time.perf_counter()
+                logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
+                                           position_offset=position)
+                host_s = time.perf_counter() - h0
+                ev[1].record()
+                ev[1].synchronize()
+                use_graphs = host_s >= 0.9 * ev[0].elapsed_time(ev[1]) * 1e-3
+                self.last_decode_launch = "graphs" if use_graphs else "eager"
             else:
                 logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
                                            position_offset=position)
