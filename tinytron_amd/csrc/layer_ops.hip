@@ -185,10 +185,11 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 // bf16-rounded sum of the partials (the projection's autocast output). Every
 // load of the row (x and up to SMAX splits) is issued before the first add,
 // so the row costs one memory round trip; the splits are added in order.
-// PER float4 groups per thread (C <= 1024 * PER, C a multiple of 4; groups
-// past C are neither loaded nor stored and add 0 to the sum of squares);
-// SMAX splits loaded at once
-template <int PER, int SMAX>
+// PER float4 groups per thread (C <= 1024 * PER, C a multiple of 4; with
+// kMask, groups past C are neither loaded nor stored and add 0 to the sum of
+// squares; without it C == 1024 * PER and every load is unconditional, so
+// all of them go out before the first add); SMAX splits loaded at once
+template <int PER, int SMAX, bool kMask>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float *P, int S, int64_t MN,
                                                           const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    const bool in = c < C;
+    const bool in = !kMask || c < C;
     v[j] = in ? *reinterpret_cast<const f32x4 *>(x + row + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     if (P != nullptr) {
 #pragma unroll
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    if (c >= C) continue;
+    if (kMask && c >= C) continue;
     if (P != nullptr) {
       f32x4 d = pv[j][0];
 #pragma unroll
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    if (c >= C) continue;
+    if (kMask && c >= C) continue;
     const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
     uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
     uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(64 * 2 * NB, NB == 4 ? 1 : 2) void swiglu_gemm_kern
 // x += float(a[m]) (a: bf16 [M, C] with row stride lda, the projection's
 // autocast output; a == nullptr skips the add), then
 // y = bf16(w * x * rsqrt(mean(x^2) + eps)) as in add_rmsnorm_kernel.
-template <int PER>  // as add_rmsnorm_kernel: C <= 1024 * PER, groups past C masked
+template <int PER, bool kMask>  // as add_rmsnorm_kernel
 __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const uint16_t *a, int64_t lda,
                                                                const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    const bool in = c < C;
+    const bool in = !kMask || c < C;
     v[j] = in ? *reinterpret_cast<const f32x4 *>(x + row + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     av[j] = make_uint2(0u, 0u);
     if (a != nullptr && in) av[j] = *reinterpret_cast<const uint2 *>(a + (int64_t)blockIdx.x * lda + c);
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    if (4 * (threadIdx.x + 256 * j) >= C) continue;
+    if (kMask && 4 * (threadIdx.x + 256 * j) >= C) continue;
     if (a != nullptr) {
       v[j][0] += __builtin_bit_cast(float, av[j].x << 16);
       v[j][1] += __builtin_bit_cast(float, av[j].x & 0xffff0000u);
@@ -417,7 +418,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
-    if (c >= C) continue;
+    if (kMask && c >= C) continue;
     const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
     uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
     uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
@@ -501,8 +502,15 @@ hipError_t launch_reduce_bf16(const float *P, int S, int64_t MN, uint16_t *y, hi
 hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, const float *w, float eps, uint16_t *y,
                               hipStream_t stream) {
   const int64_t MN = (int64_t)M * C;
-#define TT_ADD_RMSNORM_LAUNCH(n, smax) \
-  hipLaunchKernelGGL((add_rmsnorm_kernel<n, smax>), dim3(M), dim3(256), 0, stream, x, P, S, MN, w, eps, y, C)
+#define TT_ADD_RMSNORM_LAUNCH(n, smax)                                                                       \
+  do {                                                                                                      \
+    if (C % 1024 == 0)                                                                                      \
+      hipLaunchKernelGGL((add_rmsnorm_kernel<n, smax, false>), dim3(M), dim3(256), 0, stream, x, P, S, MN, w, eps, \
+                         y, C);                                                                             \
+    else                                                                                                    \
+      hipLaunchKernelGGL((add_rmsnorm_kernel<n, smax, true>), dim3(M), dim3(256), 0, stream, x, P, S, MN, w, eps, \
+                         y, C);                                                                             \
+  } while (0)
 #define TT_ADD_RMSNORM_CASE(n)                  \
   case n:                                       \
     if (S <= 4)                                 \
@@ -572,7 +580,10 @@ hipError_t launch_add_rmsnorm_rows(float *x, const uint16_t *a, int64_t lda, int
   switch ((C + 1023) / 1024) {  // C a multiple of 4 in [4, 8192], checked by the caller
 #define TT_ROWS_CASE(n)                                                                                              \
   case n:                                                                                                            \
-    hipLaunchKernelGGL((add_rmsnorm_rows_kernel<n>), dim3(M), dim3(256), 0, stream, x, a, lda, w, eps, y, C);     \
+    if (C % 1024 == 0)                                                                                               \
+      hipLaunchKernelGGL((add_rmsnorm_rows_kernel<n, false>), dim3(M), dim3(256), 0, stream, x, a, lda, w, eps, y, C); \
+    else                                                                                                             \
+      hipLaunchKernelGGL((add_rmsnorm_rows_kernel<n, true>), dim3(M), dim3(256), 0, stream, x, a, lda, w, eps, y, C); \
     break;
     TT_ROWS_CASE(1)
     TT_ROWS_CASE(2)
