@@ -67,7 +67,9 @@ def parse_args():
                    help="comma-separated configs measured after the headline one and reported in nested records "
                         "('' for none)")
     p.add_argument("--seed", type=int, default=1337)
-    p.add_argument("--split-tokens", type=int, default=0)
+    p.add_argument("--split-tokens", type=int, default=None,
+                   help="decode attention partition: 0 balanced, -1 one workgroup per (sequence, KV head), "
+                        "128-1024 fixed splits; default: what the KV cache picks for the workload's lengths")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of timed CPU-baseline work per config")
     p.add_argument("--no-c1", action="store_true", help="skip config C1 (the reference's CPU-sized model)")
@@ -596,7 +598,11 @@ def run_config(name, args, torch, ops):
     q_rot = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
     out = torch.empty(B, hq, D, dtype=torch.bfloat16, device="cuda")
     ws = ops.Workspace("cuda")
-    split = args.split_tokens
+    # the partition the KV cache picks for these lengths (LayerPagedKVCache._attention_split): one
+    # workgroup per (sequence, KV head) when all lengths are equal and B * H_kv fills the GPU
+    split = args.split_tokens if args.split_tokens is not None else \
+        ops.pick_split(wl["total"].tolist(), cfg["hkv"], D, "fp8" if cfg["fp8"] else "bf16")
+    per_segment = split == ops.SPLIT_PER_SEGMENT
     lens_out = torch.empty_like(wl["positions"])
     fused = args.step_path == "fused" or (args.step_path == "auto" and not cfg["fp8"])
 
@@ -606,13 +612,13 @@ def run_config(name, args, torch, ops):
                              split_tokens=split, workspace=ws)
 
     def step():
-        # the fused decode step: RoPE + append of the new token inside the attention launch pair
-        if split or not fused:
+        # the fused decode step: RoPE + append of the new token inside the attention launch(es)
+        if split > 0 or not fused:
             two_launch_step()
             return
         ops.decode_attention_append(wl["rope"], wl["positions"], layout, wl["max_len"], q=wl["q_in"][:, :, 0],
                                     k=wl["k_in"][:, :, 0], v=wl["v_in"][:, :, 0], lens_out=lens_out, out=out,
-                                    workspace=ws)
+                                    workspace=ws, split_tokens=split)
 
     def attn_only():
         ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
@@ -641,15 +647,20 @@ def run_config(name, args, torch, ops):
             "workload": cfg["name"],
             "batch": B, "q_heads": hq, "kv_heads": cfg["hkv"], "head_dim": D,
             "context": [cfg["lo"], cfg["hi"]], "page_size": cfg["page"], "paged": cfg["paged"],
-            "cached_tokens": tokens, "split_tokens": split or "balanced (equal 32-token tiles per wave)",
+            "cached_tokens": tokens,
+            "split_tokens": ("per segment (-1: one workgroup per (sequence, KV head), merged in LDS; all lengths "
+                             "equal)" if per_segment else split or "balanced (equal 32-token tiles per wave)"),
             "parallelism": "single GPU",
-            "step_path": ("one launch pair: RoPE + append inside the attention split kernel "
+            "step_path": ("one launch: RoPE + append inside the per-segment attention kernel "
+                          "(decode_segment_append_kernel)" if fused and per_segment
+                          else "one launch pair: RoPE + append inside the attention split kernel "
                           "(decode_stream_append_kernel + decode_merge_kernel)" if fused and not split
                           else "rope_append_kernel, then the attention kernels"),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("decode attention (decode_stream_kernel + decode_merge_kernel)" if not split
+            "kernel": ("decode attention (decode_segment_kernel)" if per_segment
+                       else "decode attention (decode_stream_kernel + decode_merge_kernel)" if not split
                        else "decode attention (decode_split_kernel + decode_combine_kernel)"),
             "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBS,

@@ -51,12 +51,16 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 3
+#define TT_ABI_VERSION 4
 
 #define TT_OK 0
 #define TT_ERR_INVALID_ARGUMENT (-1)
 #define TT_ERR_UNSUPPORTED (-2)
 #define TT_ERR_WORKSPACE_TOO_SMALL (-3)
+
+/* split_tokens of the decode attention entry points: one workgroup per
+ * (sequence, KV head), merged inside the launch. */
+#define TT_SPLIT_PER_SEGMENT (-1)
 
 /* A hipStream_t, kept opaque so that the header needs no HIP include. */
 typedef void *tt_stream_t;
@@ -225,13 +229,22 @@ int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3]
  * sm_scale: softmax scale (1/sqrt(D) for the reference's SDPA default).
  * split_tokens: 0 = balanced partition: the 32-token tiles of all
  *   (sequence, KV head) pairs are dealt out in equal contiguous runs to the
- *   resident waves, whatever the length mix (bf16 and fp8; fp32 uses the
- *   automatic fixed split); 128, 256, 512 or 1024 = fixed splits of that
- *   many tokens.
+ *   resident waves, whatever the length mix, and a second launch merges each
+ *   pair's pieces (bf16 and fp8; fp32 uses the automatic fixed split);
+ *   TT_SPLIT_PER_SEGMENT (-1) = one workgroup per (sequence, KV head) pair,
+ *   its 4 waves taking equal quarters of the pair's tiles and merging in LDS:
+ *   one launch, no workspace; correct for any lengths, balanced when every
+ *   sequence has the same length and batch * num_kv_heads fills whole rounds
+ *   of the GPU (tt_decode_pick_split says when); the VALU kernel (fp32
+ *   caches, head dims the MFMA tiles do not take) treats it as 0;
+ *   128, 256, 512 or 1024 = fixed splits of that many tokens.
  * workspace: device scratch of at least tt_decode_workspace_bytes(...) bytes
  *   for the same (batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
- *   split_tokens); its contents need no initialisation.
- * Requirements: head_dim in {64, 128}; H_q % H_kv == 0 and
+ *   split_tokens); its contents need no initialisation. May be NULL when the
+ *   call needs none (TT_SPLIT_PER_SEGMENT on the MFMA kernels).
+ * Requirements: head_dim even and <= 128 (a multiple of 8 for a bf16 cache
+ *   or 16 for an fp8 cache runs the MFMA kernels, other head dims and fp32
+ *   caches the VALU kernel); H_q % H_kv == 0 and
  *   H_q / H_kv <= 16; a paged pool has a power-of-two page_size >= 16; the
  *   contiguous store has dense pages (cache_strides[1] == page_size *
  *   head_dim, as the reference's [B, H, pages, P, D] store), any page_size,
@@ -305,7 +318,8 @@ int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2],
  * max_seq_len: host-side bound of positions[b] + new_lens[b] (the keys read
  *   are clamped to it).
  * out [B, T, H_q, D] bf16, strides out_strides = {b, t, h}.
- * Requirements as tt_gqa_decode_attn_bf16 (head_dim 64/128, G <= 16, ...).
+ * Requirements as tt_gqa_decode_attn_bf16 (G <= 16, ...), with head_dim a
+ * multiple of 8 (bf16 cache) or 16 (fp8 cache), <= 128.
  */
 int tt_prefill_attn_bf16(const void *q, const int64_t q_strides[3],
                          const void *k_cache, const void *v_cache, const int64_t cache_strides[3],
@@ -337,8 +351,10 @@ int tt_prefill_attn_fp8(const void *q, const int64_t q_strides[3],
  * of the projection (split stride split_stride), each element the bf16 sum of
  * the splits in order. The wave that reads a segment's last tile writes that
  * segment's new k / v first, so no other launch is needed. max_seq_len must
- * bound positions[b] + 1 and the cache capacity. Balanced partition only
- * (bf16 / fp8 caches); workspace as tt_decode_workspace_bytes(..., 0).
+ * bound positions[b] + 1 and the cache capacity. split_tokens: 0 (balanced
+ * partition) or TT_SPLIT_PER_SEGMENT, as for tt_gqa_decode_attn_bf16 (bf16 /
+ * fp8 caches); workspace as tt_decode_workspace_bytes(..., split_tokens)
+ * (NULL for TT_SPLIT_PER_SEGMENT).
  */
 int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
                                const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
@@ -347,8 +363,8 @@ int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], 
                                const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *k_cache,
                                void *v_cache, const int64_t cache_strides[3], int64_t capacity, void *out,
                                const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                               int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
-                               size_t workspace_bytes, tt_stream_t stream);
+                               int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
+                               void *workspace, size_t workspace_bytes, tt_stream_t stream);
 
 /* As tt_decode_attn_append_bf16 with an fp8-e4m3fn cache (per-(token, head) scales written by the append). */
 int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
@@ -359,7 +375,8 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               void *v_cache, float *k_scale, float *v_scale, const int64_t cache_strides[3],
                               int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                              float sm_scale, void *workspace, size_t workspace_bytes, tt_stream_t stream);
+                              float sm_scale, int64_t split_tokens, void *workspace, size_t workspace_bytes,
+                              tt_stream_t stream);
 
 /*
  * tt_decode_attn_append_bf16 without the workspace argument: the attention
@@ -428,8 +445,18 @@ int tt_rows_attn_f32(const void *q, const int64_t q_strides[2], const void *k_ca
 /* Fixed split size the fp32 entry point uses when split_tokens == 0. */
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 
+/* The split_tokens value for a decode attention call over a bf16 (fp8_cache
+ * 0) or fp8 cache: TT_SPLIT_PER_SEGMENT when every sequence has the same
+ * length (equal_lengths != 0), the MFMA kernels take head_dim and
+ * batch * num_kv_heads is a multiple of the workgroups resident in one round
+ * of the current GPU (its CUs, times 2 at tile widths <= 64); else 0. No
+ * counterpart in the reference (whose batches always have one length). */
+int64_t tt_decode_pick_split(int64_t batch, int64_t num_kv_heads, int64_t head_dim, int32_t fp8_cache,
+                             int32_t equal_lengths);
+
 /* Workspace bytes the attention entry points need; for split_tokens 0 the
- * size covers every cache dtype. */
+ * size covers every cache dtype; for TT_SPLIT_PER_SEGMENT it is what the VALU
+ * kernel's automatic split needs (the MFMA kernels need none). */
 size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                  int64_t head_dim, int64_t max_seq_len, int64_t split_tokens);
 

@@ -47,7 +47,7 @@ def test_noalloc_scratch_size_matches_header():
 
 
 def test_abi_version():
-    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_workspace_and_split_sizing():
@@ -59,6 +59,25 @@ def test_workspace_and_split_sizing():
     splits = -(-16385 // split)
     assert nbytes == 64 * 8 * splits * 4 * (128 + 2) * 4
     assert lib.tt_decode_workspace_bytes(0, 32, 8, 128, 100, 0) == 0
+    # per segment: what the VALU kernel's automatic split needs (the MFMA kernels need none)
+    assert lib.tt_decode_workspace_bytes(64, 32, 8, 128, 16385, -1) == nbytes
+
+
+@pytest.mark.skipif(not _no_gpu(), reason="the resident round is 256 workgroups per tile round only on the stand-in")
+def test_pick_split():
+    """Per segment only for equal lengths, MFMA head dims and B * H_kv a
+    multiple of the resident round (256 CUs here: one workgroup per CU at tile
+    width 128, two at 64 and 32)."""
+    lib = _lib.load()
+    assert lib.tt_decode_pick_split(32, 8, 128, 0, 1) == -1   # C2: 256 segments, D 128
+    assert lib.tt_decode_pick_split(64, 8, 64, 0, 1) == -1    # 512 segments, D 64
+    assert lib.tt_decode_pick_split(32, 8, 64, 0, 1) == 0     # 256 segments at D 64: half a round
+    assert lib.tt_decode_pick_split(32, 8, 128, 0, 0) == 0    # ragged
+    assert lib.tt_decode_pick_split(33, 8, 128, 0, 1) == 0
+    assert lib.tt_decode_pick_split(64, 8, 96, 1, 1) == -1    # fp8, padded tile 128
+    assert lib.tt_decode_pick_split(64, 8, 24, 1, 1) == 0     # fp8 rows not whole 16-byte fragments
+    assert lib.tt_decode_pick_split(64, 8, 30, 0, 1) == 0     # VALU head_dim
+    assert lib.tt_decode_pick_split(0, 8, 128, 0, 1) == 0
 
 
 FAKE = 0x10000  # 16-byte aligned, never dereferenced: validation fails first
@@ -86,6 +105,7 @@ def _attn(lib, **kw):
     (dict(hq=48, hkv=2), _lib.TT_ERR_UNSUPPORTED, "group size"),
     (dict(hq=30, hkv=8), _lib.TT_ERR_INVALID_ARGUMENT, "divisible"),
     (dict(split=300), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),
+    (dict(split=-2), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),
     (dict(ws_bytes=16), _lib.TT_ERR_WORKSPACE_TOO_SMALL, "workspace"),
     (dict(page_size=24), _lib.TT_ERR_UNSUPPORTED, "power-of-two"),
     (dict(max_len=161), _lib.TT_ERR_INVALID_ARGUMENT, "exceeds the page table"),
@@ -96,6 +116,17 @@ def test_attention_rejects_invalid_arguments(kw, code, msg):
     lib = _lib.load()
     assert _attn(lib, **kw) == code
     assert msg in lib.tt_last_error_string().decode()
+
+
+@pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
+def test_fused_step_rejects_fixed_splits():
+    """The fused decode step runs the balanced (0) or per-segment (-1) partition only."""
+    lib = _lib.load()
+    s2 = _lib.strides(512, 64)
+    args = [FAKE, s2, FAKE, s2, FAKE, s2, 0, 0, FAKE, 100, FAKE, None, 50, None, 0, 0, FAKE, FAKE,
+            _lib.strides(2 * 64 * 64, 16 * 64, 64 * 64), 64, FAKE, s2, 2, 8, 2, 64, 16, 0.125]
+    assert lib.tt_decode_attn_append_bf16(*args, 512, FAKE, 1 << 30, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert "split_tokens" in lib.tt_last_error_string().decode()
 
 
 @pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")

@@ -2,7 +2,8 @@
 path it replaces (rope_append, then decode_attention over positions + 1).
 
 Both paths rotate q and k with the same arithmetic, write the same cache
-slot and run the same balanced partition over the same lengths, so the
+slot and run the same partition (balanced, or per segment when the test
+asks for it) over the same lengths, so the
 comparison is bit for bit: attention output, every cache byte (and fp8
 scale) and the lengths after the step. The two-launch path is itself pinned
 to the oracle by test_gpu_rope_append.py and test_gpu_decode_attention.py.
@@ -50,7 +51,7 @@ def _restore(layout, snap):
         t.copy_(s)
 
 
-def _run_both(layer, table, g, Hq, from_partials, S=4):
+def _run_both(layer, table, g, Hq, from_partials, S=4, split_tokens=0):
     from tinytron_amd import ops
 
     lay = layer.layout
@@ -73,7 +74,7 @@ def _run_both(layer, table, g, Hq, from_partials, S=4):
         q_rot = ops.rope_append_partials(parts, Hq, table, pos, lay, lens_out=lens_a)
     else:
         q_rot = ops.rope_append(q1, k1, v1, table, pos, lay, lens_out=lens_a)
-    out_a = ops.decode_attention(q_rot.view(B, Hq, D), lay, lens_a, max_len, workspace=ws)
+    out_a = ops.decode_attention(q_rot.view(B, Hq, D), lay, lens_a, max_len, workspace=ws, split_tokens=split_tokens)
     torch.cuda.synchronize()
     after_a = _snapshot(lay)
 
@@ -82,10 +83,10 @@ def _run_both(layer, table, g, Hq, from_partials, S=4):
     ws_b = ops.Workspace(DEV)
     if from_partials:
         out_b = ops.decode_attention_append(table, pos, lay, max_len, partials=parts, num_q_heads=Hq,
-                                            lens_out=lens_b, workspace=ws_b)
+                                            lens_out=lens_b, workspace=ws_b, split_tokens=split_tokens)
     else:
         out_b = ops.decode_attention_append(table, pos, lay, max_len, q=q1[:, :, 0], k=k1[:, :, 0], v=v1[:, :, 0],
-                                            lens_out=lens_b, workspace=ws_b)
+                                            lens_out=lens_b, workspace=ws_b, split_tokens=split_tokens)
     torch.cuda.synchronize()
     after_b = _snapshot(lay)
     assert torch.equal(lens_a, lens_b)

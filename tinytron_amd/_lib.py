@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TT_OK = 0
 TT_ERR_INVALID_ARGUMENT = -1
@@ -88,9 +88,10 @@ _DECODE_APPEND_TAIL = [
     _i64p, _i64,                                     # cache_strides, capacity
     _vp, _i64p,                                      # out, out_strides
     _i64, _i64, _i64, _i64, _i64,                    # batch, H_q, H_kv, head_dim, page_size
-    _f32, _vp, _size, _vp,                           # sm_scale, workspace, workspace_bytes, stream
+    _f32, _i64,                                      # sm_scale, split_tokens
+    _vp, _size, _vp,                                 # workspace, workspace_bytes, stream
 ]
-_DECODE_APPEND_TAIL_NOALLOC = _DECODE_APPEND_TAIL[:-4] + [_f32, _vp]  # sm_scale, stream (scratch inside)
+_DECODE_APPEND_TAIL_NOALLOC = _DECODE_APPEND_TAIL[:-5] + [_f32, _vp]  # sm_scale, stream (scratch inside)
 NOALLOC_SCRATCH_BYTES = 32 << 20  # TT_NOALLOC_SCRATCH_BYTES
 
 _SAMPLE = [
@@ -127,6 +128,7 @@ SIGNATURES = {
     "tt_rows_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ROWS_TAIL, ctypes.c_int),
     "tt_rows_attn_f32": (_ATTN_HEAD + _ROWS_TAIL, ctypes.c_int),
     "tt_decode_split_tokens": ([_i64, _i64, _i64], ctypes.c_int64),
+    "tt_decode_pick_split": ([_i64, _i64, _i64, ctypes.c_int32, ctypes.c_int32], ctypes.c_int64),
     "tt_decode_workspace_bytes": ([_i64, _i64, _i64, _i64, _i64, _i64], ctypes.c_size_t),
     "tt_prefill_attn_bf16": ([_vp, _i64p, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),
     "tt_prefill_attn_fp8": ([_vp, _i64p, _vp, _vp, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),

@@ -69,6 +69,7 @@ class _LayerCacheBase:
         self._pending_new_lens = None
         self.workspace = None
         self.static_max_len = None  # graph capture: launch-size bound fixed at the capacity
+        self._segment_split = None  # ops.pick_split for equal lengths, computed on first use
 
     # -- lengths ---------------------------------------------------------------
     @property
@@ -88,6 +89,7 @@ class _LayerCacheBase:
         self._base = [int(x) for x in lens]
         self._shift = 0
         self._base_max = max(self._base) if self._base else 0
+        self._base_min = min(self._base) if self._base else 0
         self._room = None  # min over b of capacity - base, recomputed on demand
 
     def _advance_all(self, n: int) -> None:
@@ -194,6 +196,18 @@ class _LayerCacheBase:
         the stacked projection (summed and rounded inside the kernel)."""
         return self._decode_step(rope_table, out, partials=partials, num_q_heads=num_q_heads)
 
+    def _attention_split(self) -> int:
+        """split_tokens of this cache's decode attention: the per-segment
+        partition (one launch, merged in LDS) while every sequence has the same
+        length and the batch fills whole rounds of the GPU, else the balanced
+        partition (0)."""
+        if self._base_min != self._base_max:
+            return 0
+        if self._segment_split is None:
+            lay = self.layout
+            self._segment_split = ops.pick_split([0] * self.batch_size, lay.num_heads, lay.head_dim, lay.kind)
+        return self._segment_split
+
     def _decode_step(self, rope_table, out, **inputs) -> torch.Tensor:
         self._check_room([1] * self.batch_size)
         if self.workspace is None:
@@ -201,7 +215,8 @@ class _LayerCacheBase:
         bound = self.static_max_len if self.static_max_len is not None else self.current_length + 1
         nxt = 1 - self._cur
         out = ops.decode_attention_append(rope_table, self._lens_dev[self._cur], self.layout, bound,
-                                          lens_out=self._lens_dev[nxt], out=out, workspace=self.workspace, **inputs)
+                                          lens_out=self._lens_dev[nxt], out=out, workspace=self.workspace,
+                                          split_tokens=self._attention_split(), **inputs)
         self._cur = nxt
         self._advance_all(1)
         return out
@@ -234,7 +249,8 @@ class _LayerCacheBase:
         if self.workspace is None:
             self.workspace = ops.Workspace(q.device)
         bound = self.static_max_len if self.static_max_len is not None else self.current_length
-        return ops.decode_attention(q, self.layout, self.seq_lens, bound, out=out, workspace=self.workspace)
+        return ops.decode_attention(q, self.layout, self.seq_lens, bound, out=out, workspace=self.workspace,
+                                    split_tokens=self._attention_split())
 
     # -- host-state snapshots for graph capture ------------------------------------
     def host_state(self):

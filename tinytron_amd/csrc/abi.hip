@@ -309,14 +309,24 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     TT_CHECK(aligned(q, qa) && aligned(k_cache, ca) && aligned(v_cache, ca) && aligned(out, qa),
              TT_ERR_INVALID_ARGUMENT, "q, cache and out pointers must be aligned to their element size");
   }
-  // split_tokens == 0 on the MFMA path: balanced partition (equal tiles per wave); otherwise fixed splits
+  // On the MFMA path split_tokens 0 is the balanced partition (equal tiles per
+  // wave) and kSplitPerSegment one workgroup per segment; the VALU kernel
+  // takes both as 0 (its automatic fixed split). Otherwise fixed splits.
+  TT_CHECK(split_tokens >= tt::kSplitPerSegment, TT_ERR_INVALID_ARGUMENT,
+           "split_tokens must be 0 (auto), %d (per segment), 128, 256, 512 or 1024, got %lld", tt::kSplitPerSegment,
+           (long long)split_tokens);
+  if (split_tokens == tt::kSplitPerSegment && tile == 0) split_tokens = 0;
+  const bool segment = split_tokens == tt::kSplitPerSegment;
   const bool balanced = split_tokens == 0 && tile > 0;
   int64_t split = 0, splits = 0;
   size_t need = 0;
   // partial slots beyond the segments: one per wave of the largest grid, or of the launched one
   const int64_t ws_waves =
       exact_slots ? tt::balanced_stream_waves(tile, batch, num_kv_heads, max_seq_len) : tt::kMaxStreamWaves;
-  if (balanced) {
+  if (segment) {
+    TT_CHECK(batch * num_kv_heads <= INT32_MAX, TT_ERR_UNSUPPORTED, "batch * num_kv_heads is too large");
+    split = tt::kSplitPerSegment;  // no workspace
+  } else if (balanced) {
     // the per-sequence line prefix (int32) counts each sequence's tiles plus its segment start-up charge
     TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens + tt::kStreamSegCost) < ((int64_t)1 << 31),
              TT_ERR_UNSUPPORTED, "batch * max_seq_len is too large for the balanced partition");
@@ -329,7 +339,7 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
     TT_CHECK(splits <= 65535, TT_ERR_UNSUPPORTED, "too many splits (%lld)", (long long)splits);
     need = workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_seq_len, split);
   }
-  TT_CHECK(workspace != nullptr && ws_bytes >= need, TT_ERR_WORKSPACE_TOO_SMALL,
+  TT_CHECK(need == 0 || (workspace != nullptr && ws_bytes >= need), TT_ERR_WORKSPACE_TOO_SMALL,
            "%s of %zu bytes is smaller than the %zu bytes needed",
            exact_slots ? "the allocation-free entry point's scratch" : "workspace", ws_bytes, need);
   TT_CHECK(aligned(workspace, 16), TT_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
@@ -355,11 +365,13 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.o_sb = out_strides[0];
   a.o_sh = out_strides[1];
   const int64_t g = num_q_heads / num_kv_heads;
-  const int64_t rows = g * (balanced ? balanced_slots(batch, num_kv_heads, ws_waves) : batch * num_kv_heads * splits);
-  a.ws_prefix = balanced ? static_cast<int32_t *>(workspace) : nullptr;
-  a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                     (balanced ? balanced_prefix_ints(batch) * sizeof(int32_t) : 0));
-  a.ws_ml = a.ws_o + rows * tt::workspace_head_dim(head_dim);
+  if (!segment) {
+    const int64_t rows = g * (balanced ? balanced_slots(batch, num_kv_heads, ws_waves) : batch * num_kv_heads * splits);
+    a.ws_prefix = balanced ? static_cast<int32_t *>(workspace) : nullptr;
+    a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                       (balanced ? balanced_prefix_ints(batch) * sizeof(int32_t) : 0));
+    a.ws_ml = a.ws_o + rows * tt::workspace_head_dim(head_dim);
+  }
   a.head_dim = (int)head_dim;
   a.inv_head_dim = 1.0 / (double)head_dim;
   a.seq_of_row = seq_of_row;
@@ -394,9 +406,12 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
                          int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
                          float *v_scale, const int64_t cache_strides[3], int64_t capacity, void *out,
                          const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                         int64_t head_dim, int64_t page_size, float sm_scale, void *workspace, size_t ws_bytes,
-                         tt_stream_t stream, bool exact_slots = false) {
+                         int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens, void *workspace,
+                         size_t ws_bytes, tt_stream_t stream, bool exact_slots = false) {
   TT_CHECK(q_in && k_in && v_in && rope_table && positions, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(split_tokens == 0 || split_tokens == tt::kSplitPerSegment, TT_ERR_INVALID_ARGUMENT,
+           "the fused decode step takes split_tokens 0 (balanced) or %d (per segment), got %lld",
+           tt::kSplitPerSegment, (long long)split_tokens);
   TT_CHECK(q_in_strides && k_in_strides && v_in_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
   TT_CHECK(splits >= 0 && (splits == 0 || split_stride > 0), TT_ERR_INVALID_ARGUMENT, "bad split-K partial layout");
   TT_CHECK(splits <= tt::kMaxApSplits, TT_ERR_UNSUPPORTED, "the fused step sums at most %d split-K partials, got %lld",
@@ -425,7 +440,8 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
   ap.page_size = page_size;
   return decode_common(kind, nullptr, nullptr, k_cache, v_cache, k_scale, v_scale, cache_strides, positions,
                        max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
-                       num_kv_heads, head_dim, page_size, sm_scale, 0, workspace, ws_bytes, stream, &ap, exact_slots);
+                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, ws_bytes, stream, &ap,
+                       exact_slots);
 }
 
 int linear_common(const void *x, int64_t ldx, const void *weight, int64_t ldw, int packed, float *partials,
@@ -796,6 +812,14 @@ int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_
   return tt::auto_split_tokens(batch, num_kv_heads, max_seq_len);
 }
 
+int64_t tt_decode_pick_split(int64_t batch, int64_t num_kv_heads, int64_t head_dim, int32_t fp8_cache,
+                             int32_t equal_lengths) {
+  if (!equal_lengths || batch <= 0 || num_kv_heads <= 0) return 0;
+  const int tile = tt::tile_head_dim(head_dim, fp8_cache ? tt::CacheKind::kFP8 : tt::CacheKind::kBF16);
+  if (tile == 0) return 0;
+  return (batch * num_kv_heads) % tt::segment_round(tile) == 0 ? tt::kSplitPerSegment : 0;
+}
+
 size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                                  int64_t max_seq_len, int64_t split_tokens) {
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
@@ -926,13 +950,13 @@ int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], 
                                const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *k_cache,
                                void *v_cache, const int64_t cache_strides[3], int64_t capacity, void *out,
                                const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                               int64_t head_dim, int64_t page_size, float sm_scale, void *workspace,
-                               size_t workspace_bytes, tt_stream_t stream) {
+                               int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
+                               void *workspace, size_t workspace_bytes, tt_stream_t stream) {
   return decode_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
                               splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
                               page_table, max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
-                              sm_scale, workspace, workspace_bytes, stream);
+                              sm_scale, split_tokens, workspace, workspace_bytes, stream);
 }
 
 int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
@@ -943,12 +967,13 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               void *v_cache, float *k_scale, float *v_scale, const int64_t cache_strides[3],
                               int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                              float sm_scale, void *workspace, size_t workspace_bytes, tt_stream_t stream) {
+                              float sm_scale, int64_t split_tokens, void *workspace, size_t workspace_bytes,
+                              tt_stream_t stream) {
   return decode_append_common(tt::CacheKind::kFP8, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
                               splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
                               page_table, max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
-                              sm_scale, workspace, workspace_bytes, stream);
+                              sm_scale, split_tokens, workspace, workspace_bytes, stream);
 }
 
 int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
@@ -967,7 +992,7 @@ int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_stri
                               splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
                               page_table, max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
-                              sm_scale, ws, kScratchBytes, stream, /*exact_slots=*/true);
+                              sm_scale, 0, ws, kScratchBytes, stream, /*exact_slots=*/true);
 }
 
 size_t tt_sample_workspace_bytes(int64_t m, int64_t vocab, int64_t top_k) {

@@ -417,7 +417,6 @@ __device__ __forceinline__ void merge_segment(const DecodeArgs &a, int b, int hk
   }
 }
 
-// Tiles [j0, j1) of segment (b, hk) (L tokens) by wave w: one partial to workspace slot (segment + w).
 // ---- fused RoPE + append (decode_stream_append_kernel) ----------------------
 
 // Element i of a q / k / v input row: the bf16 activation, or (kPartIn) the
@@ -604,11 +603,13 @@ __device__ __forceinline__ void piece_prologue(const DecodeArgs &a, const Decode
   __builtin_amdgcn_wave_barrier();
 }
 
+// Tiles [j0, j1) of segment (b, hk) (L tokens) by this wave: the online-softmax
+// state over them (unnormalised O, the heads' maxima, lane-partial sums) in st.
 template <int D, bool kFP8, bool kAppend, bool kPartIn, bool kPad>
 __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAppend *ap, int b, int hk, int L,
-                                             int j0, int j1, bool append, int64_t w, int lane, char *vlds,
-                                             uint16_t *qs, const bf16x8 (&ident16)[2],
-                                             const u32x2 (&ident8)[2]) {
+                                             int j0, int j1, bool append, int lane, char *vlds, uint16_t *qs,
+                                             const bf16x8 (&ident16)[2], const u32x2 (&ident8)[2],
+                                             WaveState<D, kFP8> &st) {
   using TR = KVTraits<kFP8>;
   constexpr int NDB = D / 32;
   const int G = a.group;
@@ -640,7 +641,6 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
       qf[s] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  WaveState<D, kFP8> st;
 #pragma unroll
   for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = kNegInf;
@@ -708,11 +708,19 @@ __device__ __forceinline__ void stream_piece(const DecodeArgs &a, const DecodeAp
     }
     __builtin_amdgcn_s_waitcnt(0);  // nothing of this chunk still in flight
   }
+}
 
+// A piece's state to workspace slot `slot` (the balanced partition's partials).
+template <int D, bool kFP8>
+__device__ __forceinline__ void store_piece(const DecodeArgs &a, const WaveState<D, kFP8> &st, int64_t slot,
+                                            int lane) {
+  constexpr int NDB = D / 32;
+  const int G = a.group;
+  const int n = lane & 15;
+  const int g = lane >> 4;
   float l = st.l;  // lane-partial sums -> the head's sum in all 4 lanes of the head
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
-  const int64_t slot = (int64_t)b * a.hkv + hk + w;
   if (n < G) {  // lane (n + 16g): head n, four consecutive head_dim entries per block (16-byte stores)
 #pragma unroll
     for (int c = 0; c < 2 * NDB; ++c)
@@ -796,8 +804,10 @@ __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeApp
       const int L = __builtin_amdgcn_readfirstlane(min(a.seq_lens[b] + a.len_add, a.max_len));
       // The segment's last tile holds this step's token: only this wave reads
       // it, so the fused variant appends it at the start of this piece.
-      stream_piece<D, kFP8, kAppend, kPartIn, kPad>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nbe - a.seg_cost, w,
-                                                    lane, vlds, qs, ident16, ident8);
+      WaveState<D, kFP8> st;
+      stream_piece<D, kFP8, kAppend, kPartIn, kPad>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nbe - a.seg_cost, lane,
+                                                    vlds, qs, ident16, ident8, st);
+      store_piece<D, kFP8>(a, st, (int64_t)b * a.hkv + hk + w, lane);
     }
     t = stop;
   }
@@ -814,6 +824,143 @@ __global__ __launch_bounds__(256, kStreamOcc) void decode_stream_kernel(DecodeAr
 template <int D, bool kFP8, bool kPartIn, bool kPad>
 __global__ __launch_bounds__(256, kStreamOcc) void decode_stream_append_kernel(DecodeAppendArgs a) {
   stream_body<D, kFP8, true, kPartIn, kPad>(a, &a.ap);
+}
+
+// LDS of the per-segment kernel: the streaming area (V slots, q staging of
+// the fused variant) and the merge area ([4][G][D] + 2 [4][16] floats), side
+// by side when that fits in 64 KB, else the merge area over the streaming one.
+__host__ __device__ constexpr int segment_stream_lds(int tile_d, bool fp8, bool fused) {
+  return kWavesPerBlock * 2 * (tile_d * (fp8 ? 1 : 2) / 64) * 1024 + (fused ? kWavesPerBlock * 16 * tile_d * 2 : 0);
+}
+__host__ __device__ constexpr int segment_merge_lds(int tile_d, int group) {
+  return (int)sizeof(float) * merge_floats(group, tile_d);
+}
+__host__ __device__ constexpr bool segment_merge_separate(int tile_d, bool fp8, bool fused, int group) {
+  return segment_stream_lds(tile_d, fp8, fused) + segment_merge_lds(tile_d, group) <= 65536;
+}
+
+// ---------------------------------------------------------------------------
+// Per-segment partition (split_tokens == kSplitPerSegment): one workgroup per
+// (sequence, KV head) segment, workgroup index = segment index, its 4 waves
+// taking the quarters of the segment's line as the balanced partition draws it
+// (start-up positions, then the tiles). The 4 wave states merge in LDS and the
+// workgroup writes the G
+// normalised output rows itself: no workspace and no merge launch. Correct for
+// any lengths; balanced when every sequence has the same length and B * H_kv
+// fills whole rounds of the resident workgroups (the uniform batches of the
+// reference's engine).
+// LDS: segment_stream_lds, then (segment_merge_separate) the merge area.
+template <int D, bool kFP8, bool kAppend, bool kPartIn, bool kPad>
+__device__ __forceinline__ void segment_body(const DecodeArgs &a, const DecodeAppend *ap) {
+  constexpr int kVAll = kWavesPerBlock * Tile<D, kFP8>::kVBytes;
+  constexpr int NDB = D / 32;
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  char *smem_v = reinterpret_cast<char *>(smem);
+  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
+  uint16_t *qs = nullptr;
+  if constexpr (kAppend) {
+    qs = reinterpret_cast<uint16_t *>(smem_v + kVAll) + wave * 16 * D;
+    if (blockIdx.x == 0 && ap->lens_out != nullptr)  // the next step's lengths
+      for (int i = threadIdx.x; i < a.batch; i += blockDim.x) ap->lens_out[i] = a.seq_lens[i] + 1;
+  }
+  __syncthreads();  // V slots zeroed
+
+  const int G = a.group;
+  const int b = (int)(blockIdx.x / (unsigned)a.hkv);
+  const int hk = (int)(blockIdx.x - (unsigned)b * (unsigned)a.hkv);
+  const int L = __builtin_amdgcn_readfirstlane(max(min(a.seq_lens[b] + a.len_add, a.max_len), 0));
+  const int nt = (L + kTileTokens - 1) / kTileTokens;
+  // The quarters of the balanced partition's line for one segment: its
+  // kStreamSegCost start-up positions, then the nt tiles. Against quarters of
+  // the tiles alone (wave q starting at tile q nt / 4, for C2 at multiples of
+  // 256 KB into the segment in every workgroup) the waves streamed ~5 % slower
+  // (C2 mean wave end 83-85 against 88-90 us, lab timestamps).
+  const int np = nt + kStreamSegCost;
+  const int j0 = max(wave * np / kWavesPerBlock - kStreamSegCost, 0);
+  const int j1 = max((wave + 1) * np / kWavesPerBlock - kStreamSegCost, 0);
+  WaveState<D, kFP8> st;
+  if (j1 > j0) {
+    bf16x8 ident16[2];
+    u32x2 ident8[2];
+    make_identity(lane, ident16, ident8);
+    // the wave holding the last tile appends this step's token (fused variant)
+    stream_piece<D, kFP8, kAppend, kPartIn, kPad>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nt, lane,
+                                                  smem_v + wave * Tile<D, kFP8>::kVBytes, qs, ident16, ident8, st);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = kNegInf;
+    st.l = 0.f;
+  }
+  // The merge area follows the streaming area when both fit in 64 KB, so a
+  // wave stores its state as soon as it is done; otherwise it reuses the
+  // streaming area once every wave is done with it.
+  float *so;  // [4][G][D] unnormalised outputs, then [4][16] maxima and [4][16] sums
+  if (segment_merge_separate(D, kFP8, kAppend, G)) {
+    so = reinterpret_cast<float *>(smem_v + segment_stream_lds(D, kFP8, kAppend));
+  } else {
+    __syncthreads();
+    so = smem;
+  }
+  float *sm = so + kWavesPerBlock * G * D;
+  float *sl = sm + kWavesPerBlock * 16;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  float l = st.l;  // lane-partial sums -> the head's sum in all 4 lanes of the head
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (g == 0) {
+    sm[wave * 16 + n] = st.m;
+    sl[wave * 16 + n] = l;
+  }
+  if (n < G) {  // lane (n + 16g): head n, four consecutive head_dim entries per block
+#pragma unroll
+    for (int c = 0; c < 2 * NDB; ++c)
+      *reinterpret_cast<f32x4 *>(so + (wave * G + n) * D + o_col_d<kFP8>(c, 4 * g)) = st.o[c];
+  }
+  __syncthreads();
+  // Thread t merges column pairs (2p, 2p + 1) of head p / (D / 2): one set of
+  // head weights per pair, and at G * D <= 512 a single pair per thread.
+  uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * G * a.o_sh;
+  for (int pr = threadIdx.x; pr < G * (D / 2); pr += blockDim.x) {
+    const int head = pr / (D / 2);
+    const int d = 2 * (pr - head * (D / 2));
+    if (d >= a.head_dim) continue;  // head_dim is even: d + 1 < head_dim too
+    float mw[kWavesPerBlock];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      mw[w] = sm[w * 16 + head];
+      M = fmaxf(M, mw[w]);
+    }
+    float acc0 = 0.f, acc1 = 0.f, lsum = 0.f;
+    if (M != kNegInf) {  // a sequence with nothing cached gives zeros
+#pragma unroll
+      for (int w = 0; w < kWavesPerBlock; ++w) {
+        const float e = __builtin_amdgcn_exp2f(mw[w] - M);
+        const float *row = so + (w * G + head) * D + d;
+        acc0 += e * row[0];
+        acc1 += e * row[1];
+        lsum += e * sl[w * 16 + head];
+      }
+    }
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    out[(int64_t)head * a.o_sh + d] = f32_to_bf16_bits(acc0 * inv);
+    out[(int64_t)head * a.o_sh + d + 1] = f32_to_bf16_bits(acc1 * inv);
+  }
+}
+
+template <int D, bool kFP8, bool kPad>
+__global__ __launch_bounds__(256, kStreamOcc) void decode_segment_kernel(DecodeArgs a) {
+  segment_body<D, kFP8, false, false, kPad>(a, nullptr);
+}
+
+template <int D, bool kFP8, bool kPartIn, bool kPad>
+__global__ __launch_bounds__(256, kStreamOcc) void decode_segment_append_kernel(DecodeAppendArgs a) {
+  segment_body<D, kFP8, true, kPartIn, kPad>(a, &a.ap);
 }
 
 // One wave per segment (b, KV head): merge its pieces into the G output rows
@@ -1072,6 +1219,28 @@ hipError_t launch_stream(const DecodeArgs &a0, const DecodeAppend *ap, hipStream
   return hipGetLastError();
 }
 
+template <int D, bool kFP8, bool kPad>
+hipError_t launch_segment(const DecodeArgs &a, const DecodeAppend *ap, hipStream_t stream) {
+  static_assert(Tile<D, kFP8>::kVBytes * kWavesPerBlock == segment_stream_lds(D, kFP8, false),
+                "segment_stream_lds assumes this");
+  const dim3 grid((unsigned)segment_grid(a.batch, a.hkv));
+  const size_t lds = segment_lds_bytes(D, kFP8, ap != nullptr, a.group);
+  if (ap != nullptr) {
+    DecodeAppendArgs f;
+    static_cast<DecodeArgs &>(f) = a;
+    f.ap = *ap;
+    if (ap->part_splits > 0)
+      hipLaunchKernelGGL((decode_segment_append_kernel<D, kFP8, true, kPad>), grid, dim3(64 * kWavesPerBlock), lds,
+                         stream, f);
+    else
+      hipLaunchKernelGGL((decode_segment_append_kernel<D, kFP8, false, kPad>), grid, dim3(64 * kWavesPerBlock), lds,
+                         stream, f);
+  } else {
+    hipLaunchKernelGGL((decode_segment_kernel<D, kFP8, kPad>), grid, dim3(64 * kWavesPerBlock), lds, stream, a);
+  }
+  return hipGetLastError();
+}
+
 // MFMA kernels on D-wide tiles (kPad: rows of a.head_dim < D).
 template <int D, bool kPad>
 hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
@@ -1080,12 +1249,14 @@ hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
   hipError_t err = hipSuccess;
   if (kind == CacheKind::kFP8) {
     if constexpr (D >= 64) {  // fp8 tiles are at least 64 wide (one 16-byte fragment per lane and row)
+      if (a.split_tokens == kSplitPerSegment) return launch_segment<D, true, kPad>(a, nullptr, stream);
       if (a.split_tokens == 0) return launch_stream<D, true, kPad>(a, nullptr, stream);
       err = launch_mfma<D, true, kPad>(a, block, lds, stream);
     } else {
       return hipErrorInvalidValue;
     }
   } else {
+    if (a.split_tokens == kSplitPerSegment) return launch_segment<D, false, kPad>(a, nullptr, stream);
     if (a.split_tokens == 0) return launch_stream<D, false, kPad>(a, nullptr, stream);
     err = launch_mfma<D, false, kPad>(a, block, lds, stream);
   }
@@ -1130,6 +1301,16 @@ int64_t balanced_stream_waves(int head_dim, int64_t batch, int64_t hkv, int64_t 
   return blocks * kWavesPerBlock;
 }
 
+int64_t segment_grid(int64_t batch, int64_t hkv) { return batch * hkv; }
+
+size_t segment_lds_bytes(int tile_d, bool fp8, bool fused, int64_t group) {
+  const int g = (int)group;
+  const int stream = segment_stream_lds(tile_d, fp8, fused), merge = segment_merge_lds(tile_d, g);
+  return (size_t)(segment_merge_separate(tile_d, fp8, fused, g) ? stream + merge : (stream > merge ? stream : merge));
+}
+
+int64_t segment_round(int tile_d) { return (int64_t)device_cu_count() * stream_blocks_per_cu(tile_d); }
+
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
   // Aim for >= 8 workgroups per CU (256 CUs) over the longest sequence while
   // keeping splits long enough that the partial write (G*(D+2) floats) stays
@@ -1154,6 +1335,17 @@ hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim,
 hipError_t launch_decode_attn_append(const DecodeAppendArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
   const int D = tile_head_dim(head_dim, kind);
   const bool pad = D != head_dim;
+  if (a.split_tokens == kSplitPerSegment) {
+    if (kind == CacheKind::kFP8) {
+      if (D == 64) return pad ? launch_segment<64, true, true>(a, &a.ap, stream) : launch_segment<64, true, false>(a, &a.ap, stream);
+      if (D == 128) return pad ? launch_segment<128, true, true>(a, &a.ap, stream) : launch_segment<128, true, false>(a, &a.ap, stream);
+      return hipErrorInvalidValue;
+    }
+    if (D == 32) return pad ? launch_segment<32, false, true>(a, &a.ap, stream) : launch_segment<32, false, false>(a, &a.ap, stream);
+    if (D == 64) return pad ? launch_segment<64, false, true>(a, &a.ap, stream) : launch_segment<64, false, false>(a, &a.ap, stream);
+    if (D == 128) return pad ? launch_segment<128, false, true>(a, &a.ap, stream) : launch_segment<128, false, false>(a, &a.ap, stream);
+    return hipErrorInvalidValue;
+  }
   if (kind == CacheKind::kFP8) {
     if (D == 64) return pad ? launch_stream<64, true, true>(a, &a.ap, stream) : launch_stream<64, true, false>(a, &a.ap, stream);
     if (D == 128) return pad ? launch_stream<128, true, true>(a, &a.ap, stream) : launch_stream<128, true, false>(a, &a.ap, stream);

@@ -235,6 +235,14 @@ int sample_cand_chunks(int64_t rows, int64_t vocab, int64_t top_k, bool logprobs
 
 // Partition helpers shared by the ABI layer and the launchers.
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len);
+// split_tokens value of the per-segment partition: one workgroup per (sequence,
+// KV head), merged in LDS, one launch, no workspace (MFMA kernels only).
+constexpr int kSplitPerSegment = -1;
+// Its grid, its dynamic LDS bytes, and the resident workgroups of one round on
+// the current device (CUs x workgroups per CU at this tile width).
+int64_t segment_grid(int64_t batch, int64_t hkv);
+size_t segment_lds_bytes(int tile_d, bool fp8, bool fused, int64_t group);
+int64_t segment_round(int tile_d);
 // Waves of the balanced stream kernel's grid on the current device (at most
 // kMaxStreamWaves); the partial slots it writes are b * H_kv + hk + wave.
 int64_t balanced_stream_waves(int head_dim, int64_t batch, int64_t hkv, int64_t max_len);

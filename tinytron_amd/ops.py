@@ -291,6 +291,24 @@ def split_tokens_for(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
     return int(_lib.load().tt_decode_split_tokens(batch, num_kv_heads, max_seq_len))
 
 
+# split_tokens of the per-segment partition: one workgroup per (sequence, KV
+# head), merged inside the launch (no merge launch, no workspace)
+SPLIT_PER_SEGMENT = -1
+
+
+def pick_split(seq_lens_host, num_kv_heads: int, head_dim: int, kind: str) -> int:
+    """split_tokens for decode attention over these host-side lengths:
+    SPLIT_PER_SEGMENT when they are all equal and B * H_kv fills whole rounds
+    of the GPU's resident workgroups (tt_decode_pick_split), else 0 (the
+    balanced partition)."""
+    if kind not in ("bf16", "fp8") or len(seq_lens_host) == 0:
+        return 0
+    first = seq_lens_host[0]
+    equal = all(x == first for x in seq_lens_host)
+    return int(_lib.load().tt_decode_pick_split(len(seq_lens_host), num_kv_heads, head_dim, int(kind == "fp8"),
+                                                int(equal)))
+
+
 def workspace_bytes(batch: int, hq: int, hkv: int, head_dim: int, max_seq_len: int, split_tokens: int = 0) -> int:
     return int(_lib.load().tt_decode_workspace_bytes(batch, hq, hkv, head_dim, max_seq_len, split_tokens))
 
@@ -435,7 +453,7 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
                             partials: torch.Tensor | None = None, num_q_heads: int | None = None,
                             lens_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
                             sm_scale: float | None = None, workspace: Workspace | None = None,
-                            no_alloc: bool = False) -> torch.Tensor:
+                            no_alloc: bool = False, split_tokens: int = 0) -> torch.Tensor:
     """One decode step in one launch pair: RoPE of this step's q and k at
     positions[b], append of k / v at that slot, and GQA attention over the
     positions[b] + 1 cached tokens (rope_append followed by decode_attention,
@@ -446,8 +464,12 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
     [B, H_q, D] bf16. ``no_alloc`` (bf16 caches) runs the allocation-free
     entry point, whose workspace is the library's per-GPU scratch
     (``workspace`` is then unused; pass ``out`` to allocate nothing at all;
-    calls that overlap on one GPU race on that scratch)."""
+    calls that overlap on one GPU race on that scratch). ``split_tokens``: 0
+    (balanced partition) or SPLIT_PER_SEGMENT (no workspace; not with
+    ``no_alloc``)."""
     _require_cuda(table, positions, layout.k, layout.v)
+    if split_tokens not in (0, SPLIT_PER_SEGMENT):
+        raise ValueError(f"the fused decode step takes split_tokens 0 or {SPLIT_PER_SEGMENT}, got {split_tokens}")
     if layout.kind not in ("bf16", "fp8"):
         raise ValueError("the fused decode step takes a bf16 or fp8 cache")
     Hkv, D = layout.num_heads, layout.head_dim
@@ -498,12 +520,18 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
     if no_alloc:  # the library's own per-GPU scratch: nothing is allocated (HIP graph capture, serving loops)
         if layout.kind != "bf16":
             raise ValueError("the allocation-free decode step takes a bf16 cache")
+        if split_tokens != 0:
+            raise ValueError("the allocation-free decode step runs the balanced partition (split_tokens 0)")
         st = lib.tt_decode_attn_append_bf16_noalloc(*head, *tail, _stream(dev))
         _lib.check(st, "decode_attention_append (no allocation)")
         return out
-    need = workspace_bytes(B, Hq, Hkv, D, max_seq_len, 0)
-    ws = (workspace or Workspace(dev)).get(need)
-    tail += [_ptr(ws), ws.numel(), _stream(dev)]
+    tail.append(int(split_tokens))
+    if split_tokens == SPLIT_PER_SEGMENT:  # merged inside the launch: no workspace
+        tail += [None, 0, _stream(dev)]
+    else:
+        need = workspace_bytes(B, Hq, Hkv, D, max_seq_len, 0)
+        ws = (workspace or Workspace(dev)).get(need)
+        tail += [_ptr(ws), ws.numel(), _stream(dev)]
     if layout.kind == "fp8":
         st = lib.tt_decode_attn_append_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
     else:
