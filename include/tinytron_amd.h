@@ -522,7 +522,7 @@ int tt_silu_mul_bf16(const float *partials, int64_t splits, int64_t m, int64_t i
  * (as tt_linear_splitk_packed_bf16) matrix of 2I rows interleaved by 8:
  * rows 16j .. 16j+7 are gate rows 8j .. 8j+7, rows 16j+8 .. 16j+15 up rows
  * 8j .. 8j+7. x bf16 [M, K] (row stride ldx), y bf16 [M, I] (row stride
- * ldy). Requirements: K 1024 or 2048, I a multiple of 16 or 24 (tt_swiglu_gemm_supported),
+ * ldy). Requirements: K 768, 1024 or 2048, I a multiple of 16 or 24 (tt_swiglu_gemm_supported),
  * ldx % 8 == 0, ldy % 4 == 0, 16-byte aligned x and weight, 8-byte aligned y.
  * (Replaces the gate|up tt_linear_splitk_packed_bf16 + tt_silu_mul_bf16 pair;
  * the interleaved layout is this library's, no counterpart in the reference.)

@@ -130,7 +130,8 @@ def _swiglu_ref(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
 
 @pytest.mark.parametrize("M,I,K", [(1, 24, 2048), (7, 6144, 2048), (64, 6144, 2048), (100, 240, 2048),
                                    (130, 6144, 2048), (1, 24, 1024), (64, 4096, 1024), (70, 240, 1024),
-                                   (64, 8192, 2048), (33, 16, 1024), (64, 3072, 1024)])
+                                   (64, 8192, 2048), (33, 16, 1024), (64, 3072, 1024), (1, 24, 768),
+                                   (64, 3072, 768), (45, 240, 768)])
 def test_linear_swiglu(M, I, K):
     """Gate|up + SwiGLU in one launch (whole-K fp32 sums, interleaved packed
     weight) against the fp64 sums taken through the same bf16 chain. The
@@ -168,7 +169,7 @@ def test_linear_swiglu(M, I, K):
     assert torch.all(err <= tol + 1e-30), float((err / (tol + 1e-30)).max())
     assert float((got.view(torch.int16) == ref.view(torch.int16)).float().mean()) >= 0.95
     if (2 * I) % 64 == 0:  # the same projection through split-K partials + silu_mul
-        P = ops.linear_partials(x, ops.PackedWeight(torch.cat([wg, wu]).to(DEV)), k_chunk=512)
+        P = ops.linear_partials(x, ops.PackedWeight(torch.cat([wg, wu]).to(DEV)), k_chunk=512 if K % 512 == 0 else 256)
         old = ops.silu_mul(P).cpu()
         assert float((old.view(torch.int16) == got.view(torch.int16)).float().mean()) >= 0.95
         assert torch.all((old.double() - ref.double()).abs() <= tol + 1e-30)
@@ -177,13 +178,14 @@ def test_linear_swiglu(M, I, K):
 def test_linear_swiglu_rejects_unsupported():
     from tinytron_amd import ops
 
-    assert ops.swiglu_supported(2048, 6144) and ops.swiglu_supported(1024, 4096)
+    assert ops.swiglu_supported(2048, 6144) and ops.swiglu_supported(1024, 4096) and ops.swiglu_supported(768, 3072)
     assert not ops.swiglu_supported(3072, 6144) and not ops.swiglu_supported(4096, 6144)
+    assert not ops.swiglu_supported(1536, 6144) and not ops.swiglu_supported(512, 2048)
     assert not ops.swiglu_supported(2048, 100)
     x = torch.zeros(4, 3072, dtype=torch.bfloat16, device=DEV)
     w = ops.PackedWeight(torch.zeros(48, 3072, dtype=torch.bfloat16, device=DEV))
     with pytest.raises(ValueError):
-        ops.linear_swiglu(x, w)  # K must be 1024 or 2048
+        ops.linear_swiglu(x, w)  # K must be 768, 1024 or 2048
     x = torch.zeros(4, 2048, dtype=torch.bfloat16, device=DEV)
     w = ops.PackedWeight(torch.zeros(16, 2048, dtype=torch.bfloat16, device=DEV))
     with pytest.raises(ValueError):

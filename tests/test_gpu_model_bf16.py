@@ -203,9 +203,11 @@ def test_one_layer_fused_path_matches_reference_autocast(shape):
     SwiGLU) against the oracle, per sequence of a ragged batch, at d 1024
     (16/4 heads, D 64) and at the reference presets' layer shapes
     (scripts/debug/inference.sh:71-77, 52-57, 101-107): 0.1B d 768 (16/4
-    heads, D 48, ffn 3072), 0.25B d 1024 (32/4 heads, D 32, ffn 4096: gate|up
-    + SwiGLU in one K = 1024 launch), 13B d 5120 (40/8 heads: G 5, D 128,
-    ffn 13824). The fused decode step runs every step (asserted)."""
+    heads, D 48, ffn 3072: gate|up + SwiGLU in one K = 768 launch), 0.25B
+    d 1024 (32/4 heads, D 32, ffn 4096: one K = 1024 launch), 13B d 5120
+    (40/8 heads: G 5, D 128, ffn 13824: split-K gate|up and silu_mul). The
+    fused decode step runs every step (asserted), with the one-launch SwiGLU
+    wherever the kernel takes the shape (asserted)."""
     from tinytron_amd.model import GPT
 
     dims = {"d1024": (1024, 16, 4, 2048), "preset_0.1b": (768, 16, 4, 3072), "preset_0.25b": (1024, 32, 4, 4096),
@@ -213,6 +215,7 @@ def test_one_layer_fused_path_matches_reference_autocast(shape):
     cfg = _config(num_layer=1, hidden_size=dims[0], num_attention_heads=dims[1], num_key_value_heads=dims[2],
                   intermediate_size=dims[3], vocab_size=8192, block_size=256)
     model = GPT(cfg, device=DEV, dtype=BF16)
+    assert model._swiglu_fused() == (shape != "preset_13b")
     calls = []
     fused = model._decode_step_fused
     model._decode_step_fused = lambda *a, **k: (calls.append(1), fused(*a, **k))[1]

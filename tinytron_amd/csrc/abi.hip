@@ -890,7 +890,7 @@ int tt_linear_swiglu_packed_bf16(const void *x, int64_t ldx, const void *weight_
   TT_CHECK(x && weight_packed && y, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK(m >= 0 && m <= 65535 * 64 && inter > 0 && k > 0, TT_ERR_INVALID_ARGUMENT, "bad GEMM shape");
   TT_CHECK(tt::swiglu_gemm_supported(k, inter), TT_ERR_UNSUPPORTED,
-           "the fused gate|up + SwiGLU GEMM takes K 1024 or 2048 and I a multiple of 16 or 24 (K %lld, I %lld)", (long long)k,
+           "the fused gate|up + SwiGLU GEMM takes K 768, 1024 or 2048 and I a multiple of 16 or 24 (K %lld, I %lld)", (long long)k,
            (long long)inter);
   TT_CHECK(inter < ((int64_t)1 << 30), TT_ERR_UNSUPPORTED, "intermediate size too large");
   TT_CHECK(ldx >= k && ldx % 8 == 0 && ldy >= inter && ldy % 4 == 0, TT_ERR_INVALID_ARGUMENT,

@@ -285,17 +285,20 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, in
 // with the up lanes and write 4 bf16 outputs each.
 // K = 1024 R (R = 1, 2): R staging rounds, each one 512-column (1 KiB) row
 // chunk per half, so the LDS holds one round (133 KB, one workgroup per CU)
-// whatever K. NB = 2, 3 or 4 row blocks per workgroup (the launcher picks one
+// whatever K. K = 768: one round of 384 columns per half, staged by the same
+// 1 KiB row chunks (the 128 columns past a half are loaded and not used; past
+// the last row's end the buffer bound reads zero). NB = 2, 3 or 4 row blocks
+// per workgroup (the launcher picks one
 // that divides I / 8: 3 where it can, the measured layout).
 // (Register budget: two workgroups' worth per CU, as measured for NB = 3;
 // NB = 4 with 128 weight registers per lane fits one.)
 template <int K, int NB>
 __global__ __launch_bounds__(64 * 2 * NB, NB == 4 ? 1 : 2) void swiglu_gemm_kernel(SwigluGemmArgs a) {
-  constexpr int R = K / 1024;          // staging rounds
+  constexpr int R = (K + 1023) / 1024; // staging rounds
   constexpr int KS = K / 64;           // k steps per wave (its half of K)
-  constexpr int KQ = K / (2 * R);      // columns per half per round (512)
-  constexpr int ROW = KQ + 8;          // padded LDS row (elements)
-  static_assert(K % 1024 == 0 && KQ == 512 && KS <= 32, "K = 1024 or 2048");
+  constexpr int KQ = K / (2 * R);      // columns per half per round (512; 384 at K = 768)
+  constexpr int ROW = 512 + 8;         // padded LDS row (elements): one 1 KiB DMA chunk
+  static_assert((K == 768 || K == 1024 || K == 2048) && KQ <= 512 && KS <= 32, "K = 768, 1024 or 2048");
   constexpr int kWaves = 2 * NB;
   constexpr int kRows = 2 * 64;        // LDS rows per round: 2 halves x 64 x rows
   __shared__ __attribute__((aligned(16))) uint16_t xs[kRows * ROW];
@@ -538,7 +541,7 @@ hipError_t launch_add_rmsnorm(float *x, const float *P, int S, int M, int C, con
 }
 
 bool swiglu_gemm_supported(int64_t K, int64_t I) {
-  return (K == 1024 || K == 2048) && I > 0 && (I % 24 == 0 || I % 16 == 0);
+  return (K == 768 || K == 1024 || K == 2048) && I > 0 && (I % 24 == 0 || I % 16 == 0);
 }
 
 // Row blocks per workgroup for intermediate size I: 3 (the measured layout)
@@ -563,6 +566,7 @@ hipError_t launch_swiglu_k(const SwigluGemmArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_swiglu_gemm(const SwigluGemmArgs &a, hipStream_t stream) {
+  if (a.K == 768) return launch_swiglu_k<768>(a, stream);
   if (a.K == 1024) return launch_swiglu_k<1024>(a, stream);
   if (a.K == 2048) return launch_swiglu_k<2048>(a, stream);
   return hipErrorInvalidValue;
