@@ -302,12 +302,20 @@ def c1_record(args, torch):
     eng.generate(prompt, 4, top_k=1)
     torch.cuda.synchronize()
     tokens, stats = eng.generate(prompt, C1["steps"], top_k=1, return_stats=True)
+    # use_paged_kv_cache=False: the reference's per-layer (k, v) tuples grown by concatenation
+    eng_t = InferenceEngine(cfg, device="cuda", dtype=torch.float32, use_paged_kv_cache=False, model=model)
+    eng_t.generate(prompt, 4, top_k=1)
+    torch.cuda.synchronize()
+    tokens_t, stats_t = eng_t.generate(prompt, C1["steps"], top_k=1, return_stats=True)
     out = {"workload": "C1: 6 L, d 512, 8/2 heads, D 64, V 32000, fp32 weights ~N(0, 0.02) seed 1337, batch 1, "
                        "prompt 128, 64 greedy steps, contiguous KV cache",
            "decode_tokens_per_sec": round(stats["decode_tokens_per_sec"], 1),
+           "decode_tokens_per_sec_tuple_cache": round(stats_t["decode_tokens_per_sec"], 1),
+           "tuple_cache_tokens_equal": bool(torch.equal(tokens.cpu(), tokens_t.cpu())),
            "decode_path": "module path in fp32 (d 512 takes no fused kernels): RoPE + append + attention in one "
-                          "launch pair per layer, graph-replayed steps"}
-    del eng, model
+                          "launch pair per layer, graph-replayed steps; decode_tokens_per_sec_tuple_cache: "
+                          "use_paged_kv_cache=False (the tuple-concat cache held in a growing store, eager steps)"}
+    del eng, eng_t, model
     tokens = tokens.cpu()
 
     def cpu_job():
