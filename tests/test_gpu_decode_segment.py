@@ -14,7 +14,8 @@ its 4 waves on equal quarters of the tiles, merged in LDS, one launch).
 * The KV cache picks the partition from its host lengths: equal lengths with
   B * H_kv a multiple of the resident round (tt_decode_pick_split), else the
   balanced one; a model's decode steps agree with the balanced partition's to
-  a few bf16 ulps of each row's largest logit.
+  a few bf16 ulps of each row's largest logit; the engine's graph-replayed
+  steps in this partition equal its eager steps bit for bit.
 """
 import numpy as np
 import pytest
@@ -141,3 +142,37 @@ def test_cache_picks_the_partition_and_matches_balanced():
             lb, bal = model(tok, past_key_values=bal, use_cache=True, position_offset=24 + step)
             assert _ulps_of_row_max(ls.float().cpu(), lb.float().cpu()) <= 4, f"step {step}"
             tok = ls[:, -1].argmax(-1, keepdim=True)
+
+
+@pytest.mark.parametrize("kv_dtype", [None, "fp8"])
+def test_engine_uniform_batch_segment_graphs_equal_eager(kv_dtype):
+    """The reference's own kind of batch (every prompt the same length) with
+    B * H_kv filling one round of the GPU: the engine's caches pick the
+    per-segment partition (asserted through the pick), and decode steps
+    replayed from the captured graphs give the eager steps' tokens and
+    log-probabilities bit for bit (the partition's agreement with the balanced
+    one is checked on teacher-forced logits above, where greedy near-ties of a
+    random-init model cannot move the comparison)."""
+    from tinytron_amd import ops
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+    from tests.test_gpu_engine import _c1_config
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Hkv = 8
+    B = 2 * cus // Hkv
+    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=Hkv,
+                     vocab_size=4096, block_size=160)
+    model = GPT(cfg, device="cuda", dtype=torch.bfloat16)
+    kvd = torch.float8_e4m3fn if kv_dtype == "fp8" else None
+    kind = "fp8" if kv_dtype else "bf16"
+    assert ops.pick_split([48] * B, Hkv, 64, kind) == SEG
+    prompt = torch.randint(0, cfg.vocab_size, (B, 48), generator=torch.Generator().manual_seed(17))
+    runs = {}
+    for name, use_graphs in (("eager", False), ("graphs", True)):
+        eng = InferenceEngine(cfg, device="cuda", dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True,
+                              kv_cache_dtype=kvd, model=model, use_graphs=use_graphs)
+        toks, extra = eng.generate(prompt, 24, top_k=1, return_stats=True, return_logprobs=True)
+        runs[name] = (toks.cpu(), extra["token_log_probs"].float().cpu())
+    assert torch.equal(runs["eager"][0], runs["graphs"][0])
+    assert torch.equal(runs["eager"][1], runs["graphs"][1])
