@@ -149,6 +149,10 @@ def e2e_c5(args, torch):
                 raise RuntimeError("graph-replayed and eager decodes diverged")
             forced["graphs" if mode else "eager"] = round(s_m["decode_tokens_per_sec"], 1)
         eng.use_graphs = None
+    # the reference's kind of batch: every prompt of the ragged batch's mean length (the caches then
+    # pick the per-segment attention partition, one launch per layer's attention)
+    uni_len = int(round(sum(lens) / B))
+    _, uni_stats = eng.generate(prompt[:, :uni_len], steps, top_k=1, return_stats=True)
     # the same decode with an fp8-e4m3 KV cache (per-(token, head) scales; the
     # decode step is RoPE + append from the q|k|v partials, then the attention
     # pair, replayed from HIP graphs)
@@ -176,6 +180,9 @@ def e2e_c5(args, torch):
                        "than 0.9x its GPU time, else HIP-graph replay with the two captures inside the timed "
                        "window); decode_tokens_per_sec_eager / _graphs force each mode (same tokens, checked)",
         "decode_steps": int(stats["decode_tokens"] // B),
+        "decode_tokens_per_sec_uniform_prompts": round(uni_stats["decode_tokens_per_sec"], 1),
+        "uniform_prompts": f"all {B} prompts of {uni_len} tokens (the ragged batch's mean; the reference's engine "
+                           "takes one prompt length): the attention takes the per-segment partition, one launch",
         "decode_tokens_per_sec_fp8_kv": round(fp8_stats["decode_tokens_per_sec"], 1),
         "fp8_kv_first_token_agreement": round(float((gen8[:, 0] == gen[:, 0]).float().mean()), 4),
         "prefill_tokens_per_sec_fp8_kv": round(fp8_stats["prefill_tokens_per_sec"], 1),
