@@ -61,7 +61,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--step-path", choices=["auto", "fused", "two"], default="auto",
                    help="decode step as one launch pair (RoPE + append inside the attention kernel) or as the "
-                        "RoPE + append kernel then attention; auto: fused for bf16 caches, two launches for fp8")
+                        "RoPE + append kernel then attention; auto: fused")
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     p.add_argument("--nested", default="c2,c4,c5a",
                    help="comma-separated configs measured after the headline one and reported in nested records "
@@ -153,9 +153,8 @@ def e2e_c5(args, torch):
     # pick the per-segment attention partition, one launch per layer's attention)
     uni_len = int(round(sum(lens) / B))
     _, uni_stats = eng.generate(prompt[:, :uni_len], steps, top_k=1, return_stats=True)
-    # the same decode with an fp8-e4m3 KV cache (per-(token, head) scales; the
-    # decode step is RoPE + append from the q|k|v partials, then the attention
-    # pair, replayed from HIP graphs)
+    # the same decode with an fp8-e4m3 KV cache (per-(token, head) scales, written by the
+    # fused step's append; the same launches per layer as bf16)
     fp8_eng = InferenceEngine(cfg, device="cuda", dtype=torch.bfloat16, kv_cache_page_size=C5["page"], paged_pool=True,
                               kv_cache_dtype=torch.float8_e4m3fn, model=model)
     fp8_tokens, fp8_stats = fp8_eng.generate(prompt, steps, top_k=1, prompt_lens=lens, return_stats=True)
@@ -599,8 +598,8 @@ def spread(st):
 
 
 def run_config(name, args, torch, ops):
-    """Time one attention config on the GPU: the decode step (fused launch pair
-    for bf16 caches, RoPE + append then attention for fp8), the two-launch step,
+    """Time one attention config on the GPU: the decode step (RoPE + append
+    inside the attention launch(es), bf16 and fp8 caches), the two-launch step,
     and the attention operator alone, each over args.steps steps (a window of
     back-to-back steps between two HIP events on the stream the kernels run on,
     then a pass with per-step events for the spread) after a warm-up of at
@@ -619,7 +618,7 @@ def run_config(name, args, torch, ops):
         ops.pick_split(wl["total"].tolist(), cfg["hkv"], D, "fp8" if cfg["fp8"] else "bf16")
     per_segment = split == ops.SPLIT_PER_SEGMENT
     lens_out = torch.empty_like(wl["positions"])
-    fused = args.step_path == "fused" or (args.step_path == "auto" and not cfg["fp8"])
+    fused = args.step_path != "two"
 
     def two_launch_step():
         ops.rope_append(wl["q_in"], wl["k_in"], wl["v_in"], wl["rope"], wl["positions"], layout, q_out=q_rot)

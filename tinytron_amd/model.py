@@ -15,8 +15,7 @@ autocast produces from fp32 weights.
 ``Attention.forward`` is the drop-in of attn.py:378-440: with one of this
 package's caches, a decode step (T = 1) is one split-K GQA attention launch
 pair that also applies RoPE to the step's token and appends it to the cache
-(fp8 and fp32 caches: a RoPE + append kernel, then the attention kernels;
-the fused pair measured slower than the two launches on fp8); prefill
+(fp32 caches: a RoPE + append kernel, then the attention kernels); prefill
 (T > 1) writes the cache with the RoPE + append kernel and attends with the
 prefill kernel (bf16 activations; SDPA per sequence for fp32). No CPU
 fallback.
@@ -27,7 +26,7 @@ split-K GEMM for the stacked q|k|v projection, the attention launch pair
 (which sums those partials, applies RoPE and appends k / v itself), the
 c_proj GEMM, residual add + RMSNorm in one kernel, one GEMM for the stacked
 gate|up projection, SwiGLU, the down GEMM, and the next residual add +
-RMSNorm -- 9 launches instead of about 30 (10 with an fp8 cache), with the
+RMSNorm -- 9 launches instead of about 30 (bf16 and fp8 caches), with the
 same math and bf16 rounding points as the module path. A bf16 prefill with
 ``logits_index`` (the engine's) runs on the packed prompt tokens
 (``GPT.fused_prefill``): the projections, residual add + RMSNorm and SwiGLU
@@ -127,8 +126,8 @@ class Attention(nn.Module):
         if len(set(lens)) == 1 and lens[0] != position_offset:
             raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
         table = rope_table_for(past_kv.max_seq_len + T, self.head_dim, self.config.rope_theta, act, x.device)
-        if T == 1 and act == torch.bfloat16 and past_kv.layout.kind == "bf16" \
-                and ops.attention_tile_dim(self.head_dim, "bf16"):
+        if T == 1 and act == torch.bfloat16 and past_kv.layout.kind in ("bf16", "fp8") \
+                and ops.attention_tile_dim(self.head_dim, past_kv.layout.kind):
             y = past_kv.decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], table)  # RoPE + append + attention
             y = y.view(B, 1, C)
         elif T == 1:
@@ -382,8 +381,8 @@ class GPT(nn.Module):
             layer = cache.get_layer_cache(i)
             wqkv, wo, wgu, wd = self._stacked_weights(i)
             P = ops.linear_partials(h, wqkv, partials=pbuf, k_chunk=kc_c)
-            if P.shape[0] <= ops.FUSED_STEP_MAX_SPLITS and layer.layout.kind == "bf16" \
-                    and ops.attention_tile_dim(D, "bf16"):
+            if P.shape[0] <= ops.FUSED_STEP_MAX_SPLITS and layer.layout.kind in ("bf16", "fp8") \
+                    and ops.attention_tile_dim(D, layer.layout.kind):
                 y = layer.decode_step_partials(P, Hq, table)        # RoPE + append + attention, [B, Hq, D]
             else:
                 q_rot = layer.rope_append_partials(P, Hq, table)     # sums the q|k|v partials itself
