@@ -120,6 +120,7 @@ def e2e_c5(args, torch):
     """Greedy decode through the engine (config C5: 24 layers, d 2048, batch 64), tokens/s as
     engine.py:236-243 defines it, plus the reference op sequence on the host
     for a bounded sample of the same batch."""
+    from tinytron_amd import ops
     from tinytron_amd.engine import InferenceEngine
     from tinytron_amd.model import GPT, ModelConfig
 
@@ -178,6 +179,10 @@ def e2e_c5(args, torch):
                        "default picks on the second step (decode_launch: eager when the host issues a step in less "
                        "than 0.9x its GPU time, else HIP-graph replay with the two captures inside the timed "
                        "window); decode_tokens_per_sec_eager / _graphs force each mode (same tokens, checked)",
+        "attention_partition": {ops.SPLIT_PER_SEGMENT: "per segment", ops.SPLIT_PAIRED: "paired (rank pairs)",
+                                0: "balanced"}[ops.pick_split(lens, C5["num_key_value_heads"],
+                                                              C5["hidden_size"] // C5["num_attention_heads"],
+                                                              "bf16")],
         "decode_steps": int(stats["decode_tokens"] // B),
         "decode_tokens_per_sec_uniform_prompts": round(uni_stats["decode_tokens_per_sec"], 1),
         "uniform_prompts": f"all {B} prompts of {uni_len} tokens (the ragged batch's mean; the reference's engine "
@@ -613,10 +618,12 @@ def run_config(name, args, torch, ops):
     out = torch.empty(B, hq, D, dtype=torch.bfloat16, device="cuda")
     ws = ops.Workspace("cuda")
     # the partition the KV cache picks for these lengths (LayerPagedKVCache._attention_split): one
-    # workgroup per (sequence, KV head) when all lengths are equal and B * H_kv fills the GPU
+    # workgroup per (sequence, KV head) when all lengths are equal and B * H_kv fills the GPU, one per
+    # (rank pair, KV head) for a ragged batch whose pairs fill the CUs evenly, else the balanced one
     split = args.split_tokens if args.split_tokens is not None else \
         ops.pick_split(wl["total"].tolist(), cfg["hkv"], D, "fp8" if cfg["fp8"] else "bf16")
     per_segment = split == ops.SPLIT_PER_SEGMENT
+    paired = split == ops.SPLIT_PAIRED
     lens_out = torch.empty_like(wl["positions"])
     fused = args.step_path != "two"
 
@@ -663,10 +670,15 @@ def run_config(name, args, torch, ops):
             "context": [cfg["lo"], cfg["hi"]], "page_size": cfg["page"], "paged": cfg["paged"],
             "cached_tokens": tokens,
             "split_tokens": ("per segment (-1: one workgroup per (sequence, KV head), merged in LDS; all lengths "
-                             "equal)" if per_segment else split or "balanced (equal 32-token tiles per wave)"),
+                             "equal)" if per_segment
+                             else "paired (-2: the sequences ranked by length, one workgroup per KV head and rank "
+                             "pair (p, B - 1 - p), merged in LDS)" if paired
+                             else split or "balanced (equal 32-token tiles per wave)"),
             "parallelism": "single GPU",
             "step_path": ("one launch: RoPE + append inside the per-segment attention kernel "
                           "(decode_segment_append_kernel)" if fused and per_segment
+                          else "one launch: RoPE + append inside the paired attention kernel "
+                          "(decode_paired_append_kernel)" if fused and paired
                           else "one launch pair: RoPE + append inside the attention split kernel "
                           "(decode_stream_append_kernel + decode_merge_kernel)" if fused and not split
                           else "rope_append_kernel, then the attention kernels"),
@@ -674,6 +686,7 @@ def run_config(name, args, torch, ops):
         "roofline": {
             "bound": "hbm",
             "kernel": ("decode attention (decode_segment_kernel)" if per_segment
+                       else "decode attention (decode_paired_kernel)" if paired
                        else "decode attention (decode_stream_kernel + decode_merge_kernel)" if not split
                        else "decode attention (decode_split_kernel + decode_combine_kernel)"),
             "achieved": round(achieved, 2),

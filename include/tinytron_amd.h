@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 4
+#define TT_ABI_VERSION 5
 
 #define TT_OK 0
 #define TT_ERR_INVALID_ARGUMENT (-1)
@@ -61,6 +61,10 @@ extern "C" {
 /* split_tokens of the decode attention entry points: one workgroup per
  * (sequence, KV head), merged inside the launch. */
 #define TT_SPLIT_PER_SEGMENT (-1)
+/* split_tokens of the decode attention entry points: the sequences ranked by
+ * length, one workgroup per (rank pair (p, batch - 1 - p), KV head), merged
+ * inside the launch; batch <= 256. */
+#define TT_SPLIT_PAIRED (-2)
 
 /* A hipStream_t, kept opaque so that the header needs no HIP include. */
 typedef void *tt_stream_t;
@@ -235,13 +239,22 @@ int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3]
  *   its 4 waves taking equal quarters of the pair's tiles and merging in LDS:
  *   one launch, no workspace; correct for any lengths, balanced when every
  *   sequence has the same length and batch * num_kv_heads fills whole rounds
- *   of the GPU (tt_decode_pick_split says when); the VALU kernel (fp32
- *   caches, head dims the MFMA tiles do not take) treats it as 0;
+ *   of the GPU (tt_decode_pick_split says when);
+ *   TT_SPLIT_PAIRED (-2) = the sequences ranked by length (longest first,
+ *   ties by index), one workgroup per KV head and rank pair (p,
+ *   batch - 1 - p) (the middle rank of an odd batch alone), its waves taking
+ *   equal shares of the two segments' tiles and merging in LDS: one launch,
+ *   no workspace, batch <= 256; correct for any lengths, balanced when the
+ *   pairs' lengths add up to about the same total and (batch + 1) / 2 *
+ *   num_kv_heads fills whole rounds of the GPU (tt_decode_pick_split says
+ *   when); the VALU kernel (fp32 caches, head dims the MFMA tiles do not
+ *   take) treats -1 and -2 as 0;
  *   128, 256, 512 or 1024 = fixed splits of that many tokens.
  * workspace: device scratch of at least tt_decode_workspace_bytes(...) bytes
  *   for the same (batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
  *   split_tokens); its contents need no initialisation. May be NULL when the
- *   call needs none (TT_SPLIT_PER_SEGMENT on the MFMA kernels).
+ *   call needs none (TT_SPLIT_PER_SEGMENT and TT_SPLIT_PAIRED on the MFMA
+ *   kernels).
  * Requirements: head_dim even and <= 128 (a multiple of 8 for a bf16 cache
  *   or 16 for an fp8 cache runs the MFMA kernels, other head dims and fp32
  *   caches the VALU kernel); H_q % H_kv == 0 and
@@ -352,9 +365,10 @@ int tt_prefill_attn_fp8(const void *q, const int64_t q_strides[3],
  * the splits in order. The wave that reads a segment's last tile writes that
  * segment's new k / v first, so no other launch is needed. max_seq_len must
  * bound positions[b] + 1 and the cache capacity. split_tokens: 0 (balanced
- * partition) or TT_SPLIT_PER_SEGMENT, as for tt_gqa_decode_attn_bf16 (bf16 /
- * fp8 caches); workspace as tt_decode_workspace_bytes(..., split_tokens)
- * (NULL for TT_SPLIT_PER_SEGMENT).
+ * partition), TT_SPLIT_PER_SEGMENT or TT_SPLIT_PAIRED, as for
+ * tt_gqa_decode_attn_bf16 (bf16 / fp8 caches); workspace as
+ * tt_decode_workspace_bytes(..., split_tokens) (NULL for the two one-launch
+ * partitions).
  */
 int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
                                const int64_t k_in_strides[2], const void *v_in, const int64_t v_in_strides[2],
@@ -446,17 +460,22 @@ int tt_rows_attn_f32(const void *q, const int64_t q_strides[2], const void *k_ca
 int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq_len);
 
 /* The split_tokens value for a decode attention call over a bf16 (fp8_cache
- * 0) or fp8 cache: TT_SPLIT_PER_SEGMENT when every sequence has the same
- * length (equal_lengths != 0), the MFMA kernels take head_dim and
- * batch * num_kv_heads is a multiple of the workgroups resident in one round
- * of the current GPU (its CUs, times 2 at tile widths <= 64); else 0. No
- * counterpart in the reference (whose batches always have one length). */
-int64_t tt_decode_pick_split(int64_t batch, int64_t num_kv_heads, int64_t head_dim, int32_t fp8_cache,
-                             int32_t equal_lengths);
+ * 0) or fp8 cache whose batch holds the host-side lengths seq_lens_host[0 ..
+ * batch): TT_SPLIT_PER_SEGMENT when they are all equal, the MFMA kernels take
+ * head_dim and batch * num_kv_heads is a multiple of the workgroups resident
+ * in one round of the current GPU (its CUs, times 2 at tile widths <= 64);
+ * TT_SPLIT_PAIRED when they differ, batch <= 256, (batch + 1) / 2 *
+ * num_kv_heads is a multiple of the GPU's CUs and no rank pair's tiles (plus
+ * 2 tiles' worth of start-up per segment) exceed 1.06 times the pairs' mean;
+ * else 0. No counterpart in the reference (whose batches always have one
+ * length). */
+int64_t tt_decode_pick_split(const int32_t *seq_lens_host, int64_t batch, int64_t num_kv_heads, int64_t head_dim,
+                             int32_t fp8_cache);
 
 /* Workspace bytes the attention entry points need; for split_tokens 0 the
- * size covers every cache dtype; for TT_SPLIT_PER_SEGMENT it is what the VALU
- * kernel's automatic split needs (the MFMA kernels need none). */
+ * size covers every cache dtype; for TT_SPLIT_PER_SEGMENT and TT_SPLIT_PAIRED
+ * it is what the VALU kernel's automatic split needs (the MFMA kernels need
+ * none). */
 size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                  int64_t head_dim, int64_t max_seq_len, int64_t split_tokens);
 

@@ -47,7 +47,7 @@ def test_noalloc_scratch_size_matches_header():
 
 
 def test_abi_version():
-    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_workspace_and_split_sizing():
@@ -63,21 +63,49 @@ def test_workspace_and_split_sizing():
     assert lib.tt_decode_workspace_bytes(64, 32, 8, 128, 16385, -1) == nbytes
 
 
+def _pick(lib, lens, hkv, head_dim, fp8=0):
+    arr = (ctypes.c_int32 * max(len(lens), 1))(*lens)
+    return lib.tt_decode_pick_split(ctypes.addressof(arr), len(lens), hkv, head_dim, fp8)
+
+
 @pytest.mark.skipif(not _no_gpu(), reason="the resident round is 256 workgroups per tile round only on the stand-in")
 def test_pick_split():
-    """Per segment only for equal lengths, MFMA head dims and B * H_kv a
+    """Equal lengths: per segment (-1) for MFMA head dims and B * H_kv a
     multiple of the resident round (256 CUs here: one workgroup per CU at tile
-    width 128, two at 64 and 32)."""
+    width 128, two at 64 and 32). Ragged lengths: paired (-2) for B <= 256,
+    (B + 1) / 2 * H_kv a multiple of the CUs, and no rank pair's line (tiles +
+    2 per segment) above 1.06 times the pairs' mean; else balanced (0)."""
     lib = _lib.load()
-    assert lib.tt_decode_pick_split(32, 8, 128, 0, 1) == -1   # C2: 256 segments, D 128
-    assert lib.tt_decode_pick_split(64, 8, 64, 0, 1) == -1    # 512 segments, D 64
-    assert lib.tt_decode_pick_split(32, 8, 64, 0, 1) == 0     # 256 segments at D 64: half a round
-    assert lib.tt_decode_pick_split(32, 8, 128, 0, 0) == 0    # ragged
-    assert lib.tt_decode_pick_split(33, 8, 128, 0, 1) == 0
-    assert lib.tt_decode_pick_split(64, 8, 96, 1, 1) == -1    # fp8, padded tile 128
-    assert lib.tt_decode_pick_split(64, 8, 24, 1, 1) == 0     # fp8 rows not whole 16-byte fragments
-    assert lib.tt_decode_pick_split(64, 8, 30, 0, 1) == 0     # VALU head_dim
-    assert lib.tt_decode_pick_split(0, 8, 128, 0, 1) == 0
+    assert _pick(lib, [4096] * 32, 8, 128) == -1   # C2: 256 segments, D 128
+    assert _pick(lib, [100] * 64, 8, 64) == -1     # 512 segments, D 64
+    assert _pick(lib, [100] * 32, 8, 64) == 0      # 256 segments at D 64: half a round
+    assert _pick(lib, [100] * 33, 8, 128) == 0
+    assert _pick(lib, [100] * 64, 8, 96, 1) == -1  # fp8, padded tile 128
+    assert _pick(lib, [100] * 64, 8, 24, 1) == 0   # fp8 rows not whole 16-byte fragments
+    assert _pick(lib, [100] * 64, 8, 30) == 0      # VALU head_dim
+    assert _pick(lib, [], 8, 128) == 0
+    assert lib.tt_decode_pick_split(None, 64, 8, 128, 0) == 0
+    # ragged: 32 long and 32 short sequences whose rank pairs (p, 63 - p) hold
+    # 154 line positions each: long_i = 32 (100 + i) tokens (102 + i
+    # positions), short_j = 32 (50 - j) tokens (52 - j)
+    longs = [32 * (100 + i) for i in range(32)]
+    shorts = [32 * (50 - j) for j in range(32)]
+    even = longs + shorts
+    assert _pick(lib, even, 8, 64) == -2            # 32 pairs x 8 heads = 256 workgroups
+    assert _pick(lib, even[::-1], 8, 128) == -2     # order does not matter; D 128
+    assert _pick(lib, even, 8, 64, 1) == -2         # fp8
+    assert _pick(lib, even, 4, 64) == 0             # 128 workgroups: half the CUs
+    assert _pick(lib, even, 16, 64) == -2           # 512: two rounds
+    # the longest pair 8 positions heavier: 162 / (154 + 8 / 32) = 1.050 of the mean
+    assert _pick(lib, longs[:-1] + [longs[-1] + 8 * 32] + shorts, 8, 64) == -2
+    # 12 heavier: 166 / 154.375 = 1.075
+    assert _pick(lib, longs[:-1] + [longs[-1] + 12 * 32] + shorts, 8, 64) == 0
+    # odd batch: the middle rank alone (B 63: 32 workgroups x 8 heads)
+    odd = [32 * (i + 1) for i in range(63)]        # pairs 68 positions, the middle rank 34 alone
+    assert _pick(lib, odd, 8, 64) == -2             # 68 / ((31 x 68 + 34) / 32) = 1.016
+    # two long sequences among short ones: pairs of 205 and of 6 positions
+    assert _pick(lib, [32 * 200] * 2 + [32] * 62, 8, 64) == 0
+    assert _pick(lib, [1] * 257, 8, 64) == 0 and _pick(lib, list(range(1, 258)), 8, 64) == 0  # B > 256
 
 
 FAKE = 0x10000  # 16-byte aligned, never dereferenced: validation fails first
@@ -105,7 +133,8 @@ def _attn(lib, **kw):
     (dict(hq=48, hkv=2), _lib.TT_ERR_UNSUPPORTED, "group size"),
     (dict(hq=30, hkv=8), _lib.TT_ERR_INVALID_ARGUMENT, "divisible"),
     (dict(split=300), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),
-    (dict(split=-2), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),
+    (dict(split=-3), _lib.TT_ERR_INVALID_ARGUMENT, "split_tokens"),
+    (dict(split=-2, batch=257), _lib.TT_ERR_UNSUPPORTED, "at most 256 sequences"),
     (dict(ws_bytes=16), _lib.TT_ERR_WORKSPACE_TOO_SMALL, "workspace"),
     (dict(page_size=24), _lib.TT_ERR_UNSUPPORTED, "power-of-two"),
     (dict(max_len=161), _lib.TT_ERR_INVALID_ARGUMENT, "exceeds the page table"),
@@ -120,7 +149,7 @@ def test_attention_rejects_invalid_arguments(kw, code, msg):
 
 @pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
 def test_fused_step_rejects_fixed_splits():
-    """The fused decode step runs the balanced (0) or per-segment (-1) partition only."""
+    """The fused decode step runs the balanced (0), per-segment (-1) or paired (-2) partition only."""
     lib = _lib.load()
     s2 = _lib.strides(512, 64)
     args = [FAKE, s2, FAKE, s2, FAKE, s2, 0, 0, FAKE, 100, FAKE, None, 50, None, 0, 0, FAKE, FAKE,

@@ -112,7 +112,7 @@ def test_cache_picks_the_partition_and_matches_balanced():
     per-segment partition (asserted); a bf16 model's teacher-forced decode
     steps through it give the balanced partition's logits to a few bf16 ulps
     of each row's largest logit."""
-    from tinytron_amd import _lib, ops
+    from tinytron_amd import ops
     from tinytron_amd.cache import PagedKVCache
     from tinytron_amd.model import GPT
     from tests.test_gpu_engine import _c1_config, _ulps_of_row_max
@@ -121,19 +121,19 @@ def test_cache_picks_the_partition_and_matches_balanced():
     Hkv, D = 8, 64
     B = 2 * cus // Hkv  # one round of two workgroups per CU at head_dim 64
     assert ops.pick_split([100] * B, Hkv, D, "bf16") == SEG
-    assert ops.pick_split([100] * (B - 1) + [101], Hkv, D, "bf16") == 0
+    assert ops.pick_split([100] * (B - 1) + [101], Hkv, D, "bf16") != SEG
     assert ops.pick_split([100] * B, Hkv, D, "f32") == 0
-    assert _lib.load().tt_decode_pick_split(B + 1, Hkv, D, 0, 1) == 0
+    assert ops.pick_split([100] * (B + 1), Hkv, D, "bf16") == 0
     cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=Hkv, block_size=96)
     model = GPT(cfg, device="cuda", dtype=torch.bfloat16)
     prompt = torch.randint(0, cfg.vocab_size, (B, 24), generator=torch.Generator().manual_seed(8)).cuda()
     with torch.no_grad():
         seg = PagedKVCache.from_model_config(cfg, B, 16, "cuda", torch.bfloat16)
         bal = PagedKVCache.from_model_config(cfg, B, 16, "cuda", torch.bfloat16)
-        for i in range(cfg.num_layer):
-            bal.get_layer_cache(i)._segment_split = 0  # force the balanced partition
         ls, seg = model(prompt, past_key_values=seg, use_cache=True)
         lb, bal = model(prompt, past_key_values=bal, use_cache=True)
+        for i in range(cfg.num_layer):
+            bal.get_layer_cache(i)._split = 0  # force the balanced partition (decode steps keep the pick)
         assert seg.get_layer_cache(0)._attention_split() == SEG
         assert bal.get_layer_cache(0)._attention_split() == 0
         tok = ls[:, -1].argmax(-1, keepdim=True)

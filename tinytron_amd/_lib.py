@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 TT_OK = 0
 TT_ERR_INVALID_ARGUMENT = -1
@@ -128,7 +128,7 @@ SIGNATURES = {
     "tt_rows_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ROWS_TAIL, ctypes.c_int),
     "tt_rows_attn_f32": (_ATTN_HEAD + _ROWS_TAIL, ctypes.c_int),
     "tt_decode_split_tokens": ([_i64, _i64, _i64], ctypes.c_int64),
-    "tt_decode_pick_split": ([_i64, _i64, _i64, ctypes.c_int32, ctypes.c_int32], ctypes.c_int64),
+    "tt_decode_pick_split": ([_vp, _i64, _i64, _i64, ctypes.c_int32], ctypes.c_int64),
     "tt_decode_workspace_bytes": ([_i64, _i64, _i64, _i64, _i64, _i64], ctypes.c_size_t),
     "tt_prefill_attn_bf16": ([_vp, _i64p, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),
     "tt_prefill_attn_fp8": ([_vp, _i64p, _vp, _vp, _vp, _vp, _i64p] + _PREFILL_TAIL, ctypes.c_int),

@@ -69,7 +69,7 @@ class _LayerCacheBase:
         self._pending_new_lens = None
         self.workspace = None
         self.static_max_len = None  # graph capture: launch-size bound fixed at the capacity
-        self._segment_split = None  # ops.pick_split for equal lengths, computed on first use
+        self._split = None  # ops.pick_split over the base lengths, computed on first use after they change
 
     # -- lengths ---------------------------------------------------------------
     @property
@@ -89,8 +89,8 @@ class _LayerCacheBase:
         self._base = [int(x) for x in lens]
         self._shift = 0
         self._base_max = max(self._base) if self._base else 0
-        self._base_min = min(self._base) if self._base else 0
         self._room = None  # min over b of capacity - base, recomputed on demand
+        self._split = None
 
     def _advance_all(self, n: int) -> None:
         self._shift += n
@@ -197,16 +197,17 @@ class _LayerCacheBase:
         return self._decode_step(rope_table, out, partials=partials, num_q_heads=num_q_heads)
 
     def _attention_split(self) -> int:
-        """split_tokens of this cache's decode attention: the per-segment
-        partition (one launch, merged in LDS) while every sequence has the same
-        length and the batch fills whole rounds of the GPU, else the balanced
-        partition (0)."""
-        if self._base_min != self._base_max:
-            return 0
-        if self._segment_split is None:
+        """split_tokens of this cache's decode attention (ops.pick_split over
+        the host lengths): the per-segment partition while every sequence has
+        the same length, the paired one for a ragged batch whose rank pairs
+        fill the GPU evenly (both one launch, merged in LDS), else the
+        balanced partition (0). Decode steps add the same count to every
+        length, which changes neither equality nor the ranks, so the pick is
+        made once per change of the base lengths."""
+        if self._split is None:
             lay = self.layout
-            self._segment_split = ops.pick_split([0] * self.batch_size, lay.num_heads, lay.head_dim, lay.kind)
-        return self._segment_split
+            self._split = ops.pick_split(self._base, lay.num_heads, lay.head_dim, lay.kind)
+        return self._split
 
     def _decode_step(self, rope_table, out, **inputs) -> torch.Tensor:
         self._check_room([1] * self.batch_size)

@@ -2,6 +2,7 @@
 // include/tinytron_amd.h): argument validation, status codes and launches.
 // Nothing here allocates or synchronises; every launch goes on the caller's
 // stream.
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -310,13 +311,14 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
              TT_ERR_INVALID_ARGUMENT, "q, cache and out pointers must be aligned to their element size");
   }
   // On the MFMA path split_tokens 0 is the balanced partition (equal tiles per
-  // wave) and kSplitPerSegment one workgroup per segment; the VALU kernel
-  // takes both as 0 (its automatic fixed split). Otherwise fixed splits.
-  TT_CHECK(split_tokens >= tt::kSplitPerSegment, TT_ERR_INVALID_ARGUMENT,
-           "split_tokens must be 0 (auto), %d (per segment), 128, 256, 512 or 1024, got %lld", tt::kSplitPerSegment,
-           (long long)split_tokens);
-  if (split_tokens == tt::kSplitPerSegment && tile == 0) split_tokens = 0;
-  const bool segment = split_tokens == tt::kSplitPerSegment;
+  // wave), kSplitPerSegment one workgroup per segment and kSplitPaired one per
+  // pair of length ranks; the VALU kernel takes all three as 0 (its automatic
+  // fixed split). Otherwise fixed splits.
+  TT_CHECK(split_tokens >= tt::kSplitPaired, TT_ERR_INVALID_ARGUMENT,
+           "split_tokens must be 0 (auto), %d (per segment), %d (paired), 128, 256, 512 or 1024, got %lld",
+           tt::kSplitPerSegment, tt::kSplitPaired, (long long)split_tokens);
+  if (split_tokens < 0 && tile == 0) split_tokens = 0;
+  const bool segment = split_tokens < 0;  // the one-launch partitions, no workspace
   const bool balanced = split_tokens == 0 && tile > 0;
   int64_t split = 0, splits = 0;
   size_t need = 0;
@@ -325,7 +327,14 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
       exact_slots ? tt::balanced_stream_waves(tile, batch, num_kv_heads, max_seq_len) : tt::kMaxStreamWaves;
   if (segment) {
     TT_CHECK(batch * num_kv_heads <= INT32_MAX, TT_ERR_UNSUPPORTED, "batch * num_kv_heads is too large");
-    split = tt::kSplitPerSegment;  // no workspace
+    if (split_tokens == tt::kSplitPaired) {
+      TT_CHECK(batch <= tt::kMaxPairedBatch, TT_ERR_UNSUPPORTED, "the paired partition takes at most %lld sequences, got %lld",
+               (long long)tt::kMaxPairedBatch, (long long)batch);
+      TT_CHECK(tt::paired_lds_bytes(tile, kind == tt::CacheKind::kFP8, ap != nullptr, num_q_heads / num_kv_heads) > 0,
+               TT_ERR_UNSUPPORTED, "the paired partition's LDS does not fit this GQA group (%lld) and head_dim",
+               (long long)(num_q_heads / num_kv_heads));
+    }
+    split = split_tokens;  // no workspace
   } else if (balanced) {
     // the per-sequence line prefix (int32) counts each sequence's tiles plus its segment start-up charge
     TT_CHECK(batch * ((max_seq_len + tt::kTileTokens - 1) / tt::kTileTokens + tt::kStreamSegCost) < ((int64_t)1 << 31),
@@ -409,9 +418,10 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
                          int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens, void *workspace,
                          size_t ws_bytes, tt_stream_t stream, bool exact_slots = false) {
   TT_CHECK(q_in && k_in && v_in && rope_table && positions, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
-  TT_CHECK(split_tokens == 0 || split_tokens == tt::kSplitPerSegment, TT_ERR_INVALID_ARGUMENT,
-           "the fused decode step takes split_tokens 0 (balanced) or %d (per segment), got %lld",
-           tt::kSplitPerSegment, (long long)split_tokens);
+  TT_CHECK(split_tokens == 0 || split_tokens == tt::kSplitPerSegment || split_tokens == tt::kSplitPaired,
+           TT_ERR_INVALID_ARGUMENT,
+           "the fused decode step takes split_tokens 0 (balanced), %d (per segment) or %d (paired), got %lld",
+           tt::kSplitPerSegment, tt::kSplitPaired, (long long)split_tokens);
   TT_CHECK(q_in_strides && k_in_strides && v_in_strides, TT_ERR_INVALID_ARGUMENT, "a stride array is NULL");
   TT_CHECK(splits >= 0 && (splits == 0 || split_stride > 0), TT_ERR_INVALID_ARGUMENT, "bad split-K partial layout");
   TT_CHECK(splits <= tt::kMaxApSplits, TT_ERR_UNSUPPORTED, "the fused step sums at most %d split-K partials, got %lld",
@@ -812,12 +822,38 @@ int64_t tt_decode_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_
   return tt::auto_split_tokens(batch, num_kv_heads, max_seq_len);
 }
 
-int64_t tt_decode_pick_split(int64_t batch, int64_t num_kv_heads, int64_t head_dim, int32_t fp8_cache,
-                             int32_t equal_lengths) {
-  if (!equal_lengths || batch <= 0 || num_kv_heads <= 0) return 0;
-  const int tile = tt::tile_head_dim(head_dim, fp8_cache ? tt::CacheKind::kFP8 : tt::CacheKind::kBF16);
+int64_t tt_decode_pick_split(const int32_t *seq_lens_host, int64_t batch, int64_t num_kv_heads, int64_t head_dim,
+                             int32_t fp8_cache) {
+  if (seq_lens_host == nullptr || batch <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+  const tt::CacheKind kind = fp8_cache ? tt::CacheKind::kFP8 : tt::CacheKind::kBF16;
+  const int tile = tt::tile_head_dim(head_dim, kind);
   if (tile == 0) return 0;
-  return (batch * num_kv_heads) % tt::segment_round(tile) == 0 ? tt::kSplitPerSegment : 0;
+  bool equal = true;
+  for (int64_t b = 1; b < batch && equal; ++b) equal = seq_lens_host[b] == seq_lens_host[0];
+  if (equal) return (batch * num_kv_heads) % tt::segment_round(tile) == 0 ? tt::kSplitPerSegment : 0;
+  // The paired partition: one round of the GPU's CUs (one workgroup per CU,
+  // two at 4 waves a workgroup), its workgroups' work (two segments' tiles and
+  // start-up positions) within kPairedSlack of the mean. Measured against the
+  // balanced partition (ragged, fused step): C5 layer (pairs 1.034 of the
+  // mean) 35.2 -> 30.6 us, C3 (1.049) 386 -> 381 us, C4 (1.064) 747 -> 749 us.
+  constexpr double kPairedSlack = 1.06;
+  if (batch > tt::kMaxPairedBatch || (batch + 1) / 2 * num_kv_heads % tt::device_cu_count() != 0) return 0;
+  if (tt::paired_lds_bytes(tile, fp8_cache != 0, true, 16) == 0) return 0;  // fits every GQA group up to 16
+  int64_t lines[tt::kMaxPairedBatch];
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t L = seq_lens_host[b] > 0 ? seq_lens_host[b] : 0;
+    lines[b] = L > 0 ? (L + tt::kTileTokens - 1) / tt::kTileTokens + tt::kStreamSegCost : 0;
+  }
+  std::sort(lines, lines + batch);
+  int64_t worst = 0, total = 0;
+  for (int64_t p = 0; p < (batch + 1) / 2; ++p) {
+    const int64_t w = lines[batch - 1 - p] + (batch - 1 - p != p ? lines[p] : 0);
+    worst = std::max(worst, w);
+    total += w;
+  }
+  if (total == 0) return 0;
+  const double mean = (double)total / (double)((batch + 1) / 2);
+  return (double)worst <= kPairedSlack * mean ? tt::kSplitPaired : 0;
 }
 
 size_t tt_decode_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,

@@ -963,6 +963,176 @@ __global__ __launch_bounds__(256, kStreamOcc) void decode_segment_append_kernel(
   segment_body<D, kFP8, true, kPartIn, kPad>(a, &a.ap);
 }
 
+// ---------------------------------------------------------------------------
+// Paired partition (split_tokens == kSplitPaired), for ragged batches of up to
+// kMaxPairedBatch sequences: the sequences ranked by length (longest first,
+// ties by index), workgroup (p, hk) takes the segments of KV head hk of the
+// sequences ranked p and B - 1 - p (one for the middle rank of an odd batch),
+// whose lengths add up to about the same total in every workgroup. Its NWV
+// waves split the two segments' line (each segment's start-up positions, then
+// its tiles) evenly, as the balanced partition does the whole batch's, so a
+// wave holds at most one piece of each segment; the pieces merge in LDS and the
+// workgroup writes both segments' rows: one launch, no workspace.
+static_assert(kMaxPairedBatch == 256, "the paired kernel's LDS holds 256 length keys");
+// waves per paired workgroup: as many per CU as the balanced kernel at one
+// workgroup per CU
+constexpr int paired_waves(int tile_d) { return tile_d <= 64 ? 8 : 4; }
+
+// LDS of the paired kernel: the streaming area (NWV V slots, and q staging for
+// the fused variant), later the merge area [NWV][G][D] + maxima and sums
+// [NWV][16] each, taken by one segment after the other; then the length keys
+// and the pair.
+__host__ __device__ constexpr int paired_stream_lds(int tile_d, bool fp8, bool fused, int nwv) {
+  return nwv * 2 * (tile_d * (fp8 ? 1 : 2) / 64) * 1024 + (fused ? nwv * 16 * tile_d * 2 : 0);
+}
+__host__ __device__ constexpr int paired_merge_lds(int tile_d, int group, int nwv) {
+  return (int)sizeof(float) * (nwv * group * tile_d + 2 * nwv * 16);
+}
+__host__ __device__ constexpr int paired_lds(int tile_d, bool fp8, bool fused, int group, int nwv) {
+  return (paired_stream_lds(tile_d, fp8, fused, nwv) > paired_merge_lds(tile_d, group, nwv)
+              ? paired_stream_lds(tile_d, fp8, fused, nwv)
+              : paired_merge_lds(tile_d, group, nwv)) +
+         (int)sizeof(int) * ((int)kMaxPairedBatch + 2);
+}
+
+template <int D, bool kFP8, bool kAppend, bool kPartIn, bool kPad, int NWV>
+__device__ __forceinline__ void paired_body(const DecodeArgs &a, const DecodeAppend *ap) {
+  constexpr int kVAll = NWV * Tile<D, kFP8>::kVBytes;
+  constexpr int NDB = D / 32;
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = a.group;
+  const int NB = a.batch;
+  char *smem_v = reinterpret_cast<char *>(smem);
+  int *keys = reinterpret_cast<int *>(smem_v + (paired_lds(D, kFP8, kAppend, G, NWV) -
+                                               (int)sizeof(int) * ((int)kMaxPairedBatch + 2)));
+  int *pair = keys + kMaxPairedBatch;
+  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+    reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
+  uint16_t *qs = nullptr;
+  if constexpr (kAppend) {
+    qs = reinterpret_cast<uint16_t *>(smem_v + kVAll) + wave * 16 * D;
+    if (blockIdx.x == 0 && ap->lens_out != nullptr)  // the next step's lengths
+      for (int i = threadIdx.x; i < NB; i += blockDim.x) ap->lens_out[i] = a.seq_lens[i] + 1;
+  }
+  for (int b = threadIdx.x; b < NB; b += blockDim.x) keys[b] = max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
+  const int p = (int)(blockIdx.x / (unsigned)a.hkv);
+  const int hk = (int)(blockIdx.x - (unsigned)p * (unsigned)a.hkv);
+  if (threadIdx.x == 0) pair[1] = -1;
+  __syncthreads();  // V slots zeroed, keys in place
+  // rank r(b) = sequences before b: longer, or as long with a smaller index
+  for (int b = threadIdx.x; b < NB; b += blockDim.x) {
+    const int kb = keys[b];
+    int r = 0;
+    for (int c = 0; c < NB; ++c) r += (keys[c] > kb || (keys[c] == kb && c < b)) ? 1 : 0;
+    if (r == p) pair[0] = b;
+    if (r == NB - 1 - p && r != p) pair[1] = b;
+  }
+  __syncthreads();
+  const int bA = __builtin_amdgcn_readfirstlane(pair[0]);
+  const int bB = __builtin_amdgcn_readfirstlane(pair[1]);  // -1: the middle rank alone
+  const int LA = __builtin_amdgcn_readfirstlane(keys[bA]);
+  const int LB = bB >= 0 ? __builtin_amdgcn_readfirstlane(keys[bB]) : 0;
+  const int ntA = (LA + kTileTokens - 1) / kTileTokens;
+  const int ntB = (LB + kTileTokens - 1) / kTileTokens;
+  const int lineA = ntA > 0 ? ntA + kStreamSegCost : 0;
+  const int lineB = ntB > 0 ? ntB + kStreamSegCost : 0;
+  const int W = lineA + lineB;
+  const int s0 = wave * W / NWV;
+  const int s1 = (wave + 1) * W / NWV;
+
+  WaveState<D, kFP8> stA, st;
+#pragma unroll
+  for (int c = 0; c < 2 * NDB; ++c) stA.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  stA.m = kNegInf;
+  stA.l = 0.f;
+  bf16x8 ident16[2];
+  u32x2 ident8[2];
+  make_identity(lane, ident16, ident8);
+  for (int sg = 0; sg < 2; ++sg) {  // this wave's piece of segment A, then of segment B
+    const int base = sg == 0 ? 0 : lineA;
+    const int line = sg == 0 ? lineA : lineB;
+    const int nt = sg == 0 ? ntA : ntB;
+    const int b = sg == 0 ? bA : bB;
+    const int L = sg == 0 ? LA : LB;
+    const int j0 = max(max(s0 - base, 0) - kStreamSegCost, 0);
+    const int j1 = max(min(s1 - base, line) - kStreamSegCost, 0);
+#pragma unroll
+    for (int c = 0; c < 2 * NDB; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = kNegInf;
+    st.l = 0.f;
+    if (j1 > j0)  // the wave holding a segment's last tile appends its token (fused variant)
+      stream_piece<D, kFP8, kAppend, kPartIn, kPad>(a, ap, b, hk, L, j0, j1, kAppend && j1 == nt, lane,
+                                                    smem_v + wave * Tile<D, kFP8>::kVBytes, qs, ident16, ident8, st);
+    if (sg == 0) stA = st;
+  }
+  // The two segments merge one after the other in the same LDS area (over the
+  // streaming one): [NWV][G][D] unnormalised outputs, [NWV][16] maxima, sums.
+  float *so = smem;
+  float *sm = so + NWV * G * D;
+  float *sl = sm + NWV * 16;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  for (int sg = 0; sg < 2; ++sg) {
+    const int b = sg == 0 ? bA : bB;
+    if (b < 0) break;  // the middle rank of an odd batch: no second segment
+    __syncthreads();   // every wave is done with its V slot and q staging, or with the last merge
+    const WaveState<D, kFP8> &x = sg == 0 ? stA : st;
+    float l = x.l;  // lane-partial sums -> the head's sum in all 4 lanes of the head
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (g == 0) {
+      sm[wave * 16 + n] = x.m;
+      sl[wave * 16 + n] = l;
+    }
+    if (n < G) {
+#pragma unroll
+      for (int c = 0; c < 2 * NDB; ++c)
+        *reinterpret_cast<f32x4 *>(so + (wave * G + n) * D + o_col_d<kFP8>(c, 4 * g)) = x.o[c];
+    }
+    __syncthreads();
+    // column pairs (2p, 2p + 1) of every head
+    uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * G * a.o_sh;
+    for (int pr = threadIdx.x; pr < G * (D / 2); pr += blockDim.x) {
+      const int head = pr / (D / 2);
+      const int d = 2 * (pr - head * (D / 2));
+      if (d >= a.head_dim) continue;  // head_dim is even: d + 1 < head_dim too
+      float mw[NWV];
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        mw[w] = sm[w * 16 + head];
+        M = fmaxf(M, mw[w]);
+      }
+      float acc0 = 0.f, acc1 = 0.f, lsum = 0.f;
+      if (M != kNegInf) {  // a sequence with nothing cached gives zeros
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+          const float e = __builtin_amdgcn_exp2f(mw[w] - M);
+          const float *row = so + (w * G + head) * D + d;
+          acc0 += e * row[0];
+          acc1 += e * row[1];
+          lsum += e * sl[w * 16 + head];
+        }
+      }
+      const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+      out[(int64_t)head * a.o_sh + d] = f32_to_bf16_bits(acc0 * inv);
+      out[(int64_t)head * a.o_sh + d + 1] = f32_to_bf16_bits(acc1 * inv);
+    }
+  }
+}
+
+template <int D, bool kFP8, bool kPad, int NWV>
+__global__ __launch_bounds__(64 * NWV, NWV == 4 ? kStreamOcc : 1) void decode_paired_kernel(DecodeArgs a) {
+  paired_body<D, kFP8, false, false, kPad, NWV>(a, nullptr);
+}
+
+template <int D, bool kFP8, bool kPartIn, bool kPad, int NWV>
+__global__ __launch_bounds__(64 * NWV, NWV == 4 ? kStreamOcc : 1) void decode_paired_append_kernel(DecodeAppendArgs a) {
+  paired_body<D, kFP8, true, kPartIn, kPad, NWV>(a, &a.ap);
+}
+
 // One wave per segment (b, KV head): merge its pieces into the G output rows
 // (zeros for a sequence with nothing cached). kMaxG bounds the group size.
 template <int D, int kMaxG>
@@ -1241,6 +1411,35 @@ hipError_t launch_segment(const DecodeArgs &a, const DecodeAppend *ap, hipStream
   return hipGetLastError();
 }
 
+template <int D, bool kFP8, bool kPad>
+hipError_t launch_paired(const DecodeArgs &a, const DecodeAppend *ap, hipStream_t stream) {
+  constexpr int NWV = paired_waves(D);
+  static_assert(Tile<D, kFP8>::kVBytes * NWV == paired_stream_lds(D, kFP8, false, NWV), "paired_stream_lds assumes this");
+  const dim3 grid((unsigned)paired_grid(a.batch, a.hkv));
+  const size_t lds = paired_lds_bytes(D, kFP8, ap != nullptr, a.group);
+  if (lds == 0) return hipErrorInvalidValue;
+  if (ap != nullptr) {
+    DecodeAppendArgs f;
+    static_cast<DecodeArgs &>(f) = a;
+    f.ap = *ap;
+    if (ap->part_splits > 0)
+      hipLaunchKernelGGL((decode_paired_append_kernel<D, kFP8, true, kPad, NWV>), grid, dim3(64 * NWV), lds, stream, f);
+    else
+      hipLaunchKernelGGL((decode_paired_append_kernel<D, kFP8, false, kPad, NWV>), grid, dim3(64 * NWV), lds, stream,
+                         f);
+  } else {
+    hipLaunchKernelGGL((decode_paired_kernel<D, kFP8, kPad, NWV>), grid, dim3(64 * NWV), lds, stream, a);
+  }
+  return hipGetLastError();
+}
+
+// The one-launch partitions (split_tokens < 0).
+template <int D, bool kFP8, bool kPad>
+hipError_t launch_onepass(const DecodeArgs &a, const DecodeAppend *ap, hipStream_t stream) {
+  if (a.split_tokens == kSplitPaired) return launch_paired<D, kFP8, kPad>(a, ap, stream);
+  return launch_segment<D, kFP8, kPad>(a, ap, stream);
+}
+
 // MFMA kernels on D-wide tiles (kPad: rows of a.head_dim < D).
 template <int D, bool kPad>
 hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
@@ -1249,14 +1448,14 @@ hipError_t launch_d(const DecodeArgs &a, CacheKind kind, hipStream_t stream) {
   hipError_t err = hipSuccess;
   if (kind == CacheKind::kFP8) {
     if constexpr (D >= 64) {  // fp8 tiles are at least 64 wide (one 16-byte fragment per lane and row)
-      if (a.split_tokens == kSplitPerSegment) return launch_segment<D, true, kPad>(a, nullptr, stream);
+      if (a.split_tokens < 0) return launch_onepass<D, true, kPad>(a, nullptr, stream);
       if (a.split_tokens == 0) return launch_stream<D, true, kPad>(a, nullptr, stream);
       err = launch_mfma<D, true, kPad>(a, block, lds, stream);
     } else {
       return hipErrorInvalidValue;
     }
   } else {
-    if (a.split_tokens == kSplitPerSegment) return launch_segment<D, false, kPad>(a, nullptr, stream);
+    if (a.split_tokens < 0) return launch_onepass<D, false, kPad>(a, nullptr, stream);
     if (a.split_tokens == 0) return launch_stream<D, false, kPad>(a, nullptr, stream);
     err = launch_mfma<D, false, kPad>(a, block, lds, stream);
   }
@@ -1309,6 +1508,14 @@ size_t segment_lds_bytes(int tile_d, bool fp8, bool fused, int64_t group) {
   return (size_t)(segment_merge_separate(tile_d, fp8, fused, g) ? stream + merge : (stream > merge ? stream : merge));
 }
 
+int64_t paired_grid(int64_t batch, int64_t hkv) { return (batch + 1) / 2 * hkv; }
+
+size_t paired_lds_bytes(int tile_d, bool fp8, bool fused, int64_t group) {
+  if (group < 1 || group > 16) return 0;
+  const int bytes = paired_lds(tile_d, fp8, fused, (int)group, paired_waves(tile_d));
+  return bytes <= 65536 ? (size_t)bytes : 0;
+}
+
 int64_t segment_round(int tile_d) { return (int64_t)device_cu_count() * stream_blocks_per_cu(tile_d); }
 
 int64_t auto_split_tokens(int64_t batch, int64_t hkv, int64_t max_len) {
@@ -1335,15 +1542,15 @@ hipError_t launch_decode_attn(const DecodeArgs &a, CacheKind kind, int head_dim,
 hipError_t launch_decode_attn_append(const DecodeAppendArgs &a, CacheKind kind, int head_dim, hipStream_t stream) {
   const int D = tile_head_dim(head_dim, kind);
   const bool pad = D != head_dim;
-  if (a.split_tokens == kSplitPerSegment) {
+  if (a.split_tokens < 0) {
     if (kind == CacheKind::kFP8) {
-      if (D == 64) return pad ? launch_segment<64, true, true>(a, &a.ap, stream) : launch_segment<64, true, false>(a, &a.ap, stream);
-      if (D == 128) return pad ? launch_segment<128, true, true>(a, &a.ap, stream) : launch_segment<128, true, false>(a, &a.ap, stream);
+      if (D == 64) return pad ? launch_onepass<64, true, true>(a, &a.ap, stream) : launch_onepass<64, true, false>(a, &a.ap, stream);
+      if (D == 128) return pad ? launch_onepass<128, true, true>(a, &a.ap, stream) : launch_onepass<128, true, false>(a, &a.ap, stream);
       return hipErrorInvalidValue;
     }
-    if (D == 32) return pad ? launch_segment<32, false, true>(a, &a.ap, stream) : launch_segment<32, false, false>(a, &a.ap, stream);
-    if (D == 64) return pad ? launch_segment<64, false, true>(a, &a.ap, stream) : launch_segment<64, false, false>(a, &a.ap, stream);
-    if (D == 128) return pad ? launch_segment<128, false, true>(a, &a.ap, stream) : launch_segment<128, false, false>(a, &a.ap, stream);
+    if (D == 32) return pad ? launch_onepass<32, false, true>(a, &a.ap, stream) : launch_onepass<32, false, false>(a, &a.ap, stream);
+    if (D == 64) return pad ? launch_onepass<64, false, true>(a, &a.ap, stream) : launch_onepass<64, false, false>(a, &a.ap, stream);
+    if (D == 128) return pad ? launch_onepass<128, false, true>(a, &a.ap, stream) : launch_onepass<128, false, false>(a, &a.ap, stream);
     return hipErrorInvalidValue;
   }
   if (kind == CacheKind::kFP8) {

@@ -243,6 +243,14 @@ constexpr int kSplitPerSegment = -1;
 int64_t segment_grid(int64_t batch, int64_t hkv);
 size_t segment_lds_bytes(int tile_d, bool fp8, bool fused, int64_t group);
 int64_t segment_round(int tile_d);
+// split_tokens value of the paired partition: the sequences ranked by length,
+// workgroup (p, KV head) takes ranks p and B - 1 - p, its waves split the two
+// segments' tiles, merged in LDS: one launch, no workspace, B <= kMaxPairedBatch.
+constexpr int kSplitPaired = -2;
+constexpr int64_t kMaxPairedBatch = 256;
+// Its grid and dynamic LDS bytes (0: the GQA group does not fit in 64 KB).
+int64_t paired_grid(int64_t batch, int64_t hkv);
+size_t paired_lds_bytes(int tile_d, bool fp8, bool fused, int64_t group);
 // Waves of the balanced stream kernel's grid on the current device (at most
 // kMaxStreamWaves); the partial slots it writes are b * H_kv + hk + wave.
 int64_t balanced_stream_waves(int head_dim, int64_t batch, int64_t hkv, int64_t max_len);

@@ -7,6 +7,7 @@ and CUDA(HIP) tensors.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -294,19 +295,23 @@ def split_tokens_for(batch: int, num_kv_heads: int, max_seq_len: int) -> int:
 # split_tokens of the per-segment partition: one workgroup per (sequence, KV
 # head), merged inside the launch (no merge launch, no workspace)
 SPLIT_PER_SEGMENT = -1
+# split_tokens of the paired partition: one workgroup per pair of length ranks
+# (p, B - 1 - p) and KV head, merged inside the launch (B <= 256)
+SPLIT_PAIRED = -2
 
 
 def pick_split(seq_lens_host, num_kv_heads: int, head_dim: int, kind: str) -> int:
-    """split_tokens for decode attention over these host-side lengths:
-    SPLIT_PER_SEGMENT when they are all equal and B * H_kv fills whole rounds
-    of the GPU's resident workgroups (tt_decode_pick_split), else 0 (the
-    balanced partition)."""
+    """split_tokens for decode attention over these host-side lengths
+    (tt_decode_pick_split): SPLIT_PER_SEGMENT when they are all equal and
+    B * H_kv fills whole rounds of the GPU's resident workgroups;
+    SPLIT_PAIRED when they differ, B <= 256, the rank pairs' workgroups fill
+    whole rounds of the GPU's CUs and their work is within 6 % of the mean;
+    else 0 (the balanced partition)."""
     if kind not in ("bf16", "fp8") or len(seq_lens_host) == 0:
         return 0
-    first = seq_lens_host[0]
-    equal = all(x == first for x in seq_lens_host)
-    return int(_lib.load().tt_decode_pick_split(len(seq_lens_host), num_kv_heads, head_dim, int(kind == "fp8"),
-                                                int(equal)))
+    lens = (ctypes.c_int32 * len(seq_lens_host))(*[int(x) for x in seq_lens_host])
+    return int(_lib.load().tt_decode_pick_split(ctypes.addressof(lens), len(seq_lens_host), num_kv_heads, head_dim,
+                                                int(kind == "fp8")))
 
 
 def workspace_bytes(batch: int, hq: int, hkv: int, head_dim: int, max_seq_len: int, split_tokens: int = 0) -> int:
@@ -468,8 +473,9 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
     (balanced partition) or SPLIT_PER_SEGMENT (no workspace; not with
     ``no_alloc``)."""
     _require_cuda(table, positions, layout.k, layout.v)
-    if split_tokens not in (0, SPLIT_PER_SEGMENT):
-        raise ValueError(f"the fused decode step takes split_tokens 0 or {SPLIT_PER_SEGMENT}, got {split_tokens}")
+    if split_tokens not in (0, SPLIT_PER_SEGMENT, SPLIT_PAIRED):
+        raise ValueError(f"the fused decode step takes split_tokens 0, {SPLIT_PER_SEGMENT} or {SPLIT_PAIRED}, "
+                         f"got {split_tokens}")
     if layout.kind not in ("bf16", "fp8"):
         raise ValueError("the fused decode step takes a bf16 or fp8 cache")
     Hkv, D = layout.num_heads, layout.head_dim
@@ -526,7 +532,7 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
         _lib.check(st, "decode_attention_append (no allocation)")
         return out
     tail.append(int(split_tokens))
-    if split_tokens == SPLIT_PER_SEGMENT:  # merged inside the launch: no workspace
+    if split_tokens < 0:  # merged inside the launch: no workspace
         tail += [None, 0, _stream(dev)]
     else:
         need = workspace_bytes(B, Hq, Hkv, D, max_seq_len, 0)
