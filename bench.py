@@ -19,9 +19,10 @@ headline config; --e2e-only runs C5 end to end alone.
 
 value = algorithmic bytes per step / time per step (GB/s, 1 GB = 1e9 B), with
 algorithmic bytes = unique K/V bytes read (+ fp8 scales) + q/out/new-token/page
-table I/O. The roofline object covers the decode-attention operator (the
-balanced stream kernel and its merge kernel) timed alone with HIP events on the
-stream it runs on. CPU baselines time the reference's own op sequence (torch
+table I/O. The roofline object covers the decode-attention operator in the
+partition the KV cache picks for the workload's lengths (C3 and c5a: the paired
+kernel, one launch; C2: the per-segment kernel; C4: the balanced stream kernel
+and its merge kernel) timed alone with HIP events on the stream it runs on. CPU baselines time the reference's own op sequence (torch
 on the host: rope_impl, gqa_impl, the H_q-expanded LayerPagedKVCache, mask,
 SDPA; for C1 / C5 the whole model and generate loop) on bounded samples of
 the same workloads, with the host's CPU model and thread count recorded.
@@ -69,7 +70,8 @@ def parse_args():
     p.add_argument("--seed", type=int, default=1337)
     p.add_argument("--split-tokens", type=int, default=None,
                    help="decode attention partition: 0 balanced, -1 one workgroup per (sequence, KV head), "
-                        "128-1024 fixed splits; default: what the KV cache picks for the workload's lengths")
+                        "-2 one workgroup per (rank pair, KV head), 128-1024 fixed splits; default: what the KV "
+                        "cache picks for the workload's lengths")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of timed CPU-baseline work per config")
     p.add_argument("--no-c1", action="store_true", help="skip config C1 (the reference's CPU-sized model)")
@@ -174,10 +176,11 @@ def e2e_c5(args, torch):
         "decode_launch": launch,
         "decode_tokens_per_sec_eager": forced.get("eager"),
         "decode_tokens_per_sec_graphs": forced.get("graphs"),
-        "decode_path": "fused bf16 decode step (8 launches per layer: RoPE + append inside the attention launch "
-                       "pair, gate|up and SwiGLU in one launch) + one-launch sampler, launched as the engine's "
-                       "default picks on the second step (decode_launch: eager when the host issues a step in less "
-                       "than 0.9x its GPU time, else HIP-graph replay with the two captures inside the timed "
+        "decode_path": "fused bf16 decode step (7 launches per layer: RoPE + append inside the attention launch, "
+                       "one launch in the paired partition the caches pick for this batch, gate|up and SwiGLU in one "
+                       "launch) + one-launch sampler, launched as the engine's "
+                       "default picks after the third step (decode_launch: eager when the host issues steps in less "
+                       "than 0.97x their GPU time, else HIP-graph replay with the two captures inside the timed "
                        "window); decode_tokens_per_sec_eager / _graphs force each mode (same tokens, checked)",
         "attention_partition": {ops.SPLIT_PER_SEGMENT: "per segment", ops.SPLIT_PAIRED: "paired (rank pairs)",
                                 0: "balanced"}[ops.pick_split(lens, C5["num_key_value_heads"],

@@ -15,13 +15,11 @@ loop (the reference syncs once per layer at attn.py:395).
 With ``use_graphs=True`` the one-token model call is captured in HIP graphs
 after the first decode step and replayed for the rest, which removes the
 per-kernel launch cost; ``False`` launches every step eagerly. By default
-(``None``) the engine times the second step eagerly, alone (one
-synchronisation), and replays graphs only when the host needs at least 0.9x
-the step's GPU time to issue it: the fused bf16 step issues 8 launches per
-layer, about as fast as a fast host issues them (C5: eager 28.5-29.3 k
-tokens/s against 27.7-28.6 k replayed with the two captures inside the loop;
-a slower host read 26.8 k eager against 28.4 k replayed), the fused step
-with an fp8 cache one launch more, and the module-by-module step about 30.
+(``None``) the engine times the second and third decode steps eagerly from
+one synchronisation, and replays graphs only when the host needs at least
+GRAPH_HOST_RATIO of those steps' GPU time to issue them: the fused bf16 step
+issues 7 or 8 launches per layer, about as fast as a fast host issues them,
+and the module-by-module step about 30.
 The caches keep their lengths in two device buffers that swap every step, so
 two graphs are captured, one per buffer parity. The attention launch bound is
 fixed at the largest sequence capacity for the whole decode loop, so the
@@ -38,6 +36,16 @@ import torch
 from .cache import PagedKVCache
 from .model import GPT, ModelConfig
 from .sampler import sample_next_token, sample_next_token_with_log_prob
+
+
+# Launch mode of the default engine: replay graphs when issuing two eager
+# steps takes the host at least this fraction of their GPU time. The ratio of
+# a GPU-bound host is host / GPU time; a host-bound one reads ~0.97-0.99 (the
+# GPU's time then is the host's plus the last kernels). Measured at C5 on a
+# host issuing at 0.9-1.0x of the GPU: eager 31.3 k tokens/s against 30.3 k
+# replayed (the two captures inside the loop); a host well below the GPU's
+# pace gains from replay (26.8 k eager against 28.4 k replayed).
+GRAPH_HOST_RATIO = 0.97
 
 
 class DecodeGraphs:
@@ -156,10 +164,11 @@ class InferenceEngine:
         graphs = None
         # the tuple cache's tensors change every step: it launches eagerly. The
         # paged caches replay graphs when asked (use_graphs=True), launch
-        # eagerly when told not to (False), and by default (None) decide on the
-        # second step: replay when the host takes at least 0.9x the GPU's time
-        # to issue one eager step (the GPU would wait on the host), else stay
-        # eager (replay would only add the two captures to the loop).
+        # eagerly when told not to (False), and by default (None) decide after
+        # the third decode step: replay when the host took at least GRAPH_HOST_RATIO of
+        # the GPU's time to issue eager steps 1 and 2 (the GPU waits on the
+        # host), else stay eager (replay would only add the two captures and
+        # the replays' own cost to the loop).
         use_graphs = paged and bool(self.use_graphs)
         auto = paged and self.use_graphs is None
         self.last_decode_launch = "graphs" if use_graphs else "eager"
@@ -182,19 +191,22 @@ class InferenceEngine:
                 graphs = DecodeGraphs(self.model, cache, batch_size, position, uniform, self.device)
             if graphs is not None:
                 logits = graphs.step(next_token)
-            elif auto and step == 1:
-                # one eager step timed alone: host issue time against its GPU time
-                torch.cuda.synchronize(self.device)
-                ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-                ev[0].record()
-                h0 = time.perf_counter()
+            elif auto and step in (1, 2):
+                # steps 1 and 2 eager, timed from one synchronisation: the host's
+                # issue time against the GPU time of the same work
+                if step == 1:
+                    torch.cuda.synchronize(self.device)
+                    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+                    ev[0].record()
+                    h0 = time.perf_counter()
                 logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
                                            position_offset=position)
-                host_s = time.perf_counter() - h0
-                ev[1].record()
-                ev[1].synchronize()
-                use_graphs = host_s >= 0.9 * ev[0].elapsed_time(ev[1]) * 1e-3
-                self.last_decode_launch = "graphs" if use_graphs else "eager"
+                if step == 2:
+                    host_s = time.perf_counter() - h0
+                    ev[1].record()
+                    ev[1].synchronize()
+                    use_graphs = host_s >= GRAPH_HOST_RATIO * ev[0].elapsed_time(ev[1]) * 1e-3
+                    self.last_decode_launch = "graphs" if use_graphs else "eager"
             else:
                 logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
                                            position_offset=position)
