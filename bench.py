@@ -627,13 +627,15 @@ def run_config(name, args, torch, ops):
         ops.pick_split(wl["total"].tolist(), cfg["hkv"], D, "fp8" if cfg["fp8"] else "bf16")
     per_segment = split == ops.SPLIT_PER_SEGMENT
     paired = split == ops.SPLIT_PAIRED
+    # as the KV cache does: the length order uploaded once (every step shifts all lengths alike)
+    order = torch.tensor(ops.length_order(wl["total"].tolist()), dtype=torch.int32, device="cuda") if paired else None
     lens_out = torch.empty_like(wl["positions"])
     fused = args.step_path != "two"
 
     def two_launch_step():
         ops.rope_append(wl["q_in"], wl["k_in"], wl["v_in"], wl["rope"], wl["positions"], layout, q_out=q_rot)
         ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
-                             split_tokens=split, workspace=ws)
+                             split_tokens=split, workspace=ws, length_order=order)
 
     def step():
         # the fused decode step: RoPE + append of the new token inside the attention launch(es)
@@ -642,11 +644,11 @@ def run_config(name, args, torch, ops):
             return
         ops.decode_attention_append(wl["rope"], wl["positions"], layout, wl["max_len"], q=wl["q_in"][:, :, 0],
                                     k=wl["k_in"][:, :, 0], v=wl["v_in"][:, :, 0], lens_out=lens_out, out=out,
-                                    workspace=ws, split_tokens=split)
+                                    workspace=ws, split_tokens=split, length_order=order)
 
     def attn_only():
         ops.decode_attention(q_rot.view(B, hq, D), layout, wl["seq_lens"], wl["max_len"], out=out,
-                             split_tokens=split, workspace=ws)
+                             split_tokens=split, workspace=ws, length_order=order)
 
     # each timed region gets its own warm-up: a kernel's first launch loads its code
     # object (~0.6 ms), which untimed warm-up keeps out of the per-step figures
@@ -674,8 +676,8 @@ def run_config(name, args, torch, ops):
             "cached_tokens": tokens,
             "split_tokens": ("per segment (-1: one workgroup per (sequence, KV head), merged in LDS; all lengths "
                              "equal)" if per_segment
-                             else "paired (-2: the sequences ranked by length, one workgroup per KV head and rank "
-                             "pair (p, B - 1 - p), merged in LDS)" if paired
+                             else "paired (-2: the sequences ordered by length on the host, one workgroup per KV "
+                             "head and rank pair (p, B - 1 - p), merged in LDS)" if paired
                              else split or "balanced (equal 32-token tiles per wave)"),
             "parallelism": "single GPU",
             "step_path": ("one launch: RoPE + append inside the per-segment attention kernel "

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 5
+#define TT_ABI_VERSION 6
 
 #define TT_OK 0
 #define TT_ERR_INVALID_ARGUMENT (-1)
@@ -250,6 +250,15 @@ int tt_rope_append_partials_fp8(const float *q_in, const int64_t q_in_strides[3]
  *   when); the VALU kernel (fp32 caches, head dims the MFMA tiles do not
  *   take) treats -1 and -2 as 0;
  *   128, 256, 512 or 1024 = fixed splits of that many tokens.
+ * length_order: NULL, or with TT_SPLIT_PAIRED a device int32 [batch] array
+ *   holding the batch's sequence indices ordered by seq_lens, longest first,
+ *   ties by the smaller index (a permutation of 0 .. batch - 1; entries are
+ *   clamped into that range). Workgroup p then takes the sequences
+ *   length_order[p] and length_order[batch - 1 - p] instead of ranking the
+ *   lengths itself (which costs each workgroup a few microseconds before its
+ *   first tile). The order does not change when every length grows by the
+ *   same count, so a decode loop uploads it once per change of its batch.
+ *   Ignored by the other partitions.
  * workspace: device scratch of at least tt_decode_workspace_bytes(...) bytes
  *   for the same (batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
  *   split_tokens); its contents need no initialisation. May be NULL when the
@@ -277,8 +286,8 @@ int tt_gqa_decode_attn_bf16(const void *q, const int64_t q_strides[2],
                             void *out, const int64_t out_strides[2],
                             int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                             int64_t head_dim, int64_t page_size, float sm_scale,
-                            int64_t split_tokens, void *workspace, size_t workspace_bytes,
-                            tt_stream_t stream);
+                            int64_t split_tokens, const int32_t *length_order,
+                            void *workspace, size_t workspace_bytes, tt_stream_t stream);
 
 /*
  * As tt_gqa_decode_attn_bf16 with an fp8-e4m3fn cache and per-(token, head)
@@ -295,13 +304,13 @@ int tt_gqa_decode_attn_fp8(const void *q, const int64_t q_strides[2],
                            void *out, const int64_t out_strides[2],
                            int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                            int64_t head_dim, int64_t page_size, float sm_scale,
-                           int64_t split_tokens, void *workspace, size_t workspace_bytes,
-                           tt_stream_t stream);
+                           int64_t split_tokens, const int32_t *length_order,
+                           void *workspace, size_t workspace_bytes, tt_stream_t stream);
 
 /*
  * As tt_gqa_decode_attn_bf16 with fp32 q, cache and out (the reference
- * without autocast). Requirements as above except that 4-byte alignment
- * suffices.
+ * without autocast), without length_order (the VALU kernel has no paired
+ * partition). Requirements as above except that 4-byte alignment suffices.
  */
 int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2],
                            const void *k_cache, const void *v_cache,
@@ -365,8 +374,9 @@ int tt_prefill_attn_fp8(const void *q, const int64_t q_strides[3],
  * the splits in order. The wave that reads a segment's last tile writes that
  * segment's new k / v first, so no other launch is needed. max_seq_len must
  * bound positions[b] + 1 and the cache capacity. split_tokens: 0 (balanced
- * partition), TT_SPLIT_PER_SEGMENT or TT_SPLIT_PAIRED, as for
- * tt_gqa_decode_attn_bf16 (bf16 / fp8 caches); workspace as
+ * partition), TT_SPLIT_PER_SEGMENT or TT_SPLIT_PAIRED, and length_order
+ * (ordered by positions), as for tt_gqa_decode_attn_bf16 (bf16 / fp8
+ * caches); workspace as
  * tt_decode_workspace_bytes(..., split_tokens) (NULL for the two one-launch
  * partitions).
  */
@@ -378,7 +388,8 @@ int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], 
                                void *v_cache, const int64_t cache_strides[3], int64_t capacity, void *out,
                                const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
-                               void *workspace, size_t workspace_bytes, tt_stream_t stream);
+                               const int32_t *length_order, void *workspace, size_t workspace_bytes,
+                               tt_stream_t stream);
 
 /* As tt_decode_attn_append_bf16 with an fp8-e4m3fn cache (per-(token, head) scales written by the append). */
 int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
@@ -389,8 +400,8 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               void *v_cache, float *k_scale, float *v_scale, const int64_t cache_strides[3],
                               int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                              float sm_scale, int64_t split_tokens, void *workspace, size_t workspace_bytes,
-                              tt_stream_t stream);
+                              float sm_scale, int64_t split_tokens, const int32_t *length_order, void *workspace,
+                              size_t workspace_bytes, tt_stream_t stream);
 
 /*
  * tt_decode_attn_append_bf16 without the workspace argument: the attention

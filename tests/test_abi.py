@@ -47,7 +47,7 @@ def test_noalloc_scratch_size_matches_header():
 
 
 def test_abi_version():
-    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 5
+    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_workspace_and_split_sizing():
@@ -122,7 +122,7 @@ def _attn(lib, **kw):
         a["q"], _lib.strides(*a["q_strides"]), a["k"], a["v"], _lib.strides(*a["cache_strides"]),
         a["seq_lens"], a["max_len"], a["page_table"], a["max_pages"], a["num_pages"], a["out"],
         _lib.strides(*a["out_strides"]), a["batch"], a["hq"], a["hkv"], a["head_dim"], a["page_size"],
-        a["sm_scale"], a["split"], a["ws"], a["ws_bytes"], None)
+        a["sm_scale"], a["split"], None, a["ws"], a["ws_bytes"], None)
 
 
 @pytest.mark.skipif(not _no_gpu(), reason="fake-pointer validation cases run only without a GPU")
@@ -154,7 +154,7 @@ def test_fused_step_rejects_fixed_splits():
     s2 = _lib.strides(512, 64)
     args = [FAKE, s2, FAKE, s2, FAKE, s2, 0, 0, FAKE, 100, FAKE, None, 50, None, 0, 0, FAKE, FAKE,
             _lib.strides(2 * 64 * 64, 16 * 64, 64 * 64), 64, FAKE, s2, 2, 8, 2, 64, 16, 0.125]
-    assert lib.tt_decode_attn_append_bf16(*args, 512, FAKE, 1 << 30, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert lib.tt_decode_attn_append_bf16(*args, 512, None, FAKE, 1 << 30, None) == _lib.TT_ERR_INVALID_ARGUMENT
     assert "split_tokens" in lib.tt_last_error_string().decode()
 
 

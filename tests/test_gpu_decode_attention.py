@@ -27,7 +27,7 @@ def _dev(arr, dtype):
 
 
 def run_case(lengths, Hq=32, Hkv=8, D=128, P=16, paged=False, fp8=False, seed=0, split_tokens=0, f32=False,
-             zero_first=False, workspace=None):
+             zero_first=False, workspace=None, length_order=None):
     from tinytron_amd import ops
 
     rng = np.random.default_rng(seed)
@@ -81,7 +81,12 @@ def run_case(lengths, Hq=32, Hkv=8, D=128, P=16, paged=False, fp8=False, seed=0,
     if zero_first:
         dev_lens[0] = 0
     seq = torch.from_numpy(dev_lens).to(DEV)
-    out = ops.decode_attention(q, kv, seq, max_len, split_tokens=split_tokens, workspace=workspace)
+    if isinstance(length_order, str):  # "sorted": the order of the lengths the kernel attends
+        length_order = ops.length_order(dev_lens.tolist())
+    if length_order is not None:
+        length_order = torch.tensor(length_order, dtype=torch.int32, device=DEV)
+    out = ops.decode_attention(q, kv, seq, max_len, split_tokens=split_tokens, workspace=workspace,
+                               length_order=length_order)
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     ref = ref_attention(qf, data["keys"], data["values"], Hkv, sm_scale(D))

@@ -13,6 +13,10 @@ segments' tiles, merged in LDS, one launch, no workspace; B <= 256).
   caches run the VALU kernel, which takes -2 as 0.
 * The fused decode step in this partition against the two-launch path in the
   same partition, bit for bit (output, cache bytes, fp8 scales, lengths).
+* With the caller's length order (length_order, the order the device ranks)
+  the outputs equal the device-ranked ones bit for bit (same pairs, same
+  arithmetic), for the two-launch and the fused step; any other permutation
+  pairs differently and stays within the oracle tolerance.
 * More than 256 sequences are refused.
 * The KV cache picks the partition from its host lengths (ragged, B <= 256,
   rank pairs filling the CUs evenly: tt_decode_pick_split); a model's decode
@@ -86,7 +90,7 @@ def test_paired_refuses_more_than_256_sequences():
     st = _lib.load().tt_gqa_decode_attn_bf16(
         q.data_ptr(), _lib.strides(*q.stride()[:2]), k.data_ptr(), k.data_ptr(),
         _lib.strides(Hkv * cap * D, 16 * D, cap * D), lens.data_ptr(), 8, None, 0, 0,
-        out.data_ptr(), _lib.strides(*out.stride()[:2]), B, Hq, Hkv, D, 16, 0.125, PAIRED, None, 0, None)
+        out.data_ptr(), _lib.strides(*out.stride()[:2]), B, Hq, Hkv, D, 16, 0.125, PAIRED, None, None, 0, None)
     assert st == _lib.TT_ERR_UNSUPPORTED
     assert "256" in _lib.load().tt_last_error_string().decode()
 
@@ -147,9 +151,90 @@ def test_cache_picks_paired_for_ragged_lengths_and_matches_balanced():
                 for i in range(cfg.num_layer):
                     cache.get_layer_cache(i)._split = 0  # force the balanced partition
             assert cache.get_layer_cache(0)._attention_split() == (PAIRED if name == "paired" else 0)
+            if name == "paired":  # the host's length order, uploaded once for the decode loop
+                order = cache.get_layer_cache(0)._order
+                assert order is not None and order.tolist() == ops.length_order(lens)
             rows = []
             for s in range(steps.shape[1]):
                 out, cache = model(steps[:, s:s + 1], past_key_values=cache, use_cache=True)
                 rows.append(out[:, -1].float().cpu())
             logits[name] = torch.stack(rows)
     assert _ulps_of_row_max(logits["paired"], logits["balanced"]) <= 4
+
+
+@pytest.mark.parametrize("i", [0, 1, 6, 9, 10])
+def test_paired_host_order_equals_device_ranking(i):
+    lengths, Hq, Hkv, D, P, paged, fp8 = CASES[i]
+    print(f"paired order case {i}: {CASES[i]}", flush=True)
+    dev, ref, _ = run_case(lengths, Hq=Hq, Hkv=Hkv, D=D, P=P, paged=paged, fp8=fp8, seed=170 + i, split_tokens=PAIRED)
+    host, _, _ = run_case(lengths, Hq=Hq, Hkv=Hkv, D=D, P=P, paged=paged, fp8=fp8, seed=170 + i, split_tokens=PAIRED,
+                          length_order="sorted")
+    assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))
+    assert_close(host, ref)
+
+
+def test_paired_other_permutation_stays_correct():
+    lengths = [300, 1, 2000, 65, 640, 33, 900, 12]
+    perm = [3, 0, 7, 5, 1, 6, 2, 4]  # not the length order: other pairs, same coverage
+    got, ref, _ = run_case(lengths, Hq=16, Hkv=4, D=64, paged=True, seed=9, split_tokens=PAIRED, length_order=perm)
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_fused_paired_step_host_order_equals_device_ranking(kv):
+    """The fused step with the caller's order writes the same cache bytes and
+    outputs as with the device's ranking (the order of positions + 1), from
+    the same cache state."""
+    from tinytron_amd import ops
+    from tests.test_gpu_decode_fused import _restore, _snapshot
+
+    lens = [7, 300, 64, 1000, 2, 129, 129]
+    layer, table, g = _setup(kv, True, 64, 16, 4, lens, seed=31)
+    lay = layer.layout
+    pos = layer._lens_dev[layer._cur].clone()
+    B = pos.shape[0]
+    q1 = torch.randn(B, 16, 64, generator=g).to(torch.bfloat16).cuda()
+    k1 = torch.randn(B, 4, 64, generator=g).to(torch.bfloat16).cuda()
+    v1 = torch.randn(B, 4, 64, generator=g).to(torch.bfloat16).cuda()
+    snap = _snapshot(lay)
+    runs = []
+    for use_order in (False, True):
+        _restore(lay, snap)
+        order = torch.tensor(ops.length_order(lens), dtype=torch.int32, device="cuda") if use_order else None
+        out = ops.decode_attention_append(table, pos, lay, max(lens) + 1, q=q1, k=k1, v=v1, split_tokens=PAIRED,
+                                          length_order=order)
+        torch.cuda.synchronize()
+        runs.append([out.clone()] + _snapshot(lay))
+    for x, y in zip(runs[0], runs[1]):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+
+
+def test_engine_paired_graphs_equal_eager():
+    """A ragged batch that picks the paired partition (asserted) decodes the
+    same tokens and log-probabilities bit for bit with the step replayed from
+    captured graphs as eagerly. Regression: capture restores the caches' host
+    lengths, which re-picks the partition; the length order must stay in the
+    buffer the graphs captured (a fresh tensor each pick left the graphs
+    reading freed memory and pairing wrongly)."""
+    from tinytron_amd import ops
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+    from tests.test_gpu_engine import _c1_config
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Hkv = 8
+    B = 2 * cus // Hkv
+    lens = [16 * (i + 1) for i in range(B)]
+    assert ops.pick_split(lens, Hkv, 64, "bf16") == PAIRED
+    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=Hkv,
+                     vocab_size=4096, block_size=max(lens) + 32)
+    model = GPT(cfg, device="cuda", dtype=torch.bfloat16)
+    prompt = torch.randint(0, cfg.vocab_size, (B, max(lens)), generator=torch.Generator().manual_seed(23))
+    runs = {}
+    for name, use_graphs in (("eager", False), ("graphs", True)):
+        eng = InferenceEngine(cfg, device="cuda", dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True,
+                              model=model, use_graphs=use_graphs)
+        toks, extra = eng.generate(prompt, 24, top_k=1, prompt_lens=lens, return_stats=True, return_logprobs=True)
+        runs[name] = (toks.cpu(), extra["token_log_probs"].float().cpu())
+    assert torch.equal(runs["eager"][0], runs["graphs"][0])
+    assert torch.equal(runs["eager"][1], runs["graphs"][1])

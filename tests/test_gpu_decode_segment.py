@@ -78,7 +78,7 @@ def test_segment_without_workspace():
     st = _lib.load().tt_gqa_decode_attn_bf16(
         q.data_ptr(), _lib.strides(*q.stride()[:2]), k.data_ptr(), v.data_ptr(),
         _lib.strides(2 * 48 * 64, 16 * 64, 48 * 64), lens.data_ptr(), 40, None, 0, 0,
-        out.data_ptr(), _lib.strides(*out.stride()[:2]), 3, 8, 2, 64, 16, 0.125, SEG, None, 0, None)
+        out.data_ptr(), _lib.strides(*out.stride()[:2]), 3, 8, 2, 64, 16, 0.125, SEG, None, None, 0, None)
     assert st == _lib.TT_OK, _lib.load().tt_last_error_string()
     ref_out = ops.decode_attention(q, ops.KVLayout(k=k, v=v, strides=(2 * 48 * 64, 16 * 64, 48 * 64), num_heads=2,
                                                    head_dim=64, page_size=16, capacity=48, kind="bf16"),

@@ -362,8 +362,8 @@ def test_sampled_generation_is_seeded_and_graph_invariant():
 
 
 def test_auto_launch_mode_gives_the_eager_tokens():
-    """The engine's default launch mode (eager or graph replay, chosen on the
-    second step from the host's issue time) changes no token or
+    """The engine's default launch mode (eager or graph replay, chosen after
+    the third decode step from the host's issue time) changes no token or
     log-probability: it equals a forced-eager run bit for bit, and says which
     mode it took."""
     from tinytron_amd.engine import InferenceEngine

@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 TT_OK = 0
 TT_ERR_INVALID_ARGUMENT = -1
@@ -66,6 +66,8 @@ _ATTN_TAIL = [
     _vp, _size,                                      # workspace, workspace_bytes
     _vp,                                             # stream
 ]
+# bf16 / fp8 decode attention: the length order (paired partition) after split_tokens
+_ATTN_TAIL_ORDER = _ATTN_TAIL[:-3] + [_i32p] + _ATTN_TAIL[-3:]
 
 _ROWS_TAIL = [
     _i64p,                                           # cache_strides
@@ -88,10 +90,10 @@ _DECODE_APPEND_TAIL = [
     _i64p, _i64,                                     # cache_strides, capacity
     _vp, _i64p,                                      # out, out_strides
     _i64, _i64, _i64, _i64, _i64,                    # batch, H_q, H_kv, head_dim, page_size
-    _f32, _i64,                                      # sm_scale, split_tokens
+    _f32, _i64, _i32p,                               # sm_scale, split_tokens, length_order
     _vp, _size, _vp,                                 # workspace, workspace_bytes, stream
 ]
-_DECODE_APPEND_TAIL_NOALLOC = _DECODE_APPEND_TAIL[:-5] + [_f32, _vp]  # sm_scale, stream (scratch inside)
+_DECODE_APPEND_TAIL_NOALLOC = _DECODE_APPEND_TAIL[:-6] + [_f32, _vp]  # sm_scale, stream (scratch inside)
 NOALLOC_SCRATCH_BYTES = 32 << 20  # TT_NOALLOC_SCRATCH_BYTES
 
 _SAMPLE = [
@@ -121,8 +123,8 @@ SIGNATURES = {
         ctypes.c_int, _vp], ctypes.c_int),           # fp8_cache, stream
     "tt_rope_append_partials_bf16": (_ROPE_PART_HEAD + _ROPE_TAIL, ctypes.c_int),
     "tt_rope_append_partials_fp8": (_ROPE_PART_HEAD + [_vp, _vp] + _ROPE_TAIL, ctypes.c_int),
-    "tt_gqa_decode_attn_bf16": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
-    "tt_gqa_decode_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ATTN_TAIL, ctypes.c_int),
+    "tt_gqa_decode_attn_bf16": (_ATTN_HEAD + _ATTN_TAIL_ORDER, ctypes.c_int),
+    "tt_gqa_decode_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ATTN_TAIL_ORDER, ctypes.c_int),
     "tt_gqa_decode_attn_f32": (_ATTN_HEAD + _ATTN_TAIL, ctypes.c_int),
     "tt_rows_attn_bf16": (_ATTN_HEAD + _ROWS_TAIL, ctypes.c_int),
     "tt_rows_attn_fp8": (_ATTN_HEAD + [_vp, _vp] + _ROWS_TAIL, ctypes.c_int),

@@ -70,6 +70,8 @@ class _LayerCacheBase:
         self.workspace = None
         self.static_max_len = None  # graph capture: launch-size bound fixed at the capacity
         self._split = None  # ops.pick_split over the base lengths, computed on first use after they change
+        self._order = None  # the paired partition's length order (_order_buf once filled), with _split
+        self._order_buf = None  # device int32 [B]: one buffer for the cache's life, so captured graphs keep it
 
     # -- lengths ---------------------------------------------------------------
     @property
@@ -206,7 +208,19 @@ class _LayerCacheBase:
         made once per change of the base lengths."""
         if self._split is None:
             lay = self.layout
-            self._split = ops.pick_split(self._base, lay.num_heads, lay.head_dim, lay.kind)
+            split = ops.pick_split(self._base, lay.num_heads, lay.head_dim, lay.kind)
+            if split == ops.SPLIT_PAIRED and not torch.cuda.is_current_stream_capturing():
+                # the rank order, once per change of the lengths (a step adds the same count to
+                # every length): the kernel reads its pair instead of ranking the batch itself.
+                # Written in place into one buffer, so a graph captured with it reads the current
+                # order; any permutation gives correct results (a stale one only pairs worse).
+                # Under graph capture no host copy can be recorded: the buffer keeps its last
+                # order, or the kernel ranks on the device while there is none.
+                if self._order_buf is None:
+                    self._order_buf = torch.empty(self.batch_size, dtype=torch.int32, device=lay.k.device)
+                self._order_buf.copy_(torch.tensor(ops.length_order(self._base), dtype=torch.int32))
+                self._order = self._order_buf
+            self._split = split
         return self._split
 
     def _decode_step(self, rope_table, out, **inputs) -> torch.Tensor:
@@ -215,9 +229,10 @@ class _LayerCacheBase:
             self.workspace = ops.Workspace(rope_table.device)
         bound = self.static_max_len if self.static_max_len is not None else self.current_length + 1
         nxt = 1 - self._cur
+        split = self._attention_split()
         out = ops.decode_attention_append(rope_table, self._lens_dev[self._cur], self.layout, bound,
                                           lens_out=self._lens_dev[nxt], out=out, workspace=self.workspace,
-                                          split_tokens=self._attention_split(), **inputs)
+                                          split_tokens=split, length_order=self._order, **inputs)
         self._cur = nxt
         self._advance_all(1)
         return out
@@ -250,8 +265,9 @@ class _LayerCacheBase:
         if self.workspace is None:
             self.workspace = ops.Workspace(q.device)
         bound = self.static_max_len if self.static_max_len is not None else self.current_length
+        split = self._attention_split()
         return ops.decode_attention(q, self.layout, self.seq_lens, bound, out=out, workspace=self.workspace,
-                                    split_tokens=self._attention_split())
+                                    split_tokens=split, length_order=self._order)
 
     # -- host-state snapshots for graph capture ------------------------------------
     def host_state(self):

@@ -249,7 +249,8 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
                   int64_t num_pages, void *out, const int64_t out_strides[2], int64_t batch, int64_t num_q_heads,
                   int64_t num_kv_heads, int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
                   void *workspace, size_t ws_bytes, tt_stream_t stream, const tt::DecodeAppend *ap = nullptr,
-                  bool exact_slots = false, const int32_t *seq_of_row = nullptr, int64_t num_seqs = 0) {
+                  bool exact_slots = false, const int32_t *seq_of_row = nullptr, int64_t num_seqs = 0,
+                  const int32_t *length_order = nullptr) {
   // ap != null: the fused step (q / k / v from ap, seq_lens = lengths before the step)
   // exact_slots: the balanced workspace holds slots for the launched grid only (allocation-free entry point)
   // seq_of_row != null: `batch` query rows, row b reading the cache of sequence seq_of_row[b] < num_seqs
@@ -392,6 +393,7 @@ int decode_common(tt::CacheKind kind, const void *q, const int64_t q_strides[2],
   a.page_shift = page_shift;
   a.split_tokens = (int)split;
   a.max_splits = (int)splits;
+  a.order = split == tt::kSplitPaired ? length_order : nullptr;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   (void)hipGetLastError();
   if (ap != nullptr) {
@@ -415,8 +417,9 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
                          int64_t max_pages, int64_t num_pages, void *k_cache, void *v_cache, float *k_scale,
                          float *v_scale, const int64_t cache_strides[3], int64_t capacity, void *out,
                          const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
-                         int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens, void *workspace,
-                         size_t ws_bytes, tt_stream_t stream, bool exact_slots = false) {
+                         int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
+                         const int32_t *length_order, void *workspace, size_t ws_bytes, tt_stream_t stream,
+                         bool exact_slots = false) {
   TT_CHECK(q_in && k_in && v_in && rope_table && positions, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
   TT_CHECK(split_tokens == 0 || split_tokens == tt::kSplitPerSegment || split_tokens == tt::kSplitPaired,
            TT_ERR_INVALID_ARGUMENT,
@@ -451,7 +454,7 @@ int decode_append_common(tt::CacheKind kind, const void *q_in, const int64_t q_i
   return decode_common(kind, nullptr, nullptr, k_cache, v_cache, k_scale, v_scale, cache_strides, positions,
                        max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
                        num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, ws_bytes, stream, &ap,
-                       exact_slots);
+                       exact_slots, nullptr, 0, length_order);
 }
 
 int linear_common(const void *x, int64_t ldx, const void *weight, int64_t ldw, int packed, float *partials,
@@ -749,10 +752,12 @@ int tt_gqa_decode_attn_bf16(const void *q, const int64_t q_strides[2], const voi
                             const int32_t *page_table, int64_t max_pages, int64_t num_pages, void *out,
                             const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                             int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
-                            void *workspace, size_t workspace_bytes, tt_stream_t stream) {
+                            const int32_t *length_order, void *workspace, size_t workspace_bytes,
+                            tt_stream_t stream) {
   return decode_common(tt::CacheKind::kBF16, q, q_strides, k_cache, v_cache, nullptr, nullptr, cache_strides,
                        seq_lens, max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
-                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream,
+                       nullptr, false, nullptr, 0, length_order);
 }
 
 int tt_gqa_decode_attn_fp8(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
@@ -760,11 +765,12 @@ int tt_gqa_decode_attn_fp8(const void *q, const int64_t q_strides[2], const void
                            const int32_t *seq_lens, int64_t max_seq_len, const int32_t *page_table,
                            int64_t max_pages, int64_t num_pages, void *out, const int64_t out_strides[2],
                            int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                           int64_t page_size, float sm_scale, int64_t split_tokens, void *workspace,
-                           size_t workspace_bytes, tt_stream_t stream) {
+                           int64_t page_size, float sm_scale, int64_t split_tokens, const int32_t *length_order,
+                           void *workspace, size_t workspace_bytes, tt_stream_t stream) {
   return decode_common(tt::CacheKind::kFP8, q, q_strides, k_cache, v_cache, k_scale, v_scale, cache_strides,
                        seq_lens, max_seq_len, page_table, max_pages, num_pages, out, out_strides, batch, num_q_heads,
-                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream);
+                       num_kv_heads, head_dim, page_size, sm_scale, split_tokens, workspace, workspace_bytes, stream,
+                       nullptr, false, nullptr, 0, length_order);
 }
 
 int tt_gqa_decode_attn_f32(const void *q, const int64_t q_strides[2], const void *k_cache, const void *v_cache,
@@ -987,12 +993,13 @@ int tt_decode_attn_append_bf16(const void *q_in, const int64_t q_in_strides[2], 
                                void *v_cache, const int64_t cache_strides[3], int64_t capacity, void *out,
                                const int64_t out_strides[2], int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                int64_t head_dim, int64_t page_size, float sm_scale, int64_t split_tokens,
-                               void *workspace, size_t workspace_bytes, tt_stream_t stream) {
+                               const int32_t *length_order, void *workspace, size_t workspace_bytes,
+                               tt_stream_t stream) {
   return decode_append_common(tt::CacheKind::kBF16, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
                               splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
                               page_table, max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
-                              sm_scale, split_tokens, workspace, workspace_bytes, stream);
+                              sm_scale, split_tokens, length_order, workspace, workspace_bytes, stream);
 }
 
 int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
@@ -1003,13 +1010,13 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               void *v_cache, float *k_scale, float *v_scale, const int64_t cache_strides[3],
                               int64_t capacity, void *out, const int64_t out_strides[2], int64_t batch,
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                              float sm_scale, int64_t split_tokens, void *workspace, size_t workspace_bytes,
-                              tt_stream_t stream) {
+                              float sm_scale, int64_t split_tokens, const int32_t *length_order, void *workspace,
+                              size_t workspace_bytes, tt_stream_t stream) {
   return decode_append_common(tt::CacheKind::kFP8, q_in, q_in_strides, k_in, k_in_strides, v_in, v_in_strides,
                               splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
                               page_table, max_pages, num_pages, k_cache, v_cache, k_scale, v_scale, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
-                              sm_scale, split_tokens, workspace, workspace_bytes, stream);
+                              sm_scale, split_tokens, length_order, workspace, workspace_bytes, stream);
 }
 
 int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_strides[2], const void *k_in,
@@ -1028,7 +1035,7 @@ int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_stri
                               splits, split_stride, rope_table, rope_table_len, positions, lens_out, max_seq_len,
                               page_table, max_pages, num_pages, k_cache, v_cache, nullptr, nullptr, cache_strides,
                               capacity, out, out_strides, batch, num_q_heads, num_kv_heads, head_dim, page_size,
-                              sm_scale, 0, ws, kScratchBytes, stream, /*exact_slots=*/true);
+                              sm_scale, 0, nullptr, ws, kScratchBytes, stream, /*exact_slots=*/true);
 }
 
 size_t tt_sample_workspace_bytes(int64_t m, int64_t vocab, int64_t top_k) {

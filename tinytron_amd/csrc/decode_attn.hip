@@ -45,6 +45,10 @@
 
 namespace tt {
 namespace {
+// Threads of every 4-wave kernel here (all but the paired one). Loops stride
+// by this constant rather than blockDim.x: that is a global load from the
+// dispatch's arguments (~1 us at kernel start, ahead of the first loop).
+constexpr int kBlockThreads = 64 * kWavesPerBlock;
 
 // floats of the LDS merge area: [4][G][D] outputs, [4][16] maxima, [4][16] sums
 __host__ __device__ constexpr int merge_floats(int G, int D) { return kWavesPerBlock * G * D + 2 * kWavesPerBlock * 16; }
@@ -196,7 +200,7 @@ __device__ __forceinline__ void split_item(const DecodeArgs &a, int b, int hk, i
   }
   __syncthreads();
   const int64_t item = ((int64_t)b * a.hkv + hk) * a.max_splits + split;
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < G * D; idx += kBlockThreads) {
     const int head = idx / D;
     const int d = idx - head * D;
     float M = kNegInf;
@@ -231,7 +235,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int per = (B + blockDim.x - 1) / blockDim.x;
+  const int per = (B + kBlockThreads - 1) / kBlockThreads;
   const int first = tid * per;
   int local = 0;
   for (int i = 0; i < per; ++i) {
@@ -261,7 +265,7 @@ __device__ __forceinline__ void build_split_prefix(const DecodeArgs &a, int spli
       run += split_count(L, split_tokens, extra);
     }
   }
-  if (tid == blockDim.x - 1) prefix[B] = base + v;
+  if (tid == kBlockThreads - 1) prefix[B] = base + v;
   __syncthreads();
 }
 
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeArgs a) {
   float *merge = reinterpret_cast<float *>(smem_v + kVAll);
   // V slots start at zero: rows past a sequence's end are never written, so
   // what P = 0 meets there is a previous tile's finite V or zero.
-  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+  for (int i = threadIdx.x; i < kVAll / 16; i += kBlockThreads)
     reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
   int *wave_sums = reinterpret_cast<int *>(merge + merge_floats(a.group, D));
   int *lens = wave_sums + kWavesPerBlock;
@@ -759,7 +763,7 @@ __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeApp
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char *smem_v = reinterpret_cast<char *>(smem);
-  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+  for (int i = threadIdx.x; i < kVAll / 16; i += kBlockThreads)
     reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
   int *wave_sums = reinterpret_cast<int *>(smem_v + kVAll);
   int *prefix = wave_sums + kWavesPerBlock;
@@ -769,10 +773,10 @@ __device__ __forceinline__ void stream_body(const DecodeArgs &a, const DecodeApp
          wave * 16 * D;
   build_split_prefix(a, kTileTokens, nullptr, prefix, wave_sums, a.seg_cost);  // ends with a block barrier
   if (blockIdx.x == 0) {  // for the merge kernel (and the next step's lengths)
-    for (int i = threadIdx.x; i <= a.batch; i += blockDim.x) a.ws_prefix[i] = prefix[i];
+    for (int i = threadIdx.x; i <= a.batch; i += kBlockThreads) a.ws_prefix[i] = prefix[i];
     if constexpr (kAppend)
       if (ap->lens_out != nullptr)
-        for (int i = threadIdx.x; i < a.batch; i += blockDim.x) ap->lens_out[i] = a.seq_lens[i] + 1;
+        for (int i = threadIdx.x; i < a.batch; i += kBlockThreads) ap->lens_out[i] = a.seq_lens[i] + 1;
   }
   const int64_t W = (int64_t)__builtin_amdgcn_readfirstlane(prefix[a.batch]) * a.hkv;
   const int64_t NW = a.stream_waves;
@@ -858,13 +862,13 @@ __device__ __forceinline__ void segment_body(const DecodeArgs &a, const DecodeAp
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   char *smem_v = reinterpret_cast<char *>(smem);
-  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+  for (int i = threadIdx.x; i < kVAll / 16; i += kBlockThreads)
     reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
   uint16_t *qs = nullptr;
   if constexpr (kAppend) {
     qs = reinterpret_cast<uint16_t *>(smem_v + kVAll) + wave * 16 * D;
     if (blockIdx.x == 0 && ap->lens_out != nullptr)  // the next step's lengths
-      for (int i = threadIdx.x; i < a.batch; i += blockDim.x) ap->lens_out[i] = a.seq_lens[i] + 1;
+      for (int i = threadIdx.x; i < a.batch; i += kBlockThreads) ap->lens_out[i] = a.seq_lens[i] + 1;
   }
   __syncthreads();  // V slots zeroed
 
@@ -925,7 +929,7 @@ __device__ __forceinline__ void segment_body(const DecodeArgs &a, const DecodeAp
   // Thread t merges column pairs (2p, 2p + 1) of head p / (D / 2): one set of
   // head weights per pair, and at G * D <= 512 a single pair per thread.
   uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * G * a.o_sh;
-  for (int pr = threadIdx.x; pr < G * (D / 2); pr += blockDim.x) {
+  for (int pr = threadIdx.x; pr < G * (D / 2); pr += kBlockThreads) {
     const int head = pr / (D / 2);
     const int d = 2 * (pr - head * (D / 2));
     if (d >= a.head_dim) continue;  // head_dim is even: d + 1 < head_dim too
@@ -973,7 +977,8 @@ __global__ __launch_bounds__(256, kStreamOcc) void decode_segment_append_kernel(
 // its tiles) evenly, as the balanced partition does the whole batch's, so a
 // wave holds at most one piece of each segment; the pieces merge in LDS and the
 // workgroup writes both segments' rows: one launch, no workspace.
-static_assert(kMaxPairedBatch == 256, "the paired kernel's LDS holds 256 length keys");
+static_assert(kMaxPairedBatch == 256 && kMaxPairedBatch % 16 == 0, "the paired kernel's LDS holds 256 length keys");
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 // waves per paired workgroup: as many per CU as the balanced kernel at one
 // workgroup per CU
 constexpr int paired_waves(int tile_d) { return tile_d <= 64 ? 8 : 4; }
@@ -999,6 +1004,7 @@ template <int D, bool kFP8, bool kAppend, bool kPartIn, bool kPad, int NWV>
 __device__ __forceinline__ void paired_body(const DecodeArgs &a, const DecodeAppend *ap) {
   constexpr int kVAll = NWV * Tile<D, kFP8>::kVBytes;
   constexpr int NDB = D / 32;
+  constexpr int kPairThreads = 64 * NWV;  // the launch's block size (blockDim.x is a load from the dispatch)
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1008,32 +1014,62 @@ __device__ __forceinline__ void paired_body(const DecodeArgs &a, const DecodeApp
   int *keys = reinterpret_cast<int *>(smem_v + (paired_lds(D, kFP8, kAppend, G, NWV) -
                                                (int)sizeof(int) * ((int)kMaxPairedBatch + 2)));
   int *pair = keys + kMaxPairedBatch;
-  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+  for (int i = threadIdx.x; i < kVAll / 16; i += kPairThreads)
     reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
   uint16_t *qs = nullptr;
   if constexpr (kAppend) {
     qs = reinterpret_cast<uint16_t *>(smem_v + kVAll) + wave * 16 * D;
     if (blockIdx.x == 0 && ap->lens_out != nullptr)  // the next step's lengths
-      for (int i = threadIdx.x; i < NB; i += blockDim.x) ap->lens_out[i] = a.seq_lens[i] + 1;
+      for (int i = threadIdx.x; i < NB; i += kPairThreads) ap->lens_out[i] = a.seq_lens[i] + 1;
   }
-  for (int b = threadIdx.x; b < NB; b += blockDim.x) keys[b] = max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
   const int p = (int)(blockIdx.x / (unsigned)a.hkv);
   const int hk = (int)(blockIdx.x - (unsigned)p * (unsigned)a.hkv);
-  if (threadIdx.x == 0) pair[1] = -1;
-  __syncthreads();  // V slots zeroed, keys in place
-  // rank r(b) = sequences before b: longer, or as long with a smaller index
-  for (int b = threadIdx.x; b < NB; b += blockDim.x) {
-    const int kb = keys[b];
-    int r = 0;
-    for (int c = 0; c < NB; ++c) r += (keys[c] > kb || (keys[c] == kb && c < b)) ? 1 : 0;
-    if (r == p) pair[0] = b;
-    if (r == NB - 1 - p && r != p) pair[1] = b;
+  int bA, bB;  // bB = -1: the middle rank of an odd batch, alone
+  int LA, LB;
+  if (a.order != nullptr) {
+    // the caller's length order (indices clamped into the batch): no ranking
+    // on the device, whose serial chain (lengths to LDS, two barriers, the
+    // ranking) delayed every tile request by ~2.8 us at the C5 layer
+    bA = min(max(a.order[p], 0), NB - 1);
+    bB = NB - 1 - p != p ? min(max(a.order[NB - 1 - p], 0), NB - 1) : -1;
+    LA = max(min(a.seq_lens[bA] + a.len_add, a.max_len), 0);
+    LB = bB >= 0 ? max(min(a.seq_lens[bB] + a.len_add, a.max_len), 0) : 0;
+    __syncthreads();  // V slots zeroed
+  } else {
+    // keys padded with -1 (below every length) to a multiple of 16
+    const int nb16 = (NB + 15) & ~15;
+    for (int b = threadIdx.x; b < nb16; b += kPairThreads)
+      keys[b] = b < NB ? max(min(a.seq_lens[b] + a.len_add, a.max_len), 0) : -1;
+    if (threadIdx.x == 0) pair[1] = -1;
+    __syncthreads();  // V slots zeroed, keys in place
+    // rank r(b) = sequences before b: longer, or as long with a smaller index;
+    // 16 keys per step from four broadcast 16-byte LDS reads
+    for (int b = threadIdx.x; b < NB; b += kPairThreads) {
+      const int kb = keys[b];
+      const i32x4 *k4 = reinterpret_cast<const i32x4 *>(keys);
+      int r = 0;
+      for (int c0 = 0; c0 < nb16; c0 += 16) {
+        i32x4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = k4[c0 / 4 + i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r += (v[i][e] > kb || (v[i][e] == kb && c0 + 4 * i + e < b)) ? 1 : 0;
+      }
+      if (r == p) pair[0] = b;
+      if (r == NB - 1 - p && r != p) pair[1] = b;
+    }
+    __syncthreads();
+    bA = pair[0];
+    bB = pair[1];
+    LA = keys[bA];
+    LB = bB >= 0 ? keys[bB] : 0;
   }
-  __syncthreads();
-  const int bA = __builtin_amdgcn_readfirstlane(pair[0]);
-  const int bB = __builtin_amdgcn_readfirstlane(pair[1]);  // -1: the middle rank alone
-  const int LA = __builtin_amdgcn_readfirstlane(keys[bA]);
-  const int LB = bB >= 0 ? __builtin_amdgcn_readfirstlane(keys[bB]) : 0;
+  bA = __builtin_amdgcn_readfirstlane(bA);
+  bB = __builtin_amdgcn_readfirstlane(bB);
+  LA = __builtin_amdgcn_readfirstlane(LA);
+  LB = __builtin_amdgcn_readfirstlane(LB);
   const int ntA = (LA + kTileTokens - 1) / kTileTokens;
   const int ntB = (LB + kTileTokens - 1) / kTileTokens;
   const int lineA = ntA > 0 ? ntA + kStreamSegCost : 0;
@@ -1094,7 +1130,7 @@ __device__ __forceinline__ void paired_body(const DecodeArgs &a, const DecodeApp
     __syncthreads();
     // column pairs (2p, 2p + 1) of every head
     uint16_t *out = static_cast<uint16_t *>(a.out) + (int64_t)b * a.o_sb + (int64_t)hk * G * a.o_sh;
-    for (int pr = threadIdx.x; pr < G * (D / 2); pr += blockDim.x) {
+    for (int pr = threadIdx.x; pr < G * (D / 2); pr += kPairThreads) {
       const int head = pr / (D / 2);
       const int d = 2 * (pr - head * (D / 2));
       if (d >= a.head_dim) continue;  // head_dim is even: d + 1 < head_dim too
@@ -1204,7 +1240,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
   float *sl = sm + kWavesPerBlock * 16;              // [4][16]
   float *sq = sl + kWavesPerBlock * 16;              // [G][hd] query rows
   float *sp = sq + G * hd + wave * 64;               // per-wave [64] probabilities
-  for (int idx = threadIdx.x; idx < G * hd; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < G * hd; idx += kBlockThreads) {
     const int h = idx / hd;
     const int64_t qi = (int64_t)b * a.q_sb + (int64_t)(hk * G + h) * a.q_sh + (idx - h * hd);
     sq[idx] = K == CacheKind::kF32 ? static_cast<const float *>(a.q)[qi]
@@ -1274,7 +1310,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel_valu(DecodeArgs a, in
   }
   __syncthreads();
   const int64_t item = ((int64_t)b * a.hkv + hk) * a.max_splits + split;
-  for (int idx = threadIdx.x; idx < G * hd; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < G * hd; idx += kBlockThreads) {
     const int head = idx / hd;
     const int d = idx - head * hd;
     float M = kNegInf;

@@ -161,7 +161,7 @@ __device__ __forceinline__ void ordered_sums(const float *P, int S, int64_t stri
 
 // y[i] = bf16(sum_s P[s][i]), four elements per thread.
 __global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *P, int S, int64_t MN, uint16_t *y) {
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= MN) return;
   const int64_t ix[1] = {i};
   f32x4 sum[1];
@@ -250,7 +250,7 @@ __device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
 // Partials of the fused gate|up projection: columns [0, I) gate, [I, 2I) up.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float *P, int S, int64_t MN2, int I, int M,
                                                        uint16_t *y) {
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;  // index into [M, I]
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // index into [M, I]
   if (i >= (int64_t)M * I) return;
   const int64_t m = i / I;
   const int64_t c = i - m * I;
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
 // [M, I]; four columns per thread.
 __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t *g_in, int64_t ldg, const uint16_t *u_in,
                                                             int64_t ldu, int I, int64_t MI, uint16_t *y) {
-  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;  // index into [M, I]
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;  // index into [M, I]
   if (i >= MI) return;
   const int64_t m = i / I;
   const int64_t c = i - m * I;

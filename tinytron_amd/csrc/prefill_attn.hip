@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, kFP8>())) void prefill_
   extern __shared__ char smem_v[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  for (int i = threadIdx.x; i < kVAll / 16; i += blockDim.x)
+  for (int i = threadIdx.x; i < kVAll / 16; i += 64 * kWavesPerBlock)  // the block size (not a dispatch load)
     reinterpret_cast<u32x4 *>(smem_v)[i] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
 

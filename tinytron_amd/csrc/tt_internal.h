@@ -98,6 +98,9 @@ struct DecodeArgs {
   int page_shift;    // paged pools: log2(page_size); the contiguous store is addressed linearly
   float scale_log2;  // sm_scale * log2(e)
   int len_add;       // added to seq_lens[b] (1 when the kernel appends the step's token itself)
+  // paired partition: the batch's sequence indices ordered by length (longest
+  // first, ties by index), or null to rank them on the device
+  const int32_t *order;
   // balanced partition: line positions charged to each (sequence, KV head) segment
   // before its tiles, so that a wave's share counts the fixed start-up cost of
   // every segment piece it holds, not only its tiles (set by the launcher)

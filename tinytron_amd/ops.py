@@ -318,14 +318,29 @@ def workspace_bytes(batch: int, hq: int, hkv: int, head_dim: int, max_seq_len: i
     return int(_lib.load().tt_decode_workspace_bytes(batch, hq, hkv, head_dim, max_seq_len, split_tokens))
 
 
+def _check_order(length_order, B: int):
+    if length_order is not None and (length_order.dtype != torch.int32 or length_order.shape != (B,)
+                                     or not length_order.is_cuda or not length_order.is_contiguous()):
+        raise ValueError("length_order must be a contiguous int32 [B] device tensor")
+
+
+def length_order(lengths) -> list:
+    """The batch's sequence indices by length, longest first, ties by index:
+    the order the paired partition pairs (ranks p and B - 1 - p)."""
+    return sorted(range(len(lengths)), key=lambda b: (-int(lengths[b]), b))
+
+
 def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, max_seq_len: int,
                      out: torch.Tensor | None = None, sm_scale: float | None = None, split_tokens: int = 0,
-                     workspace: Workspace | None = None) -> torch.Tensor:
+                     workspace: Workspace | None = None, length_order: torch.Tensor | None = None) -> torch.Tensor:
     """GQA decode attention of q [B, H_q, D] over each sequence's seq_lens[b] cached tokens.
 
     Restates get_kv + gqa_impl + the all-True decode mask + SDPA
     (cache.py:47-51, attn.py:66-95, 420-423). ``max_seq_len`` is a host-side
-    bound of seq_lens used to size the grid.
+    bound of seq_lens used to size the grid. ``length_order`` (SPLIT_PAIRED,
+    bf16 / fp8 caches; optional): int32 [B] on the device, a permutation of
+    the batch ordered as ``length_order()`` orders seq_lens, which spares the
+    kernel its own ranking; None ranks on the device.
     """
     _require_cuda(q, layout.k, layout.v, seq_lens)
     _check_lastdim("q", q, 3)
@@ -340,6 +355,7 @@ def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, 
         raise ValueError(f"head_dim {D} does not match the cache's {layout.head_dim}")
     if seq_lens.dtype != torch.int32 or seq_lens.shape != (B,):
         raise ValueError("seq_lens must be int32 [B]")
+    _check_order(length_order, B)
     if max_seq_len > layout.capacity:
         raise ValueError(f"max_seq_len {max_seq_len} exceeds the cache capacity {layout.capacity}")
     if out is None:
@@ -359,10 +375,12 @@ def decode_attention(q: torch.Tensor, layout: KVLayout, seq_lens: torch.Tensor, 
         B, Hq, hkv, D, layout.page_size, float(sm_scale), int(split_tokens),
         _ptr(ws), ws.numel(), _stream(q.device),
     ]
+    order = [_ptr(length_order)]
     if layout.kind == "fp8":
-        st = lib.tt_gqa_decode_attn_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail)
+        st = lib.tt_gqa_decode_attn_fp8(*head, _ptr(layout.k_scale), _ptr(layout.v_scale), *tail[:-3], *order,
+                                        *tail[-3:])
     elif layout.kind == "bf16":
-        st = lib.tt_gqa_decode_attn_bf16(*head, *tail)
+        st = lib.tt_gqa_decode_attn_bf16(*head, *tail[:-3], *order, *tail[-3:])
     else:
         st = lib.tt_gqa_decode_attn_f32(*head, *tail)
     _lib.check(st, "decode_attention")
@@ -458,7 +476,8 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
                             partials: torch.Tensor | None = None, num_q_heads: int | None = None,
                             lens_out: torch.Tensor | None = None, out: torch.Tensor | None = None,
                             sm_scale: float | None = None, workspace: Workspace | None = None,
-                            no_alloc: bool = False, split_tokens: int = 0) -> torch.Tensor:
+                            no_alloc: bool = False, split_tokens: int = 0,
+                            length_order: torch.Tensor | None = None) -> torch.Tensor:
     """One decode step in one launch pair: RoPE of this step's q and k at
     positions[b], append of k / v at that slot, and GQA attention over the
     positions[b] + 1 cached tokens (rope_append followed by decode_attention,
@@ -470,8 +489,9 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
     entry point, whose workspace is the library's per-GPU scratch
     (``workspace`` is then unused; pass ``out`` to allocate nothing at all;
     calls that overlap on one GPU race on that scratch). ``split_tokens``: 0
-    (balanced partition) or SPLIT_PER_SEGMENT (no workspace; not with
-    ``no_alloc``)."""
+    (balanced partition), SPLIT_PER_SEGMENT or SPLIT_PAIRED (no workspace;
+    not with ``no_alloc``); ``length_order`` as for decode_attention, ordered
+    by positions."""
     _require_cuda(table, positions, layout.k, layout.v)
     if split_tokens not in (0, SPLIT_PER_SEGMENT, SPLIT_PAIRED):
         raise ValueError(f"the fused decode step takes split_tokens 0, {SPLIT_PER_SEGMENT} or {SPLIT_PAIRED}, "
@@ -511,6 +531,7 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
         raise ValueError("positions must be int32 [B]")
     if lens_out is not None and (lens_out.dtype != torch.int32 or lens_out.shape != (B,)):
         raise ValueError("lens_out must be int32 [B]")
+    _check_order(length_order, B)
     if not 1 <= max_seq_len <= layout.capacity:
         raise ValueError(f"max_seq_len {max_seq_len} must be in [1, capacity {layout.capacity}]")
     if out is None:
@@ -531,7 +552,7 @@ def decode_attention_append(table: torch.Tensor, positions: torch.Tensor, layout
         st = lib.tt_decode_attn_append_bf16_noalloc(*head, *tail, _stream(dev))
         _lib.check(st, "decode_attention_append (no allocation)")
         return out
-    tail.append(int(split_tokens))
+    tail += [int(split_tokens), _ptr(length_order)]
     if split_tokens < 0:  # merged inside the launch: no workspace
         tail += [None, 0, _stream(dev)]
     else:
