@@ -271,10 +271,13 @@ class _LayerCacheBase:
 
     # -- host-state snapshots for graph capture ------------------------------------
     def host_state(self):
-        return (list(self._host_lens), self._cur)
+        return (list(self._host_lens), self._cur, self._split)
 
     def set_host_state(self, state) -> None:
         self._host_lens, self._cur = list(state[0]), state[1]
+        # the lengths are those the partition was picked for (and the length order uploaded):
+        # keep the pick rather than pick and upload again
+        self._split = state[2]
 
     def advance_host(self, n: int = 1) -> None:
         """Mirror a replayed one-token step: lengths + n, length buffers swapped n times."""

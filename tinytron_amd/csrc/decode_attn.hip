@@ -1030,11 +1030,14 @@ __device__ __forceinline__ void paired_body(const DecodeArgs &a, const DecodeApp
     // the caller's length order (indices clamped into the batch): no ranking
     // on the device, whose serial chain (lengths to LDS, two barriers, the
     // ranking) delayed every tile request by ~2.8 us at the C5 layer
+    // The lengths go to LDS in the same round trip as the pair's indices (a
+    // load of seq_lens[bA] after that of bA would be a second one, cold).
+    for (int b = threadIdx.x; b < NB; b += kPairThreads) keys[b] = max(min(a.seq_lens[b] + a.len_add, a.max_len), 0);
     bA = min(max(a.order[p], 0), NB - 1);
     bB = NB - 1 - p != p ? min(max(a.order[NB - 1 - p], 0), NB - 1) : -1;
-    LA = max(min(a.seq_lens[bA] + a.len_add, a.max_len), 0);
-    LB = bB >= 0 ? max(min(a.seq_lens[bB] + a.len_add, a.max_len), 0) : 0;
-    __syncthreads();  // V slots zeroed
+    __syncthreads();  // V slots zeroed, lengths in place
+    LA = keys[bA];
+    LB = bB >= 0 ? keys[bB] : 0;
   } else {
     // keys padded with -1 (below every length) to a multiple of 16
     const int nb16 = (NB + 15) & ~15;
