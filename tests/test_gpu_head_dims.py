@@ -71,23 +71,33 @@ def test_decode_valu_head_dims(D, kind, paged):
         assert_close(got, ref)
 
 
-@pytest.mark.parametrize("D", [24, 32, 48, 96])
-@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+# fp8 MFMA tiles need head_dim % 16 == 0 (fp8 D 24 is refused below)
+@pytest.mark.parametrize("D,kv", [(24, "bf16"), (32, "bf16"), (48, "bf16"), (96, "bf16"),
+                                  (32, "fp8"), (48, "fp8"), (96, "fp8")])
 @pytest.mark.parametrize("from_partials", [False, True])
 def test_fused_step_head_dims(D, kv, from_partials):
-    if kv == "fp8" and D % 16:
-        pytest.skip("fp8 MFMA tiles need head_dim % 16 == 0 (the VALU decode kernel has no fused step)")
     lens = [31, 32, 1, 77, 250, 16, 600]
     Hq, Hkv = 10, 2  # G = 5
     layer, table, g = _setup(kv, True, D, Hq, Hkv, lens, seed=D)
     _run_both(layer, table, g, Hq, from_partials)
 
 
-@pytest.mark.parametrize("D", [24, 32, 48, 96])
+def test_fused_step_refuses_fp8_rows_off_the_tiles():
+    """fp8 rows of 24 codes are not whole 16-byte fragments: the fused step
+    (MFMA kernels only) refuses them with the library's message."""
+    from tinytron_amd import ops
+
+    layer, table, g = _setup("fp8", True, 24, 10, 2, [31, 32, 1], seed=3)
+    B = 3
+    q1 = torch.randn(B, 10, 24, generator=g).to(torch.bfloat16).cuda()
+    k1 = torch.randn(B, 2, 24, generator=g).to(torch.bfloat16).cuda()
+    with pytest.raises(ValueError, match="head_dim"):
+        ops.decode_attention_append(table, layer._lens_dev[layer._cur], layer.layout, 40, q=q1, k=k1, v=k1)
+
+
+@pytest.mark.parametrize("D,fp8", [(24, False), (32, False), (48, False), (96, False),
+                                   (32, True), (48, True), (96, True)])
 @pytest.mark.parametrize("G", [3, 5])
-@pytest.mark.parametrize("fp8", [False, True])
 def test_prefill_head_dims(D, G, fp8):
-    if fp8 and D % 16:
-        pytest.skip("fp8 MFMA tiles need head_dim % 16 == 0")
     got, ref, new = run_prefill([0, 5, 40, 0], [33, 1, 70, 16], Hq=2 * G, Hkv=2, D=D, fp8=fp8, seed=D * G + fp8)
     check(got, ref, new)
