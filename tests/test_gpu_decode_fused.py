@@ -51,7 +51,7 @@ def _restore(layout, snap):
         t.copy_(s)
 
 
-def _run_both(layer, table, g, Hq, from_partials, S=4, split_tokens=0):
+def _run_both(layer, table, g, Hq, from_partials, S=4, split_tokens=0, sorted_order=False):
     from tinytron_amd import ops
 
     lay = layer.layout
@@ -61,6 +61,7 @@ def _run_both(layer, table, g, Hq, from_partials, S=4, split_tokens=0):
     max_len = int(pos.max().item()) + 1
     snap = _snapshot(lay)
     N = (Hq + 2 * Hkv) * D
+    order = torch.tensor(ops.length_order(pos.tolist()), dtype=torch.int32, device=DEV) if sorted_order else None
     if from_partials:
         parts = (torch.randn(S, B, N, generator=g) * 0.5).to(DEV)
     else:
@@ -74,7 +75,8 @@ def _run_both(layer, table, g, Hq, from_partials, S=4, split_tokens=0):
         q_rot = ops.rope_append_partials(parts, Hq, table, pos, lay, lens_out=lens_a)
     else:
         q_rot = ops.rope_append(q1, k1, v1, table, pos, lay, lens_out=lens_a)
-    out_a = ops.decode_attention(q_rot.view(B, Hq, D), lay, lens_a, max_len, workspace=ws, split_tokens=split_tokens)
+    out_a = ops.decode_attention(q_rot.view(B, Hq, D), lay, lens_a, max_len, workspace=ws, split_tokens=split_tokens,
+                                 length_order=order)
     torch.cuda.synchronize()
     after_a = _snapshot(lay)
 
@@ -83,10 +85,12 @@ def _run_both(layer, table, g, Hq, from_partials, S=4, split_tokens=0):
     ws_b = ops.Workspace(DEV)
     if from_partials:
         out_b = ops.decode_attention_append(table, pos, lay, max_len, partials=parts, num_q_heads=Hq,
-                                            lens_out=lens_b, workspace=ws_b, split_tokens=split_tokens)
+                                            lens_out=lens_b, workspace=ws_b, split_tokens=split_tokens,
+                                            length_order=order)
     else:
         out_b = ops.decode_attention_append(table, pos, lay, max_len, q=q1[:, :, 0], k=k1[:, :, 0], v=v1[:, :, 0],
-                                            lens_out=lens_b, workspace=ws_b, split_tokens=split_tokens)
+                                            lens_out=lens_b, workspace=ws_b, split_tokens=split_tokens,
+                                            length_order=order)
     torch.cuda.synchronize()
     after_b = _snapshot(lay)
     assert torch.equal(lens_a, lens_b)

@@ -6,8 +6,9 @@ and KV-head count (H_q <= 32), head_dim (24, 32, 48, 64, 96, 128: fp8 caches
 at 24 run the VALU kernel), layout (paged with a power-of-two page, or the reference's
 contiguous store with any page size), cache dtype (bf16 / fp8) and per-sequence
 lengths from a mix of edge values (1, page and tile boundaries) and uniform
-draws, and the partition (balanced, or one workgroup per segment: split_tokens
--1). Tolerance as in test_gpu_decode_attention.py.
+draws, and the partition (balanced; one workgroup per segment, split_tokens -1;
+or one per length-rank pair, -2, ranked on the GPU or with the caller's order).
+Tolerance as in test_gpu_decode_attention.py.
 """
 import numpy as np
 import pytest
@@ -31,9 +32,10 @@ def _case(i):
     P = int(rng.choice([16, 32, 64])) if paged else int(rng.choice([16, 48, 100]))
     fp8 = bool(rng.integers(0, 2))
     lengths = [int(rng.choice(EDGES)) if rng.random() < 0.4 else int(rng.integers(1, 900)) for _ in range(B)]
-    split = int(rng.choice([0, 0, -1]))  # balanced partition, or one workgroup per segment
+    split = int(rng.choice([0, 0, -1, -2, -2]))  # balanced, one workgroup per segment, or per rank pair
+    order = "sorted" if split == -2 and rng.integers(0, 2) else None  # paired: the caller's order, or ranked on the GPU
     return dict(lengths=lengths, Hq=G * hkv, Hkv=hkv, D=D, P=P, paged=paged, fp8=fp8, seed=100 + i,
-                split_tokens=split)
+                split_tokens=split, length_order=order)
 
 
 @pytest.mark.parametrize("i", range(40))

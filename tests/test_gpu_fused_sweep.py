@@ -3,7 +3,8 @@ attention launch, tt_decode_attn_append_*) against the two-launch path, bit
 for bit (test_gpu_decode_fused._run_both: output, every cache byte, fp8
 scales, lengths): batch sizes, group sizes (3, 5, 6 too), head_dim 24-128, bf16 / fp8 caches,
 paged / contiguous layouts and page sizes, bf16 inputs or 1-4 split-K
-partials, edge and random lengths, balanced or per-segment partition.
+partials, edge and random lengths, balanced, per-segment or paired partition
+(ranked on the GPU or with the caller's length order).
 """
 import numpy as np
 import pytest
@@ -28,9 +29,11 @@ def test_fused_step_sweep(i):
     paged = bool(rng.integers(0, 2))
     page = int(rng.choice([16, 32, 64]))
     S = int(rng.integers(0, 5))
-    split = int(rng.choice([0, 0, -1]))  # balanced partition, or one workgroup per segment
+    split = int(rng.choice([0, 0, -1, -2, -2]))  # balanced, one workgroup per segment, or per rank pair
+    sorted_order = bool(split == -2 and rng.integers(0, 2))  # paired: the caller's order, or ranked on the GPU
     lens = [int(rng.choice(EDGES)) if rng.random() < 0.4 else int(rng.integers(1, 700)) for _ in range(B)]
     print(f"sweep case {i}: B {B} G {G} hkv {hkv} D {D} kv {kv} paged {paged} page {page} S {S} split {split} "
           f"lens {lens}", flush=True)
     layer, table, g = _setup(kv, paged, D, G * hkv, hkv, lens, page=page, seed=i)
-    _run_both(layer, table, g, G * hkv, from_partials=S > 0, S=max(S, 1), split_tokens=split)
+    _run_both(layer, table, g, G * hkv, from_partials=S > 0, S=max(S, 1), split_tokens=split,
+              sorted_order=sorted_order)
