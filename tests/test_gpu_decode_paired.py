@@ -238,3 +238,46 @@ def test_engine_paired_graphs_equal_eager():
         runs[name] = (toks.cpu(), extra["token_log_probs"].float().cpu())
     assert torch.equal(runs["eager"][0], runs["graphs"][0])
     assert torch.equal(runs["eager"][1], runs["graphs"][1])
+
+
+def test_graph_captured_before_the_first_pick_ranks_on_the_device():
+    """A decode step captured before the cache has picked its partition picks
+    the paired one under capture, where no host copy can be recorded: the
+    graph ranks the lengths on the device (no order uploaded) and its replay
+    gives the logits of an eager step that uses the host's order, bit for
+    bit (the same pairs)."""
+    from tinytron_amd import ops
+    from tinytron_amd.cache import PagedKVCache
+    from tinytron_amd.engine import DecodeGraphs
+    from tinytron_amd.model import GPT
+    from tests.test_gpu_engine import _c1_config
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    Hkv = 8
+    B = 2 * cus // Hkv
+    lens = [16 * (i + 1) for i in range(B)]
+    cfg = _c1_config(num_layer=2, hidden_size=1024, num_attention_heads=16, num_key_value_heads=Hkv,
+                     block_size=max(lens) + 16)
+    model = GPT(cfg, device="cuda", dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(41)
+    prompt = torch.randint(0, cfg.vocab_size, (B, max(lens)), generator=g).cuda()
+    tok = torch.randint(0, cfg.vocab_size, (B, 1), generator=g).cuda()
+    last = torch.tensor(lens, device="cuda") - 1
+    outs = {}
+    with torch.no_grad():
+        for name in ("graph", "eager"):
+            cache = PagedKVCache.from_model_config(cfg, B, 16, "cuda", torch.bfloat16,
+                                                   seq_capacity=[n + 8 for n in lens])
+            cache.set_pending_new_lens(lens)
+            model(prompt, past_key_values=cache, use_cache=True, logits_index=last)
+            cache.set_pending_new_lens(None)
+            if name == "graph":
+                graphs = DecodeGraphs(model, cache, B, 0, False, torch.device("cuda"))
+                assert cache.get_layer_cache(0)._order is None  # nothing uploaded under capture
+                outs[name] = graphs.step(tok)[:, -1].float().cpu()
+            else:
+                out, cache = model(tok, past_key_values=cache, use_cache=True)
+                assert cache.get_layer_cache(0)._attention_split() == PAIRED
+                assert cache.get_layer_cache(0)._order is not None
+                outs[name] = out[:, -1].float().cpu()
+    assert torch.equal(outs["graph"], outs["eager"])
