@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TT_ABI_VERSION 6
+#define TT_ABI_VERSION 7
 
 #define TT_OK 0
 #define TT_ERR_INVALID_ARGUMENT (-1)
@@ -402,6 +402,65 @@ int tt_decode_attn_append_fp8(const void *q_in, const int64_t q_in_strides[2], c
                               int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                               float sm_scale, int64_t split_tokens, const int32_t *length_order, void *workspace,
                               size_t workspace_bytes, tt_stream_t stream);
+
+/*
+ * One fused bf16 decode step of a layer, as the library's kernels run it
+ * (gpt.py:98-109 with attn.py:378-440, mlp.py:24-26 + 44-45 and norm.py:6-19
+ * per layer, the reference's Block.forward for T = 1 under bf16 autocast):
+ *   P  = h . Wqkv^T                       split-K partials (kc_qkv-wide chunks)
+ *   y  = attention step from P            tt_decode_attn_append_bf16 / _fp8
+ *                                         (RoPE, append, attention; positions ->
+ *                                         lens_out)
+ *   P  = y . Wo^T                          split-K partials (kc_o)
+ *   h  = RMSNorm_2(x += bf16(sum P))       tt_add_rmsnorm_bf16
+ *   a  = SwiGLU(h . Wg^T, h . Wu^T)        one launch (kc_gu 0: tt_linear_swiglu_packed_bf16)
+ *                                         or split-K partials (kc_gu) + tt_silu_mul_bf16
+ *   P  = a . Wd^T                          split-K partials (kc_down)
+ *   h  = RMSNorm_next(x += bf16(sum P))    the next layer's first norm (or the final one)
+ * Every step is the entry point named beside it with these arguments, so the
+ * results equal those calls made one by one, bit for bit; this entry point
+ * issues them from the host in one call (a decode step's ~170 launches cost
+ * the host ~0.5 ms instead of ~1.7 ms through per-call bindings), so an eager
+ * decode loop keeps ahead of the GPU. No counterpart in the reference.
+ * Weights are the packed fragment-order layouts (w_gu rows interleaved by 8
+ * for the one-launch SwiGLU); h / attn_out / act are bf16 row-major
+ * [batch, hidden] / [batch, num_q_heads * head_dim] / [batch, intermediate];
+ * partials holds the largest split-K product of the layer.
+ */
+typedef struct tt_decode_layer {
+  float *x;                 /* fp32 residual [batch, hidden], updated in place */
+  void *h;                  /* bf16 [batch, hidden]: in: this layer's norm-1 output; out: the next norm's */
+  float *partials;          /* fp32 split-K scratch */
+  void *attn_out;           /* bf16 [batch, num_q_heads * head_dim] */
+  void *act;                /* bf16 [batch, intermediate] */
+  const void *w_qkv, *w_o, *w_gu, *w_down;
+  const float *ln2_weight, *next_norm_weight;
+  float eps;
+  int64_t batch, hidden, intermediate, num_q_heads, num_kv_heads, head_dim;
+  int64_t kc_qkv, kc_o, kc_gu, kc_down;
+  int32_t fp8_cache;        /* 0: bf16 cache; 1: fp8-e4m3fn cache with k_scale / v_scale */
+  const void *rope_table;
+  int64_t rope_table_len;
+  const int32_t *positions; /* tokens cached before the step, [batch] */
+  int32_t *lens_out;        /* positions + 1 after the step, or NULL */
+  const int32_t *page_table;
+  int64_t max_pages, num_pages;
+  void *k_cache, *v_cache;
+  float *k_scale, *v_scale;
+  int64_t cache_strides[3];
+  int64_t capacity, page_size;
+  float sm_scale;
+  int64_t split_tokens;
+  const int32_t *length_order;
+  void *workspace;
+  size_t workspace_bytes;
+} tt_decode_layer_t;
+
+/* layers[0 .. num_layers) in order on one stream, each with the attention
+ * launch bound max_seq_len. Stops at the first failing step and returns its
+ * status (tt_last_error_string names the layer). */
+int tt_decode_layers_bf16(const tt_decode_layer_t *layers, int64_t num_layers, int64_t max_seq_len,
+                          tt_stream_t stream);
 
 /*
  * tt_decode_attn_append_bf16 without the workspace argument: the attention

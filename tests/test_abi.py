@@ -41,13 +41,50 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
 
 
+def test_decode_layer_struct_matches_header(tmp_path):
+    """The ctypes tt_decode_layer_t has the C struct's size and field offsets
+    (compiled from the header with the host C compiler)."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    fields = [f[0] for f in _lib.DecodeLayer._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text("#include <stdio.h>\n#include <stddef.h>\n#include \"tinytron_amd.h\"\nint main(void) {\n"
+                   "  printf(\"%zu\\n\", sizeof(tt_decode_layer_t));\n"
+                   + "".join(f"  printf(\"%zu\\n\", offsetof(tt_decode_layer_t, {f}));\n" for f in fields)
+                   + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(HEADER.parent), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    want = [ctypes.sizeof(_lib.DecodeLayer)] + [getattr(_lib.DecodeLayer, f).offset for f in fields]
+    assert got == want
+
+
+def test_decode_layers_validates_before_launching():
+    """tt_decode_layers_bf16: no layers is a no-op; a NULL array, a bad
+    k_chunk and a NULL buffer are refused, the message naming the layer and
+    the step (every case fails validation before any launch)."""
+    lib = _lib.load()
+    assert lib.tt_decode_layers_bf16(None, 0, 1, None) == _lib.TT_OK
+    assert lib.tt_decode_layers_bf16(None, 1, 1, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    arr = (_lib.DecodeLayer * 1)()
+    assert lib.tt_decode_layers_bf16(ctypes.addressof(arr), 1, 1, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert b"layer 0: bad k_chunk" in lib.tt_last_error_string()
+    arr[0].kc_qkv = arr[0].kc_o = arr[0].kc_down = 256
+    assert lib.tt_decode_layers_bf16(ctypes.addressof(arr), 1, 1, None) == _lib.TT_ERR_INVALID_ARGUMENT
+    assert lib.tt_last_error_string().startswith(b"layer 0, q|k|v: ")
+
+
 def test_noalloc_scratch_size_matches_header():
     m = re.search(r"#define TT_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", HEADER.read_text())
     assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
 
 
 def test_abi_version():
-    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 6
+    assert _lib.load().tt_abi_version() == _lib.ABI_VERSION == 7
 
 
 def test_workspace_and_split_sizing():

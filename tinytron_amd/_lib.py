@@ -10,7 +10,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libtinytron_amd.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 TT_OK = 0
 TT_ERR_INVALID_ARGUMENT = -1
@@ -149,7 +149,30 @@ SIGNATURES = {
     "tt_sample_bf16": (_SAMPLE, ctypes.c_int),
     "tt_sample_f32": (_SAMPLE, ctypes.c_int),
     "tt_sample_workspace_bytes": ([_i64, _i64, _i64], _size),
+    "tt_decode_layers_bf16": ([_vp, _i64, _i64, _vp], ctypes.c_int),
 }
+
+
+
+class DecodeLayer(ctypes.Structure):
+    """tt_decode_layer_t: one layer's fused bf16 decode step (buffers, packed
+    weights, cache and attention arguments) for tt_decode_layers_bf16."""
+    _fields_ = [
+        ("x", _vp), ("h", _vp), ("partials", _vp), ("attn_out", _vp), ("act", _vp),
+        ("w_qkv", _vp), ("w_o", _vp), ("w_gu", _vp), ("w_down", _vp),
+        ("ln2_weight", _vp), ("next_norm_weight", _vp), ("eps", _f32),
+        ("batch", _i64), ("hidden", _i64), ("intermediate", _i64), ("num_q_heads", _i64),
+        ("num_kv_heads", _i64), ("head_dim", _i64),
+        ("kc_qkv", _i64), ("kc_o", _i64), ("kc_gu", _i64), ("kc_down", _i64),
+        ("fp8_cache", ctypes.c_int32), ("rope_table", _vp), ("rope_table_len", _i64),
+        ("positions", _vp), ("lens_out", _vp),
+        ("page_table", _vp), ("max_pages", _i64), ("num_pages", _i64),
+        ("k_cache", _vp), ("v_cache", _vp), ("k_scale", _vp), ("v_scale", _vp),
+        ("cache_strides", _i64 * 3), ("capacity", _i64), ("page_size", _i64),
+        ("sm_scale", _f32), ("split_tokens", _i64), ("length_order", _vp),
+        ("workspace", _vp), ("workspace_bytes", _size),
+    ]
+
 
 _LIB = None
 

@@ -237,6 +237,19 @@ class _LayerCacheBase:
         self._advance_all(1)
         return out
 
+    def begin_decode_step(self):
+        """For a caller that issues this layer's one-token decode step itself
+        (the model's one-call layer sequence): checks that every sequence has
+        room for one more token and returns (positions, lens_out, bound,
+        split_tokens, length_order), the arguments decode_step would pass: the
+        lengths before the step, the buffer the kernel writes the lengths
+        after it into, the launch bound, the attention partition and its rank
+        order (or None). Follow the launch with advance_host(1)."""
+        self._check_room([1] * self.batch_size)
+        bound = self.static_max_len if self.static_max_len is not None else self.current_length + 1
+        split = self._attention_split()
+        return self._lens_dev[self._cur], self._lens_dev[1 - self._cur], bound, split, self._order
+
     def prefill_attend(self, q_rot: torch.Tensor, new_lens, out: torch.Tensor | None = None,
                        kernel: bool = True) -> torch.Tensor:
         """Causal attention of the chunk just appended by rope_append (q_rot

@@ -1038,6 +1038,69 @@ int tt_decode_attn_append_bf16_noalloc(const void *q_in, const int64_t q_in_stri
                               sm_scale, 0, nullptr, ws, kScratchBytes, stream, /*exact_slots=*/true);
 }
 
+int tt_decode_layers_bf16(const tt_decode_layer_t *layers, int64_t num_layers, int64_t max_seq_len,
+                          tt_stream_t stream) {
+  TT_CHECK(layers != nullptr || num_layers == 0, TT_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+  TT_CHECK(num_layers >= 0, TT_ERR_INVALID_ARGUMENT, "num_layers must be >= 0");
+  for (int64_t i = 0; i < num_layers; ++i) {
+    const tt_decode_layer_t &L = layers[i];
+    const int64_t B = L.batch, C = L.hidden, I = L.intermediate, Hq = L.num_q_heads, Hkv = L.num_kv_heads;
+    const int64_t D = L.head_dim, Nqkv = (Hq + 2 * Hkv) * D;
+    int rc = TT_OK;
+    auto step = [&](int status, const char *what) {
+      if (status != TT_OK && rc == TT_OK) {
+        rc = status;
+        const std::string msg = g_last_error;  // prefix the step that failed
+        fail(status, "layer %lld, %s: %s", (long long)i, what, msg.c_str());
+      }
+      return rc == TT_OK;
+    };
+    TT_CHECK(L.kc_qkv > 0 && L.kc_o > 0 && L.kc_down > 0 && L.kc_gu >= 0, TT_ERR_INVALID_ARGUMENT,
+             "layer %lld: bad k_chunk", (long long)i);
+    // q|k|v projection: split-K partials read by the attention step
+    if (!step(tt_linear_splitk_packed_bf16(L.h, C, L.w_qkv, L.partials, B, Nqkv, C, L.kc_qkv, stream), "q|k|v"))
+      return rc;
+    const int64_t S = C / L.kc_qkv;
+    const int64_t pst[2] = {Nqkv, D};
+    const int64_t ost[2] = {Hq * D, D};
+    const char *base = reinterpret_cast<const char *>(L.partials);
+    const void *q_in = base, *k_in = base + Hq * D * 4, *v_in = base + (Hq + Hkv) * D * 4;
+    const int attn =
+        L.fp8_cache
+            ? tt_decode_attn_append_fp8(q_in, pst, k_in, pst, v_in, pst, S, B * Nqkv, L.rope_table, L.rope_table_len,
+                                        L.positions, L.lens_out, max_seq_len, L.page_table, L.max_pages, L.num_pages,
+                                        L.k_cache, L.v_cache, L.k_scale, L.v_scale, L.cache_strides, L.capacity,
+                                        L.attn_out, ost, B, Hq, Hkv, D, L.page_size, L.sm_scale, L.split_tokens,
+                                        L.length_order, L.workspace, L.workspace_bytes, stream)
+            : tt_decode_attn_append_bf16(q_in, pst, k_in, pst, v_in, pst, S, B * Nqkv, L.rope_table, L.rope_table_len,
+                                         L.positions, L.lens_out, max_seq_len, L.page_table, L.max_pages, L.num_pages,
+                                         L.k_cache, L.v_cache, L.cache_strides, L.capacity, L.attn_out, ost, B, Hq,
+                                         Hkv, D, L.page_size, L.sm_scale, L.split_tokens, L.length_order, L.workspace,
+                                         L.workspace_bytes, stream);
+    if (!step(attn, "attention")) return rc;
+    if (!step(tt_linear_splitk_packed_bf16(L.attn_out, Hq * D, L.w_o, L.partials, B, C, Hq * D, L.kc_o, stream),
+              "c_proj"))
+      return rc;
+    if (!step(tt_add_rmsnorm_bf16(L.x, L.partials, (Hq * D) / L.kc_o, L.ln2_weight, L.eps, L.h, B, C, stream),
+              "residual + norm 2"))
+      return rc;
+    if (L.kc_gu == 0) {
+      if (!step(tt_linear_swiglu_packed_bf16(L.h, C, L.w_gu, L.act, I, B, I, C, stream), "gate|up + SwiGLU"))
+        return rc;
+    } else {
+      if (!step(tt_linear_splitk_packed_bf16(L.h, C, L.w_gu, L.partials, B, 2 * I, C, L.kc_gu, stream), "gate|up"))
+        return rc;
+      if (!step(tt_silu_mul_bf16(L.partials, C / L.kc_gu, B, I, L.act, stream), "SwiGLU")) return rc;
+    }
+    if (!step(tt_linear_splitk_packed_bf16(L.act, I, L.w_down, L.partials, B, C, I, L.kc_down, stream), "down"))
+      return rc;
+    if (!step(tt_add_rmsnorm_bf16(L.x, L.partials, I / L.kc_down, L.next_norm_weight, L.eps, L.h, B, C, stream),
+              "residual + next norm"))
+      return rc;
+  }
+  return ok();
+}
+
 size_t tt_sample_workspace_bytes(int64_t m, int64_t vocab, int64_t top_k) {
   if (m <= 0 || vocab <= 0) return 0;
   const int chunks = tt::sample_cand_chunks(m, vocab, top_k > 0 && top_k < vocab ? top_k : 0, false);

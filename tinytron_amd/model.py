@@ -34,6 +34,7 @@ see only the sum(new_lens) real tokens, not the B x T padded grid.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -41,7 +42,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops
+from . import _lib, ops
 from .cache import ConcatKVStore, LayerPagedKVCache, PagedLayerKVCache
 
 
@@ -262,6 +263,10 @@ class GPT(nn.Module):
         self._stacked = {}         # layer -> (source key, packed q|k|v, c_proj, gate|up, down weights)
         self._stacked_rows = {}    # layer -> (source key, plain q|k|v weight, plain gate|up weight)
         self._decode_bufs = {}     # (device, rows) -> split-K partial buffer
+        self.native_decode_step = True  # the fused step's layer sequence issued in one library call
+        self._native_plans = {}    # (cache, parity) -> (signature, tt_decode_layer_t array, kept objects)
+        self._native_bufs = {}     # (device, rows) -> residual x, norm output h, attention output, SwiGLU output
+        self._native_ws = {}       # device -> workspace of the balanced attention partition
 
     def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
         # reference checkpoints carry the tied lm_head as its own key (gpt.py:60-62)
@@ -375,6 +380,12 @@ class GPT(nn.Module):
             raise ValueError(f"position_offset {position_offset} does not match the cache length {lens[0]}")
         table = rope_table_for(first.max_seq_len + 1, D, c.rope_theta, torch.bfloat16, idx.device)
         pbuf = self._partials(idx.device, B)
+        if self.native_decode_step and C // kc_c <= ops.FUSED_STEP_MAX_SPLITS and all(
+                cache.get_layer_cache(i).layout.kind in ("bf16", "fp8")
+                and ops.attention_tile_dim(D, cache.get_layer_cache(i).layout.kind) for i in range(len(self.blocks))):
+            logits = self._decode_step_native(idx, cache, table, pbuf)
+            if logits is not None:
+                return logits.view(B, 1, -1)
         x = self.wte(idx).view(B, C).float().contiguous()          # fp32 residual stream
         h = ops.add_rmsnorm(x, self.blocks[0].ln_1.weight, eps)      # bf16 [B, C]
         for i, blk in enumerate(self.blocks):
@@ -398,6 +409,107 @@ class GPT(nn.Module):
             h = ops.add_rmsnorm(x, nxt, eps, partials=P)             # residual add + next norm (or lnf)
         logits = F.linear(h, self.lm_head_weight())
         return logits.view(B, 1, -1)
+
+    def _decode_step_native(self, idx: torch.Tensor, cache, table: torch.Tensor, pbuf: torch.Tensor):
+        """_decode_step_fused's layer sequence (every layer's cache taking the
+        one-launch-pair attention step) issued by the library in one call,
+        tt_decode_layers_bf16: the same kernels with the same arguments, so
+        the same logits bit for bit, for about a third of the host time. The
+        argument array is built once per cache, length-buffer parity,
+        partition, weights and buffers, and checked against them every step.
+        Returns the [B, V] logits, or None (then the per-op path runs) when the
+        layers do not share one launch bound."""
+        c = self.config
+        B = idx.shape[0]
+        C, Hq, Hkv, I = c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.intermediate_size
+        D = C // Hq
+        dev = idx.device
+        n = len(self.blocks)
+        layers = [cache.get_layer_cache(i) for i in range(n)]
+        steps = [layer.begin_decode_step() for layer in layers]   # (positions, lens_out, bound, split, order)
+        bound = steps[0][2]
+        if any(st[2] != bound for st in steps):
+            return None
+        for layer in layers:
+            if not 1 <= bound <= layer.layout.capacity:
+                raise ValueError(f"max_seq_len {bound} must be in [1, capacity {layer.layout.capacity}]")
+        ws_ptr = ws_n = 0
+        if any(st[3] == 0 for st in steps):  # the balanced partition's split-K workspace, shared by the layers
+            need = ops.workspace_bytes(B, Hq, Hkv, D, bound, 0)
+            ws = self._native_ws.get(str(dev))
+            if ws is None:
+                ws = self._native_ws[str(dev)] = ops.Workspace(dev)
+            buf = ws.get(need)
+            ws_ptr, ws_n = buf.data_ptr(), buf.numel()
+        weights = [self._stacked_weights(i) for i in range(n)]
+        norms = [blk.ln_2.weight for blk in self.blocks] + [blk.ln_1.weight for blk in self.blocks[1:]] \
+            + [self.lnf.weight]
+        sig = [B, table.data_ptr(), table.shape[0], pbuf.data_ptr(), ws_ptr, ws_n]
+        for layer, st, w in zip(layers, steps, weights):
+            sig += [id(layer.layout), id(st[0]), st[3], id(st[4]), id(w[0]), id(w[1]), id(w[2]), id(w[3])]
+        sig += [id(t) for t in norms]
+        key = (id(cache), layers[0]._cur)
+        plan = self._native_plans.get(key)
+        if plan is None or plan[0] != sig:
+            plan = self._native_plan(sig, layers, steps, weights, table, pbuf, ws_ptr, ws_n, dev, B)
+            self._native_plans[key] = plan
+        x, h = plan[2][0], plan[2][1]
+        x.copy_(self.wte(idx).view(B, C))                                   # fp32 residual stream
+        ops.add_rmsnorm(x, self.blocks[0].ln_1.weight, self.lnf.variance_epsilon, out=h)
+        _lib.check(_lib.load().tt_decode_layers_bf16(ctypes.addressof(plan[1]), n, bound, ops._stream(dev)),
+                   "decode step")
+        for layer in layers:
+            layer.advance_host(1)
+        return F.linear(h, self.lm_head_weight())
+
+    def _native_plan(self, sig, layers, steps, weights, table, pbuf, ws_ptr, ws_n, dev, B):
+        """The tt_decode_layer_t array of one decode step; keeps every object
+        whose identity the signature records alive with it."""
+        c = self.config
+        C, Hq, Hkv, I = c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.intermediate_size
+        D = C // Hq
+        bkey = (str(dev), B)
+        bufs = self._native_bufs.get(bkey)
+        if bufs is None:
+            bufs = (torch.empty(B, C, dtype=torch.float32, device=dev),
+                    torch.empty(B, C, dtype=torch.bfloat16, device=dev),
+                    torch.empty(B, Hq * D, dtype=torch.bfloat16, device=dev),
+                    torch.empty(B, I, dtype=torch.bfloat16, device=dev))
+            self._native_bufs[bkey] = bufs
+        x, h, y, a = bufs
+        n = len(layers)
+        arr = (_lib.DecodeLayer * n)()
+        kc_gu = 0 if self._swiglu_fused() else self._k_chunk_wide(C)
+        for i, (layer, st, w) in enumerate(zip(layers, steps, weights)):
+            lay = layer.layout
+            nxt = self.blocks[i + 1].ln_1.weight if i + 1 < n else self.lnf.weight
+            for t in (self.blocks[i].ln_2.weight, nxt):
+                if t.dtype != torch.float32 or not t.is_contiguous():
+                    raise ValueError("the fused decode step takes contiguous fp32 norm weights")
+            L = arr[i]
+            L.x, L.h, L.partials, L.attn_out, L.act = x.data_ptr(), h.data_ptr(), pbuf.data_ptr(), y.data_ptr(), \
+                a.data_ptr()
+            L.w_qkv, L.w_o, L.w_gu, L.w_down = (pw.data.data_ptr() for pw in w)
+            L.ln2_weight, L.next_norm_weight = self.blocks[i].ln_2.weight.data_ptr(), nxt.data_ptr()
+            L.eps = self.lnf.variance_epsilon
+            L.batch, L.hidden, L.intermediate, L.num_q_heads, L.num_kv_heads, L.head_dim = B, C, I, Hq, Hkv, D
+            L.kc_qkv, L.kc_o, L.kc_gu, L.kc_down = self._k_chunk(C), self._k_chunk_small(C), kc_gu, self._k_chunk(I)
+            L.fp8_cache = 1 if lay.kind == "fp8" else 0
+            L.rope_table, L.rope_table_len = table.data_ptr(), table.shape[0]
+            L.positions, L.lens_out = st[0].data_ptr(), st[1].data_ptr()
+            L.page_table = ops._ptr(lay.page_table)
+            L.max_pages, L.num_pages = lay.max_pages, lay.num_pages
+            L.k_cache, L.v_cache = lay.k.data_ptr(), lay.v.data_ptr()
+            L.k_scale, L.v_scale = ops._ptr(lay.k_scale), ops._ptr(lay.v_scale)
+            L.cache_strides[:] = [int(s) for s in lay.strides]
+            L.capacity, L.page_size = lay.capacity, lay.page_size
+            L.sm_scale = 1.0 / math.sqrt(D)
+            L.split_tokens = st[3]
+            L.length_order = ops._ptr(st[4])
+            L.workspace, L.workspace_bytes = (ws_ptr, ws_n) if st[3] == 0 else (None, 0)
+        keep = [layers, [layer.layout for layer in layers], [st[0] for st in steps], [st[4] for st in steps], weights,
+                [blk.ln_2.weight for blk in self.blocks], [blk.ln_1.weight for blk in self.blocks], self.lnf.weight]
+        return sig, arr, bufs, keep
 
     # -- packed bf16 prefill ---------------------------------------------------------
     def _fused_prefill_ok(self, cache, idx: torch.Tensor, logits_index: torch.Tensor) -> bool:
