@@ -183,8 +183,10 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
 
 // One workgroup per row m. With P != null the residual row first takes the
 // bf16-rounded sum of the partials (the projection's autocast output). Every
-// load of the row (x and up to SMAX splits) is issued before the first add,
-// so the row costs one memory round trip; the splits are added in order.
+// load of the row (x, up to SMAX splits and the norm weight) is issued before
+// the first add, so the row costs one memory round trip; the splits are added
+// in order. (Loaded after the block reduction, the weight cost two more round
+// trips: the compiler keeps loads below a barrier where the source puts them.)
 // PER float4 groups per thread (C <= 1024 * PER, C a multiple of 4; with
 // kMask, groups past C are neither loaded nor stored and add 0 to the sum of
 // squares; without it C == 1024 * PER and every load is unconditional, so
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
                                                           const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
   const int64_t row = (int64_t)blockIdx.x * C;
-  f32x4 v[PER];
+  f32x4 v[PER], wv[PER];
   f32x4 pv[PER][SMAX];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -207,6 +209,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
         pv[j][s] = in ? *reinterpret_cast<const f32x4 *>(P + (int64_t)(s < S ? s : 0) * MN + row + c)
                       : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {  // issued after the row's loads, which are needed first
+    const int c = 4 * (threadIdx.x + 256 * j);
+    wv[j] = !kMask || c < C ? *reinterpret_cast<const f32x4 *>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float ss = 0.f;
 #pragma unroll
@@ -232,9 +239,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *x, const float 
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
     if (kMask && c >= C) continue;
-    const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
-    uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
-    uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
+    uint32_t lo = pack_bf16x2(wv[j][0] * (v[j][0] * r), wv[j][1] * (v[j][1] * r));
+    uint32_t hi = pack_bf16x2(wv[j][2] * (v[j][2] * r), wv[j][3] * (v[j][3] * r));
     *reinterpret_cast<uint2 *>(y + row + c) = make_uint2(lo, hi);
   }
 }
@@ -392,7 +398,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
                                                                const float *w, float eps, uint16_t *y, int C) {
   __shared__ float red[4];
   const int64_t row = (int64_t)blockIdx.x * C;
-  f32x4 v[PER];
+  f32x4 v[PER], wv[PER];
   uint2 av[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -401,6 +407,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
     v[j] = in ? *reinterpret_cast<const f32x4 *>(x + row + c) : f32x4{0.f, 0.f, 0.f, 0.f};
     av[j] = make_uint2(0u, 0u);
     if (a != nullptr && in) av[j] = *reinterpret_cast<const uint2 *>(a + (int64_t)blockIdx.x * lda + c);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {  // the weight with the row's loads: one round trip
+    const int c = 4 * (threadIdx.x + 256 * j);
+    wv[j] = !kMask || c < C ? *reinterpret_cast<const f32x4 *>(w + c) : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float ss = 0.f;
 #pragma unroll
@@ -422,9 +433,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(float *x, const u
   for (int j = 0; j < PER; ++j) {
     const int c = 4 * (threadIdx.x + 256 * j);
     if (kMask && c >= C) continue;
-    const f32x4 wv = *reinterpret_cast<const f32x4 *>(w + c);
-    uint32_t lo = pack_bf16x2(wv[0] * (v[j][0] * r), wv[1] * (v[j][1] * r));
-    uint32_t hi = pack_bf16x2(wv[2] * (v[j][2] * r), wv[3] * (v[j][3] * r));
+    uint32_t lo = pack_bf16x2(wv[j][0] * (v[j][0] * r), wv[j][1] * (v[j][1] * r));
+    uint32_t hi = pack_bf16x2(wv[j][2] * (v[j][2] * r), wv[j][3] * (v[j][3] * r));
     *reinterpret_cast<uint2 *>(y + row + c) = make_uint2(lo, hi);
   }
 }

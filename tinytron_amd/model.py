@@ -418,7 +418,9 @@ class GPT(nn.Module):
         argument array is built once per cache, length-buffer parity,
         partition, weights and buffers, and checked against them every step.
         Returns the [B, V] logits, or None (then the per-op path runs) when the
-        layers do not share one launch bound."""
+        layers do not share one launch bound. A library error is raised with
+        the layer it names; the layers before it have appended the step's
+        token but their host lengths are not advanced (reset the cache)."""
         c = self.config
         B = idx.shape[0]
         C, Hq, Hkv, I = c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.intermediate_size
