@@ -458,7 +458,8 @@ typedef struct tt_decode_layer {
 
 /* layers[0 .. num_layers) in order on one stream, each with the attention
  * launch bound max_seq_len. Stops at the first failing step and returns its
- * status (tt_last_error_string names the layer). */
+ * status (tt_last_error_string names the layer and the step); the layers
+ * before it have run, so their caches already hold the step's token. */
 int tt_decode_layers_bf16(const tt_decode_layer_t *layers, int64_t num_layers, int64_t max_seq_len,
                           tt_stream_t stream);
 
