@@ -145,7 +145,6 @@ class InferenceEngine:
                 raise ValueError("ragged prompts (prompt_lens) need the paged KV cache (use_paged_kv_cache=True)")
             cache = None
         lens_t = torch.tensor(lens, device=self.device)
-        rows = torch.arange(batch_size, device=self.device)
 
         prefill_tokens = int(sum(lens))
         prefill_t0 = time.perf_counter()
@@ -159,7 +158,9 @@ class InferenceEngine:
 
         decode_steps = 0
         token_log_probs = []
-        cur = lens_t.clone()
+        # step j's tokens go to column j of one buffer (a plain copy per step) and to their
+        # places lens[b] + j in `tokens` by one scatter after the loop
+        generated = torch.empty(batch_size, max(max_new_tokens, 1), dtype=tokens.dtype, device=self.device)
         uniform = len(set(lens)) == 1
         graphs = None
         # the tuple cache's tensors change every step: it launches eagerly. The
@@ -181,8 +182,7 @@ class InferenceEngine:
                 token_log_probs.append(next_log_prob)
             else:
                 next_token = sample_next_token(next_logits, temperature, top_k, top_p)
-            tokens[rows, cur] = next_token
-            cur += 1
+            generated[:, step] = next_token
             decode_steps += 1
             if eos_token_id is not None and torch.all(next_token == eos_token_id):
                 break
@@ -211,6 +211,9 @@ class InferenceEngine:
                 logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
                                            position_offset=position)
             next_logits = logits[:, -1, :]
+        if decode_steps:
+            cols = lens_t.unsqueeze(1) + torch.arange(decode_steps, device=self.device)
+            tokens.scatter_(1, cols, generated[:, :decode_steps])
         torch.cuda.synchronize(self.device)
         decode_t1 = time.perf_counter()
         if paged:
