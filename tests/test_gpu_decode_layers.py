@@ -131,10 +131,52 @@ def test_one_call_step_refuses_a_bad_layer_and_names_it():
     _steps(model, cache, first, lens, 1, True)
     plan = next(iter(model._native_plans.values()))
     arr = (_lib.DecodeLayer * 2)()
-    ctypes.memmove(arr, plan[1], ctypes.sizeof(arr))
+    ctypes.memmove(arr, plan[3], ctypes.sizeof(arr))
     arr[0].kc_down = 0
     lib, stream = _lib.load(), ops._stream(torch.device(DEV))
     assert lib.tt_decode_layers_bf16(ctypes.addressof(arr), 0, 1, stream) == _lib.TT_OK
     with pytest.raises(ValueError, match="layer 0: bad k_chunk"):
         _lib.check(lib.tt_decode_layers_bf16(ctypes.addressof(arr), 2, 128, stream), "decode step")
     torch.cuda.synchronize()
+
+
+def test_plan_follows_alternating_caches():
+    """Two caches of different batches and partitions stepped in turn on one
+    model: the argument array is rebuilt for each switch (its signature names
+    the cache's layouts and length buffers), and every step equals the
+    op-by-op path's."""
+    model, cfg = _model(1024, 16, 8, 2048)
+    cases = [([100 + 3 * b for b in range(64)], 21), ([70, 9, 33], 22)]
+    out = {}
+    for native in (True, False):
+        model.native_decode_step = native
+        runs = [list(_prefilled(model, cfg, lens, 4, True, BF16, seed)) for lens, seed in cases]
+        got = []
+        with torch.no_grad():
+            for s in range(4):
+                for k, (lens, _) in enumerate(cases):
+                    cache, row = runs[k]
+                    t = row.float().argmax(-1)
+                    logits, _ = model(t.view(-1, 1), use_cache=True, past_key_values=cache, position_offset=0)
+                    runs[k][1] = logits[:, -1]
+                    got.append(logits[:, -1].clone())
+        out[native] = got
+    for i, (a, b) in enumerate(zip(out[True], out[False])):
+        assert torch.equal(a, b), f"step {i // 2} of cache {i % 2} differs"
+
+
+def test_plan_does_not_keep_a_finished_cache_alive():
+    """The model's argument array holds the cache's objects weakly: a cache
+    dropped by its caller is freed (its K pool with it)."""
+    import gc
+    import weakref
+
+    model, cfg = _model(1024, 16, 4, 2048)
+    lens = [70, 9, 33]
+    cache, first = _prefilled(model, cfg, lens, 2, True, BF16, seed=5)
+    _steps(model, cache, first, lens, 2, True)
+    assert model._native_plans
+    pool = weakref.ref(cache.get_layer_cache(0).layout.k)
+    del cache, first
+    gc.collect()
+    assert pool() is None

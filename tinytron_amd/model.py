@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -76,6 +77,11 @@ def rope_table_for(n_positions: int, head_dim: int, theta: float, dtype: torch.d
         t = ops.build_rope_table(n, head_dim, theta, dtype=dtype, device=device)
         _ROPE_TABLES[key] = t
     return t
+
+
+def _same_objects(refs, objs) -> bool:
+    """Whether weak references (None for None) still name exactly these objects."""
+    return len(refs) == len(objs) and all((o is None) if r is None else (r() is o) for r, o in zip(refs, objs))
 
 
 def _is_fused_cache(past_kv) -> bool:
@@ -264,7 +270,7 @@ class GPT(nn.Module):
         self._stacked_rows = {}    # layer -> (source key, plain q|k|v weight, plain gate|up weight)
         self._decode_bufs = {}     # (device, rows) -> split-K partial buffer
         self.native_decode_step = True  # the fused step's layer sequence issued in one library call
-        self._native_plans = {}    # (cache, parity) -> (signature, tt_decode_layer_t array, kept objects)
+        self._native_plans = {}    # length-buffer parity -> (scalars, cache objects, model objects, array, buffers)
         self._native_bufs = {}     # (device, rows) -> residual x, norm output h, attention output, SwiGLU output
         self._native_ws = {}       # device -> workspace of the balanced attention partition
 
@@ -446,27 +452,30 @@ class GPT(nn.Module):
         weights = [self._stacked_weights(i) for i in range(n)]
         norms = [blk.ln_2.weight for blk in self.blocks] + [blk.ln_1.weight for blk in self.blocks[1:]] \
             + [self.lnf.weight]
-        sig = [B, table.data_ptr(), table.shape[0], pbuf.data_ptr(), ws_ptr, ws_n]
-        for layer, st, w in zip(layers, steps, weights):
-            sig += [id(layer.layout), id(st[0]), st[3], id(st[4]), id(w[0]), id(w[1]), id(w[2]), id(w[3])]
-        sig += [id(t) for t in norms]
-        key = (id(cache), layers[0]._cur)
-        plan = self._native_plans.get(key)
-        if plan is None or plan[0] != sig:
-            plan = self._native_plan(sig, layers, steps, weights, table, pbuf, ws_ptr, ws_n, dev, B)
-            self._native_plans[key] = plan
-        x, h = plan[2][0], plan[2][1]
+        scalars = (B, table.data_ptr(), table.shape[0], pbuf.data_ptr(), ws_ptr, ws_n, tuple(st[3] for st in steps))
+        cached = [o for layer, st in zip(layers, steps) for o in (layer.layout, st[0], st[4])]  # the cache's objects
+        owned = [pw for w in weights for pw in w] + norms                                    # the model's objects
+        plan = self._native_plans.get(layers[0]._cur)
+        if plan is None or plan[0] != scalars or not _same_objects(plan[1], cached) \
+                or len(plan[2]) != len(owned) or any(a is not b for a, b in zip(plan[2], owned)):
+            arr, bufs = self._native_plan(layers, steps, weights, table, pbuf, ws_ptr, ws_n, dev, B)
+            # the cache's objects are held weakly (a plan must not keep a finished cache alive), the
+            # model's strongly (their identities cannot be reused while the plan compares them)
+            plan = (scalars, [None if o is None else weakref.ref(o) for o in cached], owned, arr, bufs)
+            self._native_plans[layers[0]._cur] = plan
+        arr, (x, h) = plan[3], plan[4][:2]
         x.copy_(self.wte(idx).view(B, C))                                   # fp32 residual stream
         ops.add_rmsnorm(x, self.blocks[0].ln_1.weight, self.lnf.variance_epsilon, out=h)
-        _lib.check(_lib.load().tt_decode_layers_bf16(ctypes.addressof(plan[1]), n, bound, ops._stream(dev)),
+        _lib.check(_lib.load().tt_decode_layers_bf16(ctypes.addressof(arr), n, bound, ops._stream(dev)),
                    "decode step")
         for layer in layers:
             layer.advance_host(1)
         return F.linear(h, self.lm_head_weight())
 
-    def _native_plan(self, sig, layers, steps, weights, table, pbuf, ws_ptr, ws_n, dev, B):
-        """The tt_decode_layer_t array of one decode step; keeps every object
-        whose identity the signature records alive with it."""
+    def _native_plan(self, layers, steps, weights, table, pbuf, ws_ptr, ws_n, dev, B):
+        """The tt_decode_layer_t array of one decode step and the model-owned
+        buffers it points at (residual x, norm output h, attention output,
+        SwiGLU output)."""
         c = self.config
         C, Hq, Hkv, I = c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.intermediate_size
         D = C // Hq
@@ -509,9 +518,7 @@ class GPT(nn.Module):
             L.split_tokens = st[3]
             L.length_order = ops._ptr(st[4])
             L.workspace, L.workspace_bytes = (ws_ptr, ws_n) if st[3] == 0 else (None, 0)
-        keep = [layers, [layer.layout for layer in layers], [st[0] for st in steps], [st[4] for st in steps], weights,
-                [blk.ln_2.weight for blk in self.blocks], [blk.ln_1.weight for blk in self.blocks], self.lnf.weight]
-        return sig, arr, bufs, keep
+        return arr, bufs
 
     # -- packed bf16 prefill ---------------------------------------------------------
     def _fused_prefill_ok(self, cache, idx: torch.Tensor, logits_index: torch.Tensor) -> bool:
