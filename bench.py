@@ -143,6 +143,7 @@ def e2e_c5(args, torch):
     tokens, stats = eng.generate(prompt, steps, top_k=1, prompt_lens=lens, return_stats=True)
     tps = stats["decode_tokens_per_sec"]
     launch = eng.last_decode_launch
+    issue = eng.last_decode_issue  # host issue and GPU time of eager steps 1 and 2 (the launch-mode decision)
     forced = {}
     if not args.no_eager_compare:  # both launch modes forced, same tokens checked
         for mode in (False, True):
@@ -174,6 +175,10 @@ def e2e_c5(args, torch):
                     "random-init weights, B 64, prompts U[64, 2048], paged KV page 16",
         "decode_tokens_per_sec": round(tps, 1),
         "decode_launch": launch,
+        "decode_issue_ms_per_step": None if issue is None else {
+            "host": round(issue[0] * 500.0, 3), "gpu": round(issue[1] * 500.0, 3),
+            "note": "eager steps 1 and 2 timed from one synchronisation: host clock around their issue, HIP events "
+                    "around their GPU work (per step; the engine replays graphs only when host >= 0.97 x gpu)"},
         "decode_tokens_per_sec_eager": forced.get("eager"),
         "decode_tokens_per_sec_graphs": forced.get("graphs"),
         "decode_path": "fused bf16 decode step (7 launches per layer: RoPE + append inside the attention launch, "

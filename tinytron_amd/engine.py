@@ -173,6 +173,7 @@ class InferenceEngine:
         use_graphs = paged and bool(self.use_graphs)
         auto = paged and self.use_graphs is None
         self.last_decode_launch = "graphs" if use_graphs else "eager"
+        self.last_decode_issue = None  # (host, GPU) seconds of eager steps 1 and 2 when the default decided
         if paged:
             cache.set_static_max_len(max(lens) + max_new_tokens)
         decode_t0 = time.perf_counter()
@@ -205,7 +206,9 @@ class InferenceEngine:
                     host_s = time.perf_counter() - h0
                     ev[1].record()
                     ev[1].synchronize()
-                    use_graphs = host_s >= GRAPH_HOST_RATIO * ev[0].elapsed_time(ev[1]) * 1e-3
+                    gpu_s = ev[0].elapsed_time(ev[1]) * 1e-3
+                    self.last_decode_issue = (host_s, gpu_s)
+                    use_graphs = host_s >= GRAPH_HOST_RATIO * gpu_s
                     self.last_decode_launch = "graphs" if use_graphs else "eager"
             else:
                 logits, cache = self.model(next_token.unsqueeze(-1), use_cache=True, past_key_values=cache,
