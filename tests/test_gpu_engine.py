@@ -383,3 +383,38 @@ def test_auto_launch_mode_gives_the_eager_tokens():
     (t0, lp0, mode0), (t1, lp1, mode1) = runs
     assert mode0 in ("eager", "graphs") and mode1 == "eager"
     assert torch.equal(t0, t1) and torch.equal(lp0, lp1)
+
+
+def test_eos_stops_the_batch_and_keeps_the_tokens_so_far():
+    """generate() stops at the step where every sequence drew eos_token_id
+    (engine.py:209-211): the output ends with that token, equals the run
+    without eos up to it, and the stats count the steps taken (ragged rows:
+    each sequence's tokens start at its own prompt end, the rest pad 0)."""
+    from tinytron_amd.engine import InferenceEngine
+    from tinytron_amd.model import GPT
+
+    cfg = _c1_config(num_layer=2, block_size=256, vocab_size=512)
+    model = GPT(cfg, device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(5)
+    prompt = torch.randint(0, cfg.vocab_size, (1, 20), generator=g)
+    eng = InferenceEngine(cfg, device=DEV, dtype=torch.bfloat16, kv_cache_page_size=16, paged_pool=True, model=model)
+    full, st = eng.generate(prompt, 12, top_k=1, return_stats=True)
+    full = full.cpu()
+    gen = full[0, 20:].tolist()
+    stop = next((k for k in range(2, len(gen)) if gen[k] not in gen[:k]), None)
+    if stop is None:
+        pytest.skip("greedy output repeats one token from the start")
+    cut, st2 = eng.generate(prompt, 12, top_k=1, eos_token_id=gen[stop], return_stats=True)
+    cut = cut.cpu()
+    assert cut.shape == (1, 20 + stop + 1)
+    assert torch.equal(cut[0], full[0, :20 + stop + 1])
+    assert st2["lengths"] == [20 + stop + 1]
+    # ragged batch, no early stop: every row's tokens follow its own prompt, then pad 0
+    lens = [5, 20]
+    prompt2 = torch.randint(0, cfg.vocab_size, (2, 20), generator=g)
+    toks, st3 = eng.generate(prompt2, 6, top_k=1, prompt_lens=lens, return_stats=True, return_logprobs=True)
+    toks = toks.cpu()
+    assert toks.shape == (2, 26) and st3["lengths"] == [11, 26]
+    assert torch.equal(toks[0, :5], prompt2[0, :5]) and torch.equal(toks[1, :20], prompt2[1])
+    assert bool((toks[0, 11:] == 0).all())
+    assert st3["token_log_probs"].shape == (2, 6)
